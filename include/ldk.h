@@ -1,0 +1,141 @@
+/*
+ * ldk.h: C ABI of the MI355X (gfx950) decode hot-path library `libldk_amd.so`.
+ *
+ * Covers the W4A16 int4-weight matmul, the FP8 (OCP e4m3) weight-only matmul, fused
+ * RMSNorm(+residual) and fused SwiGLU of Charlie-Gzz/llm-decode-kernels, plus the int4/fp8 weight
+ * format routines. Each entry point names the reference interface it replaces (paths relative to
+ * the reference repository).
+ *
+ * Conventions shared by every entry point:
+ *  - All tensor pointers are DEVICE pointers owned by the caller. The library never allocates,
+ *    frees, synchronizes or keeps a reference, so every call is safe inside hipGraph capture.
+ *  - `stream` is a hipStream_t (passed as void*); 0 means the legacy default stream.
+ *  - Matrices are row-major. `ld*` arguments are row strides in elements.
+ *  - Activations, scales, zeros and outputs are fp16 unless a `dtype` argument says otherwise.
+ *  - Return value: LDK_OK (0) or one of the LDK_ERR_* codes. On failure nothing is launched and
+ *    ldk_last_error() returns a message for the calling thread.
+ *  - Sizes are int64_t; every count must be > 0 unless stated.
+ */
+#ifndef LDK_H_
+#define LDK_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LDK_ABI_VERSION 1
+
+enum ldk_status {
+  LDK_OK = 0,
+  LDK_ERR_INVALID = 1,     /* bad argument: null pointer, size, shape or dtype */
+  LDK_ERR_ALIGN = 2,       /* pointer or row stride not aligned as the kernel requires */
+  LDK_ERR_UNSUPPORTED = 3, /* valid but not covered (e.g. M > 16 on the decode entry point) */
+  LDK_ERR_LAUNCH = 4       /* the HIP runtime rejected the launch */
+};
+
+enum ldk_dtype { LDK_F16 = 0, LDK_BF16 = 1, LDK_F32 = 2 };
+
+/* Flags for the matmul entry points (`flags`). Zero = let the library choose. */
+enum ldk_flags {
+  LDK_FACTORED = 1,  /* W4A16: sum x*(q - z) per group, scale once (w4a16.py:116-119, FACTORED) */
+  LDK_EXACT = 2,     /* W4A16: dequantize each weight to fp16 exactly as dequantize_ref first  */
+  LDK_PATH_VALU = 4, /* force the wave64 VALU (dot2) skinny kernel */
+  LDK_PATH_MFMA = 8  /* force the MFMA kernel */
+};
+
+/* ABI version (LDK_ABI_VERSION) the library was built with. */
+int ldk_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* ldk_last_error(void);
+
+/* ---------------------------------------------------------------------- int4 weight format */
+
+/* Packs q [K, N] int32 (values 0..15) into packed [K/8, N] int32: nibble i of word [r, n] is
+ * q[8r+i, n]. Replaces kernels/quant.py:20-28 (pack_int4). K % 8 == 0. */
+int ldk_int4_pack(const int32_t* q, int32_t* packed, int64_t K, int64_t N, void* stream);
+
+/* Inverse of ldk_int4_pack: packed [K/8, N] -> q [K, N] int32 in 0..15.
+ * Replaces kernels/quant.py:31-35 (unpack_int4). */
+int ldk_int4_unpack(const int32_t* packed, int32_t* q, int64_t K, int64_t N, void* stream);
+
+/* Round-to-nearest asymmetric int4 quantization of w [N, K] (dtype LDK_F16/BF16/F32) with group
+ * `group_size` along K: writes qweight [K/8, N] int32 and scales/zeros [K/group, N] in `dtype`.
+ * Bit-identical to kernels/quant.py:38-49 (quantize_rtn). K % group_size == 0, group_size % 8 == 0. */
+int ldk_quantize_rtn(const void* w, int dtype, int32_t* qweight, void* scales, void* zeros,
+                     int64_t N, int64_t K, int group_size, void* stream);
+
+/* Dequantizes to out [N, K] fp16 = (q - z) * s with one fp16 rounding, bit-identical to
+ * kernels/reference.py:27-36 (dequantize_ref). group_size a power of two >= 8. */
+int ldk_w4a16_dequant(const int32_t* qweight, const void* scales, const void* zeros, void* out,
+                      int64_t N, int64_t K, int group_size, void* stream);
+
+/* ------------------------------------------------------------------------------ W4A16 matmul */
+
+/* out [M, N] = x [M, K] @ dequant(qweight, scales, zeros)^T (+ bias [N]), fp32 accumulation,
+ * fp16 output. Replaces kernels/w4a16.py:301-330 (w4a16_matmul) and its launch paths
+ * w4a16.py:214-279. group_size a power of two >= 8 dividing K; N % 4 == 0; x, qweight, scales,
+ * zeros 16-byte aligned with ldx % 8 == 0.
+ *   block_n: output columns per workgroup (0 = tuned table),
+ *   split_k: K-slices reduced inside one workgroup (0 = tuned table),
+ *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_* (0 = tuned table).
+ * M <= 16 runs the decode kernels; M > 16 runs the MFMA GEMM. */
+int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                     const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M,
+                     int64_t N, int64_t K, int group_size, int block_n, int split_k, int flags,
+                     void* stream);
+
+/* Decode-only entry (M <= 16; M > 16 returns LDK_ERR_UNSUPPORTED). Replaces the native
+ * extension entry w4a16_decode of kernels/cuda/w4a16_decode.cu:136-181 and its wrapper
+ * kernels/cuda/w4a16_cuda.py:45-56. split_k as in ldk_w4a16_matmul (0 = tuned). */
+int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                     const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M,
+                     int64_t N, int64_t K, int group_size, int split_k, void* stream);
+
+/* The configuration the library would use for (M, N, K, group_size) with all-zero tuning
+ * arguments. Replaces the choice tables of kernels/w4a16.py:282-298 (_pick_decode_path) and
+ * kernels/cuda/w4a16_cuda.py:29-42 (_pick_split), which are exported by w4a16.py:333-355. */
+int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n,
+                     int* split_k, int* flags);
+
+/* ----------------------------------------------------------------------------- FP8 (W8A16) */
+
+/* Per-output-channel OCP e4m3 quantization of w [N, K] (dtype F16/BF16/F32): writes wq [K, N]
+ * (e4m3fn bytes) and scale [N] in `dtype`. Bit-identical to kernels/fp8.py:25-30 (quantize_fp8). */
+int ldk_fp8_quantize(const void* w, int dtype, uint8_t* wq, void* scale, int64_t N, int64_t K,
+                     void* stream);
+
+/* out [N, K] (scale's dtype, F16/BF16/F32) = e4m3(wq)^T * scale with one rounding.
+ * Bit-identical to kernels/fp8.py:33-35 (dequantize_fp8). */
+int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, void* out, int64_t N,
+                    int64_t K, void* stream);
+
+/* out [M, N] = x [M, K] @ (e4m3(wq) * scale)^T (+ bias), fp32 accumulation, fp16 out.
+ * wq [K, N] e4m3fn, scale [N] fp16. Replaces kernels/fp8.py:200-223 (w8a16_matmul) and its
+ * kernels fp8.py:42-127. N % 16 == 0 and 16-byte aligned wq; block_n/split_k/flags as W4A16. */
+int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale,
+                     const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                     int block_n, int split_k, int flags, void* stream);
+
+/* ---------------------------------------------------------------------- RMSNorm and SwiGLU */
+
+/* Per row of x [M, N]: h = x (+ residual, fp16 add, written to res_out); out = weight * fp16(
+ * h * rsqrt(mean(h^2) + eps)). residual/res_out both NULL or both set. Replaces
+ * kernels/rmsnorm.py:44-68 (rmsnorm) and its kernel rmsnorm.py:15-37. */
+int ldk_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight,
+                void* out, int64_t ldo, void* res_out, int64_t ldro, int64_t M, int64_t N,
+                float eps, void* stream);
+
+/* out [M, I] = fp16(silu(gate)) * up, silu in fp32. gate/up may be strided views of one fused
+ * [M, 2I] tensor. Replaces kernels/swiglu.py:49-61 (swiglu, swiglu_fused) and its kernel
+ * swiglu.py:14-28. */
+int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out, int64_t ldo,
+               int64_t M, int64_t I, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LDK_H_ */

@@ -1,0 +1,152 @@
+// Fused RMSNorm(+residual) and fused SwiGLU for gfx950.
+//
+// RMSNorm replaces kernels/rmsnorm.py:15-68 of the reference, SwiGLU replaces
+// kernels/swiglu.py:14-61. Both keep the reference's fp16 rounding steps (kernels/reference.py:9-24):
+//   rmsnorm: h = fp16(x + r) (written as the new residual); var = sum(h^2) / N in fp32;
+//            out = w * fp16(h * (1 / sqrt(var + eps)))  (fp16 multiply, one rounding)
+//   swiglu:  out = fp16(g / (1 + exp(-g))) * u        (silu in fp32, fp16 multiply)
+// Both are pure streaming kernels: every element is read once and written once, 16 bytes per lane.
+#include "ldk_common.h"
+
+namespace {
+
+struct RmsArgs {
+  const half_t* x;
+  int64_t ldx;
+  const half_t* r;
+  int64_t ldr;
+  const half_t* w;
+  half_t* out;
+  int64_t ldo;
+  half_t* res_out;
+  int64_t ldro;
+  int M, N;
+  float eps;
+};
+
+// One workgroup per row; each thread keeps CPT chunks of VEC halves in registers between the
+// sum-of-squares pass and the normalize pass, so the row is read from memory once.
+template <int VEC, int CPT, bool RES>
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
+  typedef _Float16 hv_t __attribute__((ext_vector_type(VEC)));
+  __shared__ float wsum[16];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int nchunk = a.N / VEC;
+  const half_t* x = a.x + (int64_t)row * a.ldx;
+  hv_t h[CPT];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + i * NT;
+    if (c < nchunk) {
+      hv_t v = *reinterpret_cast<const hv_t*>(x + c * VEC);
+      if constexpr (RES) {
+        v = v + *reinterpret_cast<const hv_t*>(a.r + (int64_t)row * a.ldr + c * VEC);  // fp16 add
+        *reinterpret_cast<hv_t*>(a.res_out + (int64_t)row * a.ldro + c * VEC) = v;
+      }
+      h[i] = v;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float f = (float)v[j];
+        ss = __builtin_fmaf(f, f, ss);
+      }
+    }
+  }
+  ss = ldk::sum_lanes_strided<1>(ss);
+  const int nw = NT >> 6;
+  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int i = 0; i < nw; ++i) tot += wsum[i];
+  const float rs = 1.0f / __builtin_sqrtf(tot / (float)a.N + a.eps);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + i * NT;
+    if (c < nchunk) {
+      const hv_t wv = *reinterpret_cast<const hv_t*>(a.w + c * VEC);
+      hv_t o;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) o[j] = (half_t)((float)h[i][j] * rs);
+      *reinterpret_cast<hv_t*>(a.out + (int64_t)row * a.ldo + c * VEC) = wv * o;  // fp16 multiply
+    }
+  }
+}
+
+struct SwigluArgs {
+  const half_t* g;
+  int64_t ldg;
+  const half_t* u;
+  int64_t ldu;
+  half_t* out;
+  int64_t ldo;
+  int64_t M, I;
+};
+
+// One thread per VEC consecutive outputs of one row.
+template <int VEC>
+__global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
+  typedef _Float16 hv_t __attribute__((ext_vector_type(VEC)));
+  const int64_t per_row = a.I / VEC;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.M * per_row) return;
+  const int64_t row = i / per_row, c = (i - row * per_row) * VEC;
+  const hv_t g = *reinterpret_cast<const hv_t*>(a.g + row * a.ldg + c);
+  const hv_t u = *reinterpret_cast<const hv_t*>(a.u + row * a.ldu + c);
+  hv_t s;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const float f = (float)g[j];
+    s[j] = (half_t)(f / (1.0f + expf(-f)));
+  }
+  *reinterpret_cast<hv_t*>(a.out + row * a.ldo + c) = s * u;  // fp16 multiply
+}
+
+template <int VEC, bool RES>
+int launch_rms(const RmsArgs& a, hipStream_t s) {
+  const int nchunk = a.N / VEC;
+  int nt = ((nchunk + 63) / 64) * 64;
+  if (nt > 1024) nt = 1024;
+  const int cpt = (nchunk + nt - 1) / nt;
+  (void)hipGetLastError();
+  if (cpt <= 1) rmsnorm_kernel<VEC, 1, RES><<<a.M, nt, 0, s>>>(a);
+  else if (cpt <= 2) rmsnorm_kernel<VEC, 2, RES><<<a.M, nt, 0, s>>>(a);
+  else if (cpt <= 4) rmsnorm_kernel<VEC, 4, RES><<<a.M, nt, 0, s>>>(a);
+  else if (cpt <= 8) rmsnorm_kernel<VEC, 8, RES><<<a.M, nt, 0, s>>>(a);
+  else return ldk::fail(LDK_ERR_UNSUPPORTED, "rmsnorm: N=%d too large", a.N);
+  return ldk::check_launch("rmsnorm");
+}
+
+}  // namespace
+
+extern "C" int ldk_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight, void* out,
+                           int64_t ldo, void* res_out, int64_t ldro, int64_t M, int64_t N, float eps, void* stream) {
+  if (!x || !weight || !out) return ldk::fail(LDK_ERR_INVALID, "rmsnorm: null pointer");
+  if ((residual == nullptr) != (res_out == nullptr)) return ldk::fail(LDK_ERR_INVALID, "rmsnorm: residual and res_out must both be given or both be null");
+  if (M <= 0 || N <= 0) return ldk::fail(LDK_ERR_INVALID, "rmsnorm: M=%lld N=%lld must be positive", (long long)M, (long long)N);
+  if (M > INT32_MAX || N > 65536) return ldk::fail(LDK_ERR_UNSUPPORTED, "rmsnorm: M=%lld N=%lld too large", (long long)M, (long long)N);
+  if (ldx < N || ldo < N || (residual && (ldr < N || ldro < N))) return ldk::fail(LDK_ERR_INVALID, "rmsnorm: row stride smaller than N");
+  const RmsArgs a{(const half_t*)x, ldx, (const half_t*)residual, ldr, (const half_t*)weight, (half_t*)out, ldo,
+                  (half_t*)res_out, ldro, (int)M, (int)N, eps};
+  bool vec = N % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0 && ldk::aligned(x, 16) && ldk::aligned(out, 16) && ldk::aligned(weight, 16);
+  if (residual) vec = vec && ldr % 8 == 0 && ldro % 8 == 0 && ldk::aligned(residual, 16) && ldk::aligned(res_out, 16);
+  hipStream_t s = (hipStream_t)stream;
+  if (vec) return residual ? launch_rms<8, true>(a, s) : launch_rms<8, false>(a, s);
+  return residual ? launch_rms<1, true>(a, s) : launch_rms<1, false>(a, s);
+}
+
+extern "C" int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out, int64_t ldo, int64_t M,
+                          int64_t I, void* stream) {
+  if (!gate || !up || !out) return ldk::fail(LDK_ERR_INVALID, "swiglu: null pointer");
+  if (M <= 0 || I <= 0) return ldk::fail(LDK_ERR_INVALID, "swiglu: M=%lld I=%lld must be positive", (long long)M, (long long)I);
+  if (ldg < I || ldu < I || ldo < I) return ldk::fail(LDK_ERR_INVALID, "swiglu: row stride smaller than I");
+  const SwigluArgs a{(const half_t*)gate, ldg, (const half_t*)up, ldu, (half_t*)out, ldo, M, I};
+  const bool vec = I % 8 == 0 && ldg % 8 == 0 && ldu % 8 == 0 && ldo % 8 == 0 && ldk::aligned(gate, 16) &&
+                   ldk::aligned(up, 16) && ldk::aligned(out, 16);
+  const int64_t n = M * (vec ? I / 8 : I);
+  if ((n + 255) / 256 > INT32_MAX) return ldk::fail(LDK_ERR_UNSUPPORTED, "swiglu: too large");
+  (void)hipGetLastError();
+  if (vec) swiglu_kernel<8><<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(a);
+  else swiglu_kernel<1><<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(a);
+  return ldk::check_launch("swiglu");
+}

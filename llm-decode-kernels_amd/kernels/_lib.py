@@ -1,0 +1,143 @@
+"""ctypes binding of libldk_amd.so, the gfx950 HIP kernel library (C ABI in include/ldk.h).
+
+Every public op of this package calls into this library with raw device pointers and the torch
+current stream. There is no CPU path: if the library is missing or the tensors are not on a
+ROCm GPU, the ops raise.
+
+The library links the HIP runtime by soname (libamdhip64.so.7). torch is imported first so that
+the runtime torch already loaded satisfies that soname: one HIP runtime per process, so streams
+and device pointers are shared with torch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).with_name("libldk_amd.so")
+
+# Status codes (enum ldk_status).
+OK, ERR_INVALID, ERR_ALIGN, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3, 4
+# dtype codes (enum ldk_dtype).
+F16, BF16, F32 = 0, 1, 2
+# flags (enum ldk_flags).
+FACTORED, EXACT, PATH_VALU, PATH_MFMA = 1, 2, 4, 8
+
+_DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+_vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> argtypes, mirroring include/ldk.h.
+SIGNATURES = {
+    "ldk_abi_version": [],
+    "ldk_last_error": [],
+    "ldk_int4_pack": [_vp, _vp, _i64, _i64, _vp],
+    "ldk_int4_unpack": [_vp, _vp, _i64, _i64, _vp],
+    "ldk_quantize_rtn": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "ldk_w4a16_dequant": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "ldk_w4a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32,
+                         _i32, _i32, _i32, _vp],
+    "ldk_w4a16_decode": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
+                         _vp],
+    "ldk_w4a16_config": [_i64, _i64, _i64, _i32, _ip, _ip, _ip],
+    "ldk_fp8_quantize": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
+    "ldk_fp8_dequant": [_vp, _vp, _i32, _vp, _i64, _i64, _vp],
+    "ldk_w8a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
+                         _vp],
+    "ldk_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _f32, _vp],
+    "ldk_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    """libldk_amd.so has not been built (run `python -c "import __graft_entry__ as g; g.build()"`
+    or `python llm-decode-kernels_amd/build.py`)."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library with argument/return types set."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryMissing(f"{LIB_PATH} not found: build it first")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, argtypes in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = ctypes.c_char_p if name == "ldk_last_error" else ctypes.c_int
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise for a non-zero status: ValueError for bad arguments, RuntimeError otherwise (the
+    reference's native extension raises RuntimeError from TORCH_CHECK)."""
+    if status == OK:
+        return
+    msg = (load().ldk_last_error() or b"").decode(errors="replace")
+    if status in (ERR_INVALID, ERR_ALIGN):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float16, bfloat16 or float32") from None
+
+
+def require_gpu(*tensors: torch.Tensor | None, what: str) -> torch.device:
+    """All given tensors must live on one ROCm GPU. There is no CPU implementation."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"{what}: tensors must be on a ROCm GPU (got {t.device}); "
+                               "this library has no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{what}: tensors on different devices ({dev} and {t.device})")
+    if dev is None:
+        raise RuntimeError(f"{what}: no tensor given")
+    return dev
+
+
+class device_guard:
+    """Make `dev` current for the duration of a launch when it is not already."""
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.dev.index is not None and self.dev.index != cur:
+            self.prev = cur
+            torch.cuda.set_device(self.dev.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False

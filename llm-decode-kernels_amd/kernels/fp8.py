@@ -1,0 +1,84 @@
+"""FP8 weight-only matmul (W8A16) on gfx950: y = x @ (Wq * s).T, OCP e4m3 weights.
+
+Drop-in for the reference's `kernels/fp8.py`: weights are float8 e4m3fn with one scale per output
+channel, stored [K, N] (N contiguous). gfx950 decodes OCP e4m3 natively (v_cvt_pk_f32_fp8), so
+the weight bytes go straight from a 128-bit load to fp32 FMAs; the scale is applied once after
+the K reduction (fp8.py:120). Quantize/dequantize run HIP kernels that reproduce the reference
+bit for bit. Decode shapes (M <= 16) run the wave64 HIP GEMV with an in-workgroup split-K;
+M > 16 dequantizes once and runs a torch fp16 GEMM.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from kernels import _lib
+
+FP8 = torch.float8_e4m3fn
+FP8_MAX = 448.0
+
+
+def quantize_fp8(weight: torch.Tensor):
+    """[N, K] -> (wq float8_e4m3fn [K, N], scale [N] in weight's dtype) with per-output-channel
+    absmax scaling (fp8.py:25-30)."""
+    N, K = weight.shape
+    dev = _lib.require_gpu(weight, what="quantize_fp8")
+    w = weight.contiguous()
+    code = _lib.dtype_code(w.dtype)
+    wq = torch.empty((K, N), dtype=FP8, device=dev)
+    scale = torch.empty((N,), dtype=w.dtype, device=dev)
+    with _lib.device_guard(dev):
+        _lib.check(_lib.load().ldk_fp8_quantize(_lib.ptr(w), code, _lib.ptr(wq), _lib.ptr(scale),
+                                                N, K, _lib.stream(dev)), "quantize_fp8")
+    return wq, scale
+
+
+def dequantize_fp8(wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """-> [N, K] in scale's dtype (fp8.py:33-35)."""
+    K, N = wq.shape
+    dev = _lib.require_gpu(wq, scale, what="dequantize_fp8")
+    code = _lib.dtype_code(scale.dtype)
+    out = torch.empty((N, K), dtype=scale.dtype, device=dev)
+    q = wq.contiguous()
+    s = scale.contiguous()
+    with _lib.device_guard(dev):
+        _lib.check(_lib.load().ldk_fp8_dequant(_lib.ptr(q), _lib.ptr(s), code, _lib.ptr(out), N, K,
+                                               _lib.stream(dev)), "dequantize_fp8")
+    return out
+
+
+def fp8_bytes(N: int, K: int) -> int:
+    """Weight bytes plus fp16 scales (fp8.py:38-39)."""
+    return N * K + N * 2
+
+
+def w8a16_matmul(x, wq, scale, bias=None, config=None):
+    """y = x @ (wq * scale).T (+ bias). x: [..., K] fp16, wq: float8 [K, N], scale: fp16 [N]
+    (fp8.py:200-223). `config` honours `GEMV`, `block_n` and `split_k`; Triton tile keys are
+    ignored."""
+    K = x.shape[-1]
+    N = wq.shape[1]
+    assert wq.shape[0] == K
+    dev = _lib.require_gpu(x, wq, scale, bias, what="w8a16_matmul")
+    if x.dtype != torch.float16 or scale.dtype != torch.float16:
+        raise ValueError("w8a16_matmul: x and scale must be float16")
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    q = wq if wq.is_contiguous() else wq.contiguous()
+    s = scale.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    if M <= 16:
+        cfg = config or {}
+        flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        with _lib.device_guard(dev):
+            st = _lib.load().ldk_w8a16_matmul(
+                _lib.ptr(x2), x2.stride(0), _lib.ptr(q), _lib.ptr(s), _lib.ptr(b), _lib.ptr(out),
+                out.stride(0), M, N, K, int(cfg.get("block_n", 0)), int(cfg.get("split_k", 0)),
+                flags, _lib.stream(dev))
+        _lib.check(st, "w8a16_matmul")
+    else:
+        out = torch.nn.functional.linear(x2, dequantize_fp8(q, s), b)
+    return out.view(*x.shape[:-1], N)

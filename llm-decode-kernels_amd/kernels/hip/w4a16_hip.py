@@ -1,0 +1,53 @@
+"""The native W4A16 decode entry point, `ldk_w4a16_decode`, for M <= 16 rows.
+
+Counterpart of the reference's `kernels/cuda/w4a16_cuda.py` (`w4a16_decode_cuda`, lines 45-56)
+with the same contract: same arguments, M <= 16 rows, RuntimeError for more rows (the reference's
+TORCH_CHECK, tested at tests/test_w4a16_cuda.py:43-45). `split_k` is the number of K lanes per
+output column inside one workgroup (0/None = the library's table); the reference's split is a
+grid dimension with fp32 atomics instead.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from kernels import _lib
+
+_split_choice: dict[tuple, int] = {}
+
+
+def w4a16_decode_hip(x, qweight, scales, zeros, group_size=128, bias=None, split_k=None):
+    """y = x @ dequant(W).T for M <= 16 rows. Same contract as kernels.w4a16.w4a16_matmul."""
+    K = x.shape[-1]
+    N = qweight.shape[1]
+    dev = _lib.require_gpu(x, qweight, scales, zeros, bias, what="w4a16_decode_hip")
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    with _lib.device_guard(dev):
+        st = _lib.load().ldk_w4a16_decode(
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(qweight.contiguous()),
+            _lib.ptr(scales.contiguous()), _lib.ptr(zeros.contiguous()), _lib.ptr(b),
+            _lib.ptr(out), out.stride(0), M, N, K, group_size, int(split_k or 0),
+            _lib.stream(dev))
+    if st == _lib.ERR_UNSUPPORTED:
+        raise RuntimeError(_lib.load().ldk_last_error().decode())
+    _lib.check(st, "w4a16_decode_hip")
+    if split_k:
+        _split_choice[(min(1 << (M - 1).bit_length(), 16), N, K, bias is not None)] = split_k
+    return out.view(*x.shape[:-1], N)
+
+
+def split_choices() -> dict:
+    return {str(k): v for k, v in _split_choice.items()}
+
+
+def export_choices() -> dict:
+    return {",".join(map(str, k)): v for k, v in _split_choice.items()}
+
+
+def import_choices(choices: dict) -> None:
+    for k, v in choices.items():
+        m, n, kk, b = k.split(",")
+        _split_choice[(int(m), int(n), int(kk), b == "True")] = v

@@ -1,0 +1,125 @@
+"""W4A16 matmul on gfx950: y = x @ dequant(W).T (+ bias), int4 weights, fp16 activations.
+
+Drop-in for the reference's `kernels/w4a16.py` (same `w4a16_matmul` signature, same int4 format
+from `kernels.quant`). Decode shapes (M <= 16) run one hand-written HIP kernel from
+libldk_amd.so whose tile and K-split come from the library's per-shape table:
+
+- each workgroup owns a strip of output columns and ALL of K; lanes split K and the partial sums
+  are reduced inside the workgroup (DPP/permlane within a wave, LDS across waves), so there is
+  no atomic, zero-fill or cast launch (the reference's split paths add two elementwise launches,
+  w4a16.py:218-219,272-275);
+- M = 1 uses the FACTORED inner loop s * (sum x*q - z * sum x) (w4a16.py:116-119); 2 <= M <= 16
+  dequantizes each weight exactly as dequantize_ref and accumulates with v_dot2_f32_f16.
+
+Prefill shapes (M > 16) dequantize the weight once with the bit-exact HIP dequantizer and run
+one hipBLASLt/rocBLAS fp16 GEMM through torch (the reference runs its Triton tensor-core GEMM
+there, w4a16.py:264-268).
+
+`config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
+`GEMV` (force the VALU decode kernel), `FACTORED` (True: factored M=1 loop; False: exact
+dequantize-then-dot), `block_n` (columns per workgroup, 4..64) and `split_k` (K lanes per
+column inside the workgroup). Triton tile keys (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, GROUP_M)
+describe Triton programs and are ignored.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from kernels import _lib
+from kernels.quant import PACK, dequantize
+
+_decode_choice: dict[tuple, str] = {}  # (m_key, N, K, bias) -> chosen configuration, for export
+
+
+def _next_pow2(n: int) -> int:
+    return 1 << max(0, (n - 1).bit_length())
+
+
+def _flags_from_config(config: dict | None, M: int) -> tuple[int, int, int]:
+    if not config:
+        return 0, 0, 0
+    flags = 0
+    if config.get("GEMV"):
+        flags |= _lib.PATH_VALU
+    if "FACTORED" in config:
+        if config["FACTORED"] and M == 1:
+            flags |= _lib.FACTORED
+        elif not config["FACTORED"]:
+            flags |= _lib.EXACT
+    return int(config.get("block_n", 0)), int(config.get("split_k", 0)), flags
+
+
+def _decode(x2, qweight, scales, zeros, bias, group_size, block_n, split_k, flags, out):
+    M, K = x2.shape
+    N = qweight.shape[1]
+    dev = x2.device
+    with _lib.device_guard(dev):
+        st = _lib.load().ldk_w4a16_matmul(
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(qweight), _lib.ptr(scales), _lib.ptr(zeros),
+            _lib.ptr(bias), _lib.ptr(out), out.stride(0), M, N, K, group_size, block_n, split_k,
+            flags, _lib.stream(dev))
+    _lib.check(st, "w4a16_matmul")
+    return out
+
+
+def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=None):
+    """y = x @ dequant(W).T (+ bias). x: [..., K] fp16. Returns [..., N] fp16 (w4a16.py:301-330)."""
+    K = x.shape[-1]
+    N = qweight.shape[1]
+    assert qweight.shape[0] * 8 == K and K % group_size == 0
+    dev = _lib.require_gpu(x, qweight, scales, zeros, bias, what="w4a16_matmul")
+    if x.dtype != torch.float16 or scales.dtype != torch.float16 or zeros.dtype != torch.float16:
+        raise ValueError("w4a16_matmul: x, scales and zeros must be float16")
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    qw = qweight if qweight.is_contiguous() else qweight.contiguous()
+    s = scales if scales.is_contiguous() else scales.contiguous()
+    z = zeros if zeros.is_contiguous() else zeros.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    if M <= 16:
+        block_n, split_k, flags = _flags_from_config(config, M)
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
+        key = (min(_next_pow2(M), 16), N, K, bias is not None)
+        if key not in _decode_choice:
+            _decode_choice[key] = config_for(M, N, K, group_size)
+    else:
+        w = dequantize(qw, s, z, group_size)
+        out = torch.nn.functional.linear(x2, w, b)
+    return out.view(*x.shape[:-1], N)
+
+
+def config_for(M: int, N: int, K: int, group_size: int = 128) -> str:
+    """The library's table choice for a decode shape, as 'block_n=..,split_k=..,flags=..'."""
+    bn, sk, fl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(_lib.load().ldk_w4a16_config(M, N, K, group_size, ctypes.byref(bn),
+                                            ctypes.byref(sk), ctypes.byref(fl)), "w4a16_config")
+    mode = "factored" if fl.value & _lib.FACTORED else "exact"
+    return f"block_n={bn.value},split_k={sk.value},{mode}"
+
+
+def export_choices() -> dict:
+    """Configurations used so far (w4a16.py:333-335)."""
+    return {",".join(map(str, k)): v for k, v in _decode_choice.items()}
+
+
+def import_choices(choices: dict) -> None:
+    """Accepts an export_choices() dict (w4a16.py:338-342). The library's choice is a pure
+    function of the shape, so importing only records the entries."""
+    for k, v in choices.items():
+        m, n, kk, b = k.split(",")
+        _decode_choice[(int(m), int(n), int(kk), b == "True")] = v
+
+
+def best_configs() -> dict:
+    """Configurations used so far, for the results JSON (w4a16.py:345-355)."""
+    return {"decode_path": {str(k): v for k, v in _decode_choice.items()}}
+
+
+__all__ = ["w4a16_matmul", "export_choices", "import_choices", "best_configs", "config_for",
+           "PACK"]

@@ -1,0 +1,135 @@
+"""The C-ABI library (libldk_amd.so) on the CPU: it loads, exports every entry point declared in
+include/ldk.h, shares torch's HIP runtime, and rejects bad arguments with status codes before
+launching anything (no GPU is touched by these tests)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from kernels import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ldk.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:int|const char\*)\s+(ldk_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_what_the_binding_binds():
+    assert _declared() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define LDK_ABI_VERSION (\d+)", HEADER.read_text())
+    assert _lib.load().ldk_abi_version() == int(m.group(1))
+
+
+def test_one_hip_runtime_per_process():
+    """The library binds the libamdhip64 that torch loaded (one runtime, shared streams)."""
+    _lib.load()
+    maps = Path("/proc/self/maps").read_text().splitlines()
+    hip = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(hip) == 1, hip
+
+
+def _err(st):
+    return st, _lib.load().ldk_last_error().decode()
+
+
+def test_null_pointer_rejected():
+    lib = _lib.load()
+    st, msg = _err(lib.ldk_w4a16_matmul(None, 1536, None, None, None, None, None, 17920, 1, 17920,
+                                        1536, 128, 0, 0, 0, None))
+    assert st == _lib.ERR_INVALID and "null" in msg
+
+
+def test_decode_rejects_more_than_16_rows():
+    """Reference: w4a16_decode_cuda raises for M = 17 (tests/test_w4a16_cuda.py:43-45)."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, msg = _err(lib.ldk_w4a16_decode(p, 128, p, p, p, None, p, 128, 17, 128, 128, 128, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "16" in msg
+
+
+@pytest.mark.parametrize("K,gs", [(1536, 96), (1536, 4), (1000, 128)])
+def test_bad_group_size_rejected(K, gs):
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, _ = _err(lib.ldk_w4a16_matmul(p, K, p, p, p, None, p, 64, 1, 64, K, gs, 0, 0, 0, None))
+    assert st == _lib.ERR_INVALID
+
+
+def test_misaligned_pointer_rejected():
+    lib = _lib.load()
+    p, bad = ctypes.c_void_p(256), ctypes.c_void_p(258)
+    st, _ = _err(lib.ldk_w4a16_matmul(bad, 256, p, p, p, None, p, 64, 1, 64, 256, 128, 0, 0, 0, None))
+    assert st == _lib.ERR_ALIGN
+
+
+def test_factored_needs_one_row():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, _ = _err(lib.ldk_w4a16_matmul(p, 256, p, p, p, None, p, 64, 2, 64, 256, 128, 0, 0,
+                                      _lib.FACTORED, None))
+    assert st == _lib.ERR_UNSUPPORTED
+
+
+def test_rmsnorm_residual_pairing_rejected():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, _ = _err(lib.ldk_rmsnorm(p, 64, p, 64, p, p, 64, None, 64, 1, 64, 1e-6, None))
+    assert st == _lib.ERR_INVALID
+
+
+def test_w8a16_n_multiple_of_16():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, _ = _err(lib.ldk_w8a16_matmul(p, 64, p, p, None, p, 40, 1, 40, 64, 0, 0, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED
+
+
+def test_config_query():
+    bn, sk, fl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    st = _lib.load().ldk_w4a16_config(1, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
+                                      ctypes.byref(fl))
+    assert st == 0 and bn.value in (4, 8, 16, 32, 64) and sk.value > 0
+    assert fl.value & _lib.FACTORED
+
+
+def test_python_ops_refuse_cpu_tensors():
+    """No CPU path: the product ops raise instead of computing on the host."""
+    from kernels.quant import quantize_rtn
+    from kernels.rmsnorm import rmsnorm
+    from kernels.w4a16 import w4a16_matmul
+
+    w = torch.randn(64, 128).half()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        quantize_rtn(w)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        rmsnorm(torch.randn(2, 64).half(), torch.ones(64).half())
+    qw = torch.zeros(16, 64, dtype=torch.int32)
+    s = torch.ones(1, 64).half()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        w4a16_matmul(torch.randn(1, 128).half(), qw, s, s)
+
+
+def test_reference_assertions_kept():
+    """Shape asserts of the reference wrappers are kept (w4a16.py:309, quant.py:41)."""
+    from kernels.quant import quantize_rtn
+    from kernels.w4a16 import w4a16_matmul
+
+    with pytest.raises(AssertionError):
+        quantize_rtn(torch.randn(8, 100).half())
+    with pytest.raises(AssertionError):
+        w4a16_matmul(torch.randn(1, 128).half(), torch.zeros(8, 4, dtype=torch.int32),
+                     torch.ones(1, 4).half(), torch.ones(1, 4).half())

@@ -1,0 +1,90 @@
+"""FP8 (OCP e4m3) kernels vs the oracle: quantize and dequantize bit-exact, gfx950's hardware
+e4m3 decode checked on every finite code, W8A16 matmul within the north-star tolerance."""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_north_star, bits16, dev, to_np
+from kernels.bench import cases
+from kernels.fp8 import FP8, dequantize_fp8, quantize_fp8, w8a16_matmul
+from oracle import fp8 as of
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("N,K", [(17920, 1536), (1536, 8960), (64, 256)])
+def test_quantize_bit_exact(N, K):
+    w, _ = cases.w4a16_case(1, N, K, seed=3)
+    wq, s = quantize_fp8(w.cuda())
+    owq, os_ = of.quantize_fp8(w.numpy())
+    assert wq.dtype == FP8 and wq.shape == (K, N) and s.dtype == torch.float16
+    assert np.array_equal(to_np(wq.view(torch.uint8)), owq)
+    assert np.array_equal(bits16(s), bits16(os_))
+
+
+def test_quantize_fp32_and_bf16_weights():
+    w = torch.randn(48, 384, generator=cases.gen(11)) * 0.03
+    wq, s = quantize_fp8(w.cuda())
+    owq, os_ = of.quantize_fp8(w.numpy())
+    assert np.array_equal(to_np(wq.view(torch.uint8)), owq)
+    assert np.array_equal(to_np(s).view(np.uint32), os_.view(np.uint32))
+    wb = w.bfloat16()
+    wq, s = quantize_fp8(wb.cuda())
+    owq, os_ = of.quantize_fp8(wb.float().numpy())
+    assert np.array_equal(to_np(wq.view(torch.uint8)), owq)
+    assert torch.equal(s.cpu().view(torch.int16), torch.from_numpy(os_).bfloat16().view(torch.int16))
+
+
+def test_dequantize_bit_exact():
+    w, _ = cases.w4a16_case(1, 1536, 1536, seed=3)
+    owq, os_ = of.quantize_fp8(w.numpy())
+    out = dequantize_fp8(dev(owq).view(FP8), dev(os_))
+    assert np.array_equal(bits16(out), bits16(of.dequantize_fp8(owq, os_)))
+
+
+def test_hardware_decode_every_finite_code():
+    """x row m = e_m and scale 1: y[m, n] = e4m3(wq[m, n]) exactly (fp16 holds every e4m3 value).
+    16 rows x 256 columns cover all 254 finite codes."""
+    K, N = 16, 256
+    codes = ((np.arange(K)[:, None] * 16 + np.arange(N)[None, :]) % 256).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    x = torch.zeros(16, K, dtype=torch.float16, device="cuda")
+    x[torch.arange(16), torch.arange(16)] = 1.0
+    out = w8a16_matmul(x, dev(codes).view(FP8), torch.ones(N, dtype=torch.float16, device="cuda"))
+    ref = of.e4m3_decode(codes).astype(np.float16)
+    got = to_np(out)
+    nz = ref != 0
+    assert np.array_equal(bits16(got)[nz], bits16(ref)[nz])
+    assert np.all(got[~nz] == 0)
+
+
+def _run(M, N, K, seed=3, bias=False, config=None):
+    w, x = cases.w4a16_case(M, N, K, seed)
+    owq, os_ = of.quantize_fp8(w.numpy())
+    b = (torch.randn(N, generator=cases.gen(seed + 50)) * 0.1).half() if bias else None
+    out = w8a16_matmul(x.cuda(), dev(owq).view(FP8), dev(os_), bias=None if b is None else b.cuda(),
+                       config=config)
+    assert out.shape == (M, N) and out.dtype == torch.float16
+    return assert_north_star(out, of.w8a16_ref(x.numpy(), owq, os_, None if b is None else b.numpy()))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (5, 48, 96), (17, 96, 256), (2, 48, 256)])
+def test_small(M, N, K):
+    _run(M, N, K)
+
+
+def test_bias_and_gemv_config():
+    _run(1, 48, 256, bias=True, config={"GEMV": True})
+    _run(3, 64, 256, bias=True)
+
+
+@pytest.mark.parametrize("block_n", [16, 32, 64, 128])
+def test_block_n(block_n):
+    _run(1, 1536, 1536, config={"block_n": block_n})
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
+@pytest.mark.parametrize("name,N,K", cases.QWEN_LINEARS)
+def test_config3_qwen_shapes(name, N, K, M):
+    _run(M, N, K)

@@ -1,0 +1,159 @@
+"""W4A16 HIP kernels vs the oracle's fp32 dequantize-then-matmul (kernels/reference.py:39-45) on
+the same seeded inputs, through the C ABI. Acceptance (north star): max-abs <= 2e-2 and
+relative-L2 <= 1e-3 against the fp32 reference; dequantized weights bit-exact (checked directly
+by the one-hot tests: x = e_k returns column k of the dequantized weight exactly)."""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_north_star, bits16, dev, to_np
+from kernels.bench import cases
+from kernels.hip.w4a16_hip import w4a16_decode_hip
+from kernels.w4a16 import w4a16_matmul
+from oracle import quant as oq
+from oracle.reference import dequantize_ref, w4a16_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _make(M, N, K, seed, gs=128, bias=False):
+    w, x = cases.w4a16_case(M, N, K, seed)
+    qw, s, z = oq.quantize_rtn(w.numpy(), gs)
+    b = (torch.randn(N, generator=cases.gen(seed + 100)) * 0.1).half().numpy() if bias else None
+    return x.numpy(), qw, s, z, b
+
+
+def _run(M, N, K, seed=2, gs=128, bias=False, config=None, entry=w4a16_matmul):
+    x, qw, s, z, b = _make(M, N, K, seed, gs, bias)
+    out = entry(dev(x), dev(qw), dev(s), dev(z), gs, bias=None if b is None else dev(b),
+                **({"config": config} if config is not None else {}))
+    assert out.shape == (M, N) and out.dtype == torch.float16
+    return assert_north_star(out, w4a16_ref(x, qw, s, z, gs, b))
+
+
+# ---------------------------------------------------------------- reference test shapes
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (3, 40, 128), (17, 96, 384), (5, 64, 256)])
+def test_small(M, N, K):
+    _run(M, N, K)
+
+
+def test_bias():
+    _run(1, 64, 256, bias=True)
+    _run(4, 64, 256, bias=True)
+
+
+@pytest.mark.parametrize("factored", [True, False])
+@pytest.mark.parametrize("N,K", [(64, 256), (40, 384), (96, 128)])
+def test_gemv_modes(N, K, factored):
+    _run(1, N, K, config={"GEMV": True, "FACTORED": factored})
+
+
+@pytest.mark.parametrize("block_n", [4, 8, 16, 32, 64])
+def test_block_n_variants(block_n):
+    _run(1, 1536, 1536, config={"block_n": block_n})
+    _run(4, 1536, 1536, config={"block_n": block_n})
+
+
+@pytest.mark.parametrize("split_k", [16, 32, 64, 128])
+def test_split_k_variants(split_k):
+    _run(1, 1536, 1536, config={"block_n": 32, "split_k": split_k})
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256])
+def test_group_sizes(gs):
+    _run(1, 256, 1024, gs=gs)
+    _run(2, 256, 1024, gs=gs)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 7, 8, 9, 12, 16])
+def test_all_decode_rows(M):
+    _run(M, 1536, 1536)
+
+
+def test_odd_n_and_bias():
+    _run(5, 1000, 1024, bias=True)
+    _run(1, 132, 256, bias=True)
+
+
+def test_3d_input():
+    x, qw, s, z, _ = _make(6, 32, 128, 3)
+    out = w4a16_matmul(dev(x).view(2, 3, 128), dev(qw), dev(s), dev(z))
+    assert out.shape == (2, 3, 32)
+    assert_north_star(out.view(6, 32), w4a16_ref(x, qw, s, z))
+
+
+def test_strided_rows():
+    """x given as a row-strided view (ldx > K) is handled without a copy."""
+    x, qw, s, z, _ = _make(4, 256, 512, 4)
+    big = torch.zeros(4, 1024, dtype=torch.float16, device="cuda")
+    big[:, :512] = dev(x)
+    out = w4a16_matmul(big[:, :512], dev(qw), dev(s), dev(z))
+    assert_north_star(out, w4a16_ref(x, qw, s, z))
+
+
+# ---------------------------------------------------------------- exactness of the unpacking
+@pytest.mark.parametrize("factored", [True, False])
+def test_one_hot_rows_reproduce_dequantized_weight(factored):
+    """x = e_k: the output is column k of dequant(W), exactly (every product and sum is exact).
+    Checks the nibble order, the x pairing and the per-group scale/zero for every k."""
+    N, K = 256, 512
+    _, qw, s, z, _ = _make(1, N, K, 9)
+    deq = dequantize_ref(qw, s, z, 128)  # [N, K] fp16
+    qwd, sd, zd = dev(qw), dev(s), dev(z)
+    for k0 in range(0, K, 16):
+        rows = []
+        for k in range(k0, k0 + 16):
+            x = torch.zeros(1, K, dtype=torch.float16, device="cuda")
+            x[0, k] = 1.0
+            rows.append(w4a16_matmul(x, qwd, sd, zd, config={"FACTORED": factored}))
+        got = torch.cat(rows).cpu().numpy()
+        assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, k0:k0 + 16].T))), k0
+
+
+def test_one_hot_multi_row():
+    """M = 16 rows, row m = e_m: the exact path returns dequantized weights too."""
+    N, K = 128, 256
+    _, qw, s, z, _ = _make(1, N, K, 10)
+    deq = dequantize_ref(qw, s, z, 128)
+    x = torch.zeros(16, K, dtype=torch.float16, device="cuda")
+    x[torch.arange(16), torch.arange(16) * 3] = 1.0
+    out = w4a16_matmul(x, dev(qw), dev(s), dev(z))
+    assert np.array_equal(bits16(out), bits16(np.ascontiguousarray(deq[:, ::3][:, :16].T)))
+
+
+# ---------------------------------------------------------------- config 0 and config 2
+def test_config0_headline():
+    """Config 0: M=1, gate_up 17920 x 1536, seed 0 (weights quantized by the oracle)."""
+    e = _run(1, 17920, 1536, seed=0)
+    assert e["rel_l2"] < 1e-3
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("name,N,K", cases.QWEN_LINEARS)
+def test_config2_qwen_shapes(name, N, K, M):
+    _run(M, N, K, seed=2)
+
+
+def test_qkv_fused_with_bias():
+    """The e2e qkv projection: 2048 x 1536 with bias (decode key (1, 2048, 1536, True))."""
+    _run(1, 2048, 1536, bias=True)
+
+
+# ---------------------------------------------------------------- the native decode entry
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 16])
+def test_decode_entry(M):
+    _run(M, 1536, 1536, entry=w4a16_decode_hip)
+
+
+def test_decode_entry_rejects_17_rows():
+    """As the reference's CUDA entry (tests/test_w4a16_cuda.py:43-45)."""
+    with pytest.raises(RuntimeError):
+        _run(17, 128, 128, entry=w4a16_decode_hip)
+
+
+def test_deterministic():
+    x, qw, s, z, _ = _make(1, 17920, 1536, 0)
+    a = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z))
+    b = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z))
+    assert torch.equal(a, b)
