@@ -74,28 +74,36 @@ int ldk_w4a16_dequant(const int32_t* qweight, const void* scales, const void* ze
 
 /* ------------------------------------------------------------------------------ W4A16 matmul */
 
+/* Size of the split-K workspace the matmul entry points can use (bytes). The caller allocates
+ * it once per device, zero-filled, 256-byte aligned, and passes it to every call; the kernels
+ * leave its counter region zero again after each launch, so it never needs re-clearing.
+ * Calls that share one workspace must be ordered (same stream or synchronized). */
+int64_t ldk_workspace_bytes(void);
+
 /* out [M, N] = x [M, K] @ dequant(qweight, scales, zeros)^T (+ bias [N]), fp32 accumulation,
  * fp16 output. Replaces kernels/w4a16.py:301-330 (w4a16_matmul) and its launch paths
- * w4a16.py:214-279. group_size a power of two >= 8 dividing K; N % 4 == 0; x, qweight, scales,
- * zeros 16-byte aligned with ldx % 8 == 0.
- *   block_n: output columns per workgroup (0 = tuned table),
- *   split_k: K-slices reduced inside one workgroup (0 = tuned table),
- *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_* (0 = tuned table).
- * M <= 16 runs the decode kernels; M > 16 runs the MFMA GEMM. */
+ * w4a16.py:214-279. group_size a power of two in 32..256 dividing K; N % 4 == 0; x, qweight
+ * 16-byte aligned with ldx % 8 == 0; scales, zeros 8-byte aligned. M <= 16.
+ *   block_n: output columns per workgroup, 16/32/64 (0 = table),
+ *   split_k: workgroups splitting K per column tile (0 = table; > 1 needs the workspace),
+ *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_VALU / LDK_PATH_MFMA (0 = table),
+ *   workspace, workspace_bytes: the split-K workspace (NULL, 0: no cross-workgroup split). */
 int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
                      const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M,
                      int64_t N, int64_t K, int group_size, int block_n, int split_k, int flags,
-                     void* stream);
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Decode-only entry (M <= 16; M > 16 returns LDK_ERR_UNSUPPORTED). Replaces the native
  * extension entry w4a16_decode of kernels/cuda/w4a16_decode.cu:136-181 and its wrapper
- * kernels/cuda/w4a16_cuda.py:45-56. split_k as in ldk_w4a16_matmul (0 = tuned). */
+ * kernels/cuda/w4a16_cuda.py:45-56. split_k as in ldk_w4a16_matmul (0 = table). */
 int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
                      const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M,
-                     int64_t N, int64_t K, int group_size, int split_k, void* stream);
+                     int64_t N, int64_t K, int group_size, int split_k, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /* The configuration the library would use for (M, N, K, group_size) with all-zero tuning
- * arguments. Replaces the choice tables of kernels/w4a16.py:282-298 (_pick_decode_path) and
+ * arguments and a workspace of ldk_workspace_bytes(): block_n, split_k (workgroups per column
+ * tile) and the path/mode flags. Replaces the choice tables of kernels/w4a16.py:282-298 (_pick_decode_path) and
  * kernels/cuda/w4a16_cuda.py:29-42 (_pick_split), which are exported by w4a16.py:333-355. */
 int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n,
                      int* split_k, int* flags);
@@ -114,10 +122,12 @@ int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, void* out, 
 
 /* out [M, N] = x [M, K] @ (e4m3(wq) * scale)^T (+ bias), fp32 accumulation, fp16 out.
  * wq [K, N] e4m3fn, scale [N] fp16. Replaces kernels/fp8.py:200-223 (w8a16_matmul) and its
- * kernels fp8.py:42-127. N % 16 == 0 and 16-byte aligned wq; block_n/split_k/flags as W4A16. */
+ * kernels fp8.py:42-127. N % 16 == 0 and 16-byte aligned wq; M <= 16; block_n, split_k, flags
+ * and the workspace as for ldk_w4a16_matmul. */
 int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale,
                      const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
-                     int block_n, int split_k, int flags, void* stream);
+                     int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
+                     void* stream);
 
 /* ---------------------------------------------------------------------- RMSNorm and SwiGLU */
 

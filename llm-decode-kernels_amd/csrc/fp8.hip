@@ -102,7 +102,11 @@ __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* __restr
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= N * K) return;
   const int64_t n = i / K, k = i - n * K;
-  out[i] = from_f32<T>(e4m3_decode(wq[k * N + n]) * to_f32<T>(scale[n]));
+  float p = e4m3_decode(wq[k * N + n]) * to_f32<T>(scale[n]);
+  // Keep the f32 product: fused into one v_fma_mix with a +0 addend, the fp16 conversion would
+  // turn a -0 product (code 0x80) into +0.
+  asm volatile("" : "+v"(p));
+  out[i] = from_f32<T>(p);
 }
 
 // --------------------------------------------------------------------------------- W8A16 GEMV
@@ -355,7 +359,10 @@ extern "C" int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, 
 }
 
 extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias, void* out,
-                                int64_t ldo, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int flags, void* stream) {
+                                int64_t ldo, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int flags,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: null pointer");
   if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: M, N, K must be positive");
   if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld > 16 (prefill GEMM not built yet)", (long long)M);

@@ -98,12 +98,13 @@ __device__ __forceinline__ uint32_t vgpr_const() {
   return r;
 }
 
-// a.x*b.x + a.y*b.y + c in fp32 with the three-operand VOP3 v_dot2_f32_f16. The builtin is
-// lowered to the two-operand v_dot2c form, which costs a v_mov whenever c is reused.
-__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
-  float d;
-  asm("v_dot2_f32_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
+// Orders LDS accesses of one wavefront (lanes exchanging data through LDS inside a wave): no
+// s_barrier is needed since a wave's LDS operations complete in order, but the compiler must not
+// move the reads above the writes.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
 // Workgroup barrier that orders LDS only: it does not wait for outstanding global loads, so
@@ -112,6 +113,55 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Sum of the first n (<= 16) floats at p (16-byte aligned, zero padding not required), in index
+// order: the partials of one output from the n waves of a workgroup. Four independent LDS vector
+// reads are in flight at once instead of n dependent scalar reads.
+__device__ __forceinline__ float sum_partials(const float* p, int n) {
+  float4_t v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (4 * i < n) v[i] = reinterpret_cast<const float4_t*>(p)[i];
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i < n) s += v[i / 4][i % 4];
+  return s;
+}
+
+// Cross-workgroup split-K finalization. The `splits` workgroups of one output tile each hold a
+// partial tile `part(o)` for o < n (fp32, already reduced inside the workgroup). Each writes it to
+// its slot of `ws` ([tile][split][n] floats) with agent-scope stores that write through the
+// per-XCD L2, waits for them, and increments the tile's counter once; the workgroup that observes
+// splits-1 reads the slots back with agent-scope loads (served past the L2), sums them in split
+// order (deterministic), calls store(o, value) and resets the counter to 0, so the counters are
+// zero again after every launch and never need a clearing launch. No L2 write-back or invalidate
+// is issued (an agent-scope fence would flush the whole L2 of every XCD, per workgroup). Must be
+// called by every thread of the workgroup (it contains barriers).
+template <typename Part, typename Store>
+__device__ __forceinline__ void splitk_finalize(int tile, int split, int splits, int n, float* ws,
+                                                uint32_t* counters, Part part, Store store) {
+  __shared__ int s_last;
+  float* mine = ws + ((size_t)tile * splits + split) * n;
+  for (int o = threadIdx.x; o < n; o += blockDim.x)
+    __hip_atomic_store(mine + o, part(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();                // ... and every thread's
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (uint32_t)(splits - 1);
+  __syncthreads();
+  if (s_last) {
+    const float* all = ws + (size_t)tile * splits * n;
+    for (int o = threadIdx.x; o < n; o += blockDim.x) {
+      float v = 0.0f;
+      for (int sp = 0; sp < splits; ++sp)
+        v += __hip_atomic_load(all + (size_t)sp * n + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      store(o, v);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace ldk

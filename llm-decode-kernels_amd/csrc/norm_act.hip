@@ -67,7 +67,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
       const hv_t wv = *reinterpret_cast<const hv_t*>(a.w + c * VEC);
       hv_t o;
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) o[j] = (half_t)((float)h[i][j] * rs);
+      for (int j = 0; j < VEC; ++j) {
+        float v = (float)h[i][j] * rs;
+        asm volatile("" : "+v"(v));  // a -0 * rs must stay -0 (no v_fma_mix with a +0 addend)
+        o[j] = (half_t)v;
+      }
       *reinterpret_cast<hv_t*>(a.out + (int64_t)row * a.ldo + c * VEC) = wv * o;  // fp16 multiply
     }
   }

@@ -39,15 +39,16 @@ SIGNATURES = {
     "ldk_int4_unpack": [_vp, _vp, _i64, _i64, _vp],
     "ldk_quantize_rtn": [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "ldk_w4a16_dequant": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "ldk_workspace_bytes": [],
     "ldk_w4a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32,
-                         _i32, _i32, _i32, _vp],
+                         _i32, _i32, _i32, _vp, _i64, _vp],
     "ldk_w4a16_decode": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
-                         _vp],
+                         _vp, _i64, _vp],
     "ldk_w4a16_config": [_i64, _i64, _i64, _i32, _ip, _ip, _ip],
     "ldk_fp8_quantize": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
     "ldk_fp8_dequant": [_vp, _vp, _i32, _vp, _i64, _i64, _vp],
     "ldk_w8a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
-                         _vp],
+                         _vp, _i64, _vp],
     "ldk_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _f32, _vp],
     "ldk_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
 }
@@ -74,7 +75,8 @@ def load() -> ctypes.CDLL:
             for name, argtypes in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
-                fn.restype = ctypes.c_char_p if name == "ldk_last_error" else ctypes.c_int
+                fn.restype = {"ldk_last_error": ctypes.c_char_p,
+                              "ldk_workspace_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
             _lib = lib
     return _lib
 
@@ -121,6 +123,23 @@ def require_gpu(*tensors: torch.Tensor | None, what: str) -> torch.device:
     if dev is None:
         raise RuntimeError(f"{what}: no tensor given")
     return dev
+
+
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def workspace(dev: torch.device):
+    """(pointer, bytes) of this device's split-K workspace: allocated zero-filled on first use and
+    kept for the life of the process. Its counters are reset by the kernels themselves, so it is
+    valid for every later call, including calls replayed from a captured graph. Make the first
+    call (which allocates) outside graph capture. Calls sharing it must be stream-ordered."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(idx)
+    if ws is None:
+        nbytes = int(load().ldk_workspace_bytes())
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _workspaces[idx] = ws
+    return ctypes.c_void_p(ws.data_ptr()), ws.numel()
 
 
 class device_guard:

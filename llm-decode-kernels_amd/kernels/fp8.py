@@ -74,10 +74,11 @@ def w8a16_matmul(x, wq, scale, bias=None, config=None):
         flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         with _lib.device_guard(dev):
+            ws, ws_bytes = _lib.workspace(dev)
             st = _lib.load().ldk_w8a16_matmul(
                 _lib.ptr(x2), x2.stride(0), _lib.ptr(q), _lib.ptr(s), _lib.ptr(b), _lib.ptr(out),
                 out.stride(0), M, N, K, int(cfg.get("block_n", 0)), int(cfg.get("split_k", 0)),
-                flags, _lib.stream(dev))
+                flags, ws, ws_bytes, _lib.stream(dev))
         _lib.check(st, "w8a16_matmul")
     else:
         out = torch.nn.functional.linear(x2, dequantize_fp8(q, s), b)

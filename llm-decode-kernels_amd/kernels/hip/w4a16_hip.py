@@ -2,9 +2,9 @@
 
 Counterpart of the reference's `kernels/cuda/w4a16_cuda.py` (`w4a16_decode_cuda`, lines 45-56)
 with the same contract: same arguments, M <= 16 rows, RuntimeError for more rows (the reference's
-TORCH_CHECK, tested at tests/test_w4a16_cuda.py:43-45). `split_k` is the number of K lanes per
-output column inside one workgroup (0/None = the library's table); the reference's split is a
-grid dimension with fp32 atomics instead.
+TORCH_CHECK, tested at tests/test_w4a16_cuda.py:43-45). `split_k` is the number of workgroups that
+split K for one column tile (0/None = the library's table); they meet in the library workspace
+instead of the reference's zero-filled fp32 buffer, atomics and cast launch.
 """
 
 from __future__ import annotations
@@ -25,11 +25,12 @@ def w4a16_decode_hip(x, qweight, scales, zeros, group_size=128, bias=None, split
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     b = None if bias is None else bias.to(torch.float16).contiguous()
+    qw, s, z = qweight.contiguous(), scales.contiguous(), zeros.contiguous()
     with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
         st = _lib.load().ldk_w4a16_decode(
-            _lib.ptr(x2), x2.stride(0), _lib.ptr(qweight.contiguous()),
-            _lib.ptr(scales.contiguous()), _lib.ptr(zeros.contiguous()), _lib.ptr(b),
-            _lib.ptr(out), out.stride(0), M, N, K, group_size, int(split_k or 0),
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(qw), _lib.ptr(s), _lib.ptr(z), _lib.ptr(b),
+            _lib.ptr(out), out.stride(0), M, N, K, group_size, int(split_k or 0), ws, ws_bytes,
             _lib.stream(dev))
     if st == _lib.ERR_UNSUPPORTED:
         raise RuntimeError(_lib.load().ldk_last_error().decode())

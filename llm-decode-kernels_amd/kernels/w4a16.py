@@ -16,10 +16,10 @@ one hipBLASLt/rocBLAS fp16 GEMM through torch (the reference runs its Triton ten
 there, w4a16.py:264-268).
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
-`GEMV` (force the VALU decode kernel), `FACTORED` (True: factored M=1 loop; False: exact
-dequantize-then-dot), `block_n` (columns per workgroup, 4..64) and `split_k` (K lanes per
-column inside the workgroup). Triton tile keys (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, GROUP_M)
-describe Triton programs and are ignored.
+`GEMV` (force the VALU decode kernel, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
+(True: factored M=1 loop; False: exact dequantize-then-dot), `block_n` (columns per workgroup:
+16, 32 or 64) and `split_k` (workgroups splitting K per column tile). Triton tile keys (BLOCK_M,
+BLOCK_N, BLOCK_K, SPLIT_K, GROUP_M) describe Triton programs and are ignored.
 """
 
 from __future__ import annotations
@@ -44,6 +44,8 @@ def _flags_from_config(config: dict | None, M: int) -> tuple[int, int, int]:
     flags = 0
     if config.get("GEMV"):
         flags |= _lib.PATH_VALU
+    if config.get("MFMA"):
+        flags |= _lib.PATH_MFMA
     if "FACTORED" in config:
         if config["FACTORED"] and M == 1:
             flags |= _lib.FACTORED
@@ -57,10 +59,11 @@ def _decode(x2, qweight, scales, zeros, bias, group_size, block_n, split_k, flag
     N = qweight.shape[1]
     dev = x2.device
     with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
         st = _lib.load().ldk_w4a16_matmul(
             _lib.ptr(x2), x2.stride(0), _lib.ptr(qweight), _lib.ptr(scales), _lib.ptr(zeros),
             _lib.ptr(bias), _lib.ptr(out), out.stride(0), M, N, K, group_size, block_n, split_k,
-            flags, _lib.stream(dev))
+            flags, ws, ws_bytes, _lib.stream(dev))
     _lib.check(st, "w4a16_matmul")
     return out
 
@@ -100,7 +103,8 @@ def config_for(M: int, N: int, K: int, group_size: int = 128) -> str:
     _lib.check(_lib.load().ldk_w4a16_config(M, N, K, group_size, ctypes.byref(bn),
                                             ctypes.byref(sk), ctypes.byref(fl)), "w4a16_config")
     mode = "factored" if fl.value & _lib.FACTORED else "exact"
-    return f"block_n={bn.value},split_k={sk.value},{mode}"
+    path = "mfma" if fl.value & _lib.PATH_MFMA else "valu"
+    return f"{path},block_n={bn.value},split_k={sk.value},{mode}"
 
 
 def export_choices() -> dict:

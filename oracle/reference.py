@@ -62,6 +62,17 @@ def rmsnorm_ref(x, weight, eps: float = 1e-6, residual=None):
     return out if residual is None else (out, x)
 
 
+def rmsnorm_parts(x, weight, eps: float = 1e-6, residual=None):
+    """rmsnorm_ref with its fp16 intermediate exposed: returns (h, normed, out), where h is the
+    (residual-added) fp16 input, normed = fp16(h * rsqrt(mean(h^2) + eps)) and out = w * normed."""
+    x = np.asarray(x)
+    h = x if residual is None else x + np.asarray(residual)
+    hf = h.astype(np.float32)
+    var = np.mean(hf * hf, axis=-1, keepdims=True, dtype=np.float32)
+    normed = (hf * (np.float32(1.0) / np.sqrt(var + np.float32(eps)))).astype(h.dtype)
+    return h, normed, np.asarray(weight) * normed
+
+
 def silu_ref(gate) -> np.ndarray:
     """F.silu on fp16: g / (1 + exp(-g)) in float32, rounded once to the input dtype."""
     g = np.asarray(gate)

@@ -44,3 +44,19 @@ def ulp_diff_fp16(a, b) -> np.ndarray:
         mag = u & 0x7FFF
         return np.where(u & 0x8000, -mag, mag)
     return np.abs(ordered(a) - ordered(b))
+
+
+def within_one_ulp_of_intermediate(out, inter, other) -> np.ndarray:
+    """True where the fp16 output equals fp16(other * i') for some i' within one fp16 ulp of the
+    reference's rounded fp16 intermediate `inter` (the product itself rounded once). This is the
+    fp16 1-ulp tolerance stated on the one rounding step whose input depends on a transcendental
+    or a reduction order (rsqrt of the mean square, exp in silu)."""
+    o = bits16(out)
+    inter = np.asarray(inter, dtype=np.float16)
+    other = np.asarray(other, dtype=np.float16)
+    ok = np.zeros(o.shape, dtype=bool)
+    for cand in (np.nextafter(inter, np.float16(-np.inf)), inter, np.nextafter(inter, np.float16(np.inf))):
+        prod = (other.astype(np.float32) * cand.astype(np.float32)).astype(np.float16)
+        ok |= bits16(prod) == o
+        ok |= (bits16(prod) & 0x7FFF) + (o & 0x7FFF) == 0  # +0 / -0
+    return ok

@@ -16,7 +16,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "ldk.h"
 
 def _declared() -> set[str]:
     text = HEADER.read_text()
-    return set(re.findall(r"^\s*(?:int|const char\*)\s+(ldk_\w+)\s*\(", text, flags=re.M))
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(ldk_\w+)\s*\(", text, flags=re.M))
 
 
 def test_header_declares_what_the_binding_binds():
@@ -49,7 +49,7 @@ def _err(st):
 def test_null_pointer_rejected():
     lib = _lib.load()
     st, msg = _err(lib.ldk_w4a16_matmul(None, 1536, None, None, None, None, None, 17920, 1, 17920,
-                                        1536, 128, 0, 0, 0, None))
+                                        1536, 128, 0, 0, 0, None, 0, None))
     assert st == _lib.ERR_INVALID and "null" in msg
 
 
@@ -57,7 +57,8 @@ def test_decode_rejects_more_than_16_rows():
     """Reference: w4a16_decode_cuda raises for M = 17 (tests/test_w4a16_cuda.py:43-45)."""
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    st, msg = _err(lib.ldk_w4a16_decode(p, 128, p, p, p, None, p, 128, 17, 128, 128, 128, 0, None))
+    st, msg = _err(lib.ldk_w4a16_decode(p, 128, p, p, p, None, p, 128, 17, 128, 128, 128, 0, None, 0,
+                                        None))
     assert st == _lib.ERR_UNSUPPORTED and "16" in msg
 
 
@@ -65,14 +66,24 @@ def test_decode_rejects_more_than_16_rows():
 def test_bad_group_size_rejected(K, gs):
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    st, _ = _err(lib.ldk_w4a16_matmul(p, K, p, p, p, None, p, 64, 1, 64, K, gs, 0, 0, 0, None))
+    st, _ = _err(lib.ldk_w4a16_matmul(p, K, p, p, p, None, p, 64, 1, 64, K, gs, 0, 0, 0, None, 0,
+                                      None))
     assert st == _lib.ERR_INVALID
+
+
+def test_split_without_workspace_rejected():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, msg = _err(lib.ldk_w4a16_matmul(p, 1536, p, p, p, None, p, 1536, 1, 1536, 1536, 128, 0, 4,
+                                        0, None, 0, None))
+    assert st == _lib.ERR_INVALID and "workspace" in msg
 
 
 def test_misaligned_pointer_rejected():
     lib = _lib.load()
     p, bad = ctypes.c_void_p(256), ctypes.c_void_p(258)
-    st, _ = _err(lib.ldk_w4a16_matmul(bad, 256, p, p, p, None, p, 64, 1, 64, 256, 128, 0, 0, 0, None))
+    st, _ = _err(lib.ldk_w4a16_matmul(bad, 256, p, p, p, None, p, 64, 1, 64, 256, 128, 0, 0, 0, None,
+                                      0, None))
     assert st == _lib.ERR_ALIGN
 
 
@@ -80,7 +91,7 @@ def test_factored_needs_one_row():
     lib = _lib.load()
     p = ctypes.c_void_p(256)
     st, _ = _err(lib.ldk_w4a16_matmul(p, 256, p, p, p, None, p, 64, 2, 64, 256, 128, 0, 0,
-                                      _lib.FACTORED, None))
+                                      _lib.FACTORED, None, 0, None))
     assert st == _lib.ERR_UNSUPPORTED
 
 
@@ -94,7 +105,7 @@ def test_rmsnorm_residual_pairing_rejected():
 def test_w8a16_n_multiple_of_16():
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    st, _ = _err(lib.ldk_w8a16_matmul(p, 64, p, p, None, p, 40, 1, 40, 64, 0, 0, 0, None))
+    st, _ = _err(lib.ldk_w8a16_matmul(p, 64, p, p, None, p, 40, 1, 40, 64, 0, 0, 0, None, 0, None))
     assert st == _lib.ERR_UNSUPPORTED
 
 
@@ -102,8 +113,15 @@ def test_config_query():
     bn, sk, fl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     st = _lib.load().ldk_w4a16_config(1, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
-    assert st == 0 and bn.value in (4, 8, 16, 32, 64) and sk.value > 0
-    assert fl.value & _lib.FACTORED
+    assert st == 0 and bn.value in (16, 32, 64) and sk.value >= 1
+    assert fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU
+    st = _lib.load().ldk_w4a16_config(16, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
+                                      ctypes.byref(fl))
+    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 64
+
+
+def test_workspace_size():
+    assert _lib.load().ldk_workspace_bytes() >= 1 << 20
 
 
 def test_python_ops_refuse_cpu_tensors():

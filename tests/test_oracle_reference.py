@@ -107,3 +107,17 @@ def test_byte_formulas_kat():
     assert rmsnorm_bytes(2048, 1536, True) == 25_168_896
     assert rmsnorm_bytes(1, 1536, True) == 15_360 and rmsnorm_bytes(1, 1536, False) == 9_216
     assert swiglu_bytes(2048, 8960) == 110_100_480 and swiglu_bytes(1, 8960) == 53_760
+
+
+def test_rmsnorm_parts_consistent_with_rmsnorm_ref():
+    from oracle.reference import rmsnorm_parts
+
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 512)).astype(np.float16)
+    r = rng.standard_normal((3, 512)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(512)).astype(np.float16)
+    h, normed, out = rmsnorm_parts(x, w, 1e-6, r)
+    ref_out, ref_h = rmsnorm_ref(x, w, 1e-6, residual=r)
+    assert np.array_equal(out.view(np.uint16), ref_out.view(np.uint16))
+    assert np.array_equal(h.view(np.uint16), ref_h.view(np.uint16))
+    assert np.array_equal((w * normed).view(np.uint16), out.view(np.uint16))
