@@ -42,7 +42,12 @@ enum ldk_flags {
   LDK_FACTORED = 1,  /* W4A16: sum x*(q - z) per group, scale once (w4a16.py:116-119, FACTORED) */
   LDK_EXACT = 2,     /* W4A16: dequantize each weight to fp16 exactly as dequantize_ref first  */
   LDK_PATH_VALU = 4, /* force the wave64 VALU (dot2) skinny kernel */
-  LDK_PATH_MFMA = 8  /* force the MFMA kernel */
+  LDK_PATH_MFMA = 8, /* force the MFMA kernel */
+  /* W4A16 tuning: chunks of loads a wave keeps in flight per round (bits 4-5; 0 = table) */
+  LDK_CPW_1 = 16,
+  LDK_CPW_2 = 32,
+  LDK_CPW_4 = 48,
+  LDK_CPW_MASK = 48
 };
 
 /* ABI version (LDK_ABI_VERSION) the library was built with. */
@@ -75,8 +80,9 @@ int ldk_w4a16_dequant(const int32_t* qweight, const void* scales, const void* ze
 /* ------------------------------------------------------------------------------ W4A16 matmul */
 
 /* Size of the split-K workspace the matmul entry points can use (bytes). The caller allocates
- * it once per device, zero-filled, 256-byte aligned, and passes it to every call; the kernels
- * leave its counter region zero again after each launch, so it never needs re-clearing.
+ * it once per device, zero-filled, 256-byte aligned, and passes it to every call. It holds one
+ * 64-bit fixed-point accumulator per output of a split launch; the kernels leave every word
+ * zero again by the end of each launch, so it never needs re-clearing (also under graph replay).
  * Calls that share one workspace must be ordered (same stream or synchronized). */
 int64_t ldk_workspace_bytes(void);
 
@@ -86,7 +92,7 @@ int64_t ldk_workspace_bytes(void);
  * 16-byte aligned with ldx % 8 == 0; scales, zeros 8-byte aligned. M <= 16.
  *   block_n: output columns per workgroup, 16/32/64 (0 = table),
  *   split_k: workgroups splitting K per column tile (0 = table; > 1 needs the workspace),
- *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_VALU / LDK_PATH_MFMA (0 = table),
+ *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_VALU / LDK_PATH_MFMA, LDK_CPW_* (0 = table),
  *   workspace, workspace_bytes: the split-K workspace (NULL, 0: no cross-workgroup split). */
 int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
                      const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M,
@@ -103,7 +109,7 @@ int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const v
 
 /* The configuration the library would use for (M, N, K, group_size) with all-zero tuning
  * arguments and a workspace of ldk_workspace_bytes(): block_n, split_k (workgroups per column
- * tile) and the path/mode flags. Replaces the choice tables of kernels/w4a16.py:282-298 (_pick_decode_path) and
+ * tile) and the path/mode/LDK_CPW_* flags. Replaces the choice tables of kernels/w4a16.py:282-298 (_pick_decode_path) and
  * kernels/cuda/w4a16_cuda.py:29-42 (_pick_split), which are exported by w4a16.py:333-355. */
 int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n,
                      int* split_k, int* flags);

@@ -115,52 +115,51 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Sum of the first n (<= 16) floats at p (16-byte aligned, zero padding not required), in index
-// order: the partials of one output from the n waves of a workgroup. Four independent LDS vector
-// reads are in flight at once instead of n dependent scalar reads.
-__device__ __forceinline__ float sum_partials(const float* p, int n) {
-  float4_t v[4];
+// Sum of p[0], p[stride], ..., p[(n-1)*stride] (n <= 16) in index order: the partials of one
+// output from the n waves of a workgroup, stored wave-major. All reads are issued before the
+// first add, so their LDS latencies overlap instead of adding up.
+__device__ __forceinline__ float sum_waves(const float* p, int stride, int n) {
+  float v[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (4 * i < n) v[i] = reinterpret_cast<const float4_t*>(p)[i];
-  float s = 0.0f;
+  for (int i = 0; i < 16; ++i) v[i] = i < n ? p[i * stride] : 0.0f;
+  float s = v[0];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    if (i < n) s += v[i / 4][i % 4];
+  for (int i = 1; i < 16; ++i)
+    if (i < n) s += v[i];
   return s;
 }
 
-// Cross-workgroup split-K finalization. The `splits` workgroups of one output tile each hold a
-// partial tile `part(o)` for o < n (fp32, already reduced inside the workgroup). Each writes it to
-// its slot of `ws` ([tile][split][n] floats) with agent-scope stores that write through the
-// per-XCD L2, waits for them, and increments the tile's counter once; the workgroup that observes
-// splits-1 reads the slots back with agent-scope loads (served past the L2), sums them in split
-// order (deterministic), calls store(o, value) and resets the counter to 0, so the counters are
-// zero again after every launch and never need a clearing launch. No L2 write-back or invalidate
-// is issued (an agent-scope fence would flush the whole L2 of every XCD, per workgroup). Must be
-// called by every thread of the workgroup (it contains barriers).
+// Cross-workgroup split-K reduction in one memory round trip. The `splits` workgroups of one
+// output tile each hold a partial p(o) for o < n (fp32, already reduced inside the workgroup).
+// Each adds it to a 64-bit word per output with one agent-scope atomic add: bits [63:8] carry
+// the sum of round(p * 2^24) in two's complement (fixed point, 2^-24 resolution), bits [7:0]
+// count the contributions. The add returns the previous word, so the workgroup whose add brings
+// the count to `splits` holds the complete sum: it stores the output and writes the word back to
+// zero, leaving the workspace zeroed for the next launch (no clearing launch, no counters, no
+// barrier, no waiting on other workgroups). Integer addition is associative, so the result does
+// not depend on arrival order (deterministic). Partials are clamped to +-2^20 (an fp16 output
+// saturates at 65504); a non-finite partial poisons the sum and the output becomes NaN.
+// Requires splits <= 32 and a zero-filled `acc` of n words for this tile.
+constexpr float kFixScale = 16777216.0f;          // 2^24
+constexpr float kFixClamp = 1048576.0f;           // 2^20
+constexpr int64_t kFixPoison = int64_t(1) << 50;  // > 32 * 2^44, the largest legal sum
+constexpr int64_t kFixPoisonSeen = int64_t(3) << 48;
+
 template <typename Part, typename Store>
-__device__ __forceinline__ void splitk_finalize(int tile, int split, int splits, int n, float* ws,
-                                                uint32_t* counters, Part part, Store store) {
-  __shared__ int s_last;
-  float* mine = ws + ((size_t)tile * splits + split) * n;
-  for (int o = threadIdx.x; o < n; o += blockDim.x)
-    __hip_atomic_store(mine + o, part(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();                // ... and every thread's
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             (uint32_t)(splits - 1);
-  __syncthreads();
-  if (s_last) {
-    const float* all = ws + (size_t)tile * splits * n;
-    for (int o = threadIdx.x; o < n; o += blockDim.x) {
-      float v = 0.0f;
-      for (int sp = 0; sp < splits; ++sp)
-        v += __hip_atomic_load(all + (size_t)sp * n + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      store(o, v);
+__device__ __forceinline__ void splitk_accumulate(uint64_t* acc, int splits, int n, Part part, Store store) {
+  for (int o = threadIdx.x; o < n; o += blockDim.x) {
+    const float p = part(o);
+    const int64_t v = __builtin_isfinite(p)
+                          ? (int64_t)__builtin_rintf(__builtin_fminf(__builtin_fmaxf(p, -kFixClamp), kFixClamp) * kFixScale)
+                          : kFixPoison;
+    const uint64_t inc = ((uint64_t)v << 8) + 1u;
+    const uint64_t old = __hip_atomic_fetch_add(acc + o, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((int)(old & 0xffu) == splits - 1) {
+      const int64_t tot = (int64_t)(old + inc) >> 8;
+      const bool poisoned = tot >= kFixPoisonSeen || tot <= -kFixPoisonSeen;
+      store(o, poisoned ? __builtin_nanf("") : (float)tot * (1.0f / kFixScale));
+      __hip_atomic_store(acc + o, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -6,19 +6,25 @@
 //
 //  * Tiles and groups. A workgroup owns CW output columns and a range of quantization groups
 //    (all of K, or 1/splits of it). Inside the workgroup each wave takes whole groups, so every
-//    lane applies one scale and one zero point per chunk of work and a group's partial sums never
-//    leave the lane until the final reduction.
-//  * Memory-level parallelism. A lane issues all its loads for a chunk (its x rows, its packed
-//    weight rows, one scale and one zero word) before using any of them and consumes them in
-//    issue order, so each s_waitcnt vmcnt(n) releases work as data lands and the whole launch's
+//    lane applies one scale and one zero point per group and a group's partial sums never leave
+//    the lane until the final reduction.
+//  * Memory-level parallelism. A wave works in rounds of CPW chunks (a chunk is the groups its
+//    lanes cover with one 128-bit load each per row). Per round a lane issues every load first:
+//    its x rows, then chunk by chunk the packed weight rows with their scale and zero words. It
+//    consumes them in issue order, so each s_waitcnt vmcnt(n) releases work as data lands:
+//    the compute of an early chunk overlaps the arrival of the later ones, and a launch's whole
 //    weight stream is in flight at once. Row segments are CW*4 >= 64 bytes long (shorter runs
 //    per row were measured to cost 2-7x on MI355X).
 //  * No workgroup barrier before the compute: x rows are staged through LDS by the wave that
-//    uses them (wave-local exchange), so weight loads never wait on other waves.
+//    uses them (wave-local exchange), so weight loads never wait on other waves. Rows outside the
+//    workgroup's groups and x rows >= M are staged as zeros, which makes their products exact
+//    zeros without any masking in the inner loops.
 //  * Split-K. Partials are reduced inside the workgroup (DPP row rotations and gfx950 permlane
 //    swaps within a wave, then LDS across waves). Narrow shapes (few column tiles) also split the
-//    groups over `splits` workgroups that meet in a caller-provided workspace; the last one to
-//    arrive sums the partials and resets its counter (one launch, no zero-fill, no cast kernel).
+//    groups over `splits` workgroups that meet in a caller-provided workspace through one 64-bit
+//    fixed-point atomic add per output that also counts arrivals; the add that completes the
+//    count stores the output and re-zeroes the word (one launch, no zero-fill, no cast kernel,
+//    one memory round trip, deterministic).
 //
 // Dequantization happens in registers: a nibble q ORed into the mantissa of fp16 1024.0
 // (0x6400) is exactly the fp16 value 1024 + q, so one v_and_or_b32 per pair turns packed nibbles
@@ -29,13 +35,13 @@
 //      FACTORED (M = 1): s * (sum x*q - z * sum x) per group, the reference's FACTORED identity
 //      (kernels/w4a16.py:116-119). Nibbles 1/3/5/7 are masked in place as 16*q and meet x pairs
 //      pre-scaled by 1/16; one v_dot2_f32_f16 chain per column runs over all of the lane's rows
-//      and starts at -1024*(offset-weighted sum of x) - z*(sum of x). ~9.5 VALU ops per 8 weights.
+//      of a group, starting at -1024*(offset-weighted sum of x); ~9 VALU ops per 8 weights.
 //      EXACT: ((1024+q) - (1024+z)) * s in packed fp16 is exactly the reference's dequantized
 //      weight (one RNE rounding, kernels/reference.py:35), then dot2 with each x row.
-//  - MFMA kernel (9 <= M <= 16): an int32 word holds 8 consecutive K of one column, which is
-//    exactly one lane's B operand of v_mfma_f32_16x16x32_f16. A lane's 128-bit load feeds four
-//    16x16 tiles; B = (q - z) exactly in fp16, A = x rows permuted to the nibble-pair order, the
-//    fp32 tile of one group is scaled by s once.
+//  - MFMA kernel (larger M): an int32 word holds 8 consecutive K of one column, which is exactly
+//    one lane's B operand of v_mfma_f32_16x16x32_f16. A lane's 128-bit load feeds four 16x16
+//    tiles; B = (q - z) exactly in fp16, A = x rows permuted to the nibble-pair order, the fp32
+//    tile of one group is scaled by s once.
 #include <algorithm>
 #include <cmath>
 
@@ -44,7 +50,7 @@
 namespace {
 
 constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024.0 in both halves
-constexpr size_t kCounterBytes = 4096;    // split-K counters at the start of the workspace
+constexpr int kMaxSplits = 32;            // arrival count field of the split-K accumulators
 
 struct W4Args {
   const half_t* x;
@@ -59,10 +65,9 @@ struct W4Args {
 };
 
 struct SplitArgs {
-  int splits;          // workgroups per column tile
-  int gps;             // groups per split
-  float* ws;           // [tiles][splits][MT*CW] partials (splits > 1)
-  uint32_t* counters;  // [tiles], zero between launches
+  int splits;     // workgroups per column tile
+  int gps;        // groups per split
+  uint64_t* acc;  // [tiles][n] fixed-point accumulators (splits > 1), zero between launches
 };
 
 __device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (lo16(a), lo16(b))
@@ -95,18 +100,36 @@ __device__ __forceinline__ void store_x_record(unsigned char* dst, u32x4 d) {
   *reinterpret_cast<u32x4*>(dst) = p;
 }
 
+// Shared epilogue: the workgroup's NW wave partials of n outputs sit wave-major in `red`; sum
+// them and store (or hand them to the cross-workgroup split-K reduction).
+template <typename Store>
+__device__ __forceinline__ void finish_tile(const float* red, int n, int NW, int tile,
+                                            const SplitArgs& sp, Store store) {
+  auto part = [&](int o) { return ldk::sum_waves(red + o, n, NW); };
+  if (sp.splits == 1) {
+    for (int o = threadIdx.x; o < n; o += blockDim.x) store(o, part(o));
+  } else {
+    ldk::splitk_accumulate(sp.acc + (size_t)tile * n, sp.splits, n, part, store);
+  }
+}
+
 // ------------------------------------------------------------------------------ VALU kernel
 //
 // Lane (ln, lkw) of a wave: ln < LN runs along N (columns n0 + 4ln .. +3), lkw < LKW = 64/LN along
 // K. LG = rows_per_group / RPL lanes share a group, each taking RPL of its packed rows
-// (sub, sub + LG, ...); a wave covers GW = LKW / LG groups per chunk, a workgroup NW * GW.
-template <int MT, int LN, int RPL, bool FACT>
+// (sub, sub + LG, ...); a chunk is GW = LKW / LG groups (LKW*RPL packed rows). Chunk k of the
+// workgroup's range covers groups gb + k*GW ..; wave w takes chunks w, w + NW, ... in rounds of
+// CPW chunks.
+template <int MT, int LN, int RPL, bool FACT, int CPW>
 __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp) {
   static_assert(!FACT || MT == 1, "FACTORED is the M = 1 kernel");
   constexpr int CW = 4 * LN;
   constexpr int LKW = 64 / LN;
   constexpr int ROWB = FACT ? 32 : 16;
-  constexpr int PXW = (RPL * MT + LN - 1) / LN;  // x records a lane prepares per chunk
+  constexpr int RPC = LKW * RPL;                // packed rows per chunk
+  constexpr int ITEMS = CPW * RPC * MT;         // x records a wave stages per round
+  constexpr int PXW = (ITEMS + 63) / 64;        // ... per lane
+  constexpr int SLOTS = 64 * PXW;
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int rpg = 1 << a.gsh_rows;
@@ -122,9 +145,10 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
   const int n0 = tile * CW;
   const int col = min(n0 + 4 * ln, a.N - 4);  // clamped: tail lanes load valid memory, store nothing
   const int gb = split * sp.gps, ge = min(ng, gb + sp.gps);
-  const int rows_w = GW * rpg;                // packed rows of one wave chunk
-  unsigned char* xw = smem + (size_t)wave * rows_w * MT * ROWB;
-  float* red = reinterpret_cast<float*>(smem + (size_t)NW * rows_w * MT * ROWB);  // [MT*CW][NWP]
+  const int rb = gb << a.gsh_rows, re = ge << a.gsh_rows;  // packed rows of this workgroup
+  const int nchunks = (ge - gb + GW - 1) / GW;
+  unsigned char* xw = smem + (size_t)wave * SLOTS * ROWB;
+  float* red = reinterpret_cast<float*>(smem + (size_t)NW * SLOTS * ROWB);  // [NW][MT*CW]
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
@@ -134,103 +158,109 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
 
-  for (int gc = gb + wave * GW; gc < ge; gc += NW * GW) {
-    // ---- loads, in consumption order: x rows of the chunk, weights, scale, zero
+  for (int k0 = wave; k0 < nchunks; k0 += NW * CPW) {
+    // ---- loads, in consumption order: x rows of the round's chunks, then per chunk the weight
+    // rows with the scale and zero (FACTORED uses them after its dot chain, EXACT before)
     u32x4 xr[PXW];
 #pragma unroll
     for (int i = 0; i < PXW; ++i) {
-      const int item = min(lane + 64 * i, rows_w * MT - 1);  // item = rr * MT + m
-      const int rr = item / MT, m = min(item % MT, a.M - 1);
-      const int row = min(gc * rpg + rr, R - 1);
+      const int item = min(lane + 64 * i, ITEMS - 1);  // item = (c * RPC + rr) * MT + m
+      const int m = min(item % MT, a.M - 1), rc = item / MT;
+      const int c = rc / RPC, rr = rc - c * RPC;
+      const int row = min(rb + (k0 + NW * c) * GW * rpg + rr, R - 1);
       xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.ldx + 8 * row);
     }
-    const int g = gc + gi;
-    const bool gok = g < ge;
-    const int gg = gok ? g : ge - 1;
-    // FACTORED needs the scale and zero only after its dot chain, EXACT before its first row.
-    u32x2 sv, zv;
-    if constexpr (!FACT) {
-      sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
-      zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
-    }
-    u32x4 w[RPL];
+    u32x4 w[CPW][RPL];
+    u32x2 sv[CPW], zv[CPW];
 #pragma unroll
-    for (int t = 0; t < RPL; ++t) {
-      const int r = gg * rpg + sub + LG * t;
-      w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
-    }
-    if constexpr (FACT) {
-      sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
-      zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
+    for (int c = 0; c < CPW; ++c) {
+      const int gg = min(gb + (k0 + NW * c) * GW + gi, ge - 1);  // clamped; such lanes meet zero x
+      if constexpr (!FACT) {
+        sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
+        zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
+      }
+#pragma unroll
+      for (int t = 0; t < RPL; ++t) {
+        const int r = gg * rpg + sub + LG * t;
+        w[c][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
+      }
+      if constexpr (FACT) {
+        sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
+        zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
+      }
     }
 
-    // ---- wave-local x staging
+    // ---- wave-local x staging: every lane writes its own slots (no branches, no conflicts)
 #pragma unroll
     for (int i = 0; i < PXW; ++i) {
       const int item = lane + 64 * i;
-      if (item < rows_w * MT) {
-        u32x4 d = xr[i];
-        if (item % MT >= a.M) d = u32x4{0u, 0u, 0u, 0u};
-        store_x_record<FACT>(xw + (size_t)item * ROWB, d);
-      }
+      const int m = item % MT, rc = item / MT;
+      const int c = rc / RPC, rr = rc - c * RPC;
+      const int row = rb + (k0 + NW * c) * GW * rpg + rr;
+      const bool ok = item < ITEMS && m < a.M && row < re;
+      store_x_record<FACT>(xw + (size_t)item * ROWB, ok ? xr[i] : u32x4{0u, 0u, 0u, 0u});
     }
     ldk::wave_lds_sync();
-    if (!gok) continue;
 
-    if constexpr (FACT) {
-      u32x4 xp[RPL];
-      float c0 = 0.0f, xs = 0.0f;
 #pragma unroll
-      for (int t = 0; t < RPL; ++t) {
-        const unsigned char* rec = xw + (size_t)(gi * rpg + sub + LG * t) * ROWB;
-        xp[t] = *reinterpret_cast<const u32x4*>(rec);
-        const float2_t k = *reinterpret_cast<const float2_t*>(rec + 16);
-        c0 += k[0];
-        xs += k[1];
-      }
-      float tt[4] = {c0, c0, c0, c0};
+    for (int c = 0; c < CPW; ++c) {
+      if (k0 + NW * c >= nchunks) break;  // uniform: the rest of the round is past the range
+      const unsigned char* xc = xw + (size_t)(c * RPC + gi * rpg + sub) * MT * ROWB;
+      if constexpr (FACT) {
+        u32x4 xp[RPL];
+        float c0 = 0.0f, xs = 0.0f;
 #pragma unroll
-      for (int t = 0; t < RPL; ++t) {  // rows in arrival order
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t wc = w[t][c];
-          const uint32_t v = wc >> 8;
-          tt[c] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][3]), ldk::u2h2((v & mhi) | magic), tt[c], false);
-          tt[c] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][2]), ldk::u2h2((v & mlo) | magic), tt[c], false);
-          tt[c] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][1]), ldk::u2h2((wc & mhi) | magic), tt[c], false);
-          tt[c] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][0]), ldk::u2h2((wc & mlo) | magic), tt[c], false);
+        for (int t = 0; t < RPL; ++t) {
+          const unsigned char* rec = xc + (size_t)(LG * t) * ROWB;
+          xp[t] = *reinterpret_cast<const u32x4*>(rec);
+          const float2_t k = *reinterpret_cast<const float2_t*>(rec + 16);
+          c0 += k[0];
+          xs += k[1];
         }
-      }
-      const half4_t s4 = __builtin_bit_cast(half4_t, sv);
-      const half4_t z4 = __builtin_bit_cast(half4_t, zv);
+        float tt[4] = {c0, c0, c0, c0};
 #pragma unroll
-      for (int c = 0; c < 4; ++c)  // s * (sum x*q - z * sum x)
-        acc[0][c] = __builtin_fmaf((float)s4[c], __builtin_fmaf(-(float)z4[c], xs, tt[c]), acc[0][c]);
-    } else {
-      const half4_t s4 = __builtin_bit_cast(half4_t, sv);
-      const half4_t z4 = __builtin_bit_cast(half4_t, zv);
+        for (int t = 0; t < RPL; ++t) {  // rows in arrival order
 #pragma unroll
-      for (int t = 0; t < RPL; ++t) {
-        u32x4 xp[MT];
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t wc = w[c][t][q];
+            const uint32_t v = wc >> 8;
+            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][3]), ldk::u2h2((v & mhi) | magic), tt[q], false);
+            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][2]), ldk::u2h2((v & mlo) | magic), tt[q], false);
+            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][1]), ldk::u2h2((wc & mhi) | magic), tt[q], false);
+            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][0]), ldk::u2h2((wc & mlo) | magic), tt[q], false);
+          }
+        }
+        const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
+        const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-          xp[m] = *reinterpret_cast<const u32x4*>(xw + (size_t)((gi * rpg + sub + LG * t) * MT + m) * ROWB);
+        for (int q = 0; q < 4; ++q)  // s * (sum x*q - z * sum x)
+          acc[0][q] = __builtin_fmaf((float)s4[q], __builtin_fmaf(-(float)z4[q], xs, tt[q]), acc[0][q]);
+      } else {
+        const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
+        const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t wc = w[t][c];
-          const half_t zb1 = -((half_t)1024.0f + z4[c]);
-          const half2_t zb = {zb1, zb1};
-          const half2_t s2 = {s4[c], s4[c]};
-          const half2_t d0 = (ldk::u2h2((wc & mlo) | magic) + zb) * s2;
-          const half2_t d1 = (ldk::u2h2(((wc >> 4) & mlo) | magic) + zb) * s2;
-          const half2_t d2 = (ldk::u2h2(((wc >> 8) & mlo) | magic) + zb) * s2;
-          const half2_t d3 = (ldk::u2h2(((wc >> 12) & mlo) | magic) + zb) * s2;
+        for (int t = 0; t < RPL; ++t) {
+          u32x4 xp[MT];
 #pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            float tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][0]), d0, acc[m][c], false);
-            tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][1]), d1, tt, false);
-            tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][2]), d2, tt, false);
-            acc[m][c] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][3]), d3, tt, false);
+          for (int m = 0; m < MT; ++m)
+            xp[m] = *reinterpret_cast<const u32x4*>(xc + (size_t)(LG * t * MT + m) * ROWB);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t wc = w[c][t][q];
+            const half_t zb1 = -((half_t)1024.0f + z4[q]);
+            const half2_t zb = {zb1, zb1};
+            const half2_t s2 = {s4[q], s4[q]};
+            const half2_t d0 = (ldk::u2h2((wc & mlo) | magic) + zb) * s2;
+            const half2_t d1 = (ldk::u2h2(((wc >> 4) & mlo) | magic) + zb) * s2;
+            const half2_t d2 = (ldk::u2h2(((wc >> 8) & mlo) | magic) + zb) * s2;
+            const half2_t d3 = (ldk::u2h2(((wc >> 12) & mlo) | magic) + zb) * s2;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+              float tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][0]), d0, acc[m][q], false);
+              tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][1]), d1, tt, false);
+              tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][2]), d2, tt, false);
+              acc[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][3]), d3, tt, false);
+            }
           }
         }
       }
@@ -241,28 +271,21 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[m][c] = ldk::sum_lanes_strided<LN>(acc[m][c]);
-  const int NWP = (NW + 3) & ~3;  // partials of one output, wave-minor
+    for (int q = 0; q < 4; ++q) acc[m][q] = ldk::sum_lanes_strided<LN>(acc[m][q]);
   if (lane < LN) {
 #pragma unroll
     for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) red[(size_t)(m * CW + 4 * lane + c) * NWP + wave] = acc[m][c];
+      *reinterpret_cast<float4_t*>(red + (size_t)(wave * MT + m) * CW + 4 * lane) =
+          float4_t{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
   }
   __syncthreads();
-  auto part = [&](int o) { return ldk::sum_partials(red + (size_t)o * NWP, NW); };
-  auto store = [&](int o, float v) {
+  finish_tile(red, MT * CW, NW, tile, sp, [&](int o, float v) {
     const int m = o / CW, n = n0 + (o - m * CW);
     if (m < a.M && n < a.N) {
       if (a.bias) v += (float)a.bias[n];
       a.out[(int64_t)m * a.ldo + n] = (half_t)v;
     }
-  };
-  if (sp.splits == 1) {
-    for (int o = threadIdx.x; o < MT * CW; o += blockDim.x) store(o, part(o));
-  } else {
-    ldk::splitk_finalize(tile, split, sp.splits, MT * CW, sp.ws, sp.counters, part, store);
-  }
+  });
 }
 
 // ------------------------------------------------------------------------------ MFMA kernel
@@ -270,8 +293,9 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 // Lane l of a wave: c16 = l % 16 is the column inside each 16x16 tile and the A row, kb = l / 16
 // the 8-wide K block inside a 32-wide K step. The lane's 128-bit load of packed row
 // (g*rpg + 4*ks + kb) at columns n0 + 4*c16 .. +3 feeds tiles j = 0..3, whose column c16 is the
-// real column n0 + 4*c16 + j. A wave handles whole groups (rpg/4 K steps each).
-template <int KS>  // 32-wide K steps per group (group_size / 32)
+// real column n0 + 4*c16 + j. A wave handles whole groups (rpg/4 K steps each): groups
+// gb + w, gb + w + NW, ... in rounds of CPW groups whose loads are all issued first.
+template <int KS, int CPW>  // KS: 32-wide K steps per group (group_size / 32)
 __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs sp) {
   constexpr int CW = 64;
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
@@ -288,7 +312,8 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
   const int gb = split * sp.gps, ge = min(ng, gb + sp.gps);
   const int xrow = min(c16, a.M - 1);
   const bool xok = c16 < a.M;
-  float* red = reinterpret_cast<float*>(smem);  // [16 rows * 64 cols][NWP]
+  const int mrows = min(a.M, 16);
+  float* red = reinterpret_cast<float*>(smem);  // [NW][mrows * 64]
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>();
@@ -296,31 +321,38 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int g = gb + wave; g < ge; g += NW) {
-    // loads in consumption order: zero point, per K step the A fragment and the weight word row,
-    // then the scale (used after the group's MFMAs)
-    const u32x2 zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
-    u32x4 ar[KS], w[KS];
+  for (int g0 = gb + wave; g0 < ge; g0 += NW * CPW) {
+    // loads in consumption order, group by group: zero point, per K step the A fragment and the
+    // weight word row, then the scale (used after the group's MFMAs)
+    u32x2 zv[CPW], sv[CPW];
+    u32x4 ar[CPW][KS], w[CPW][KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int r = g * rpg + 4 * ks + kb;
-      ar[ks] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)xrow * a.ldx + 8 * r);
-      w[ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
+    for (int c = 0; c < CPW; ++c) {
+      const int g = min(g0 + NW * c, ge - 1);
+      zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int r = g * rpg + 4 * ks + kb;
+        ar[c][ks] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)xrow * a.ldx + 8 * r);
+        w[c][ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
+      }
+      sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
     }
-    const u32x2 sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
-    const half4_t z4 = __builtin_bit_cast(half4_t, zv);
-    float4_t tmp[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) tmp[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < CPW; ++c) {
+      if (g0 + NW * c >= ge) break;  // uniform
+      const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
+      float4_t tmp[4];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      {
-        u32x4 ap = x_pairs(ar[ks]);
+      for (int j = 0; j < 4; ++j) tmp[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        u32x4 ap = x_pairs(ar[c][ks]);
         if (!xok) ap = u32x4{0u, 0u, 0u, 0u};
         const half8v A = __builtin_bit_cast(half8v, ap);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t wc = w[ks][j];
+          const uint32_t wc = w[c][ks][j];
           const half_t zb1 = -((half_t)1024.0f + z4[j]);
           const half2_t zb = {zb1, zb1};
           u32x4 b;
@@ -331,115 +363,145 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
           tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), tmp[j], 0, 0, 0);
         }
       }
-    }
-    const half4_t s4 = __builtin_bit_cast(half4_t, sv);
+      const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float sj = (float)s4[j];
+      for (int j = 0; j < 4; ++j) {
+        const float sj = (float)s4[j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(sj, tmp[j][i], acc[j][i]);
+        for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(sj, tmp[j][i], acc[j][i]);
+      }
     }
   }
 
-  // tile j, element i of lane l: row 4*kb + i, column 4*c16 + j of the workgroup's 64 columns;
-  // partials stored wave-minor ([16*64][NWP])
-  const int NWP = (NW + 3) & ~3;
+  // tile j, element i of lane l: row 4*kb + i, column 4*c16 + j of the workgroup's 64 columns.
+  // Rows >= M are all zero and not stored; each lane writes 4 consecutive columns per row.
+  const int n = mrows * CW;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[((size_t)(4 * kb + i) * CW + 4 * c16 + j) * NWP + wave] = acc[j][i];
-  __syncthreads();
-  auto part = [&](int o) { return ldk::sum_partials(red + (size_t)o * NWP, NW); };
-  auto store = [&](int o, float v) {
-    const int m = o / CW, n = n0 + (o - m * CW);
-    if (m < a.M && n < a.N) {
-      if (a.bias) v += (float)a.bias[n];
-      a.out[(int64_t)m * a.ldo + n] = (half_t)v;
-    }
-  };
-  if (sp.splits == 1) {
-    for (int o = threadIdx.x; o < 16 * CW; o += blockDim.x) store(o, part(o));
-  } else {
-    ldk::splitk_finalize(tile, split, sp.splits, 16 * CW, sp.ws, sp.counters, part, store);
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * kb + i;
+    if (row < mrows)
+      *reinterpret_cast<float4_t*>(red + (size_t)wave * n + row * CW + 4 * c16) =
+          float4_t{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
   }
+  __syncthreads();
+  finish_tile(red, n, NW, tile, sp, [&](int o, float v) {
+    const int m = o / CW, nn = n0 + (o - m * CW);
+    if (nn < a.N) {
+      if (a.bias) v += (float)a.bias[nn];
+      a.out[(int64_t)m * a.ldo + nn] = (half_t)v;
+    }
+  });
 }
 
 // ------------------------------------------------------------------------------------ dispatch
 
 struct Plan {
   bool mfma;
-  int mt, ln, rpl;  // VALU kernel shape
+  int mt, ln, rpl, cpw;  // row tile, lanes along N, rows per lane, chunks per wave and round
   bool fact;
   int nw, splits, gps;
 };
 
 int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-size_t plan_lds_bytes(const Plan& p, int gsh_rows) {
-  const size_t nwp = (size_t)((p.nw + 3) & ~3);
-  if (p.mfma) return nwp * 16 * 64 * 4;
-  const int rpg = 1 << gsh_rows;
-  const int LG = rpg / p.rpl, GW = (64 / p.ln) / LG;
-  return (size_t)p.nw * GW * rpg * p.mt * (p.fact ? 32 : 16) + nwp * p.mt * 4 * p.ln * 4;
+// Instantiated (MT, LN, RPL, CPW) shapes of the VALU kernel: those that fit the register budget
+// of 1024-thread workgroups (128 VGPRs) without spilling. RPL = 8 is only needed for LN = 16
+// with 32-row groups (the plan takes RPL = 4 otherwise).
+constexpr bool gemv_shape_ok(bool fact, int mt, int ln, int rpl, int cpw) {
+  if (ln != 4 && ln != 8 && ln != 16) return false;
+  if (rpl == 8) return ln == 16 && cpw == 1;
+  if (rpl != 4) return false;
+  if (fact) return cpw == 1 || cpw == 2 || (cpw == 4 && ln == 16);
+  if (mt <= 2) return cpw == 1 || cpw == 2;
+  if (mt == 4) return cpw == 1 || (cpw == 2 && ln >= 8);
+  return mt == 8 && cpw == 1 && ln >= 8;
 }
 
-size_t workspace_need(const Plan& p, int64_t N) {
+int gemv_pxw(const Plan& p) { return (p.cpw * p.rpl * p.mt + p.ln - 1) / p.ln; }
+
+size_t plan_lds_bytes(const Plan& p, int64_t M) {
+  if (p.mfma) return (size_t)p.nw * std::min<int64_t>(M, 16) * 64 * 4;
+  return (size_t)p.nw * 64 * gemv_pxw(p) * (p.fact ? 32 : 16) + (size_t)p.nw * p.mt * 4 * p.ln * 4;
+}
+
+size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
   if (p.splits <= 1) return 0;
   const int cw = p.mfma ? 64 : 4 * p.ln;
   const int64_t tiles = (N + cw - 1) / cw;
-  const int n = p.mfma ? 16 * 64 : p.mt * cw;
-  if (tiles > kCounterBytes / 4) return SIZE_MAX;  // one counter per tile
-  return kCounterBytes + (size_t)tiles * p.splits * n * 4;
+  const int64_t n = p.mfma ? std::min<int64_t>(M, 16) * 64 : (int64_t)p.mt * cw;
+  return (size_t)tiles * n * 8;
 }
 
-// Chooses the kernel, column tile, rows per lane, workgroup size and split count for a shape.
-// Measured on MI355X: row runs of >= 64 B per tile, ~8-16 waves per CU across >= 256 CUs and a
-// single chunk of loads per lane are what reach the memory-system floor.
+int cpw_from_flags(int flags) {
+  const int v = (flags & LDK_CPW_MASK) >> 4;
+  return v ? 1 << (v - 1) : 0;
+}
+
+// Chooses the kernel, column tile, rows per lane, chunks per wave, workgroup size and split
+// count for a shape. Measured on MI355X (decode shapes of Qwen2.5-1.5B, graph-timed sweeps over
+// block_n, split_k and chunks per wave): 128-byte row runs per tile read best on shapes of a few
+// MB; fewer than ~150 workgroups leave bandwidth unused once a shape moves more than a couple of
+// MB (the down projection reads 3.0 us at 192 workgroups against 5.7 us at 48), while a split
+// costs one dependent atomic round trip (~0.5 us), so only large, narrow shapes split. One chunk
+// per wave (more, smaller waves) beat deeper per-wave pipelining on every decode shape.
 Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int split_k, int flags,
                size_t ws_bytes) {
   Plan p{};
   const int rpg = 1 << gsh_rows;
   const int64_t ng = (K / 8) >> gsh_rows;
-  p.mfma = (M > 8 && !(flags & LDK_PATH_VALU)) || (flags & LDK_PATH_MFMA);
+  const int64_t wbytes = N * K / 2;
+  // MFMA from 5 rows (3 on shapes of > 4 MB): its B operand costs 11 VALU ops per 8 weights for
+  // all 16 rows, the VALU kernel's dequantize-then-dot grows by 4 dot2 per 8 weights per row.
+  const bool mfma_auto = M > 4 || (M > 2 && wbytes > (4 << 20));
+  p.mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
   p.mt = p.mfma ? 16 : round_mt(M);
   p.fact = !p.mfma && p.mt == 1 && !(flags & LDK_EXACT);
   if (p.mfma) {
     p.ln = 16;
   } else if (block_n) {
     p.ln = block_n / 4;
+  } else if (p.mt == 1) {  // 64-byte rows keep more workgroups busy on small shapes
+    p.ln = (N >= 4096 || wbytes > (2 << 20)) ? 8 : 4;
+  } else if (p.mt == 8) {
+    p.ln = N >= 1024 ? 16 : 8;
   } else {
-    p.ln = N >= 8192 ? 16 : N >= 512 ? 8 : 4;
+    p.ln = N >= 512 ? 8 : 4;
   }
   const int cw = p.mfma ? 64 : 4 * p.ln;
   const int lkw = 64 / p.ln;
-  // rows per lane: a group's packed rows over LG lanes with LG | LKW
-  p.rpl = rpg;
-  for (int rpl : {4, 8, 2, 16, 1, 32}) {
-    if (rpl <= rpg && rpg % rpl == 0 && lkw % (rpg / rpl) == 0) { p.rpl = rpl; break; }
-  }
+  p.rpl = (lkw % (rpg / std::min(rpg, 4)) == 0) ? std::min(rpg, 4) : 8;  // LG = rpg/rpl divides LKW
   const int gw = p.mfma ? 1 : lkw / (rpg / p.rpl);
   const int64_t tiles = (N + cw - 1) / cw;
-  // split count: enough workgroups for the 256 CUs, at most 16 waves per workgroup
   int64_t splits = split_k > 0 ? split_k : 1;
-  if (split_k <= 0) {
-    while (tiles * splits < 240 && splits * 2 <= ng) splits *= 2;
-    while ((ng + splits - 1) / splits > 16 * gw && splits < ng) ++splits;
-  }
-  splits = std::min<int64_t>(splits, ng);
+  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20)) splits = (192 + tiles - 1) / tiles;
+  splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
   p.splits = (int)((ng + p.gps - 1) / p.gps);
-  p.nw = (int)std::min<int64_t>(16, (p.gps + gw - 1) / gw);
-  if (p.splits > 1 && workspace_need(p, N) > ws_bytes) {  // no room for partials: one split
+  if (p.splits > 1 && workspace_need(p, M, N) > ws_bytes) {  // no room for partials: one split
     p.splits = 1;
     p.gps = (int)ng;
-    p.nw = (int)std::min<int64_t>(16, (ng + gw - 1) / gw);
   }
+  const int64_t chunks = (p.gps + gw - 1) / gw;
+  // chunks per wave and round: the smallest that fits all chunks in one round of <= 16 waves
+  int cpw = cpw_from_flags(flags);
+  if (!cpw) {
+    cpw = 4;
+    for (int c : {1, 2, 4})
+      if (chunks <= 16 * c) { cpw = c; break; }
+  }
+  if (p.mfma) {
+    cpw = std::min(cpw, rpg <= 16 ? 2 : 1);
+  } else {
+    while (cpw > 1 && !gemv_shape_ok(p.fact, p.mt, p.ln, p.rpl, cpw)) cpw >>= 1;
+  }
+  p.cpw = cpw;
+  p.nw = (int)std::min<int64_t>(16, (chunks + cpw - 1) / cpw);
   return p;
 }
 
-template <int MT, int LN, int RPL, bool FACT>
+template <int MT, int LN, int RPL, bool FACT, int CPW>
 int launch_gemv_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipStream_t stream) {
-  auto kern = w4a16_gemv_kernel<MT, LN, RPL, FACT>;
+  auto kern = w4a16_gemv_kernel<MT, LN, RPL, FACT, CPW>;
   if (lds > 64 * 1024) {
     if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: LDS need %zu B exceeds 160 KiB", lds);
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -451,54 +513,65 @@ int launch_gemv_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
   return ldk::check_launch("w4a16_gemv");
 }
 
-template <int MT, int LN, bool FACT>
-int launch_gemv_rpl(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
-  switch (p.rpl) {
-    case 1: return launch_gemv_t<MT, LN, 1, FACT>(a, sp, p.nw, lds, s);
-    case 2: return launch_gemv_t<MT, LN, 2, FACT>(a, sp, p.nw, lds, s);
-    case 4: return launch_gemv_t<MT, LN, 4, FACT>(a, sp, p.nw, lds, s);
-    case 8: return launch_gemv_t<MT, LN, 8, FACT>(a, sp, p.nw, lds, s);
-    case 16: return launch_gemv_t<MT, LN, 16, FACT>(a, sp, p.nw, lds, s);
+template <int MT, int LN, bool FACT, int RPL, int CPW>
+int try_gemv(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s, bool* done) {
+  if constexpr (gemv_shape_ok(FACT, MT, LN, RPL, CPW)) {
+    if (p.rpl == RPL && p.cpw == CPW) {
+      *done = true;
+      return launch_gemv_t<MT, LN, RPL, FACT, CPW>(a, sp, p.nw, lds, s);
+    }
   }
-  return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %d rows per lane not instantiated", p.rpl);
+  return LDK_OK;
+}
+
+template <int MT, int LN, bool FACT>
+int launch_gemv_shape(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
+  bool done = false;
+  int st = try_gemv<MT, LN, FACT, 4, 1>(a, sp, p, lds, s, &done);
+  if (!done) st = try_gemv<MT, LN, FACT, 4, 2>(a, sp, p, lds, s, &done);
+  if (!done) st = try_gemv<MT, LN, FACT, 4, 4>(a, sp, p, lds, s, &done);
+  if (!done) st = try_gemv<MT, LN, FACT, 8, 1>(a, sp, p, lds, s, &done);
+  if (!done)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: VALU shape mt=%d block_n=%d rpl=%d cpw=%d not instantiated", MT,
+                     4 * LN, p.rpl, p.cpw);
+  return st;
 }
 
 template <int MT, bool FACT>
 int launch_gemv_ln(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
   switch (p.ln) {
-    case 4: return launch_gemv_rpl<MT, 4, FACT>(a, sp, p, lds, s);
-    case 8: return launch_gemv_rpl<MT, 8, FACT>(a, sp, p, lds, s);
-    case 16: return launch_gemv_rpl<MT, 16, FACT>(a, sp, p, lds, s);
+    case 4: return launch_gemv_shape<MT, 4, FACT>(a, sp, p, lds, s);
+    case 8: return launch_gemv_shape<MT, 8, FACT>(a, sp, p, lds, s);
+    case 16: return launch_gemv_shape<MT, 16, FACT>(a, sp, p, lds, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
 }
 
+template <int KS, int CPW>
+int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipStream_t s) {
+  auto kern = w4a16_mfma16_kernel<KS, CPW>;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
+  const int64_t tiles = (a.N + 63) / 64;
+  (void)hipGetLastError();
+  kern<<<(unsigned)(tiles * sp.splits), nw * 64, lds, s>>>(a, sp);
+  return ldk::check_launch("w4a16_mfma16");
+}
+
 int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
-  SplitArgs sp{p.splits, p.gps, nullptr, nullptr};
-  if (p.splits > 1) {
-    sp.counters = reinterpret_cast<uint32_t*>(ws);
-    sp.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
-  }
-  const size_t lds = plan_lds_bytes(p, a.gsh_rows);
+  SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr};
+  const size_t lds = plan_lds_bytes(p, a.M);
+  if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: LDS need %zu B exceeds 160 KiB", lds);
   if (p.mfma) {
-    (void)hipGetLastError();
-    const int64_t tiles = (a.N + 63) / 64;
-    const unsigned grid = (unsigned)(tiles * p.splits);
-    if (lds > 64 * 1024) {
-      const void* k[] = {(const void*)w4a16_mfma16_kernel<1>, (const void*)w4a16_mfma16_kernel<2>,
-                         (const void*)w4a16_mfma16_kernel<4>, (const void*)w4a16_mfma16_kernel<8>};
-      for (const void* f : k)
-        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-          return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
-    }
+    const bool two = p.cpw == 2;
     switch (1 << a.gsh_rows) {
-      case 4: w4a16_mfma16_kernel<1><<<grid, p.nw * 64, lds, s>>>(a, sp); break;
-      case 8: w4a16_mfma16_kernel<2><<<grid, p.nw * 64, lds, s>>>(a, sp); break;
-      case 16: w4a16_mfma16_kernel<4><<<grid, p.nw * 64, lds, s>>>(a, sp); break;
-      case 32: w4a16_mfma16_kernel<8><<<grid, p.nw * 64, lds, s>>>(a, sp); break;
-      default: return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
+      case 4: return two ? launch_mfma_t<1, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<1, 1>(a, sp, p.nw, lds, s);
+      case 8: return two ? launch_mfma_t<2, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<2, 1>(a, sp, p.nw, lds, s);
+      case 16: return two ? launch_mfma_t<4, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<4, 1>(a, sp, p.nw, lds, s);
+      case 32: return launch_mfma_t<8, 1>(a, sp, p.nw, lds, s);
     }
-    return ldk::check_launch("w4a16_mfma16");
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
   }
   if (p.fact) return launch_gemv_ln<1, true>(a, sp, p, lds, s);
   switch (p.mt) {
@@ -533,6 +606,11 @@ int validate(const char* fn, const void* x, int64_t ldx, const int32_t* qw, cons
   return LDK_OK;
 }
 
+int plan_flags(const Plan& p) {
+  const int cpw_code = p.mfma || p.cpw == 0 ? 0 : (p.cpw == 1 ? 1 : p.cpw == 2 ? 2 : 3);
+  return (p.mfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.fact ? LDK_FACTORED : LDK_EXACT) | (cpw_code << 4);
+}
+
 }  // namespace
 
 extern "C" int64_t ldk_workspace_bytes(void) { return (int64_t)32 << 20; }
@@ -545,7 +623,7 @@ extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size,
   const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
   if (block_n) *block_n = p.mfma ? 64 : 4 * p.ln;
   if (split_k) *split_k = p.splits;
-  if (flags) *flags = (p.mfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.fact ? LDK_FACTORED : LDK_EXACT);
+  if (flags) *flags = plan_flags(p);
   return LDK_OK;
 }
 
@@ -557,6 +635,8 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   int st = validate("w4a16_matmul", x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
   if (st) return st;
   if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: M=%lld > 16 (prefill GEMM not built yet)", (long long)M);
+  if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_CPW_MASK))
+    return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: unknown flags 0x%x", flags);
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: FACTORED and EXACT are exclusive");
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: VALU and MFMA paths are exclusive");
   if ((flags & LDK_FACTORED) && M > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED is the M = 1 kernel");
@@ -564,11 +644,12 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   if (block_n && block_n != 16 && block_n != 32 && block_n != 64)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=%d must be 16, 32 or 64", block_n);
   if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d must be >= 0", split_k);
+  if (split_k > kMaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: split_k=%d above %d", split_k, kMaxSplits);
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul: workspace must be a 256-byte aligned pointer");
   const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
   if (p.mfma && block_n && block_n != 64) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n=64");
-  if (split_k > 1 && p.splits == 1)
+  if (split_k > 1 && p.splits == 1 && (K / group_size) > 1)
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
                  (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, gsh_rows};

@@ -25,6 +25,8 @@ OK, ERR_INVALID, ERR_ALIGN, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3, 4
 F16, BF16, F32 = 0, 1, 2
 # flags (enum ldk_flags).
 FACTORED, EXACT, PATH_VALU, PATH_MFMA = 1, 2, 4, 8
+CPW_FLAGS = {1: 16, 2: 32, 4: 48}  # chunks of loads per wave and round (LDK_CPW_*)
+CPW_MASK = 48
 
 _DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
 

@@ -4,10 +4,11 @@ Drop-in for the reference's `kernels/w4a16.py` (same `w4a16_matmul` signature, s
 from `kernels.quant`). Decode shapes (M <= 16) run one hand-written HIP kernel from
 libldk_amd.so whose tile and K-split come from the library's per-shape table:
 
-- each workgroup owns a strip of output columns and ALL of K; lanes split K and the partial sums
-  are reduced inside the workgroup (DPP/permlane within a wave, LDS across waves), so there is
-  no atomic, zero-fill or cast launch (the reference's split paths add two elementwise launches,
-  w4a16.py:218-219,272-275);
+- each workgroup owns a strip of output columns and a range of K; lanes split K and the partial
+  sums are reduced inside the workgroup (DPP/permlane within a wave, LDS across waves); narrow
+  shapes with many bytes (the down projection) also split K across workgroups that meet in a
+  per-device workspace, all within the one launch, so there is no zero-fill or cast launch (the
+  reference's split paths add two elementwise launches, w4a16.py:218-219,272-275);
 - M = 1 uses the FACTORED inner loop s * (sum x*q - z * sum x) (w4a16.py:116-119); 2 <= M <= 16
   dequantizes each weight exactly as dequantize_ref and accumulates with v_dot2_f32_f16.
 
@@ -18,8 +19,9 @@ there, w4a16.py:264-268).
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
 `GEMV` (force the VALU decode kernel, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
 (True: factored M=1 loop; False: exact dequantize-then-dot), `block_n` (columns per workgroup:
-16, 32 or 64) and `split_k` (workgroups splitting K per column tile). Triton tile keys (BLOCK_M,
-BLOCK_N, BLOCK_K, SPLIT_K, GROUP_M) describe Triton programs and are ignored.
+16, 32 or 64), `split_k` (workgroups splitting K per column tile) and `chunks_per_wave` (1, 2 or
+4: load chunks a wave keeps in flight per round). Triton tile keys (BLOCK_M, BLOCK_N, BLOCK_K,
+SPLIT_K, GROUP_M) describe Triton programs and are ignored.
 """
 
 from __future__ import annotations
@@ -51,6 +53,8 @@ def _flags_from_config(config: dict | None, M: int) -> tuple[int, int, int]:
             flags |= _lib.FACTORED
         elif not config["FACTORED"]:
             flags |= _lib.EXACT
+    if config.get("chunks_per_wave"):
+        flags |= _lib.CPW_FLAGS[int(config["chunks_per_wave"])]
     return int(config.get("block_n", 0)), int(config.get("split_k", 0)), flags
 
 
@@ -104,7 +108,9 @@ def config_for(M: int, N: int, K: int, group_size: int = 128) -> str:
                                             ctypes.byref(sk), ctypes.byref(fl)), "w4a16_config")
     mode = "factored" if fl.value & _lib.FACTORED else "exact"
     path = "mfma" if fl.value & _lib.PATH_MFMA else "valu"
-    return f"{path},block_n={bn.value},split_k={sk.value},{mode}"
+    cpw = {v: k for k, v in _lib.CPW_FLAGS.items()}.get(fl.value & _lib.CPW_MASK)
+    extra = f",chunks_per_wave={cpw}" if cpw else ""
+    return f"{path},block_n={bn.value},split_k={sk.value},{mode}{extra}"
 
 
 def export_choices() -> dict:

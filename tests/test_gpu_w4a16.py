@@ -63,6 +63,28 @@ def test_split_k_variants(split_k):
     _run(16, 1536, 1536, config={"split_k": split_k})
 
 
+@pytest.mark.parametrize("cpw", [1, 2, 4])
+def test_chunks_per_wave_variants(cpw):
+    """Several load chunks in flight per wave (rounds of cpw chunks, runtime loop over rounds),
+    with and without a cross-workgroup split, ragged chunk counts included (K=8960: 70 groups)."""
+    for bn in (16, 32, 64):
+        _run(1, 1536, 8960, config={"block_n": bn, "chunks_per_wave": cpw})
+        _run(1, 512, 8960, config={"block_n": bn, "chunks_per_wave": cpw, "split_k": 3})
+    _run(1, 17920 // 8, 1536, config={"chunks_per_wave": cpw})
+    if cpw <= 2:
+        for M in (2, 3, 4):
+            _run(M, 1536, 8960, config={"chunks_per_wave": cpw, "block_n": 32})
+        _run(16, 1536, 8960, config={"chunks_per_wave": cpw})
+        _run(12, 512, 8960, config={"chunks_per_wave": cpw, "split_k": 5})
+        _run(4, 512, 1536, config={"MFMA": True, "chunks_per_wave": cpw})
+
+
+@pytest.mark.parametrize("gs", [32, 256])
+def test_chunks_per_wave_group_sizes(gs):
+    _run(1, 512, 4096, gs=gs, config={"chunks_per_wave": 2})
+    _run(16, 512, 4096, gs=gs, config={"chunks_per_wave": 2})
+
+
 def test_split_k_repeated_calls_keep_counters_clean():
     """The last workgroup of a tile resets its counter: many calls in a row stay correct."""
     x, qw, s, z, _ = _make(1, 1536, 8960, 7)
@@ -72,6 +94,38 @@ def test_split_k_repeated_calls_keep_counters_clean():
         out = w4a16_matmul(*args, config={"split_k": 7})
     torch.cuda.synchronize()
     assert_north_star(out, ref)
+
+
+def test_split_k_deterministic():
+    """Split partials meet as fixed-point integers: any arrival order gives the same bits."""
+    x, qw, s, z, _ = _make(4, 1536, 8960, 11)
+    args = (dev(x), dev(qw), dev(s), dev(z))
+    for cfg in ({"split_k": 7}, {"split_k": 5, "MFMA": True}):
+        outs = [w4a16_matmul(*args, config=cfg) for _ in range(8)]
+        for o in outs[1:]:
+            assert torch.equal(o, outs[0])
+
+
+def test_split_k_nonfinite_input_propagates():
+    """An inf in x makes every output non-finite on the split path, as on the unsplit one."""
+    x, qw, s, z, _ = _make(1, 256, 2048, 12)
+    x = x.copy()
+    x[0, 5] = np.inf
+    args = (dev(x), dev(qw), dev(s), dev(z))
+    a = w4a16_matmul(*args, config={"split_k": 1})
+    b = w4a16_matmul(*args, config={"split_k": 4})
+    assert not torch.isfinite(a).any() and not torch.isfinite(b).any()
+
+
+def test_split_k_large_partials():
+    """Partial sums of magnitude ~1e4 (outputs near the fp16 limit) stay within tolerance."""
+    x, qw, s, z, _ = _make(2, 512, 8960, 13)
+    s = (s.astype(np.float32) * 160).astype(np.float16)
+    out = w4a16_matmul(dev(x * 4), dev(qw), dev(s), dev(z), config={"split_k": 6})
+    ref = w4a16_ref(x * 4, qw, s, z)
+    assert 1e3 < np.abs(ref).max() < 6e4
+    got = out.float().cpu().numpy()
+    assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(ref) + 0.5)
 
 
 @pytest.mark.parametrize("M", [1, 4, 9, 16])
