@@ -145,21 +145,27 @@ constexpr float kFixClamp = 1048576.0f;           // 2^20
 constexpr int64_t kFixPoison = int64_t(1) << 50;  // > 32 * 2^44, the largest legal sum
 constexpr int64_t kFixPoisonSeen = int64_t(3) << 48;
 
+// Adds partial p of one output to its accumulator word. Returns true in the one contribution that
+// completes the count; *total then holds the reduced value and the word is back to zero.
+__device__ __forceinline__ bool splitk_add(uint64_t* word, int splits, float p, float* total) {
+  const int64_t v = __builtin_isfinite(p)
+                        ? (int64_t)__builtin_rintf(__builtin_fminf(__builtin_fmaxf(p, -kFixClamp), kFixClamp) * kFixScale)
+                        : kFixPoison;
+  const uint64_t inc = ((uint64_t)v << 8) + 1u;
+  const uint64_t old = __hip_atomic_fetch_add(word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((int)(old & 0xffu) != splits - 1) return false;
+  const int64_t tot = (int64_t)(old + inc) >> 8;
+  const bool poisoned = tot >= kFixPoisonSeen || tot <= -kFixPoisonSeen;
+  *total = poisoned ? __builtin_nanf("") : (float)tot * (1.0f / kFixScale);
+  __hip_atomic_store(word, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 template <typename Part, typename Store>
 __device__ __forceinline__ void splitk_accumulate(uint64_t* acc, int splits, int n, Part part, Store store) {
   for (int o = threadIdx.x; o < n; o += blockDim.x) {
-    const float p = part(o);
-    const int64_t v = __builtin_isfinite(p)
-                          ? (int64_t)__builtin_rintf(__builtin_fminf(__builtin_fmaxf(p, -kFixClamp), kFixClamp) * kFixScale)
-                          : kFixPoison;
-    const uint64_t inc = ((uint64_t)v << 8) + 1u;
-    const uint64_t old = __hip_atomic_fetch_add(acc + o, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((int)(old & 0xffu) == splits - 1) {
-      const int64_t tot = (int64_t)(old + inc) >> 8;
-      const bool poisoned = tot >= kFixPoisonSeen || tot <= -kFixPoisonSeen;
-      store(o, poisoned ? __builtin_nanf("") : (float)tot * (1.0f / kFixScale));
-      __hip_atomic_store(acc + o, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    float tot;
+    if (splitk_add(acc + o, splits, part(o), &tot)) store(o, tot);
   }
 }
 

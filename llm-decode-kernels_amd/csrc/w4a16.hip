@@ -1,24 +1,22 @@
 // W4A16 matmul for decode (M <= 16): y[M, N] = x[M, K] @ dequant(W)^T (+ bias).
 //
 // Replaces the reference's Triton GEMV/GEMM launch paths (kernels/w4a16.py:100-160, 214-279) and
-// its CUDA decode kernel (kernels/cuda/w4a16_decode.cu:29-121) with two gfx950 kernels that share
-// one work decomposition:
+// its CUDA decode kernel (kernels/cuda/w4a16_decode.cu:29-121) with three gfx950 kernels that
+// share one work decomposition:
 //
 //  * Tiles and groups. A workgroup owns CW output columns and a range of quantization groups
 //    (all of K, or 1/splits of it). Inside the workgroup each wave takes whole groups, so every
 //    lane applies one scale and one zero point per group and a group's partial sums never leave
-//    the lane until the final reduction.
-//  * Memory-level parallelism. A wave works in rounds of CPW chunks (a chunk is the groups its
-//    lanes cover with one 128-bit load each per row). Per round a lane issues every load first:
-//    its x rows, then chunk by chunk the packed weight rows with their scale and zero words. It
-//    consumes them in issue order, so each s_waitcnt vmcnt(n) releases work as data lands:
-//    the compute of an early chunk overlaps the arrival of the later ones, and a launch's whole
-//    weight stream is in flight at once. Row segments are CW*4 >= 64 bytes long (shorter runs
-//    per row were measured to cost 2-7x on MI355X).
+//    the lane until the final reduction. Column tiles are 128 bytes of packed weight per row (one
+//    L2 line) by default: 64-byte tiles put the two halves of a line on different XCDs, which
+//    then both fetch it (measured 1.5x slower on MI355X).
+//  * Memory-level parallelism. Every load of a pass is issued before the first wait: the x row,
+//    the scale and zero words and the packed weight rows, pinned in that order by a scheduling
+//    barrier (without it the compiler reuses registers and issues later rows only after the
+//    first data has arrived, a second serial memory round trip). Data is consumed in issue order,
+//    so each s_waitcnt vmcnt(n) releases work as it lands.
 //  * No workgroup barrier before the compute: x rows are staged through LDS by the wave that
-//    uses them (wave-local exchange), so weight loads never wait on other waves. Rows outside the
-//    workgroup's groups and x rows >= M are staged as zeros, which makes their products exact
-//    zeros without any masking in the inner loops.
+//    uses them (wave-local exchange), so weight loads never wait on other waves.
 //  * Split-K. Partials are reduced inside the workgroup (DPP row rotations and gfx950 permlane
 //    swaps within a wave, then LDS across waves). Narrow shapes (few column tiles) also split the
 //    groups over `splits` workgroups that meet in a caller-provided workspace through one 64-bit
@@ -30,14 +28,14 @@
 // (0x6400) is exactly the fp16 value 1024 + q, so one v_and_or_b32 per pair turns packed nibbles
 // into fp16 pairs (q_i, q_{i+4}); x is staged as the matching pairs (x_i, x_{i+4}).
 //
-//  - VALU kernel (M <= 8), wave64 lanes own 4 adjacent columns (one 128-bit load = one packed
-//    row of 4 columns = 32 weights):
-//      FACTORED (M = 1): s * (sum x*q - z * sum x) per group, the reference's FACTORED identity
-//      (kernels/w4a16.py:116-119). Nibbles 1/3/5/7 are masked in place as 16*q and meet x pairs
-//      pre-scaled by 1/16; one v_dot2_f32_f16 chain per column runs over all of the lane's rows
-//      of a group, starting at -1024*(offset-weighted sum of x); ~9 VALU ops per 8 weights.
-//      EXACT: ((1024+q) - (1024+z)) * s in packed fp16 is exactly the reference's dequantized
-//      weight (one RNE rounding, kernels/reference.py:35), then dot2 with each x row.
+//  - M = 1 kernel (FACTORED): s * (sum x*q - z * sum x) per group, the reference's FACTORED
+//    identity (kernels/w4a16.py:116-119). Nibbles 1/3/5/7 are masked in place as 16*q and meet x
+//    pairs pre-scaled by 1/16; one v_dot2_f32_f16 chain per column runs over the lane's four rows
+//    of a group, starting at -1024*(offset-weighted sum of x): 9 VALU ops per 8 weights. All tile
+//    parameters are compile-time, so the epilogue is straight-line code.
+//  - VALU kernel (M <= 8, EXACT): ((1024+q) - (1024+z)) * s in packed fp16 is exactly the
+//    reference's dequantized weight (one RNE rounding, kernels/reference.py:35), then dot2 with
+//    each x row. Also the M = 1 path when exact dequantization is requested.
 //  - MFMA kernel (larger M): an int32 word holds 8 consecutive K of one column, which is exactly
 //    one lane's B operand of v_mfma_f32_16x16x32_f16. A lane's 128-bit load feeds four 16x16
 //    tiles; B = (q - z) exactly in fp16, A = x rows permuted to the nibble-pair order, the fp32
@@ -82,26 +80,24 @@ __device__ __forceinline__ u32x4 x_pairs(u32x4 d) {
   return u32x4{perm_lo(d[0], d[2]), perm_hi(d[0], d[2]), perm_lo(d[1], d[3]), perm_hi(d[1], d[3])};
 }
 
-// LDS row record of one (packed row, x row): the x pairs; for FACTORED the odd pairs are scaled
-// by 1/16 and the record carries c0 = -1024*((x0+x2+x4+x6) + (x1+x3+x5+x7)/16) and x0+...+x7.
-template <bool FACT>
-__device__ __forceinline__ void store_x_record(unsigned char* dst, u32x4 d) {
+// 32-byte LDS record of one packed x row for the FACTORED loop: the x pairs with the odd pairs
+// scaled by 1/16 (exact), then c0 = -1024*((x0+x2+x4+x6) + (x1+x3+x5+x7)/16) and x0+...+x7.
+__device__ __forceinline__ void store_fact_record(unsigned char* dst, u32x4 d) {
   u32x4 p = x_pairs(d);
-  if constexpr (FACT) {
-    const half2_t a0 = ldk::u2h2(p[0]), a2 = ldk::u2h2(p[2]);
-    const half2_t b1 = ldk::u2h2(p[1]), b3 = ldk::u2h2(p[3]);
-    const float xa = ((float)a0[0] + (float)a0[1]) + ((float)a2[0] + (float)a2[1]);
-    const float xb = ((float)b1[0] + (float)b1[1]) + ((float)b3[0] + (float)b3[1]);
-    const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
-    p[1] = ldk::h22u(b1 * sixteenth);
-    p[3] = ldk::h22u(b3 * sixteenth);
-    *reinterpret_cast<float2_t*>(dst + 16) = float2_t{-1024.0f * (xa + 0.0625f * xb), xa + xb};
-  }
+  const half2_t a0 = ldk::u2h2(p[0]), a2 = ldk::u2h2(p[2]);
+  const half2_t b1 = ldk::u2h2(p[1]), b3 = ldk::u2h2(p[3]);
+  const float xa = ((float)a0[0] + (float)a0[1]) + ((float)a2[0] + (float)a2[1]);
+  const float xb = ((float)b1[0] + (float)b1[1]) + ((float)b3[0] + (float)b3[1]);
+  const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
+  p[1] = ldk::h22u(b1 * sixteenth);
+  p[3] = ldk::h22u(b3 * sixteenth);
   *reinterpret_cast<u32x4*>(dst) = p;
+  *reinterpret_cast<float2_t*>(dst + 16) = float2_t{-1024.0f * (xa + 0.0625f * xb), xa + xb};
 }
 
-// Shared epilogue: the workgroup's NW wave partials of n outputs sit wave-major in `red`; sum
-// them and store (or hand them to the cross-workgroup split-K reduction).
+// Shared epilogue of the multi-row kernels: the workgroup's NW wave partials of n outputs sit
+// wave-major in `red`; sum them and store (or hand them to the cross-workgroup split-K
+// reduction).
 template <typename Store>
 __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, int tile,
                                             const SplitArgs& sp, Store store) {
@@ -113,19 +109,131 @@ __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, int
   }
 }
 
-// ------------------------------------------------------------------------------ VALU kernel
+// ---------------------------------------------------------------------------- M = 1 kernel
+//
+// Lane (ln, lk) of a wave: ln < LN runs along N (columns n0 + 4ln .. +3), lk < LKW = 64/LN along
+// K. Each lane owns RPL = 4 packed rows of one group, so LG = rows_per_group / 4 lanes share a
+// group (sub = lk % LG takes rows sub, sub + LG, sub + 2LG, sub + 3LG) and a wave covers
+// GPW = LKW / LG groups = RPW = 4 * LKW packed rows per pass. Waves take passes over the
+// workgroup's groups at a stride of NW * GPW groups.
+// RSH > 0 fixes log2(rows per group) at compile time (the common group size 128 has RSH = 4);
+// RSH = 0 reads it from the arguments.
+template <int LN, int NW, int RSH>
+__global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec) {
+  constexpr int LKW = 64 / LN, RPL = 4, RPW = RPL * LKW, CW = 4 * LN;
+  __shared__ __align__(16) unsigned char xrec[NW][RPW][32];
+  __shared__ __align__(16) float4_t red[NW][LN];
+  const int rsh = RSH ? RSH : a.gsh_rows;  // log2(packed rows per group), >= 2
+  const int lgsh = rsh - 2;    // log2(LG)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane % LN, lk = lane / LN;
+  const int gi = lk >> lgsh, sub = lk & ((1 << lgsh) - 1);
+  const int gpw = LKW >> lgsh;
+  const int tile = blockIdx.x / sp.splits, split = blockIdx.x - tile * sp.splits;
+  const int n0 = tile * CW;
+  const int col = min(n0 + 4 * ln, a.N - 4);  // clamped: tail lanes load valid memory, store nothing
+  const int R = a.K >> 3, ng = R >> rsh;
+  const int gb = split * sp.gps, ge = min(ng, gb + sp.gps);
+
+  const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
+  const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int gp = gb + wave * gpw; gp < ge; gp += NW * gpw) {
+    const int row0 = gp << rsh;
+    const u32x4 xr = *reinterpret_cast<const u32x4*>(a.x + 8 * min(row0 + lane, R - 1));
+    const int g = min(gp + gi, ge - 1);  // clamped; such lanes are masked out below
+    const u32x2 sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
+    const u32x2 zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
+    u32x4 w[RPL];
+#pragma unroll
+    for (int t = 0; t < RPL; ++t) {
+      const int r = (g << rsh) + sub + (t << lgsh);
+      w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
+
+    if (lane < RPW) store_fact_record(&xrec[wave][lane][0], xr);
+    ldk::wave_lds_sync();
+    u32x4 xp[RPL];
+    float c0 = 0.0f, xs = 0.0f;
+#pragma unroll
+    for (int t = 0; t < RPL; ++t) {
+      const int rr = (gi << rsh) + sub + (t << lgsh);
+      xp[t] = *reinterpret_cast<const u32x4*>(&xrec[wave][rr][0]);
+      const float2_t k = *reinterpret_cast<const float2_t*>(&xrec[wave][rr][16]);
+      c0 += k[0];
+      xs += k[1];
+    }
+    float tt[4] = {c0, c0, c0, c0};
+#pragma unroll
+    for (int t = 0; t < RPL; ++t) {  // rows in arrival order
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t wc = w[t][q], v = wc >> 8;
+        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][3]), ldk::u2h2((v & mhi) | magic), tt[q], false);
+        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][2]), ldk::u2h2((v & mlo) | magic), tt[q], false);
+        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][1]), ldk::u2h2((wc & mhi) | magic), tt[q], false);
+        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][0]), ldk::u2h2((wc & mlo) | magic), tt[q], false);
+      }
+    }
+    const bool gok = gp + gi < ge;
+    const half4_t s4 = __builtin_bit_cast(half4_t, sv), z4 = __builtin_bit_cast(half4_t, zv);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // s * (sum x*q - z * sum x)
+      const float v = (float)s4[q] * __builtin_fmaf(-(float)z4[q], xs, tt[q]);
+      acc[q] += gok ? v : 0.0f;
+    }
+    ldk::wave_lds_sync();  // the next pass rewrites this wave's records
+  }
+
+  // ---- reduction: lanes sharing ln within the wave, then the NW waves through LDS
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = ldk::sum_lanes_strided<LN>(acc[q]);
+  if (lane < LN) red[wave][lane] = float4_t{acc[0], acc[1], acc[2], acc[3]};
+  __syncthreads();
+  if (wave != 0) return;
+  if (sp.splits == 1) {
+    const int c = n0 + 4 * lane;
+    if (lane >= LN || c >= a.N) return;
+    float4_t v = red[0][lane];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) v += red[i][lane];
+    if (a.bias) v += float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
+    const half4_t o{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+    if (out_vec) {
+      *reinterpret_cast<half4_t*>(a.out + c) = o;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a.out[c + q] = o[q];
+    }
+  } else {
+    // one output per lane, so the CW returning atomics of the tile are in flight together
+    const int c = n0 + lane;
+    if (lane >= CW || c >= a.N) return;
+    const float* rf = reinterpret_cast<const float*>(&red[0][0]);
+    float v = rf[lane];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) v += rf[i * CW + lane];
+    float tot;
+    if (ldk::splitk_add(sp.acc + (size_t)tile * CW + lane, sp.splits, v, &tot)) {
+      if (a.bias) tot += (float)a.bias[c];
+      a.out[c] = (half_t)tot;
+    }
+  }
+}
+
+// --------------------------------------------------------------------- VALU kernel (EXACT)
 //
 // Lane (ln, lkw) of a wave: ln < LN runs along N (columns n0 + 4ln .. +3), lkw < LKW = 64/LN along
 // K. LG = rows_per_group / RPL lanes share a group, each taking RPL of its packed rows
 // (sub, sub + LG, ...); a chunk is GW = LKW / LG groups (LKW*RPL packed rows). Chunk k of the
 // workgroup's range covers groups gb + k*GW ..; wave w takes chunks w, w + NW, ... in rounds of
 // CPW chunks.
-template <int MT, int LN, int RPL, bool FACT, int CPW>
+template <int MT, int LN, int RPL, int CPW>
 __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp) {
-  static_assert(!FACT || MT == 1, "FACTORED is the M = 1 kernel");
   constexpr int CW = 4 * LN;
   constexpr int LKW = 64 / LN;
-  constexpr int ROWB = FACT ? 32 : 16;
+  constexpr int ROWB = 16;
   constexpr int RPC = LKW * RPL;                // packed rows per chunk
   constexpr int ITEMS = CPW * RPC * MT;         // x records a wave stages per round
   constexpr int PXW = (ITEMS + 63) / 64;        // ... per lane
@@ -150,8 +258,8 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
   unsigned char* xw = smem + (size_t)wave * SLOTS * ROWB;
   float* red = reinterpret_cast<float*>(smem + (size_t)NW * SLOTS * ROWB);  // [NW][MT*CW]
 
-  const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
-  const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
+  const uint32_t magic = ldk::vgpr_const<kMagic>();
+  const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>();
   float acc[MT][4];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
@@ -159,8 +267,8 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
 
   for (int k0 = wave; k0 < nchunks; k0 += NW * CPW) {
-    // ---- loads, in consumption order: x rows of the round's chunks, then per chunk the weight
-    // rows with the scale and zero (FACTORED uses them after its dot chain, EXACT before)
+    // ---- loads, in consumption order: x rows of the round's chunks, then per chunk the scale
+    // and zero words and the weight rows
     u32x4 xr[PXW];
 #pragma unroll
     for (int i = 0; i < PXW; ++i) {
@@ -175,22 +283,18 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       const int gg = min(gb + (k0 + NW * c) * GW + gi, ge - 1);  // clamped; such lanes meet zero x
-      if constexpr (!FACT) {
-        sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
-        zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
-      }
+      sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
+      zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
 #pragma unroll
       for (int t = 0; t < RPL; ++t) {
         const int r = gg * rpg + sub + LG * t;
         w[c][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
       }
-      if constexpr (FACT) {
-        sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)gg * a.N + col);
-        zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)gg * a.N + col);
-      }
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the round is in flight before the first wait
 
-    // ---- wave-local x staging: every lane writes its own slots (no branches, no conflicts)
+    // ---- wave-local x staging: every lane writes its own slots (no branches, no conflicts).
+    // Rows outside the workgroup's groups and x rows >= M are staged as zeros.
 #pragma unroll
     for (int i = 0; i < PXW; ++i) {
       const int item = lane + 64 * i;
@@ -198,7 +302,7 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
       const int c = rc / RPC, rr = rc - c * RPC;
       const int row = rb + (k0 + NW * c) * GW * rpg + rr;
       const bool ok = item < ITEMS && m < a.M && row < re;
-      store_x_record<FACT>(xw + (size_t)item * ROWB, ok ? xr[i] : u32x4{0u, 0u, 0u, 0u});
+      *reinterpret_cast<u32x4*>(xw + (size_t)item * ROWB) = x_pairs(ok ? xr[i] : u32x4{0u, 0u, 0u, 0u});
     }
     ldk::wave_lds_sync();
 
@@ -206,65 +310,35 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
     for (int c = 0; c < CPW; ++c) {
       if (k0 + NW * c >= nchunks) break;  // uniform: the rest of the round is past the range
       const unsigned char* xc = xw + (size_t)(c * RPC + gi * rpg + sub) * MT * ROWB;
-      if constexpr (FACT) {
-        u32x4 xp[RPL];
-        float c0 = 0.0f, xs = 0.0f;
+      const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
+      const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
 #pragma unroll
-        for (int t = 0; t < RPL; ++t) {
-          const unsigned char* rec = xc + (size_t)(LG * t) * ROWB;
-          xp[t] = *reinterpret_cast<const u32x4*>(rec);
-          const float2_t k = *reinterpret_cast<const float2_t*>(rec + 16);
-          c0 += k[0];
-          xs += k[1];
-        }
-        float tt[4] = {c0, c0, c0, c0};
+      for (int t = 0; t < RPL; ++t) {
+        u32x4 xp[MT];
 #pragma unroll
-        for (int t = 0; t < RPL; ++t) {  // rows in arrival order
+        for (int m = 0; m < MT; ++m)
+          xp[m] = *reinterpret_cast<const u32x4*>(xc + (size_t)(LG * t * MT + m) * ROWB);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t wc = w[c][t][q];
-            const uint32_t v = wc >> 8;
-            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][3]), ldk::u2h2((v & mhi) | magic), tt[q], false);
-            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][2]), ldk::u2h2((v & mlo) | magic), tt[q], false);
-            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][1]), ldk::u2h2((wc & mhi) | magic), tt[q], false);
-            tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][0]), ldk::u2h2((wc & mlo) | magic), tt[q], false);
-          }
-        }
-        const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
-        const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t wc = w[c][t][q];
+          const half_t zb1 = -((half_t)1024.0f + z4[q]);
+          const half2_t zb = {zb1, zb1};
+          const half2_t s2 = {s4[q], s4[q]};
+          const half2_t d0 = (ldk::u2h2((wc & mlo) | magic) + zb) * s2;
+          const half2_t d1 = (ldk::u2h2(((wc >> 4) & mlo) | magic) + zb) * s2;
+          const half2_t d2 = (ldk::u2h2(((wc >> 8) & mlo) | magic) + zb) * s2;
+          const half2_t d3 = (ldk::u2h2(((wc >> 12) & mlo) | magic) + zb) * s2;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)  // s * (sum x*q - z * sum x)
-          acc[0][q] = __builtin_fmaf((float)s4[q], __builtin_fmaf(-(float)z4[q], xs, tt[q]), acc[0][q]);
-      } else {
-        const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
-        const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
-#pragma unroll
-        for (int t = 0; t < RPL; ++t) {
-          u32x4 xp[MT];
-#pragma unroll
-          for (int m = 0; m < MT; ++m)
-            xp[m] = *reinterpret_cast<const u32x4*>(xc + (size_t)(LG * t * MT + m) * ROWB);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t wc = w[c][t][q];
-            const half_t zb1 = -((half_t)1024.0f + z4[q]);
-            const half2_t zb = {zb1, zb1};
-            const half2_t s2 = {s4[q], s4[q]};
-            const half2_t d0 = (ldk::u2h2((wc & mlo) | magic) + zb) * s2;
-            const half2_t d1 = (ldk::u2h2(((wc >> 4) & mlo) | magic) + zb) * s2;
-            const half2_t d2 = (ldk::u2h2(((wc >> 8) & mlo) | magic) + zb) * s2;
-            const half2_t d3 = (ldk::u2h2(((wc >> 12) & mlo) | magic) + zb) * s2;
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-              float tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][0]), d0, acc[m][q], false);
-              tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][1]), d1, tt, false);
-              tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][2]), d2, tt, false);
-              acc[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][3]), d3, tt, false);
-            }
+          for (int m = 0; m < MT; ++m) {
+            float tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][0]), d0, acc[m][q], false);
+            tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][1]), d1, tt, false);
+            tt = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][2]), d2, tt, false);
+            acc[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][3]), d3, tt, false);
           }
         }
       }
     }
+    ldk::wave_lds_sync();  // the next round rewrites this wave's records
   }
 
   // ---- reduction: lanes of a wave sharing ln, then the waves through LDS
@@ -338,6 +412,7 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
       }
       sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the round is in flight before the first wait
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       if (g0 + NW * c >= ge) break;  // uniform
@@ -395,40 +470,52 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
 
 // ------------------------------------------------------------------------------------ dispatch
 
+enum Kern { kM1 = 0, kValu = 1, kMfma = 2 };
+
 struct Plan {
-  bool mfma;
+  Kern kern;
   int mt, ln, rpl, cpw;  // row tile, lanes along N, rows per lane, chunks per wave and round
-  bool fact;
   int nw, splits, gps;
 };
 
 int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-// Instantiated (MT, LN, RPL, CPW) shapes of the VALU kernel: those that fit the register budget
-// of 1024-thread workgroups (128 VGPRs) without spilling. RPL = 8 is only needed for LN = 16
-// with 32-row groups (the plan takes RPL = 4 otherwise).
-constexpr bool gemv_shape_ok(bool fact, int mt, int ln, int rpl, int cpw) {
+// Instantiated (MT, LN, RPL, CPW) shapes of the EXACT VALU kernel: those that fit the register
+// budget of 1024-thread workgroups (128 VGPRs) without spilling. RPL = 8 is only needed for
+// LN = 16 with 32-row groups (the plan takes RPL = 4 otherwise).
+constexpr bool gemv_shape_ok(int mt, int ln, int rpl, int cpw) {
   if (ln != 4 && ln != 8 && ln != 16) return false;
   if (rpl == 8) return ln == 16 && cpw == 1;
   if (rpl != 4) return false;
-  if (fact) return cpw == 1 || cpw == 2 || (cpw == 4 && ln == 16);
   if (mt <= 2) return cpw == 1 || cpw == 2;
   if (mt == 4) return cpw == 1 || (cpw == 2 && ln >= 8);
   return mt == 8 && cpw == 1 && ln >= 8;
 }
 
+// Wave counts the M = 1 kernel is instantiated for (a plan rounds up; surplus waves idle).
+constexpr int kM1Waves[] = {1, 2, 3, 4, 6, 8, 12, 16};
+
+int m1_round_nw(int64_t want) {
+  for (int w : kM1Waves)
+    if (w >= want) return w;
+  return 16;
+}
+
 int gemv_pxw(const Plan& p) { return (p.cpw * p.rpl * p.mt + p.ln - 1) / p.ln; }
 
 size_t plan_lds_bytes(const Plan& p, int64_t M) {
-  if (p.mfma) return (size_t)p.nw * std::min<int64_t>(M, 16) * 64 * 4;
-  return (size_t)p.nw * 64 * gemv_pxw(p) * (p.fact ? 32 : 16) + (size_t)p.nw * p.mt * 4 * p.ln * 4;
+  if (p.kern == kM1) return 0;  // static LDS
+  if (p.kern == kMfma) return (size_t)p.nw * std::min<int64_t>(M, 16) * 64 * 4;
+  return (size_t)p.nw * 64 * gemv_pxw(p) * 16 + (size_t)p.nw * p.mt * 4 * p.ln * 4;
 }
+
+int plan_cw(const Plan& p) { return p.kern == kMfma ? 64 : 4 * p.ln; }
 
 size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
   if (p.splits <= 1) return 0;
-  const int cw = p.mfma ? 64 : 4 * p.ln;
+  const int cw = plan_cw(p);
   const int64_t tiles = (N + cw - 1) / cw;
-  const int64_t n = p.mfma ? std::min<int64_t>(M, 16) * 64 : (int64_t)p.mt * cw;
+  const int64_t n = p.kern == kMfma ? std::min<int64_t>(M, 16) * 64 : (int64_t)p.mt * cw;
   return (size_t)tiles * n * 8;
 }
 
@@ -439,11 +526,13 @@ int cpw_from_flags(int flags) {
 
 // Chooses the kernel, column tile, rows per lane, chunks per wave, workgroup size and split
 // count for a shape. Measured on MI355X (decode shapes of Qwen2.5-1.5B, graph-timed sweeps over
-// block_n, split_k and chunks per wave): 128-byte row runs per tile read best on shapes of a few
-// MB; fewer than ~150 workgroups leave bandwidth unused once a shape moves more than a couple of
-// MB (the down projection reads 3.0 us at 192 workgroups against 5.7 us at 48), while a split
-// costs one dependent atomic round trip (~0.5 us), so only large, narrow shapes split. One chunk
-// per wave (more, smaller waves) beat deeper per-wave pipelining on every decode shape.
+// block_n, split_k and waves per workgroup): 128-byte row runs per tile read best (one L2 line);
+// fewer than ~150 workgroups leave bandwidth unused once a shape moves more than a couple of MB
+// (M = 1 down projection: 4.5 us at 240 workgroups against 7.7 us at 48), while a split costs one
+// dependent atomic round trip (~0.3 us), so only large, narrow shapes split. For M = 1 six waves of
+// two groups each (four rows per lane) beat deeper waves (three of four groups: +4%) and shallower
+// ones (twelve of one: +12%) on the gate_up shape; shapes of <= 2 MB run 16-column tiles (o
+// projection 3.2 us against 3.45 us at 32 columns).
 Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int split_k, int flags,
                size_t ws_bytes) {
   Plan p{};
@@ -452,28 +541,36 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const int64_t wbytes = N * K / 2;
   // MFMA from 5 rows (3 on shapes of > 4 MB): its B operand costs 11 VALU ops per 8 weights for
   // all 16 rows, the VALU kernel's dequantize-then-dot grows by 4 dot2 per 8 weights per row.
-  const bool mfma_auto = M > 4 || (M > 2 && wbytes > (4 << 20));
-  p.mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
-  p.mt = p.mfma ? 16 : round_mt(M);
-  p.fact = !p.mfma && p.mt == 1 && !(flags & LDK_EXACT);
-  if (p.mfma) {
+  // A block_n only the VALU kernels take (16 or 32) keeps M <= 8 on the VALU path.
+  const bool mfma_auto = M > 8 || ((M > 4 || (M > 2 && wbytes > (4 << 20))) && (block_n == 0 || block_n == 64));
+  const bool mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
+  const bool m1 = !mfma && M == 1 && !(flags & LDK_EXACT);
+  p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
+  p.mt = mfma ? 16 : round_mt(M);
+  if (mfma) {
     p.ln = 16;
   } else if (block_n) {
     p.ln = block_n / 4;
-  } else if (p.mt == 1) {  // 64-byte rows keep more workgroups busy on small shapes
-    p.ln = (N >= 4096 || wbytes > (2 << 20)) ? 8 : 4;
+  } else if (m1) {  // small shapes are latency-bound: more, narrower workgroups
+    p.ln = (wbytes <= (2 << 20) && N <= 4096) ? 4 : 8;
   } else if (p.mt == 8) {
     p.ln = N >= 1024 ? 16 : 8;
   } else {
     p.ln = N >= 512 ? 8 : 4;
   }
-  const int cw = p.mfma ? 64 : 4 * p.ln;
+  const int cw = plan_cw(p);
   const int lkw = 64 / p.ln;
-  p.rpl = (lkw % (rpg / std::min(rpg, 4)) == 0) ? std::min(rpg, 4) : 8;  // LG = rpg/rpl divides LKW
-  const int gw = p.mfma ? 1 : lkw / (rpg / p.rpl);
+  if (m1) {
+    p.rpl = 4;
+  } else {
+    p.rpl = (lkw % (rpg / std::min(rpg, 4)) == 0) ? std::min(rpg, 4) : 8;  // LG = rpg/rpl divides LKW
+  }
+  // groups a wave covers per pass / chunk
+  const int gw = mfma ? 1 : lkw / (rpg / p.rpl);
   const int64_t tiles = (N + cw - 1) / cw;
   int64_t splits = split_k > 0 ? split_k : 1;
-  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20)) splits = (192 + tiles - 1) / tiles;
+  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20))  // M = 1: about one workgroup per CU
+    splits = m1 ? std::max<int64_t>(2, 256 / tiles) : (192 + tiles - 1) / tiles;
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
   p.splits = (int)((ng + p.gps - 1) / p.gps);
@@ -482,6 +579,11 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     p.gps = (int)ng;
   }
   const int64_t chunks = (p.gps + gw - 1) / gw;
+  if (m1) {
+    p.cpw = 1;
+    p.nw = m1_round_nw(std::min<int64_t>(16, chunks));
+    return p;
+  }
   // chunks per wave and round: the smallest that fits all chunks in one round of <= 16 waves
   int cpw = cpw_from_flags(flags);
   if (!cpw) {
@@ -489,19 +591,47 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     for (int c : {1, 2, 4})
       if (chunks <= 16 * c) { cpw = c; break; }
   }
-  if (p.mfma) {
+  if (mfma) {
     cpw = std::min(cpw, rpg <= 16 ? 2 : 1);
   } else {
-    while (cpw > 1 && !gemv_shape_ok(p.fact, p.mt, p.ln, p.rpl, cpw)) cpw >>= 1;
+    while (cpw > 1 && !gemv_shape_ok(p.mt, p.ln, p.rpl, cpw)) cpw >>= 1;
   }
   p.cpw = cpw;
   p.nw = (int)std::min<int64_t>(16, (chunks + cpw - 1) / cpw);
   return p;
 }
 
-template <int MT, int LN, int RPL, bool FACT, int CPW>
+template <int LN, int NW>
+int launch_m1_t(const W4Args& a, const SplitArgs& sp, hipStream_t stream) {
+  const int64_t tiles = (a.N + 4 * LN - 1) / (4 * LN);
+  const int out_vec = ldk::aligned(a.out, 8) ? 1 : 0;
+  const unsigned grid = (unsigned)(tiles * sp.splits);
+  (void)hipGetLastError();
+  if (a.gsh_rows == 4)
+    w4a16_m1_kernel<LN, NW, 4><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec);
+  else
+    w4a16_m1_kernel<LN, NW, 0><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec);
+  return ldk::check_launch("w4a16_m1");
+}
+
+template <int LN>
+int launch_m1_ln(const W4Args& a, const SplitArgs& sp, int nw, hipStream_t s) {
+  switch (nw) {
+    case 1: return launch_m1_t<LN, 1>(a, sp, s);
+    case 2: return launch_m1_t<LN, 2>(a, sp, s);
+    case 3: return launch_m1_t<LN, 3>(a, sp, s);
+    case 4: return launch_m1_t<LN, 4>(a, sp, s);
+    case 6: return launch_m1_t<LN, 6>(a, sp, s);
+    case 8: return launch_m1_t<LN, 8>(a, sp, s);
+    case 12: return launch_m1_t<LN, 12>(a, sp, s);
+    case 16: return launch_m1_t<LN, 16>(a, sp, s);
+  }
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %d waves per workgroup not instantiated", nw);
+}
+
+template <int MT, int LN, int RPL, int CPW>
 int launch_gemv_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipStream_t stream) {
-  auto kern = w4a16_gemv_kernel<MT, LN, RPL, FACT, CPW>;
+  auto kern = w4a16_gemv_kernel<MT, LN, RPL, CPW>;
   if (lds > 64 * 1024) {
     if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: LDS need %zu B exceeds 160 KiB", lds);
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -513,36 +643,35 @@ int launch_gemv_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
   return ldk::check_launch("w4a16_gemv");
 }
 
-template <int MT, int LN, bool FACT, int RPL, int CPW>
+template <int MT, int LN, int RPL, int CPW>
 int try_gemv(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s, bool* done) {
-  if constexpr (gemv_shape_ok(FACT, MT, LN, RPL, CPW)) {
+  if constexpr (gemv_shape_ok(MT, LN, RPL, CPW)) {
     if (p.rpl == RPL && p.cpw == CPW) {
       *done = true;
-      return launch_gemv_t<MT, LN, RPL, FACT, CPW>(a, sp, p.nw, lds, s);
+      return launch_gemv_t<MT, LN, RPL, CPW>(a, sp, p.nw, lds, s);
     }
   }
   return LDK_OK;
 }
 
-template <int MT, int LN, bool FACT>
+template <int MT, int LN>
 int launch_gemv_shape(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
   bool done = false;
-  int st = try_gemv<MT, LN, FACT, 4, 1>(a, sp, p, lds, s, &done);
-  if (!done) st = try_gemv<MT, LN, FACT, 4, 2>(a, sp, p, lds, s, &done);
-  if (!done) st = try_gemv<MT, LN, FACT, 4, 4>(a, sp, p, lds, s, &done);
-  if (!done) st = try_gemv<MT, LN, FACT, 8, 1>(a, sp, p, lds, s, &done);
+  int st = try_gemv<MT, LN, 4, 1>(a, sp, p, lds, s, &done);
+  if (!done) st = try_gemv<MT, LN, 4, 2>(a, sp, p, lds, s, &done);
+  if (!done) st = try_gemv<MT, LN, 8, 1>(a, sp, p, lds, s, &done);
   if (!done)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: VALU shape mt=%d block_n=%d rpl=%d cpw=%d not instantiated", MT,
                      4 * LN, p.rpl, p.cpw);
   return st;
 }
 
-template <int MT, bool FACT>
+template <int MT>
 int launch_gemv_ln(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
   switch (p.ln) {
-    case 4: return launch_gemv_shape<MT, 4, FACT>(a, sp, p, lds, s);
-    case 8: return launch_gemv_shape<MT, 8, FACT>(a, sp, p, lds, s);
-    case 16: return launch_gemv_shape<MT, 16, FACT>(a, sp, p, lds, s);
+    case 4: return launch_gemv_shape<MT, 4>(a, sp, p, lds, s);
+    case 8: return launch_gemv_shape<MT, 8>(a, sp, p, lds, s);
+    case 16: return launch_gemv_shape<MT, 16>(a, sp, p, lds, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
 }
@@ -563,7 +692,19 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
   SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr};
   const size_t lds = plan_lds_bytes(p, a.M);
   if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: LDS need %zu B exceeds 160 KiB", lds);
-  if (p.mfma) {
+  if (p.kern == kM1) {
+    // LG = rows_per_group / 4 lanes per group must divide the 64 / LN lanes along K
+    if ((1 << a.gsh_rows) > 4 * (64 / p.ln))
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d too wide for group_size %d on the M = 1 kernel",
+                       4 * p.ln, 8 << a.gsh_rows);
+    switch (p.ln) {
+      case 4: return launch_m1_ln<4>(a, sp, p.nw, s);
+      case 8: return launch_m1_ln<8>(a, sp, p.nw, s);
+      case 16: return launch_m1_ln<16>(a, sp, p.nw, s);
+    }
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
+  }
+  if (p.kern == kMfma) {
     const bool two = p.cpw == 2;
     switch (1 << a.gsh_rows) {
       case 4: return two ? launch_mfma_t<1, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<1, 1>(a, sp, p.nw, lds, s);
@@ -573,12 +714,11 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
     }
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
   }
-  if (p.fact) return launch_gemv_ln<1, true>(a, sp, p, lds, s);
   switch (p.mt) {
-    case 1: return launch_gemv_ln<1, false>(a, sp, p, lds, s);
-    case 2: return launch_gemv_ln<2, false>(a, sp, p, lds, s);
-    case 4: return launch_gemv_ln<4, false>(a, sp, p, lds, s);
-    case 8: return launch_gemv_ln<8, false>(a, sp, p, lds, s);
+    case 1: return launch_gemv_ln<1>(a, sp, p, lds, s);
+    case 2: return launch_gemv_ln<2>(a, sp, p, lds, s);
+    case 4: return launch_gemv_ln<4>(a, sp, p, lds, s);
+    case 8: return launch_gemv_ln<8>(a, sp, p, lds, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: row tile %d not instantiated", p.mt);
 }
@@ -607,8 +747,9 @@ int validate(const char* fn, const void* x, int64_t ldx, const int32_t* qw, cons
 }
 
 int plan_flags(const Plan& p) {
-  const int cpw_code = p.mfma || p.cpw == 0 ? 0 : (p.cpw == 1 ? 1 : p.cpw == 2 ? 2 : 3);
-  return (p.mfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.fact ? LDK_FACTORED : LDK_EXACT) | (cpw_code << 4);
+  const int cpw_code = p.kern == kValu ? (p.cpw == 1 ? 1 : p.cpw == 2 ? 2 : 3) : 0;
+  return (p.kern == kMfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.kern == kM1 ? LDK_FACTORED : LDK_EXACT) |
+         (cpw_code << 4);
 }
 
 }  // namespace
@@ -621,7 +762,7 @@ extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size,
   const int gsh = log2_exact(group_size);
   if (gsh < 5 || gsh > 8 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "w4a16_config: bad group_size %d", group_size);
   const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
-  if (block_n) *block_n = p.mfma ? 64 : 4 * p.ln;
+  if (block_n) *block_n = plan_cw(p);
   if (split_k) *split_k = p.splits;
   if (flags) *flags = plan_flags(p);
   return LDK_OK;
@@ -640,6 +781,7 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: FACTORED and EXACT are exclusive");
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: VALU and MFMA paths are exclusive");
   if ((flags & LDK_FACTORED) && M > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED is the M = 1 kernel");
+  if ((flags & LDK_FACTORED) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED runs on the VALU kernel");
   if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the VALU kernel takes M <= 8");
   if (block_n && block_n != 16 && block_n != 32 && block_n != 64)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=%d must be 16, 32 or 64", block_n);
@@ -648,7 +790,7 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul: workspace must be a 256-byte aligned pointer");
   const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
-  if (p.mfma && block_n && block_n != 64) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n=64");
+  if (p.kern == kMfma && block_n && block_n != 64) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n=64");
   if (split_k > 1 && p.splits == 1 && (K / group_size) > 1)
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
