@@ -122,8 +122,10 @@ struct W8Args {
   int M, N, K;
 };
 
+// x is staged in LDS one K chunk of KC columns at a time (KC = K when the whole row fits), so the
+// LDS need stays bounded for any K: [MT][KC] fp16 + one trash chunk, then the reduction buffer.
 template <int MT, int LN, int UB>
-__global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a) {
+__global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a, int KC) {
   constexpr int CW = 16 * LN;
   constexpr int LKW = 64 / LN;
   constexpr int PXr = (MT * UB + 8 * LN - 1) / (8 * LN);
@@ -138,11 +140,13 @@ __global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a) {
   const int n0 = ldk::xcd_remap(blockIdx.x, gridDim.x) * CW;
   const int col = min(n0 + 16 * ln, a.N - 16);
 
-  // LDS: x [MT][K] fp16 + one trash chunk, then the reduction buffer [NW][MT][CW] floats.
+  // LDS: x [MT][KC] fp16 + one trash chunk, then the reduction buffer [NW][MT][CW] floats.
   half_t* xs = reinterpret_cast<half_t*>(smem);
-  float* red = reinterpret_cast<float*>(smem + (((size_t)MT * K + 8) * 2 + 15) / 16 * 16);
+  float* red = reinterpret_cast<float*>(smem + (((size_t)MT * KC + 8) * 2 + 15) / 16 * 16);
+  int kc0 = 0;                    // first K column of the staged chunk
+  int kcn = min(KC, K);           // its width
+  int nx = MT * kcn / 8;          // 16-byte x items of the chunk, item = c*MT + m
 
-  const int nx = MT * K / 8;  // 16-byte x items, item index = c*MT + m for chunk c of row m
   u32x4 xr[PX];
 #pragma unroll
   for (int i = 0; i < PX; ++i) {
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a) {
       if (k < K) {
         float xv[MT];
 #pragma unroll
-        for (int m = 0; m < MT; ++m) xv[m] = (float)xs[(size_t)m * K + k];
+        for (int m = 0; m < MT; ++m) xv[m] = (float)xs[(size_t)m * KC + (k - kc0)];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
           const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[u][d], false);
@@ -196,21 +200,36 @@ __global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a) {
     const int m = it % MT, c = it / MT;
     u32x4 d = xr[i];
     if (m >= a.M) d = u32x4{0u, 0u, 0u, 0u};
-    const size_t off = it < nx ? (size_t)m * K + 8 * c : (size_t)MT * K;  // trash chunk
+    const size_t off = it < nx ? (size_t)m * KC + 8 * c : (size_t)MT * KC;  // trash chunk
     *reinterpret_cast<u32x4*>(xs + off) = d;
   }
   for (int it = tid + PX * NT; it < nx; it += NT) {
     const int m = it % MT, c = it / MT;
     u32x4 d = *reinterpret_cast<const u32x4*>(a.x + min(m, a.M - 1) * a.ldx + 8 * c);
     if (m >= a.M) d = u32x4{0u, 0u, 0u, 0u};
-    *reinterpret_cast<u32x4*>(xs + (size_t)m * K + 8 * c) = d;
+    *reinterpret_cast<u32x4*>(xs + (size_t)m * KC + 8 * c) = d;
   }
   ldk::lds_barrier();
+  // KC is a multiple of the batch step UB * LK, so no batch straddles two chunks. The next batch's
+  // weight loads are issued before a chunk switch's barriers and stay in flight across them.
   for (int kb = 0;;) {
     compute_batch(kb);
     kb += UB * LK;
     if (kb >= K) break;
     load_batch(kb);
+    if (kb >= kc0 + kcn) {  // uniform: restage x for the next chunk
+      kc0 = kb;
+      kcn = min(KC, K - kc0);
+      nx = MT * kcn / 8;
+      ldk::lds_barrier();  // every wave is done reading the previous chunk
+      for (int it = tid; it < nx; it += NT) {
+        const int m = it % MT, c = it / MT;
+        u32x4 d = *reinterpret_cast<const u32x4*>(a.x + min(m, a.M - 1) * a.ldx + kc0 + 8 * c);
+        if (m >= a.M) d = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(xs + (size_t)m * KC + 8 * c) = d;
+      }
+      ldk::lds_barrier();
+    }
   }
 
 #pragma unroll
@@ -243,6 +262,14 @@ struct W8Cfg {
   int mt, ln, nw, ub;
 };
 
+constexpr int64_t kW8MaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+
+// LDS a configuration needs with x staged in chunks of at least one batch step.
+int64_t w8_min_lds(int mt, int ln, int nw, int ub, int64_t K) {
+  const int64_t step = (int64_t)ub * nw * (64 / ln);
+  return (int64_t)mt * std::min<int64_t>(K, step) * 2 + 48 + (int64_t)nw * mt * 16 * ln * 4;
+}
+
 int round_ub8(int rows) {
   static const int kUB[] = {2, 4, 6, 8, 12, 16};
   for (int u : kUB)
@@ -260,6 +287,7 @@ W8Cfg choose_w8(int64_t M, int64_t N, int64_t K, int block_n, int split_k) {
       if (split_k && split_k != lk) continue;
       const int64_t nwg = (N + 16 * ln - 1) / (16 * ln);
       const int64_t rows = (K + lk - 1) / lk;
+      if (w8_min_lds(best.mt, ln, nw, round_ub8((int)std::min<int64_t>(rows, 16)), K) > kW8MaxLds) continue;
       const double waves = (double)nwg * nw;
       double score = -std::abs(std::log2(std::max(waves, 1.0) / 2048.0)) * 4.0;
       score -= rows > 16 ? (rows - 16) * 0.5 : 0.0;
@@ -277,7 +305,17 @@ W8Cfg choose_w8(int64_t M, int64_t N, int64_t K, int block_n, int split_k) {
 
 template <int MT, int LN, int UB>
 int launch_w8_t(const W8Args& a, int nw, hipStream_t s) {
-  const size_t lds = (((size_t)MT * a.K + 8) * 2 + 15) / 16 * 16 + (size_t)nw * MT * 16 * LN * 4;
+  // x chunk width: all of K when [MT][K] fp16 fits 64 KiB, else the largest multiple of the
+  // batch step (UB rows for each of the nw*64/LN lanes along K) that does.
+  const int64_t step = (int64_t)UB * nw * (64 / LN);
+  const int64_t red_bytes = (int64_t)nw * MT * 16 * LN * 4;
+  int64_t kc = a.K;
+  const int64_t max_kc = ((kW8MaxLds - red_bytes - 32) / (2 * MT)) / 8 * 8;
+  if (kc > max_kc) {
+    kc = max_kc / step * step;
+    if (kc < step) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: x chunk smaller than one batch (M=%d)", a.M);
+  }
+  const size_t lds = (((size_t)MT * kc + 8) * 2 + 15) / 16 * 16 + (size_t)red_bytes;
   auto kern = w8a16_skinny_kernel<MT, LN, UB>;
   if (lds > 64 * 1024) {
     if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: LDS need %zu B exceeds 160 KiB (M*K too large for the decode kernel)", lds);
@@ -286,7 +324,7 @@ int launch_w8_t(const W8Args& a, int nw, hipStream_t s) {
   }
   const int grid = (int)((a.N + 16 * LN - 1) / (16 * LN));
   (void)hipGetLastError();
-  kern<<<grid, nw * 64, lds, s>>>(a);
+  kern<<<grid, nw * 64, lds, s>>>(a, (int)kc);
   return ldk::check_launch("w8a16_skinny");
 }
 

@@ -98,6 +98,15 @@ __device__ __forceinline__ uint32_t vgpr_const() {
   return r;
 }
 
+// Makes a uniform value (a kernel argument) live in SGPRs at this point. Kernel arguments are
+// fetched with scalar loads; without a use before the first branch, the compiler sinks some of
+// them into the branch and the kernel pays a second scalar round trip before its first vector
+// load.
+template <typename T>
+__device__ __forceinline__ void pin_sgpr(T v) {
+  asm volatile("" : : "s"(v));
+}
+
 // Orders LDS accesses of one wavefront (lanes exchanging data through LDS inside a wave): no
 // s_barrier is needed since a wave's LDS operations complete in order, but the compiler must not
 // move the reads above the writes.

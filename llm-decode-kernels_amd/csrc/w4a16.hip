@@ -42,6 +42,8 @@
 //    tile of one group is scaled by s once.
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
+#include <cstdlib>
 
 #include "ldk_common.h"
 
@@ -63,10 +65,17 @@ struct W4Args {
 };
 
 struct SplitArgs {
-  int splits;     // workgroups per column tile
+  int splits;     // workgroups per split column tile
   int gps;        // groups per split
-  uint64_t* acc;  // [tiles][n] fixed-point accumulators (splits > 1), zero between launches
+  uint64_t* acc;  // [split tiles][n] fixed-point accumulators (splits > 1), zero between launches
+  int full;       // M = 1 kernel: tiles [0, full) run whole (one workgroup, no split); the split
+                  // workgroups of tiles [full, tiles) come first in dispatch order
+  int nsplit;       // M = 1 kernel: number of those split workgroups
+  uint64_t smagic;  // ceil(2^32 / splits): b / splits == (b * smagic) >> 32 for b, splits < 2^16
 };
+
+// ceil(2^32 / d) for 1 <= d < 2^16: floor(n / d) == (n * magic) >> 32 for every n < 2^16.
+inline uint64_t div_magic(uint32_t d) { return ((uint64_t(1) << 32) + d - 1) / d; }
 
 __device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (lo16(a), lo16(b))
   return __builtin_amdgcn_perm(b, a, 0x05040100u);
@@ -129,11 +138,26 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
   const int ln = lane % LN, lk = lane / LN;
   const int gi = lk >> lgsh, sub = lk & ((1 << lgsh) - 1);
   const int gpw = LKW >> lgsh;
-  const int tile = blockIdx.x / sp.splits, split = blockIdx.x - tile * sp.splits;
+  // Dispatch order: the split workgroups of tiles [full, tiles) first, then the whole tiles.
+  // Requests are served roughly in issue order, so the split workgroups' data arrives early and
+  // their cross-workgroup round trip overlaps the streaming of the whole tiles.
+  // Branch-free scalar prologue (no runtime integer division): every kernel argument is needed
+  // before the first load, so the compiler fetches them in one scalar round trip.
+  ldk::pin_sgpr(a.x);
+  ldk::pin_sgpr(a.qw);
+  const int bid = blockIdx.x;
+  const bool in_split = bid < sp.nsplit;
+  const int q = (int)(((uint64_t)(uint32_t)bid * sp.smagic) >> 32);
+  const int tile = in_split ? sp.full + q : bid - sp.nsplit;
+  const int split = in_split ? bid - q * sp.splits : 0;
+  const bool whole = !in_split || sp.splits == 1;
   const int n0 = tile * CW;
   const int col = min(n0 + 4 * ln, a.N - 4);  // clamped: tail lanes load valid memory, store nothing
   const int R = a.K >> 3, ng = R >> rsh;
-  const int gb = split * sp.gps, ge = min(ng, gb + sp.gps);
+  const int gb = whole ? 0 : split * sp.gps, ge = whole ? ng : min(ng, gb + sp.gps);
+  // A split that fits one wave pass is reduced by wave 0 alone, with no LDS round and no barrier
+  // (the other waves find no pass in the loop below and leave after it).
+  const bool one_wave = !whole && ge - gb <= gpw;
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
@@ -189,10 +213,24 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
   // ---- reduction: lanes sharing ln within the wave, then the NW waves through LDS
 #pragma unroll
   for (int q = 0; q < 4; ++q) acc[q] = ldk::sum_lanes_strided<LN>(acc[q]);
+  if (one_wave) {
+    if (wave != 0) return;
+    // lane l < CW owns output n0 + l: element l % 4 of the lanes holding columns 4(l/4)..
+    const int src = (lane >> 2) % LN, e = lane & 3;
+    const float e0 = __shfl(acc[0], src), e1 = __shfl(acc[1], src), e2 = __shfl(acc[2], src), e3 = __shfl(acc[3], src);
+    const float v = e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3;
+    const int c = n0 + lane;
+    float tot;
+    if (lane < CW && c < a.N && ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
+      if (a.bias) tot += (float)a.bias[c];
+      a.out[c] = (half_t)tot;
+    }
+    return;
+  }
   if (lane < LN) red[wave][lane] = float4_t{acc[0], acc[1], acc[2], acc[3]};
   __syncthreads();
   if (wave != 0) return;
-  if (sp.splits == 1) {
+  if (whole || sp.splits == 1) {
     const int c = n0 + 4 * lane;
     if (lane >= LN || c >= a.N) return;
     float4_t v = red[0][lane];
@@ -215,7 +253,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
 #pragma unroll
     for (int i = 1; i < NW; ++i) v += rf[i * CW + lane];
     float tot;
-    if (ldk::splitk_add(sp.acc + (size_t)tile * CW + lane, sp.splits, v, &tot)) {
+    if (ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
       if (a.bias) tot += (float)a.bias[c];
       a.out[c] = (half_t)tot;
     }
@@ -476,6 +514,7 @@ struct Plan {
   Kern kern;
   int mt, ln, rpl, cpw;  // row tile, lanes along N, rows per lane, chunks per wave and round
   int nw, splits, gps;
+  int full;  // M = 1 kernel: leading tiles run whole while the rest split (0: all tiles alike)
 };
 
 int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
@@ -514,7 +553,7 @@ int plan_cw(const Plan& p) { return p.kern == kMfma ? 64 : 4 * p.ln; }
 size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
   if (p.splits <= 1) return 0;
   const int cw = plan_cw(p);
-  const int64_t tiles = (N + cw - 1) / cw;
+  const int64_t tiles = (N + cw - 1) / cw - p.full;
   const int64_t n = p.kern == kMfma ? std::min<int64_t>(M, 16) * 64 : (int64_t)p.mt * cw;
   return (size_t)tiles * n * 8;
 }
@@ -578,7 +617,26 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     p.splits = 1;
     p.gps = (int)ng;
   }
-  const int64_t chunks = (p.gps + gw - 1) / gw;
+  // M = 1 with more than one round of 256 tiles: whole tiles give every CU the same whole-tile
+  // count, and the remainder tiles split into one-wave-pass pieces that spread over all CUs
+  // (gate_up: 512 whole tiles + 48 tiles x 6 splits of 2 groups; 560 whole tiles leave 48 CUs
+  // with a third tile, measured 5.40 -> 5.06 us).
+  if (m1 && split_k <= 0 && tiles > 256 && tiles % 256) {
+    const int64_t rem = tiles % 256;
+    // groups per split: whole wave passes, chosen so that rem * splits lands nearest 256
+    int64_t gps_r = ng, best = INT64_MAX;
+    for (int64_t g = gw; g < ng; g += gw) {
+      const int64_t s = (ng + g - 1) / g;
+      const int64_t d = std::abs(rem * s - 256);
+      if (s <= kMaxSplits && d < best) { best = d; gps_r = g; }
+    }
+    Plan q = p;
+    q.gps = (int)gps_r;
+    q.splits = (int)((ng + gps_r - 1) / gps_r);
+    q.full = (int)(tiles - rem);
+    if (q.splits > 1 && workspace_need(q, M, N) <= ws_bytes) p = q;
+  }
+  const int64_t chunks = ((p.full ? ng : p.gps) + gw - 1) / gw;  // wave passes of the largest workgroup
   if (m1) {
     p.cpw = 1;
     p.nw = m1_round_nw(std::min<int64_t>(16, chunks));
@@ -605,7 +663,7 @@ template <int LN, int NW>
 int launch_m1_t(const W4Args& a, const SplitArgs& sp, hipStream_t stream) {
   const int64_t tiles = (a.N + 4 * LN - 1) / (4 * LN);
   const int out_vec = ldk::aligned(a.out, 8) ? 1 : 0;
-  const unsigned grid = (unsigned)(tiles * sp.splits);
+  const unsigned grid = (unsigned)(sp.full + sp.nsplit);
   (void)hipGetLastError();
   if (a.gsh_rows == 4)
     w4a16_m1_kernel<LN, NW, 4><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec);
@@ -689,7 +747,12 @@ int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
 }
 
 int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
-  SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr};
+  SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr, 0, 0, div_magic(p.splits)};
+  if (p.kern == kM1) {
+    const int64_t tiles = (a.N + 4 * p.ln - 1) / (4 * p.ln);
+    sp.full = p.full;
+    sp.nsplit = (int)((tiles - p.full) * p.splits);
+  }
   const size_t lds = plan_lds_bytes(p, a.M);
   if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: LDS need %zu B exceeds 160 KiB", lds);
   if (p.kern == kM1) {

@@ -1,0 +1,142 @@
+"""Kernel sweep over the benchmark configurations 1-3 on one MI355X (the reference's
+kernels/bench/sweep.py case generators, lines 139-207, re-done for this build):
+
+- config 1: fused RMSNorm (with and without residual) at N=1536 and fused SwiGLU at I=8960,
+  M in {1, 16, 2048}, seed 1;
+- config 2: W4A16 over the six Qwen2.5-1.5B linear shapes at M in {1, 4, 16}, seed 2;
+- config 3: W8A16 (OCP e4m3) over the same shapes at M in {1, 4, 8, 16}, seed 3.
+
+Every case is timed with `harness.GraphTimer` (rotating input sets sized to 4x the 256 MB MALL,
+one launch per set in one hipGraph, median of 7 samples) and reported as us, GB/s and % of the
+8 TB/s HBM peak with the reference's algorithmic byte formulas. Each row also records the
+kernel configuration the library chose.
+
+    python -m kernels.bench.sweep [--only w4a16,fp8,norm,act] [--json out.json]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import torch
+
+from kernels.bench import cases
+from kernels.bench.harness import GraphTimer, n_copies, tensor_bytes
+from kernels.config import PEAK_GBPS
+
+GS = 128
+
+
+def _time(fn, sets) -> float:
+    timer = GraphTimer(fn, sets)
+    try:
+        return timer.median_ms_per_call()
+    finally:
+        timer.close()
+
+
+def _row(kind, shape, M, ms, nbytes, extra=None) -> dict:
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    r = {"kernel": kind, "shape": shape, "M": M, "us": round(ms * 1e3, 3), "bytes": nbytes,
+         "gbps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 2)}
+    if extra:
+        r.update(extra)
+    return r
+
+
+def w4a16_rows(Ms=(1, 4, 16)):
+    from kernels.quant import quantize_rtn, weight_bytes
+    from kernels.w4a16 import config_for, w4a16_matmul
+
+    rows = []
+    for name, N, K in cases.QWEN_LINEARS:
+        w, _ = cases.w4a16_case(1, N, K, seed=2)
+        qw, s, z = quantize_rtn(w.cuda(), GS)
+        for M in Ms:
+            x = cases.activations(M, K, cases.gen(2)).cuda()
+            per = tensor_bytes((x, qw, s, z)) + 2 * M * N
+            sets = [(x.clone(), qw.clone(), s.clone(), z.clone()) for _ in range(n_copies(per))]
+            ms = _time(lambda xx, q, sc, zz: w4a16_matmul(xx, q, sc, zz, GS), sets)
+            nbytes = weight_bytes(N, K, GS) + 2 * M * K + 2 * M * N  # sweep.py:167-169
+            rows.append(_row("w4a16", f"{name} {N}x{K}", M, ms, nbytes,
+                             {"config": config_for(M, N, K, GS)}))
+            del sets
+    return rows
+
+
+def fp8_rows(Ms=(1, 4, 8, 16)):
+    from kernels.fp8 import fp8_bytes, quantize_fp8, w8a16_matmul
+
+    rows = []
+    for name, N, K in cases.QWEN_LINEARS:
+        w, _ = cases.w4a16_case(1, N, K, seed=3)
+        wq, sc = quantize_fp8(w.cuda())
+        for M in Ms:
+            x = cases.activations(M, K, cases.gen(3)).cuda()
+            per = tensor_bytes((x, wq, sc)) + 2 * M * N
+            sets = [(x.clone(), wq.clone(), sc.clone()) for _ in range(n_copies(per))]
+            ms = _time(lambda xx, q, ss: w8a16_matmul(xx, q, ss), sets)
+            nbytes = fp8_bytes(N, K) + 2 * M * K + 2 * M * N  # sweep.py:190-191
+            rows.append(_row("w8a16", f"{name} {N}x{K}", M, ms, nbytes))
+            del sets
+    return rows
+
+
+def norm_rows(Ms=(1, 16, 2048)):
+    from kernels.rmsnorm import rmsnorm, rmsnorm_bytes
+
+    rows = []
+    for M in Ms:
+        x, r, w = (t.cuda() for t in cases.rmsnorm_case(M, 1536, seed=1))
+        for res in (True, False):
+            per = tensor_bytes((x, r, w)) * 2
+            sets = [(x.clone(), r.clone(), w.clone()) for _ in range(n_copies(per))]
+            if res:
+                fn = lambda xx, rr, ww: rmsnorm(xx, ww, 1e-6, residual=rr)  # noqa: E731
+            else:
+                fn = lambda xx, rr, ww: rmsnorm(xx, ww, 1e-6)  # noqa: E731
+            ms = _time(fn, sets)
+            rows.append(_row("rmsnorm+res" if res else "rmsnorm", "N=1536", M, ms,
+                             rmsnorm_bytes(M, 1536, res)))
+            del sets
+    return rows
+
+
+def act_rows(Ms=(1, 16, 2048)):
+    from kernels.swiglu import swiglu_bytes, swiglu_fused
+
+    rows = []
+    for M in Ms:
+        gu = cases.swiglu_case(M, 8960, seed=1).cuda()
+        sets = [(gu.clone(),) for _ in range(n_copies(tensor_bytes(gu) * 3 // 2))]
+        ms = _time(swiglu_fused, sets)
+        rows.append(_row("swiglu", "I=8960", M, ms, swiglu_bytes(M, 8960)))
+        del sets
+    return rows
+
+
+SECTIONS = {"w4a16": w4a16_rows, "fp8": fp8_rows, "norm": norm_rows, "act": act_rows}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", default="w4a16,fp8,norm,act")
+    ap.add_argument("--json", default=None)
+    args = ap.parse_args(argv)
+    torch.cuda.init()
+    rows = []
+    for sec in args.only.split(","):
+        for r in SECTIONS[sec]():
+            print(f"{r['kernel']:12s} {r['shape']:22s} M={r['M']:<5d} {r['us']:9.3f} us "
+                  f"{r['gbps']:8.1f} GB/s {r['pct_peak']:6.2f}%  {r.get('config', '')}", flush=True)
+            rows.append(r)
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump({"peak_gbps": PEAK_GBPS, "rows": rows}, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
