@@ -74,6 +74,25 @@ def cpu_baseline(w16, x, seconds: float = 15.0) -> dict:
                       f"({_cpu_model()})"}
 
 
+def measured_traffic(kernel_config: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this
+    command (profiles/w4a16_m1_gate_up_traffic.md), or None when that summary was taken with a
+    different kernel configuration than the one the library chooses now."""
+    path = REPO / "profiles" / "w4a16_m1_gate_up_traffic.md"
+    try:
+        text = path.read_text()
+    except OSError:
+        return None
+    fields = {}
+    for line in text.splitlines():
+        if ":" in line and line.split(":", 1)[0] in ("traffic_bytes_per_launch", "kernel_config"):
+            k, v = line.split(":", 1)
+            fields[k] = v.strip()
+    if fields.get("kernel_config") != kernel_config or "traffic_bytes_per_launch" not in fields:
+        return None
+    return int(fields["traffic_bytes_per_launch"])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +139,7 @@ def main() -> int:
 
     nbytes = weight_bytes(N, K, GS) + 2 * M * K + 2 * M * N  # sweep.py:167-169
     gbps = nbytes / (ms_per_step * 1e-3) / 1e9
+    kcfg = config_for(M, N, K, GS)
     out = {
         "metric": METRIC,
         "value": round(gbps, 2),
@@ -136,12 +156,14 @@ def main() -> int:
         "config": {"workload": "W4A16 GEMV, M=1, N=17920, K=1536 (Qwen2.5-1.5B gate_up), "
                                "group 128 (config 0)",
                    "M": M, "N": N, "K": K, "group_size": GS, "rotating_sets": ncopy,
-                   "kernel_config": config_for(M, N, K, GS)},
+                   "kernel_config": kcfg},
         "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
         "us_per_call": round(ms_per_step * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / PEAK_GBPS, 4), "traffic": None,
-                     "bytes_per_launch": nbytes},
+                     "unit": "GB/s", "frac": round(gbps / PEAK_GBPS, 4),
+                     "traffic": measured_traffic(kcfg), "bytes_per_launch": nbytes,
+                     "kernel": "w4a16_m1_kernel<8, 6, 4>",
+                     "timing": "HIP events on the graph-replay stream over all timed launches"},
     }
     timer.close()
     del sets
