@@ -150,6 +150,16 @@ int ldk_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr, c
 int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out, int64_t ldo,
                int64_t M, int64_t I, void* stream);
 
+/* ------------------------------------------------------------------- greedy decode bookkeeping */
+
+/* idx = argmax(logits[0:V]) (torch.argmax order: NaN largest, lowest index on ties), then
+ * out[*pos] = idx when 0 <= *pos < out_len (out may be NULL), *tok = idx, *pos += 1; one launch,
+ * no memset, no cross-workgroup state, so it replays safely inside a hipGraph. logits dtype
+ * LDK_F16/BF16/F32; tok, out and pos are int64 device pointers. Replaces the greedy step of
+ * kernels/e2e/run.py:69-74 (argmax, out.index_copy_, tok.copy_, pos.add_). */
+int ldk_greedy_step(const void* logits, int dtype, int64_t V, int64_t* tok, int64_t* out,
+                    int64_t out_len, int64_t* pos, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

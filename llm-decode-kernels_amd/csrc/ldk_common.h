@@ -24,7 +24,7 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Maps a HIP launch status to LDK_OK / LDK_ERR_LAUNCH with a message naming `what`.
 int check_launch(const char* what);
 
-inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+__host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 }  // namespace ldk
 

@@ -53,6 +53,7 @@ SIGNATURES = {
                          _vp, _i64, _vp],
     "ldk_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _f32, _vp],
     "ldk_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
+    "ldk_greedy_step": [_vp, _i32, _i64, _vp, _vp, _i64, _vp, _vp],
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,314 @@
+"""A Qwen2 runner with swappable kernels: the consumer the hot path is a drop-in for.
+
+Same public surface as the reference's kernels/e2e/model.py (`Linear`, `Backend`, `W4RefBackend`,
+`OursBackend`, `OursFP8Backend`, `make_backend`, `QwenRunner(hf_model, backend, max_len)`,
+`QwenRunner.forward(tokens, pos, all_logits)`), re-done for one MI355X:
+
+- Only the backend's `linear`, `norm` and `act` differ between the fp16 and the swapped runs;
+  embedding, RoPE, attention and the tied fp16 lm_head are the same torch code on both sides, as
+  in the reference (model.py:1-12). q/k/v and gate/up are concatenated into one projection each
+  (model.py:168-191).
+- The KV cache keeps K transposed, [layers, batch, kv_heads, head_dim, max_len], and V as
+  [layers, batch, kv_heads, max_len, head_dim], so both attention products are plain batched
+  matmuls over contiguous operands (no transposed right operand). Grouped-query attention folds
+  the query heads of one KV head into the row dimension: scores [B, kv, group*T, max_len].
+- Every step is capturable in a hipGraph: positions are device tensors, the cache is written
+  with index_copy_, the causal mask is built from the positions inside the graph.
+
+The model comes from a Hugging Face Qwen2 module object (as in the reference) or from
+`random_qwen2`, which builds the Qwen2.5-1.5B architecture with Hugging Face's initialisation
+(linear and embedding weights N(0, 0.02), biases 0, norm weights 1) on the GPU, seeded, with no
+download.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from kernels import config
+
+
+# ----------------------------------------------------------------------------------- backends
+@dataclass
+class Linear:
+    """One projection (model.py:25-33): fp16 `w`, or the packed tensors of a quantized format."""
+
+    w: torch.Tensor | None = None
+    qweight: torch.Tensor | None = None
+    scales: torch.Tensor | None = None
+    zeros: torch.Tensor | None = None
+    bias: torch.Tensor | None = None
+
+
+def _rmsnorm_torch(x, w, eps, residual=None):
+    """Qwen2 RMSNorm with HF rounding steps in torch ops (the fp16 side of the comparison):
+    fp16 residual add, fp32 mean of squares, fp16 normalized value, multiply by w."""
+    if residual is not None:
+        x = x + residual
+    h = x.float()
+    normed = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+    out = w * normed
+    return out if residual is None else (out, x)
+
+
+class Backend:
+    """fp16 eager torch ops (rocBLAS/hipBLASLt GEMMs), HF Qwen2 numerics (model.py:36-52)."""
+
+    name = "fp16"
+    quantized = False
+    quant_lm_head = False
+
+    def linear(self, x, p: Linear):
+        return F.linear(x, p.w, p.bias)
+
+    def norm(self, x, w, eps, residual=None):
+        return _rmsnorm_torch(x, w, eps, residual)
+
+    def act(self, gate_up):
+        i = gate_up.shape[-1] // 2
+        return F.silu(gate_up[..., :i]) * gate_up[..., i:]
+
+
+class W4RefBackend(Backend):
+    """RTN int4 weights dequantized once (bit-exact HIP dequantizer) then the fp16 GEMM: the same
+    quantized model as `ours` through library GEMMs (model.py:55-67)."""
+
+    name = "w4_ref"
+    quantized = True
+
+    def linear(self, x, p: Linear):
+        from kernels.quant import dequantize
+
+        if p.w is None:
+            p.w = dequantize(p.qweight, p.scales, p.zeros, config.GROUP_SIZE)
+        return F.linear(x, p.w, p.bias)
+
+
+class OursBackend(Backend):
+    """This build's kernels: W4A16 GEMV/GEMM, fused RMSNorm+residual, fused SwiGLU
+    (model.py:70-97). `decode_kernel="hip"` routes rows <= 16 through the native decode entry,
+    the counterpart of the reference's `ours_cuda`."""
+
+    quantized = True
+
+    def __init__(self, decode_kernel: str = "library"):
+        self.decode_kernel = decode_kernel
+        self.name = "ours" if decode_kernel == "library" else f"ours_{decode_kernel}"
+
+    def linear(self, x, p: Linear):
+        rows = x.numel() // x.shape[-1]
+        if self.decode_kernel == "hip" and rows <= 16:
+            from kernels.hip.w4a16_hip import w4a16_decode_hip
+
+            return w4a16_decode_hip(x, p.qweight, p.scales, p.zeros, bias=p.bias)
+        from kernels.w4a16 import w4a16_matmul
+
+        return w4a16_matmul(x, p.qweight, p.scales, p.zeros, bias=p.bias)
+
+    def norm(self, x, w, eps, residual=None):
+        from kernels.rmsnorm import rmsnorm
+
+        return rmsnorm(x, w, eps, residual)
+
+    def act(self, gate_up):
+        from kernels.swiglu import swiglu_fused
+
+        return swiglu_fused(gate_up)
+
+
+class OursFP8Backend(OursBackend):
+    """FP8 (OCP e4m3) weight-only linears with the same fused norm and activation
+    (model.py:100-118)."""
+
+    def __init__(self):
+        super().__init__("library")
+        self.name = "ours_fp8"
+
+    def quantize(self, w, b) -> Linear:
+        from kernels.fp8 import quantize_fp8
+
+        wq, s = quantize_fp8(w)
+        return Linear(qweight=wq, scales=s, bias=b)
+
+    def linear(self, x, p: Linear):
+        from kernels.fp8 import w8a16_matmul
+
+        return w8a16_matmul(x, p.qweight, p.scales, bias=p.bias)
+
+
+def make_backend(name: str) -> Backend:
+    """`<name>_lm` = quantized backend `<name>` with lm_head quantized too (model.py:121-136)."""
+    base, quant_lm_head = (name[:-3], True) if name.endswith("_lm") else (name, False)
+    be = {
+        "fp16": Backend,
+        "w4_ref": W4RefBackend,
+        "ours": lambda: OursBackend("library"),
+        "ours_hip": lambda: OursBackend("hip"),
+        "ours_fp8": OursFP8Backend,
+    }[base]()
+    if quant_lm_head:
+        if not be.quantized:
+            raise ValueError(f"{name}: only quantized backends can quantize lm_head")
+        be.name = name
+    be.quant_lm_head = quant_lm_head
+    return be
+
+
+# -------------------------------------------------------------------------------------- model
+def qwen25_15b_config(**overrides):
+    """The Qwen2.5-1.5B architecture as a transformers Qwen2Config (no weights)."""
+    import transformers
+
+    kw = dict(config.QWEN25_15B)
+    kw.update(overrides)
+    theta = kw.pop("rope_theta")
+    kw.pop("head_dim", None)
+    cfg = transformers.Qwen2Config(**kw, rope_theta=theta, max_position_embeddings=32768)
+    return cfg
+
+
+def random_qwen2(cfg=None, seed: int = 4, device="cuda", dtype=torch.float16):
+    """A random-init Qwen2ForCausalLM (HF initialisation) built directly on `device`."""
+    import transformers
+
+    cfg = cfg or qwen25_15b_config()
+    torch.manual_seed(seed)
+    if device != "cpu":
+        torch.cuda.manual_seed(seed)
+    with torch.device(device):
+        model = transformers.Qwen2ForCausalLM(cfg)
+    return model.to(dtype).eval()
+
+
+@dataclass
+class Layer:
+    ln1: torch.Tensor
+    ln2: torch.Tensor
+    qkv: Linear
+    o: Linear
+    gate_up: Linear
+    down: Linear
+
+
+class QwenRunner:
+    """Static-cache Qwen2 forward with swappable kernels (model.py:150-253)."""
+
+    def __init__(self, hf_model, backend: Backend, max_len: int = 2048, batch: int = 1):
+        cfg = hf_model.config
+        self.backend = backend
+        self.eps = cfg.rms_norm_eps
+        self.n_heads = cfg.num_attention_heads
+        self.n_kv = cfg.num_key_value_heads
+        self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.n_heads
+        self.max_len = max_len
+        m = hf_model.model
+        dev = m.embed_tokens.weight.device
+        self.embed = m.embed_tokens.weight.data
+        self.lm_head = hf_model.lm_head.weight.data
+        self.final_norm = m.norm.weight.data
+        rp = getattr(cfg, "rope_parameters", None) or {}
+        theta = rp.get("rope_theta", getattr(cfg, "rope_theta", 10000.0))
+        d = self.head_dim
+        self.inv_freq = 1.0 / (theta ** (torch.arange(0, d, 2, device=dev, dtype=torch.float) / d))
+
+        def lin(*mods) -> Linear:
+            w = torch.cat([mm.weight.data for mm in mods], 0)
+            b = None
+            if mods[0].bias is not None:
+                b = torch.cat([mm.bias.data for mm in mods], 0)
+            if not backend.quantized:
+                return Linear(w=w, bias=b)
+            if hasattr(backend, "quantize"):
+                return backend.quantize(w, b)
+            from kernels.quant import quantize_rtn
+
+            qw, s, z = quantize_rtn(w, config.GROUP_SIZE)
+            return Linear(qweight=qw, scales=s, zeros=z, bias=b)
+
+        self.head_q = lin(hf_model.lm_head) if getattr(backend, "quant_lm_head", False) else None
+        self.layers = []
+        for layer in m.layers:
+            a, mlp = layer.self_attn, layer.mlp
+            self.layers.append(Layer(
+                ln1=layer.input_layernorm.weight.data, ln2=layer.post_attention_layernorm.weight.data,
+                qkv=lin(a.q_proj, a.k_proj, a.v_proj), o=lin(a.o_proj),
+                gate_up=lin(mlp.gate_proj, mlp.up_proj), down=lin(mlp.down_proj),
+            ))
+        L, dt = len(self.layers), self.embed.dtype
+        self.kt_cache = torch.zeros((L, batch, self.n_kv, d, max_len), device=dev, dtype=dt)
+        self.v_cache = torch.zeros((L, batch, self.n_kv, max_len, d), device=dev, dtype=dt)
+        self.keys = torch.arange(max_len, device=dev)
+
+    def weight_bytes(self) -> dict:
+        """Bytes of the swapped layers and of the parts that stay fp16 (model.py:196-210)."""
+        def nbytes(t):
+            return 0 if t is None else t.numel() * t.element_size()
+
+        def size(p: Linear):
+            if self.backend.quantized:
+                return nbytes(p.qweight) + nbytes(p.scales) + nbytes(p.zeros) + nbytes(p.bias)
+            return nbytes(p.w) + nbytes(p.bias)
+
+        layers = sum(size(p) for L in self.layers for p in (L.qkv, L.o, L.gate_up, L.down))
+        head = size(self.head_q) if self.head_q is not None else nbytes(self.lm_head)
+        return {"linear_layers": layers, "embed": nbytes(self.embed), "lm_head_read": head,
+                "lm_head_quantized": self.head_q is not None,
+                "lm_head_shared_with_embed": self.lm_head.data_ptr() == self.embed.data_ptr(),
+                "kv_cache": nbytes(self.kt_cache) + nbytes(self.v_cache)}
+
+    def _rope(self, x, cos, sin):
+        half = self.head_dim // 2
+        return x * cos + torch.cat((-x[..., half:], x[..., :half]), dim=-1) * sin
+
+    def _attend(self, i, q, k, v, pos):
+        """q [B, T, nq, hd], k/v [B, T, nkv, hd] (RoPE applied): writes the cache at `pos` and
+        returns the attention output [B, T, nq*hd]."""
+        B, T = q.shape[:2]
+        nkv, hd = self.n_kv, self.head_dim
+        g = self.n_heads // nkv
+        self.kt_cache[i].index_copy_(3, pos, k.permute(0, 2, 3, 1))
+        self.v_cache[i].index_copy_(2, pos, v.transpose(1, 2))
+        # rows ordered (query head within the group, token): [B, nkv, g*T, hd]
+        qg = q.view(B, T, nkv, g, hd).permute(0, 2, 3, 1, 4).reshape(B, nkv, g * T, hd)
+        scores = torch.matmul(qg, self.kt_cache[i]).float() * (hd ** -0.5)
+        allowed = self.keys[None, :] <= pos[:, None]  # [T, max_len]
+        scores = scores.masked_fill(~allowed.repeat(g, 1), float("-inf"))
+        p = torch.softmax(scores, dim=-1).to(q.dtype)
+        out = torch.matmul(p, self.v_cache[i])  # [B, nkv, g*T, hd]
+        return out.view(B, nkv, g, T, hd).permute(0, 3, 1, 2, 4).reshape(B, T, nkv * g * hd)
+
+    @torch.no_grad()
+    def forward(self, tokens: torch.Tensor, pos: torch.Tensor, all_logits: bool = False):
+        """tokens [B, T]; pos int64 [T] absolute positions. Graph-capturable (model.py:217-253)."""
+        be, eps = self.backend, self.eps
+        B, T = tokens.shape
+        nq, nkv, hd = self.n_heads, self.n_kv, self.head_dim
+        x = F.embedding(tokens, self.embed)
+        freqs = pos[:, None].float() * self.inv_freq[None, :]
+        emb = torch.cat((freqs, freqs), dim=-1)
+        cos = emb.cos().to(x.dtype)[None, :, None, :]
+        sin = emb.sin().to(x.dtype)[None, :, None, :]
+
+        residual, h = x, None
+        for i, L in enumerate(self.layers):
+            if h is None:
+                h = be.norm(x, L.ln1, eps)
+            else:  # the previous MLP output joins the residual inside this layer's input norm
+                h, residual = be.norm(h, L.ln1, eps, residual=residual)
+            qkv = be.linear(h, L.qkv)
+            q, k, v = qkv.split([nq * hd, nkv * hd, nkv * hd], dim=-1)
+            q = self._rope(q.view(B, T, nq, hd), cos, sin)
+            k = self._rope(k.view(B, T, nkv, hd), cos, sin)
+            attn = self._attend(i, q, k, v.view(B, T, nkv, hd), pos)
+            o = be.linear(attn, L.o)
+            h, residual = be.norm(o, L.ln2, eps, residual=residual)
+            h = be.linear(be.act(be.linear(h, L.gate_up)), L.down)
+        h, _ = be.norm(h, self.final_norm, eps, residual=residual)
+        if not all_logits:
+            h = h[:, -1:]
+        if self.head_q is not None:
+            return be.linear(h, self.head_q)
+        return F.linear(h, self.lm_head)
