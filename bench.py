@@ -2,11 +2,12 @@
 MI355X, as HBM GB/s and fraction of the 8 TB/s roofline, with the oracle's CPU path timed beside
 it on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
 
 A step is one W4A16 launch over one rotating input set (x, qweight, scales, zeros, output); the
 sets are sized to 4x the 256 MB MALL so every step reads its weights from HBM. Steps run as
 hipGraph replays of one launch per set; HIP events on the replay stream bracket the timed steps.
+The config-4 decode (fp16 vs swapped tok/s) and the CPU baseline are reported beside it.
 Prints one JSON line.
 """
 
@@ -74,6 +75,31 @@ def cpu_baseline(w16, x, seconds: float = 15.0) -> dict:
                       f"({_cpu_model()})"}
 
 
+def e2e_leg(steps: int) -> dict:
+    """Config 4, the metric's second half: batch-1 greedy decode of the random-init
+    Qwen2.5-1.5B architecture (seed 4), 128-token prompt then `steps` decode steps, each step one
+    hipGraph replay; fp16 library GEMMs against the swapped W4A16/RMSNorm/SwiGLU kernels.
+    Reported beside the headline, not as `value`."""
+    import gc
+
+    import torch
+
+    from kernels.e2e.run import run
+
+    res = run({"backends": ["fp16", "ours"], "decode_steps": steps, "prompt_len": 128})
+    gc.collect()
+    torch.cuda.empty_cache()
+    b = res["backends"]
+    return {"metric": "Qwen2.5-1.5B-arch batch-1 decode tok/s", "unit": "tok/s",
+            "workload": "random-init Qwen2.5-1.5B architecture (seed 4), prompt 128, "
+                        f"{steps} greedy steps, hipGraph per step, median of 3",
+            "tok_s": {k: round(v["decode"]["tok_s"], 1) for k, v in b.items()},
+            "ms_per_token": {k: round(v["decode"]["ms_per_token"], 3) for k, v in b.items()},
+            "layers_only_ms": {k: round(v["layers_only_ms"], 3) for k, v in b.items()},
+            "speedup_vs_fp16": round(b["ours"]["speedup_vs_fp16"], 3),
+            "linear_bytes_per_token": {k: v["weights"]["linear_layers"] for k, v in b.items()}}
+
+
 def measured_traffic(kernel_config: str):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this
     command (profiles/w4a16_m1_gate_up_traffic.md), or None when that summary was taken with a
@@ -99,6 +125,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20000)
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the config-4 decode leg (fp16 vs swapped tok/s)")
+    ap.add_argument("--e2e-steps", type=int, default=256)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -167,6 +196,8 @@ def main() -> int:
     }
     timer.close()
     del sets
+    if not args.no_e2e:
+        out["e2e"] = e2e_leg(args.e2e_steps)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w16, x)
     print(json.dumps(out), flush=True)

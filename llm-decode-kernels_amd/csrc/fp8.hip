@@ -110,7 +110,24 @@ __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* __restr
 }
 
 // --------------------------------------------------------------------------------- W8A16 GEMV
-
+//
+// out [M, N] = x [M, K] @ (e4m3(wq) * scale)^T (+ bias), wq [K, N] bytes (N contiguous).
+//
+// Work decomposition (3-D grid: column tile, K split, row block):
+//  * Column tiles of CW = 16 * LN columns; a lane owns 16 adjacent columns, so one 128-bit load
+//    is one K row of 16 weights, and LN = 8 lanes cover one 128-byte line of a row (the default
+//    tile: no line is shared between workgroups).
+//  * The LKW = 64 / LN lanes of a wave along K and the NW waves take interleaved K rows; a pass
+//    of the workgroup covers RPP = LKW * NW * RPL rows, RPL per lane, all loads of a pass issued
+//    before the first wait. A workgroup covers `kps` rows (one or a few passes); workgroups of
+//    one tile that split K meet in the fixed-point workspace (ldk::splitk_add, deterministic, one
+//    launch).
+//  * Row blocks of MT <= 4 activation rows: a lane keeps 16 * MT fp32 accumulators. More rows
+//    run as more row-block workgroups over the same weights (the 256 MB MALL serves the repeats).
+//  * x of a pass is staged in LDS transposed, [row][m], so one ds_read gives the MT values of
+//    one K row. Weights go from one 128-bit load through v_cvt_pk_f32_fp8 (gfx950's OCP e4m3
+//    decode) into fp32 FMAs; the per-channel scale is applied once after the K reduction
+//    (fp8.py:120).
 struct W8Args {
   const half_t* x;
   int64_t ldx;
@@ -122,38 +139,33 @@ struct W8Args {
   int M, N, K;
 };
 
-// x is staged in LDS one K chunk of KC columns at a time (KC = K when the whole row fits), so the
-// LDS need stays bounded for any K: [MT][KC] fp16 + one trash chunk, then the reduction buffer.
-template <int MT, int LN, int UB>
-__global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a, int KC) {
+struct W8Split {
+  int splits;     // workgroups per column tile along K (gridDim.y)
+  int kps;        // K rows per split, a multiple of 8
+  uint64_t* acc;  // [tiles][mblocks][MT * CW] fixed-point accumulators (splits > 1)
+};
+
+// Fixed-point split-K: a partial is clamped to 2^44 in magnitude and the poison threshold is
+// 3 * 2^48 = 48 * 2^44, so up to 40 legal partials can never look poisoned.
+constexpr int kW8MaxSplits = 40;
+
+template <int MT, int LN, int NW, int RPL>
+__global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split sp) {
   constexpr int CW = 16 * LN;
   constexpr int LKW = 64 / LN;
-  constexpr int PXr = (MT * UB + 8 * LN - 1) / (8 * LN);
-  constexpr int PX = PXr < 4 ? PXr : 4;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int NW = blockDim.x >> 6, NT = blockDim.x;
-  const int LK = NW * LKW;
-  const int K = a.K;
+  constexpr int RPP = LKW * NW * RPL;  // K rows per pass
+  __shared__ __align__(16) half_t xs[RPP][MT];
+  __shared__ __align__(16) float red[NW][MT][CW];
+  ldk::pin_sgpr(a.x);
+  ldk::pin_sgpr(a.wq);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ln = lane % LN;
-  const int lk = wave * LKW + lane / LN;
-  const int n0 = ldk::xcd_remap(blockIdx.x, gridDim.x) * CW;
-  const int col = min(n0 + 16 * ln, a.N - 16);
-
-  // LDS: x [MT][KC] fp16 + one trash chunk, then the reduction buffer [NW][MT][CW] floats.
-  half_t* xs = reinterpret_cast<half_t*>(smem);
-  float* red = reinterpret_cast<float*>(smem + (((size_t)MT * KC + 8) * 2 + 15) / 16 * 16);
-  int kc0 = 0;                    // first K column of the staged chunk
-  int kcn = min(KC, K);           // its width
-  int nx = MT * kcn / 8;          // 16-byte x items of the chunk, item = c*MT + m
-
-  u32x4 xr[PX];
-#pragma unroll
-  for (int i = 0; i < PX; ++i) {
-    const int it = min(tid + i * NT, nx - 1);
-    const int m = min(it % MT, a.M - 1), c = it / MT;
-    xr[i] = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c);
-  }
+  const int ln = lane % LN, lk = lane / LN;
+  const int tile = blockIdx.x, split = blockIdx.y, mb = blockIdx.z;
+  const int n0 = tile * CW;
+  const int col = min(n0 + 16 * ln, a.N - 16);  // clamped: tail lanes load valid memory, store nothing
+  const int m0 = mb * MT;
+  const int rb = split * sp.kps, re = min(a.K, rb + sp.kps);
+  const int lrow = wave * LKW + lk;  // this lane's first row inside a pass
 
   float acc[MT][16];
 #pragma unroll
@@ -161,77 +173,55 @@ __global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a, int KC) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[m][j] = 0.0f;
 
-  u32x4 w[UB];
-  auto load_batch = [&](int kb) {
+  for (int p0 = rb; p0 < re; p0 += RPP) {
+    u32x4 w[RPL];
 #pragma unroll
-    for (int u = 0; u < UB; ++u) {
-      const int k = min(kb + lk + u * LK, K - 1);
-      w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.wq + (int64_t)k * a.N + col));
+    for (int j = 0; j < RPL; ++j) {
+      const int r = min(p0 + lrow + j * LKW * NW, re - 1);  // clamped; such rows meet zero x
+      w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.wq + (int64_t)r * a.N + col));
     }
-  };
-  auto compute_batch = [&](int kb) {
+    __builtin_amdgcn_sched_barrier(0);  // every weight load of the pass is in flight first
+    // stage x[m0 .. m0+MT)[p0 .. p0+RPP) as [row][m]; rows past re and m past M are zeros
+    if (p0 != rb) ldk::lds_barrier();  // the previous pass is done reading xs
+    for (int i = tid; i < RPP * MT; i += NW * 64) {
+      const int m = i / RPP, r = i - m * RPP;
+      const int k = p0 + r;
+      half_t v = (half_t)0.0f;
+      if (m0 + m < a.M && k < re) v = a.x[(int64_t)(m0 + m) * a.ldx + k];
+      xs[r][m] = v;
+    }
+    ldk::lds_barrier();
 #pragma unroll
-    for (int u = 0; u < UB; ++u) {
-      const int k = kb + lk + u * LK;
-      if (k < K) {
-        float xv[MT];
+    for (int j = 0; j < RPL; ++j) {
+      const int rl = lrow + j * LKW * NW;
+      float xv[MT];
+      if constexpr (MT == 4) {
+        const half4_t h = *reinterpret_cast<const half4_t*>(&xs[rl][0]);
 #pragma unroll
-        for (int m = 0; m < MT; ++m) xv[m] = (float)xs[(size_t)m * KC + (k - kc0)];
+        for (int m = 0; m < 4; ++m) xv[m] = (float)h[m];
+      } else if constexpr (MT == 2) {
+        const half2_t h = *reinterpret_cast<const half2_t*>(&xs[rl][0]);
+        xv[0] = (float)h[0];
+        xv[1] = (float)h[1];
+      } else {
+        xv[0] = (float)xs[rl][0];
+      }
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[u][d], false);
-          const float2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[u][d], true);
+      for (int d = 0; d < 4; ++d) {
+        const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[j][d], false);
+        const float2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[j][d], true);
 #pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            acc[m][4 * d + 0] = __builtin_fmaf(xv[m], lo[0], acc[m][4 * d + 0]);
-            acc[m][4 * d + 1] = __builtin_fmaf(xv[m], lo[1], acc[m][4 * d + 1]);
-            acc[m][4 * d + 2] = __builtin_fmaf(xv[m], hi[0], acc[m][4 * d + 2]);
-            acc[m][4 * d + 3] = __builtin_fmaf(xv[m], hi[1], acc[m][4 * d + 3]);
-          }
+        for (int m = 0; m < MT; ++m) {
+          acc[m][4 * d + 0] = __builtin_fmaf(xv[m], lo[0], acc[m][4 * d + 0]);
+          acc[m][4 * d + 1] = __builtin_fmaf(xv[m], lo[1], acc[m][4 * d + 1]);
+          acc[m][4 * d + 2] = __builtin_fmaf(xv[m], hi[0], acc[m][4 * d + 2]);
+          acc[m][4 * d + 3] = __builtin_fmaf(xv[m], hi[1], acc[m][4 * d + 3]);
         }
       }
     }
-  };
-
-  load_batch(0);
-#pragma unroll
-  for (int i = 0; i < PX; ++i) {
-    const int it = tid + i * NT;
-    const int m = it % MT, c = it / MT;
-    u32x4 d = xr[i];
-    if (m >= a.M) d = u32x4{0u, 0u, 0u, 0u};
-    const size_t off = it < nx ? (size_t)m * KC + 8 * c : (size_t)MT * KC;  // trash chunk
-    *reinterpret_cast<u32x4*>(xs + off) = d;
-  }
-  for (int it = tid + PX * NT; it < nx; it += NT) {
-    const int m = it % MT, c = it / MT;
-    u32x4 d = *reinterpret_cast<const u32x4*>(a.x + min(m, a.M - 1) * a.ldx + 8 * c);
-    if (m >= a.M) d = u32x4{0u, 0u, 0u, 0u};
-    *reinterpret_cast<u32x4*>(xs + (size_t)m * KC + 8 * c) = d;
-  }
-  ldk::lds_barrier();
-  // KC is a multiple of the batch step UB * LK, so no batch straddles two chunks. The next batch's
-  // weight loads are issued before a chunk switch's barriers and stay in flight across them.
-  for (int kb = 0;;) {
-    compute_batch(kb);
-    kb += UB * LK;
-    if (kb >= K) break;
-    load_batch(kb);
-    if (kb >= kc0 + kcn) {  // uniform: restage x for the next chunk
-      kc0 = kb;
-      kcn = min(KC, K - kc0);
-      nx = MT * kcn / 8;
-      ldk::lds_barrier();  // every wave is done reading the previous chunk
-      for (int it = tid; it < nx; it += NT) {
-        const int m = it % MT, c = it / MT;
-        u32x4 d = *reinterpret_cast<const u32x4*>(a.x + min(m, a.M - 1) * a.ldx + kc0 + 8 * c);
-        if (m >= a.M) d = u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(xs + (size_t)m * KC + 8 * c) = d;
-      }
-      ldk::lds_barrier();
-    }
   }
 
+  // ---- reduction: the LKW lanes of a wave sharing ln (DPP/permlane), then the NW waves (LDS)
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -241,126 +231,113 @@ __global__ __launch_bounds__(512) void w8a16_skinny_kernel(W8Args a, int KC) {
     for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int d = 0; d < 4; ++d)
-        *reinterpret_cast<float4_t*>(red + ((size_t)wave * MT + m) * CW + 16 * lane + 4 * d) =
+        *reinterpret_cast<float4_t*>(&red[wave][m][16 * lane + 4 * d]) =
             float4_t{acc[m][4 * d], acc[m][4 * d + 1], acc[m][4 * d + 2], acc[m][4 * d + 3]};
   }
   ldk::lds_barrier();
-  for (int o = tid; o < MT * CW; o += NT) {
+  const int nblk = gridDim.z;
+  for (int o = tid; o < MT * CW; o += NW * 64) {
     const int m = o / CW, c = o - m * CW;
     const int n = n0 + c;
-    if (m < a.M && n < a.N) {
-      float v = 0.0f;
-      for (int wv = 0; wv < NW; ++wv) v += red[((size_t)wv * MT + m) * CW + c];
-      v *= (float)a.scale[n];
+    if (n >= a.N || (sp.splits == 1 && m0 + m >= a.M)) continue;
+    float v = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) v += red[wv][m][c];
+    v *= (float)a.scale[n];
+    if (sp.splits == 1) {
       if (a.bias) v += (float)a.bias[n];
-      a.out[(int64_t)m * a.ldo + n] = (half_t)v;
-    }
-  }
-}
-
-struct W8Cfg {
-  int mt, ln, nw, ub;
-};
-
-constexpr int64_t kW8MaxLds = 160 * 1024;  // LDS per workgroup on gfx950
-
-// LDS a configuration needs with x staged in chunks of at least one batch step.
-int64_t w8_min_lds(int mt, int ln, int nw, int ub, int64_t K) {
-  const int64_t step = (int64_t)ub * nw * (64 / ln);
-  return (int64_t)mt * std::min<int64_t>(K, step) * 2 + 48 + (int64_t)nw * mt * 16 * ln * 4;
-}
-
-int round_ub8(int rows) {
-  static const int kUB[] = {2, 4, 6, 8, 12, 16};
-  for (int u : kUB)
-    if (u >= rows) return u;
-  return 16;
-}
-
-W8Cfg choose_w8(int64_t M, int64_t N, int64_t K, int block_n, int split_k) {
-  W8Cfg best{M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16, 1, 4, 2};
-  double best_score = -1e30;
-  for (int ln : {4, 2, 1, 8}) {
-    if (block_n && block_n != 16 * ln) continue;
-    for (int nw : {4, 8, 2, 1}) {
-      const int lk = nw * 64 / ln;
-      if (split_k && split_k != lk) continue;
-      const int64_t nwg = (N + 16 * ln - 1) / (16 * ln);
-      const int64_t rows = (K + lk - 1) / lk;
-      if (w8_min_lds(best.mt, ln, nw, round_ub8((int)std::min<int64_t>(rows, 16)), K) > kW8MaxLds) continue;
-      const double waves = (double)nwg * nw;
-      double score = -std::abs(std::log2(std::max(waves, 1.0) / 2048.0)) * 4.0;
-      score -= rows > 16 ? (rows - 16) * 0.5 : 0.0;
-      score -= nwg < 256 ? (256.0 - nwg) / 64.0 : 0.0;
-      if (score > best_score) {
-        best_score = score;
-        best.ln = ln;
-        best.nw = nw;
-        best.ub = round_ub8((int)std::min<int64_t>(rows, 16));
+      a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)v;
+    } else {
+      // every (m, n) word of the tile takes part, rows past M too, so each word is re-zeroed
+      float tot;
+      uint64_t* word = sp.acc + ((size_t)tile * nblk + mb) * (MT * CW) + o;
+      if (ldk::splitk_add(word, sp.splits, v, &tot) && m0 + m < a.M) {
+        if (a.bias) tot += (float)a.bias[n];
+        a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)tot;
       }
     }
   }
-  return best;
 }
 
-template <int MT, int LN, int UB>
-int launch_w8_t(const W8Args& a, int nw, hipStream_t s) {
-  // x chunk width: all of K when [MT][K] fp16 fits 64 KiB, else the largest multiple of the
-  // batch step (UB rows for each of the nw*64/LN lanes along K) that does.
-  const int64_t step = (int64_t)UB * nw * (64 / LN);
-  const int64_t red_bytes = (int64_t)nw * MT * 16 * LN * 4;
-  int64_t kc = a.K;
-  const int64_t max_kc = ((kW8MaxLds - red_bytes - 32) / (2 * MT)) / 8 * 8;
-  if (kc > max_kc) {
-    kc = max_kc / step * step;
-    if (kc < step) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: x chunk smaller than one batch (M=%d)", a.M);
+struct W8Plan {
+  int mt, ln, nw, rpl;
+  int splits, kps, mblocks;
+};
+
+int w8_round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
+
+// Chooses the row block, column tile, rows per lane and K split. Column tiles are 128 columns
+// (one 128-byte line per K row) unless block_n asks otherwise. Each workgroup runs one pass
+// (all its weight loads in flight at once) whenever K fits 40 splits; rows per lane shrink
+// (8, 4, 2) until the grid has at least 256 workgroups (one per CU).
+W8Plan make_w8_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes) {
+  W8Plan p{};
+  p.mt = w8_round_mt(M);
+  p.mblocks = (int)((M + p.mt - 1) / p.mt);
+  p.ln = block_n ? block_n / 16 : 8;
+  p.nw = 4;
+  const int64_t tiles = (N + 16 * p.ln - 1) / (16 * p.ln);
+  const int64_t lanes_k = (int64_t)(64 / p.ln) * p.nw;
+  auto passes = [&](int rpl) { return (K + lanes_k * rpl - 1) / (lanes_k * rpl); };
+  p.rpl = 2;
+  for (int rpl : {8, 4, 2}) {
+    if (tiles * p.mblocks * std::min<int64_t>(passes(rpl), kW8MaxSplits) >= 256) { p.rpl = rpl; break; }
   }
-  const size_t lds = (((size_t)MT * kc + 8) * 2 + 15) / 16 * 16 + (size_t)red_bytes;
-  auto kern = w8a16_skinny_kernel<MT, LN, UB>;
-  if (lds > 64 * 1024) {
-    if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: LDS need %zu B exceeds 160 KiB (M*K too large for the decode kernel)", lds);
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return ldk::fail(LDK_ERR_LAUNCH, "w8a16: cannot raise the LDS limit to %zu B", lds);
+  const int64_t rpp = lanes_k * p.rpl;
+  int64_t kps;
+  if (split_k > 0) {
+    kps = (K + split_k - 1) / split_k;
+  } else {
+    const int64_t per = (passes(p.rpl) + kW8MaxSplits - 1) / kW8MaxSplits;  // passes per split
+    kps = per * rpp;
   }
-  const int grid = (int)((a.N + 16 * LN - 1) / (16 * LN));
+  kps = (kps + 7) / 8 * 8;
+  p.kps = (int)kps;
+  p.splits = (int)((K + kps - 1) / kps);
+  const int64_t need = p.splits > 1 ? tiles * p.mblocks * p.mt * 16 * p.ln * 8 : 0;
+  if (need > ws_bytes) {  // no room for the partials: whole K per workgroup
+    p.splits = 1;
+    p.kps = (int)((K + 7) / 8 * 8);
+  }
+  return p;
+}
+
+template <int MT, int LN, int NW, int RPL>
+int launch_w8_t(const W8Args& a, const W8Split& sp, int mblocks, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 16 * LN - 1) / (16 * LN)), (unsigned)sp.splits, (unsigned)mblocks);
   (void)hipGetLastError();
-  kern<<<grid, nw * 64, lds, s>>>(a, (int)kc);
-  return ldk::check_launch("w8a16_skinny");
+  w8a16_gemv_kernel<MT, LN, NW, RPL><<<grid, NW * 64, 0, s>>>(a, sp);
+  return ldk::check_launch("w8a16_gemv");
 }
 
 template <int MT, int LN>
-int launch_w8_ub(const W8Args& a, const W8Cfg& c, hipStream_t s) {
-  switch (c.ub) {
-    case 2: return launch_w8_t<MT, LN, 2>(a, c.nw, s);
-    case 4: return launch_w8_t<MT, LN, 4>(a, c.nw, s);
-    case 6: return launch_w8_t<MT, LN, 6>(a, c.nw, s);
-    case 8: return launch_w8_t<MT, LN, 8>(a, c.nw, s);
-    case 12: return launch_w8_t<MT, LN, 12>(a, c.nw, s);
-    case 16: return launch_w8_t<MT, LN, 16>(a, c.nw, s);
+int launch_w8_rpl(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  switch (p.rpl) {
+    case 2: return launch_w8_t<MT, LN, 4, 2>(a, sp, p.mblocks, s);
+    case 4: return launch_w8_t<MT, LN, 4, 4>(a, sp, p.mblocks, s);
+    case 8: return launch_w8_t<MT, LN, 4, 8>(a, sp, p.mblocks, s);
   }
-  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: rows per lane %d not instantiated", c.ub);
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d rows per lane not instantiated", p.rpl);
 }
 
 template <int MT>
-int launch_w8_ln(const W8Args& a, const W8Cfg& c, hipStream_t s) {
-  switch (c.ln) {
-    case 1: return launch_w8_ub<MT, 1>(a, c, s);
-    case 2: return launch_w8_ub<MT, 2>(a, c, s);
-    case 4: return launch_w8_ub<MT, 4>(a, c, s);
-    case 8: return launch_w8_ub<MT, 8>(a, c, s);
+int launch_w8_ln(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  switch (p.ln) {
+    case 1: return launch_w8_rpl<MT, 1>(a, sp, p, s);
+    case 2: return launch_w8_rpl<MT, 2>(a, sp, p, s);
+    case 4: return launch_w8_rpl<MT, 4>(a, sp, p, s);
+    case 8: return launch_w8_rpl<MT, 8>(a, sp, p, s);
   }
-  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: column tile %d not instantiated", 16 * c.ln);
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: block_n=%d not supported (16, 32, 64 or 128)", 16 * p.ln);
 }
 
-int launch_w8(const W8Args& a, const W8Cfg& c, hipStream_t s) {
-  switch (c.mt) {
-    case 1: return launch_w8_ln<1>(a, c, s);
-    case 2: return launch_w8_ln<2>(a, c, s);
-    case 4: return launch_w8_ln<4>(a, c, s);
-    case 8: return launch_w8_ln<8>(a, c, s);
-    case 16: return launch_w8_ln<16>(a, c, s);
+int launch_w8(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  switch (p.mt) {
+    case 1: return launch_w8_ln<1>(a, sp, p, s);
+    case 2: return launch_w8_ln<2>(a, sp, p, s);
+    case 4: return launch_w8_ln<4>(a, sp, p, s);
   }
-  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: row tile %d not instantiated", c.mt);
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: row block %d not instantiated", p.mt);
 }
 
 inline unsigned blocks_for(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
@@ -399,23 +376,25 @@ extern "C" int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, 
 extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias, void* out,
                                 int64_t ldo, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int flags,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: null pointer");
   if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: M, N, K must be positive");
   if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld > 16 (prefill GEMM not built yet)", (long long)M);
   if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N=%lld must be a multiple of 16", (long long)N);
   if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: K=%lld must be a multiple of 8", (long long)K);
   if (ldx < K || ldo < N) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: row stride smaller than K/N");
-  if (ldx % 8 || !ldk::aligned(x, 16) || !ldk::aligned(wq, 16))
-    return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: x and wq must be 16-byte aligned with ldx %% 8 == 0");
+  if (!ldk::aligned(x, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
+    return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: wq must be 16-byte aligned");
   if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N or K too large");
   if (flags & ~(LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: flags 0x%x not supported", flags);
-  if (block_n && (block_n % 16 || block_n > 128 || (block_n & (block_n - 1))))
+  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: block_n=%d must be 16, 32, 64 or 128", block_n);
-  const W8Cfg c = choose_w8(M, N, K, block_n, split_k);
-  if (split_k && c.nw * 64 / c.ln != split_k)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: split_k=%d is not nw*64/(block_n/16) for nw in {1,2,4,8}", split_k);
+  if (split_k < 0 || split_k > kW8MaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: split_k=%d outside 0..%d", split_k, kW8MaxSplits);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: workspace must be a 256-byte aligned pointer");
+  const W8Plan p = make_w8_plan(M, N, K, block_n, split_k, workspace ? workspace_bytes : 0);
+  if (split_k > 1 && p.splits == 1)
+    return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W8Args a{(const half_t*)x, ldx, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K};
-  return launch_w8(a, c, (hipStream_t)stream);
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
+  return launch_w8(a, sp, p, (hipStream_t)stream);
 }
