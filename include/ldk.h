@@ -150,6 +150,24 @@ int ldk_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr, c
 int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out, int64_t ldo,
                int64_t M, int64_t I, void* stream);
 
+/* ------------------------------------------------------------------------ decode attention */
+
+/* One decode step's attention block for one new token (batch 1) of one layer: RoPE on q and the
+ * new k (cos/sin of *pos * inv_freq[i], rotate_half pairing, the reference's fp16 rounding
+ * steps), the new k and v written at *pos into the static cache, then grouped-query softmax
+ * attention of each of the nq heads over positions 0..*pos, in one launch.
+ *   qkv:      [nq*head_dim + 2*nkv*head_dim] fp16, the qkv projection output (bias added);
+ *   pos:      int64 device scalar, the new token's position (< max_len);
+ *   inv_freq: [head_dim/2] fp32 RoPE inverse frequencies;
+ *   kt_cache: fp16 [nkv][head_dim][max_len] (K transposed), v_cache: fp16 [nkv][max_len][head_dim];
+ *   out:      [nq*head_dim] fp16; scale: the softmax scale (head_dim^-0.5).
+ * head_dim == 128, nq % nkv == 0, max_len <= 512. Replaces the per-layer attention of the
+ * reference's runner for decode steps (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into
+ * the cache, scaled_dot_product_attention with the causal mask). */
+int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* kt_cache,
+                         void* v_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
+                         float scale, void* stream);
+
 /* ------------------------------------------------------------------- greedy decode bookkeeping */
 
 /* idx = argmax(logits[0:V]) (torch.argmax order: NaN largest, lowest index on ties), then

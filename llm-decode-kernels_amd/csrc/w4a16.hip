@@ -68,14 +68,38 @@ struct SplitArgs {
   int splits;     // workgroups per split column tile
   int gps;        // groups per split
   uint64_t* acc;  // [split tiles][n] fixed-point accumulators (splits > 1), zero between launches
-  int full;       // M = 1 kernel: tiles [0, full) run whole (one workgroup, no split); the split
-                  // workgroups of tiles [full, tiles) come first in dispatch order
-  int nsplit;       // M = 1 kernel: number of those split workgroups
+  int full;       // tiles [0, full) run whole (one workgroup, no split); the split workgroups of
+                  // tiles [full, tiles) come first in dispatch order
+  int nsplit;       // number of those split workgroups
   uint64_t smagic;  // ceil(2^32 / splits): b / splits == (b * smagic) >> 32 for b, splits < 2^16
 };
 
 // ceil(2^32 / d) for 1 <= d < 2^16: floor(n / d) == (n * magic) >> 32 for every n < 2^16.
 inline uint64_t div_magic(uint32_t d) { return ((uint64_t(1) << 32) + d - 1) / d; }
+
+// Work of one workgroup: a column tile and its range of quantization groups [gb, ge).
+struct TileWork {
+  int tile, gb, ge;
+  bool whole;  // all groups of the tile: the result is stored directly, no split-K reduction
+};
+
+// Dispatch order: the split workgroups of tiles [full, tiles) first (splits per tile), then the
+// whole tiles [0, full). Requests are served roughly in issue order, so the split workgroups'
+// data arrives early and their cross-workgroup round trip overlaps the streaming of the whole
+// tiles. Branch-free scalar code with no runtime integer division, so every kernel argument is
+// fetched in one scalar round trip before the first vector load.
+__device__ __forceinline__ TileWork map_block(const SplitArgs& sp, int ng) {
+  const int bid = blockIdx.x;
+  const bool in_split = bid < sp.nsplit;
+  const int q = (int)(((uint64_t)(uint32_t)bid * sp.smagic) >> 32);
+  TileWork w;
+  w.tile = in_split ? sp.full + q : bid - sp.nsplit;
+  const int split = in_split ? bid - q * sp.splits : 0;
+  w.whole = !in_split || sp.splits == 1;
+  w.gb = w.whole ? 0 : split * sp.gps;
+  w.ge = w.whole ? ng : min(ng, w.gb + sp.gps);
+  return w;
+}
 
 __device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (lo16(a), lo16(b))
   return __builtin_amdgcn_perm(b, a, 0x05040100u);
@@ -108,13 +132,13 @@ __device__ __forceinline__ void store_fact_record(unsigned char* dst, u32x4 d) {
 // wave-major in `red`; sum them and store (or hand them to the cross-workgroup split-K
 // reduction).
 template <typename Store>
-__device__ __forceinline__ void finish_tile(const float* red, int n, int NW, int tile,
+__device__ __forceinline__ void finish_tile(const float* red, int n, int NW, const TileWork& tw,
                                             const SplitArgs& sp, Store store) {
   auto part = [&](int o) { return ldk::sum_waves(red + o, n, NW); };
-  if (sp.splits == 1) {
+  if (tw.whole) {
     for (int o = threadIdx.x; o < n; o += blockDim.x) store(o, part(o));
   } else {
-    ldk::splitk_accumulate(sp.acc + (size_t)tile * n, sp.splits, n, part, store);
+    ldk::splitk_accumulate(sp.acc + (size_t)(tw.tile - sp.full) * n, sp.splits, n, part, store);
   }
 }
 
@@ -138,23 +162,14 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
   const int ln = lane % LN, lk = lane / LN;
   const int gi = lk >> lgsh, sub = lk & ((1 << lgsh) - 1);
   const int gpw = LKW >> lgsh;
-  // Dispatch order: the split workgroups of tiles [full, tiles) first, then the whole tiles.
-  // Requests are served roughly in issue order, so the split workgroups' data arrives early and
-  // their cross-workgroup round trip overlaps the streaming of the whole tiles.
-  // Branch-free scalar prologue (no runtime integer division): every kernel argument is needed
-  // before the first load, so the compiler fetches them in one scalar round trip.
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.qw);
-  const int bid = blockIdx.x;
-  const bool in_split = bid < sp.nsplit;
-  const int q = (int)(((uint64_t)(uint32_t)bid * sp.smagic) >> 32);
-  const int tile = in_split ? sp.full + q : bid - sp.nsplit;
-  const int split = in_split ? bid - q * sp.splits : 0;
-  const bool whole = !in_split || sp.splits == 1;
+  const int R = a.K >> 3, ng = R >> rsh;
+  const TileWork tw = map_block(sp, ng);
+  const int tile = tw.tile, gb = tw.gb, ge = tw.ge;
+  const bool whole = tw.whole;
   const int n0 = tile * CW;
   const int col = min(n0 + 4 * ln, a.N - 4);  // clamped: tail lanes load valid memory, store nothing
-  const int R = a.K >> 3, ng = R >> rsh;
-  const int gb = whole ? 0 : split * sp.gps, ge = whole ? ng : min(ng, gb + sp.gps);
   // A split that fits one wave pass is reduced by wave 0 alone, with no LDS round and no barrier
   // (the other waves find no pass in the loop below and leave after it).
   const bool one_wave = !whole && ge - gb <= gpw;
@@ -287,10 +302,12 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane % LN, lkw = lane / LN;
   const int gi = lkw / LG, sub = lkw - gi * LG;
-  const int tile = blockIdx.x / sp.splits, split = blockIdx.x - tile * sp.splits;
-  const int n0 = tile * CW;
+  ldk::pin_sgpr(a.x);
+  ldk::pin_sgpr(a.qw);
+  const TileWork tw = map_block(sp, ng);
+  const int n0 = tw.tile * CW;
   const int col = min(n0 + 4 * ln, a.N - 4);  // clamped: tail lanes load valid memory, store nothing
-  const int gb = split * sp.gps, ge = min(ng, gb + sp.gps);
+  const int gb = tw.gb, ge = tw.ge;
   const int rb = gb << a.gsh_rows, re = ge << a.gsh_rows;  // packed rows of this workgroup
   const int nchunks = (ge - gb + GW - 1) / GW;
   unsigned char* xw = smem + (size_t)wave * SLOTS * ROWB;
@@ -391,7 +408,7 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
           float4_t{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
   }
   __syncthreads();
-  finish_tile(red, MT * CW, NW, tile, sp, [&](int o, float v) {
+  finish_tile(red, MT * CW, NW, tw, sp, [&](int o, float v) {
     const int m = o / CW, n = n0 + (o - m * CW);
     if (m < a.M && n < a.N) {
       if (a.bias) v += (float)a.bias[n];
@@ -418,10 +435,12 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
   const int ng = R >> a.gsh_rows;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
-  const int tile = blockIdx.x / sp.splits, split = blockIdx.x - tile * sp.splits;
-  const int n0 = tile * CW;
+  ldk::pin_sgpr(a.x);
+  ldk::pin_sgpr(a.qw);
+  const TileWork tw = map_block(sp, ng);
+  const int n0 = tw.tile * CW;
   const int col = min(n0 + 4 * c16, a.N - 4);
-  const int gb = split * sp.gps, ge = min(ng, gb + sp.gps);
+  const int gb = tw.gb, ge = tw.ge;
   const int xrow = min(c16, a.M - 1);
   const bool xok = c16 < a.M;
   const int mrows = min(a.M, 16);
@@ -497,7 +516,7 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
           float4_t{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
   }
   __syncthreads();
-  finish_tile(red, n, NW, tile, sp, [&](int o, float v) {
+  finish_tile(red, n, NW, tw, sp, [&](int o, float v) {
     const int m = o / CW, nn = n0 + (o - m * CW);
     if (nn < a.N) {
       if (a.bias) v += (float)a.bias[nn];
@@ -620,7 +639,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // M = 1 with more than one round of 256 tiles: whole tiles give every CU the same whole-tile
   // count, and the remainder tiles split into one-wave-pass pieces that spread over all CUs
   // (gate_up: 512 whole tiles + 48 tiles x 6 splits of 2 groups; 560 whole tiles leave 48 CUs
-  // with a third tile, measured 5.40 -> 5.06 us).
+  // with a third tile, measured 5.40 -> 5.06 us). The multi-row kernels keep whole tiles: their
+  // split pieces carry M times the outputs through the workspace (MFMA gate_up M=16 measured
+  // 10.15 -> 12.49 us with the same split).
   if (m1 && split_k <= 0 && tiles > 256 && tiles % 256) {
     const int64_t rem = tiles % 256;
     // groups per split: whole wave passes, chosen so that rem * splits lands nearest 256
@@ -695,9 +716,8 @@ int launch_gemv_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
   }
-  const int64_t tiles = (a.N + 4 * LN - 1) / (4 * LN);
   (void)hipGetLastError();
-  kern<<<(unsigned)(tiles * sp.splits), nw * 64, lds, stream>>>(a, sp);
+  kern<<<(unsigned)(sp.full + sp.nsplit), nw * 64, lds, stream>>>(a, sp);
   return ldk::check_launch("w4a16_gemv");
 }
 
@@ -740,19 +760,17 @@ int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
-  const int64_t tiles = (a.N + 63) / 64;
   (void)hipGetLastError();
-  kern<<<(unsigned)(tiles * sp.splits), nw * 64, lds, s>>>(a, sp);
+  kern<<<(unsigned)(sp.full + sp.nsplit), nw * 64, lds, s>>>(a, sp);
   return ldk::check_launch("w4a16_mfma16");
 }
 
 int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
-  SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr, 0, 0, div_magic(p.splits)};
-  if (p.kern == kM1) {
-    const int64_t tiles = (a.N + 4 * p.ln - 1) / (4 * p.ln);
-    sp.full = p.full;
-    sp.nsplit = (int)((tiles - p.full) * p.splits);
-  }
+  const int64_t tiles = (a.N + plan_cw(p) - 1) / plan_cw(p);
+  const SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr, p.full,
+                     (int)((tiles - p.full) * p.splits), div_magic(p.splits)};
+  if (sp.full + (int64_t)sp.nsplit >= 65536)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %lld workgroups exceed the grid mapping limit", (long long)(sp.full + (int64_t)sp.nsplit));
   const size_t lds = plan_lds_bytes(p, a.M);
   if (lds > 160 * 1024) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: LDS need %zu B exceeds 160 KiB", lds);
   if (p.kern == kM1) {

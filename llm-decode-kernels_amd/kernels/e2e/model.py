@@ -196,7 +196,11 @@ class Layer:
 class QwenRunner:
     """Static-cache Qwen2 forward with swappable kernels (model.py:150-253)."""
 
-    def __init__(self, hf_model, backend: Backend, max_len: int = 2048, batch: int = 1):
+    def __init__(self, hf_model, backend: Backend, max_len: int = 2048, batch: int = 1,
+                 attention: str = "fused"):
+        """attention: "fused" runs decode steps (one token, batch 1) through the fused HIP
+        attention kernel (RoPE + KV write + GQA softmax attention in one launch per layer) on
+        every backend; "torch" keeps the torch ops for every step. Prefill always uses torch."""
         cfg = hf_model.config
         self.backend = backend
         self.eps = cfg.rms_norm_eps
@@ -241,6 +245,13 @@ class QwenRunner:
         self.kt_cache = torch.zeros((L, batch, self.n_kv, d, max_len), device=dev, dtype=dt)
         self.v_cache = torch.zeros((L, batch, self.n_kv, max_len, d), device=dev, dtype=dt)
         self.keys = torch.arange(max_len, device=dev)
+        self.fused_attention = False
+        if attention == "fused" and dev.type == "cuda":
+            from kernels import attention as fa
+
+            self.fused_attention = fa.supported(d, max_len, batch, 1)
+        elif attention not in ("fused", "torch"):
+            raise ValueError(f"attention={attention!r}: 'fused' or 'torch'")
 
     def weight_bytes(self) -> dict:
         """Bytes of the swapped layers and of the parts that stay fp16 (model.py:196-210)."""
@@ -287,10 +298,14 @@ class QwenRunner:
         B, T = tokens.shape
         nq, nkv, hd = self.n_heads, self.n_kv, self.head_dim
         x = F.embedding(tokens, self.embed)
-        freqs = pos[:, None].float() * self.inv_freq[None, :]
-        emb = torch.cat((freqs, freqs), dim=-1)
-        cos = emb.cos().to(x.dtype)[None, :, None, :]
-        sin = emb.sin().to(x.dtype)[None, :, None, :]
+        fused = self.fused_attention and B == 1 and T == 1
+        if fused:
+            from kernels.attention import decode_attention
+        else:
+            freqs = pos[:, None].float() * self.inv_freq[None, :]
+            emb = torch.cat((freqs, freqs), dim=-1)
+            cos = emb.cos().to(x.dtype)[None, :, None, :]
+            sin = emb.sin().to(x.dtype)[None, :, None, :]
 
         residual, h = x, None
         for i, L in enumerate(self.layers):
@@ -299,10 +314,14 @@ class QwenRunner:
             else:  # the previous MLP output joins the residual inside this layer's input norm
                 h, residual = be.norm(h, L.ln1, eps, residual=residual)
             qkv = be.linear(h, L.qkv)
-            q, k, v = qkv.split([nq * hd, nkv * hd, nkv * hd], dim=-1)
-            q = self._rope(q.view(B, T, nq, hd), cos, sin)
-            k = self._rope(k.view(B, T, nkv, hd), cos, sin)
-            attn = self._attend(i, q, k, v.view(B, T, nkv, hd), pos)
+            if fused:
+                attn = decode_attention(qkv, pos, self.inv_freq, self.kt_cache[i], self.v_cache[i],
+                                        nq, nkv, hd ** -0.5)
+            else:
+                q, k, v = qkv.split([nq * hd, nkv * hd, nkv * hd], dim=-1)
+                q = self._rope(q.view(B, T, nq, hd), cos, sin)
+                k = self._rope(k.view(B, T, nkv, hd), cos, sin)
+                attn = self._attend(i, q, k, v.view(B, T, nkv, hd), pos)
             o = be.linear(attn, L.o)
             h, residual = be.norm(o, L.ln2, eps, residual=residual)
             h = be.linear(be.act(be.linear(h, L.gate_up)), L.down)

@@ -1,0 +1,71 @@
+"""The fused decode attention kernel (ldk_decode_attention) against a float64 CPU computation of
+the same block: RoPE with exact cos/sin (rotate_half pairing, kernels/e2e/model.py:212-214 of the
+reference), the cache write at pos, and grouped-query softmax attention over positions 0..pos
+(model.py:236-243)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kernels.attention import decode_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _rope64(x, pos, inv_freq):
+    """float64 RoPE of x [..., 128] at position pos (angles from the fp32 inv_freq values)."""
+    ang = float(pos) * inv_freq.astype(np.float64)
+    ang = np.concatenate([ang, ang])
+    rh = np.concatenate([-x[..., 64:], x[..., :64]], axis=-1)
+    return x * np.cos(ang) + rh * np.sin(ang)
+
+
+@pytest.mark.parametrize("nq,nkv,L,pos", [(12, 2, 392, 0), (12, 2, 392, 127), (12, 2, 392, 383),
+                                          (4, 4, 64, 63), (8, 1, 512, 511), (16, 2, 130, 64)])
+def test_against_float64(nq, nkv, L, pos):
+    g = torch.Generator().manual_seed(pos + 7 * nq)
+    hd = 128
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half()
+    kt = (torch.randn(1, nkv, hd, L, generator=g) * 0.7).half()
+    vc = torch.randn(1, nkv, L, hd, generator=g).half()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd)))
+    kt_d, vc_d = kt.cuda(), vc.cuda()
+    out = decode_attention(qkv.cuda().view(1, 1, -1), torch.tensor([pos], device="cuda"),
+                           inv_freq.cuda(), kt_d, vc_d, nq, nkv, hd ** -0.5)
+    x = qkv.double().numpy()
+    q = x[: nq * hd].reshape(nq, hd)
+    k = x[nq * hd:(nq + nkv) * hd].reshape(nkv, hd)
+    v = x[(nq + nkv) * hd:].reshape(nkv, hd)
+    fr = inv_freq.numpy()
+    qr, kr = _rope64(q, pos, fr), _rope64(k, pos, fr)
+    # the cache now holds the new k (roped) and v at pos, untouched elsewhere
+    kt_got, vc_got = kt_d.cpu().double().numpy(), vc_d.cpu().double().numpy()
+    assert np.abs(kt_got[0, :, :, pos] - kr).max() <= 4e-3 * max(1.0, np.abs(kr).max())
+    assert np.array_equal(vc_got[0, :, pos], v.astype(np.float16).astype(np.float64))
+    mask = np.ones(L, dtype=bool)
+    mask[pos] = False
+    assert np.array_equal(kt_got[0][..., mask], kt.double().numpy()[0][..., mask])
+    assert np.array_equal(vc_got[0][:, mask], vc.double().numpy()[0][:, mask])
+    # attention in float64 over positions 0..pos with the new k/v (as stored in fp16)
+    K = kt_got[0].transpose(0, 2, 1)[:, : pos + 1]  # [nkv, pos+1, hd]
+    V = vc_got[0][:, : pos + 1]
+    gq = nq // nkv
+    ref = np.zeros((nq, hd))
+    for h in range(nq):
+        s = K[h // gq] @ qr[h] / math.sqrt(hd)
+        p = np.exp(s - s.max())
+        ref[h] = (p / p.sum()) @ V[h // gq]
+    got = out.view(nq, hd).cpu().double().numpy()
+    err = np.abs(got - ref)
+    assert err.max() <= 2e-2 and np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2e-3, (err.max(),)
+
+
+def test_rejects_unsupported_shapes():
+    qkv = torch.zeros(16 * 128, dtype=torch.float16, device="cuda")
+    kt = torch.zeros(1, 2, 128, 600, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(1, 2, 600, 128, dtype=torch.float16, device="cuda")
+    inv = torch.ones(64, device="cuda")
+    with pytest.raises(RuntimeError):  # max_len 600 > 512
+        decode_attention(qkv, torch.tensor([0], device="cuda"), inv, kt, vc, 12, 2, 1.0)
