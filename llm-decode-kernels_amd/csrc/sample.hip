@@ -50,12 +50,25 @@ __global__ __launch_bounds__(kThreads) void greedy_step_kernel(const T* __restri
   const int tid = threadIdx.x;
   Best b{-__builtin_inff(), V};  // index V loses every tie against a real index
   constexpr int kVec = 16 / sizeof(T);
+  constexpr int kBatch = 20;  // 16-byte loads per thread in flight at once (a 151936-entry fp16
+                              // row is 18992 loads: one batch, one memory round trip)
   const int64_t nvec = ldk::aligned(logits, 16) ? V / kVec : 0;
   typedef T vec_t __attribute__((ext_vector_type(kVec)));
-  for (int64_t c = tid; c < nvec; c += kThreads) {
-    const vec_t v = *reinterpret_cast<const vec_t*>(logits + c * kVec);
+  for (int64_t c0 = 0; c0 < nvec; c0 += (int64_t)kBatch * kThreads) {
+    vec_t v[kBatch];
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) take(b, to_f<T>(v[j]), c * kVec + j);
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t c = c0 + tid + (int64_t)u * kThreads;
+      v[u] = c < nvec ? *reinterpret_cast<const vec_t*>(logits + c * kVec) : vec_t{};
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t c = c0 + tid + (int64_t)u * kThreads;
+      if (c < nvec) {
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) take(b, to_f<T>(v[u][j]), c * kVec + j);
+      }
+    }
   }
   for (int64_t i = nvec * kVec + tid; i < V; i += kThreads) take(b, to_f<T>(logits[i]), i);
   // wave reduction, then across the waves through LDS
