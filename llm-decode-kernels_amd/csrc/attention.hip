@@ -7,12 +7,28 @@
 //
 // Layout: qkv [nq*128 | nkv*128 | nkv*128] fp16 (projection output, bias added, before RoPE);
 // the cache keeps K transposed, kt [nkv][128][max_len], and V as v [nkv][max_len][128]; out
-// [nq*128] fp16. One workgroup per query head h (kv head h / (nq/nkv)); wave w covers positions
-// 64w .. 64w+63 (max_len <= 512, so at most 8 waves).
+// [nq*128] fp16. max_len is a multiple of 8 (16-byte rows of 8 positions).
+//
+// Work split. One workgroup per query head (kv head h / (nq/nkv)), up to 8 waves. Wave w takes
+// the 64-position chunks w, w + nw, ... that hold live positions (<= pos). A chunk is 16 KB of K
+// and 16 KB of V, and a wave issues all 32 of its 16-byte loads per lane before the first wait,
+// so the whole chunk is one memory round trip (a per-position loop would be 64 dependent ones).
+//  - Scores: lane (pg = lane % 8, dg = lane / 8) loads K^T rows dg + 8i (i < 16), positions
+//    8pg .. 8pg+7 of the chunk, and sums q[d] * K[d][p] over its 16 rows for its 8 positions;
+//    lanes sharing pg are summed with DPP/permlane (stride 8).
+//  - Softmax per chunk (max and sum over a 16-lane row, which holds every pg twice), merged
+//    online across a wave's chunks and at the end across the waves through LDS.
+//  - Output: lane (dc = lane % 16, pr = lane / 16) loads V rows 16pr + i (i < 16), dims
+//    8dc .. 8dc+7, weighted by the chunk's softmax numerators (passed through LDS); lanes sharing
+//    dc are summed with permlane swaps (stride 16).
+// The cache at `pos` is stale while the first workgroup of the group writes the new k/v, so the
+// score at pos is recomputed from the roped k in LDS and the V row at pos is replaced by the new v.
 //
 // Numerics: RoPE as the reference's fp16 torch ops (cos/sin of pos * inv_freq in fp32 rounded to
-// fp16, q*cos and rotate_half(q)*sin each rounded to fp16, their sum rounded), scores, softmax
-// and the weighted sum of V in fp32, the output rounded once to fp16.
+// fp16, q*cos and rotate_half(q)*sin each rounded to fp16, their sum rounded); scores from the
+// fp16 q and K with fp32 accumulation (v_dot2_f32_f16); softmax in fp32 with its numerators
+// rounded to fp16 before they weight V (the reference's softmax(...).to(fp16) @ v), the V sum
+// and the normalisation in fp32, the output rounded once to fp16.
 #include <algorithm>
 
 #include "ldk_common.h"
@@ -20,7 +36,9 @@
 namespace {
 
 constexpr int kHD = 128;
-constexpr int kMaxWaves = 8;  // max_len <= 512
+constexpr int kMaxWaves = 8;
+constexpr int kChunk = 64;  // positions per wave pass
+constexpr int64_t kMaxLen = 1 << 20;
 
 struct AttnArgs {
   const half_t* qkv;
@@ -34,8 +52,7 @@ struct AttnArgs {
 };
 
 // fp16 RoPE of element d of a 128-vector x (rotate_half pairs d with d +- 64).
-__device__ __forceinline__ half_t rope_elem(const half_t* x, int d, float angle_base) {
-  const float ang = angle_base;
+__device__ __forceinline__ half_t rope_elem(const half_t* x, int d, float ang) {
   const half_t c = (half_t)cosf(ang), s = (half_t)sinf(ang);
   const half_t xd = x[d];
   const half_t rh = d < 64 ? (half_t)(-(float)x[d + 64]) : x[d - 64];
@@ -44,90 +61,199 @@ __device__ __forceinline__ half_t rope_elem(const half_t* x, int d, float angle_
   return (half_t)((float)a + (float)b);
 }
 
+__device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (lo16(a), lo16(b))
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {  // (hi16(a), hi16(b))
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// Max over the 16 lanes of a DPP row.
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, ldk::row_ror<1>(v));
+  v = fmaxf(v, ldk::row_ror<2>(v));
+  v = fmaxf(v, ldk::row_ror<4>(v));
+  return fmaxf(v, ldk::row_ror<8>(v));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += ldk::row_ror<1>(v);
+  v += ldk::row_ror<2>(v);
+  v += ldk::row_ror<4>(v);
+  return v + ldk::row_ror<8>(v);
+}
+
 __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnArgs a) {
-  __shared__ float qs[kHD];              // roped q of this head, fp32
-  __shared__ half_t knew[kHD], vnew[kHD];
-  __shared__ float ps[kMaxWaves * 64];   // softmax weights by position
-  __shared__ float wred[kMaxWaves];
-  __shared__ float ored[kMaxWaves][kHD];
+  __shared__ float qs[kHD];                    // roped q of this head (fp16 values)
+  __shared__ half_t knew[kHD], vnew[kHD];      // roped new k, new v
+  __shared__ __align__(16) float pw[kMaxWaves][kChunk];  // softmax numerators of a wave's chunk
+  __shared__ __align__(16) float ow[kMaxWaves][kHD];     // per-wave unnormalized outputs
+  __shared__ float mw[kMaxWaves], lw[kMaxWaves];
   const int h = blockIdx.x;
   const int g = a.nq / a.nkv, kvh = h / g;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int64_t pos = *a.pos;
+  const int L = a.max_len;
+  const int64_t pos_in = *a.pos;
+  const bool pos_ok = pos_in >= 0 && pos_in < L;  // else: attend over the cache, write nothing
+  const int pos = pos_ok ? (int)pos_in : pos_in < 0 ? -1 : L - 1;  // last live position
+  const int npos = (int)pos_in;
   const half_t* q = a.qkv + (int64_t)h * kHD;
   const half_t* kx = a.qkv + (int64_t)a.nq * kHD + (int64_t)kvh * kHD;
   const half_t* vx = kx + (int64_t)a.nkv * kHD;
-  half_t* kt = a.kt + (int64_t)kvh * kHD * a.max_len;
-  half_t* vc = a.v + (int64_t)kvh * a.max_len * kHD;
+  half_t* kt = a.kt + (int64_t)kvh * kHD * L;
+  half_t* vc = a.v + (int64_t)kvh * L * kHD;
+
+  const int pg = lane & 7, dg = lane >> 3;    // score lanes
+  const int dc = lane & 15, pr = lane >> 4;   // output lanes
+
+  // ---- first chunk's loads go out before the RoPE work, so both latencies overlap
+  int c0 = wave * kChunk;
+  u32x4 kr[16], vr[16];
+  auto issue = [&](int base) {
+    const int p8 = min(base + 8 * pg, L - 8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      kr[i] = *reinterpret_cast<const u32x4*>(kt + (int64_t)(dg + 8 * i) * L + p8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int p = min(base + 16 * pr + i, L - 1);
+      vr[i] = *reinterpret_cast<const u32x4*>(vc + (int64_t)p * kHD + 8 * dc);
+    }
+  };
+  if (c0 <= pos) issue(c0);
 
   // ---- RoPE (q, new k), stage the new k/v, write them to the cache (first head of the group)
   if (tid < kHD) {
-    const float ang = (float)pos * a.inv_freq[tid & 63];
+    const float ang = (float)pos_in * a.inv_freq[tid & 63];
     qs[tid] = (float)rope_elem(q, tid, ang);
-    const half_t kr = rope_elem(kx, tid, ang);
-    knew[tid] = kr;
-    vnew[tid] = vx[tid];
-    if (h % g == 0 && pos < a.max_len) {
-      kt[(int64_t)tid * a.max_len + pos] = kr;
-      vc[pos * kHD + tid] = vx[tid];
+    const half_t k1 = rope_elem(kx, tid, ang);
+    const half_t v1 = vx[tid];
+    knew[tid] = k1;
+    vnew[tid] = v1;
+    if (h % g == 0 && pos_ok) {
+      kt[(int64_t)tid * L + npos] = k1;
+      vc[(int64_t)npos * kHD + tid] = v1;
     }
   }
-  __syncthreads();
+  ldk::lds_barrier();
 
-  // ---- scores: lane = position t; the new token's k comes from LDS
-  const int t = wave * 64 + lane;
-  const bool live = t <= pos && t < a.max_len;
-  float s = -__builtin_inff();
-  if (live) {
-    float acc = 0.0f;
-    if (t == pos) {
-#pragma unroll 8
-      for (int d = 0; d < kHD; ++d) acc = __builtin_fmaf(qs[d], (float)knew[d], acc);
-    } else {
-      const half_t* kc = kt + t;
-#pragma unroll 16
-      for (int d = 0; d < kHD; ++d) acc = __builtin_fmaf(qs[d], (float)kc[(int64_t)d * a.max_len], acc);
+  // score of the new token at pos (the cache row there is stale): q . knew, over the wave
+  float s_new = 0.0f;
+  if (pos_ok) {
+    s_new = qs[lane] * (float)knew[lane] + qs[lane + 64] * (float)knew[lane + 64];
+    s_new = ldk::sum_lanes_strided<1>(s_new) * a.scale;
+  }
+  half2_t qp[8];  // (q[dg + 16r], q[dg + 16r + 8]): the roped q is exactly fp16
+#pragma unroll
+  for (int r = 0; r < 8; ++r) qp[r] = half2_t{(half_t)qs[dg + 16 * r], (half_t)qs[dg + 16 * r + 8]};
+
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+
+  for (; c0 <= pos; c0 += nw * kChunk) {
+    // ---- partial scores for positions c0 + 8pg + j over rows dg + 8i: rows 2r and 2r+1 are
+    // paired with v_perm_b32 and meet the q pair in one v_dot2_f32_f16
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t a0 = kr[2 * r][j], a1 = kr[2 * r + 1][j];
+        s[2 * j] = __builtin_amdgcn_fdot2(qp[r], ldk::u2h2(perm_lo(a0, a1)), s[2 * j], false);
+        s[2 * j + 1] = __builtin_amdgcn_fdot2(qp[r], ldk::u2h2(perm_hi(a0, a1)), s[2 * j + 1], false);
+      }
     }
-    s = acc * a.scale;
-  }
-  // ---- softmax over live positions
-  float m = s;
+    float mloc = -__builtin_inff();
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if (lane == 0) wred[wave] = m;
-  __syncthreads();
-  m = wred[0];
-  for (int i = 1; i < nw; ++i) m = fmaxf(m, wred[i]);
-  const float p = live ? __expf(s - m) : 0.0f;
-  float l = p;
+    for (int j = 0; j < 8; ++j) {
+      const int p = c0 + 8 * pg + j;
+      float sj = ldk::sum_lanes_strided<8>(s[j]) * a.scale;
+      if (pos_ok && p == npos) sj = s_new;
+      s[j] = p <= pos ? sj : -__builtin_inff();
+      mloc = fmaxf(mloc, s[j]);
+    }
+    const float mc = row_max16(mloc);  // chunk max (position c0 is live, so finite)
+    const float m_new = fmaxf(m_run, mc);
+    const float alpha = __expf(m_run - m_new);
+    float lsum = 0.0f;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-  __syncthreads();  // everyone has read wred
-  if (lane == 0) wred[wave] = l;
-  ps[t] = p;
-  __syncthreads();
-  l = 0.0f;
-  for (int i = 0; i < nw; ++i) l += wred[i];
-
-  // ---- out[d] = sum_t p[t] v[t][d] / l: lane = dims 2*lane, 2*lane+1; wave = its positions
-  float o0 = 0.0f, o1 = 0.0f;
-  const int t0 = wave * 64;
-  const int t1 = (int)min<int64_t>(min(t0 + 64, a.max_len), pos + 1);
-  for (int tt = t0; tt < t1; ++tt) {
-    const float pw = ps[tt];
-    half2_t v2;
-    if (tt == pos) v2 = half2_t{vnew[2 * lane], vnew[2 * lane + 1]};
-    else v2 = *reinterpret_cast<const half2_t*>(vc + (int64_t)tt * kHD + 2 * lane);
-    o0 = __builtin_fmaf(pw, (float)v2[0], o0);
-    o1 = __builtin_fmaf(pw, (float)v2[1], o1);
+    for (int j = 0; j < 8; ++j) {
+      s[j] = __expf(s[j] - m_new);  // 0 for masked positions
+      lsum += s[j];
+    }
+    l_run = l_run * alpha + row_sum16(lsum) * 0.5f;  // the row holds every pg twice
+    m_run = m_new;
+    if (dg == 0) {
+      *reinterpret_cast<float4_t*>(&pw[wave][8 * pg]) = float4_t{s[0], s[1], s[2], s[3]};
+      *reinterpret_cast<float4_t*>(&pw[wave][8 * pg + 4]) = float4_t{s[4], s[5], s[6], s[7]};
+    }
+    ldk::wave_lds_sync();
+    // ---- weighted V rows 16pr + i, dims 8dc + e: the weights are rounded to fp16 (the
+    // reference's softmax(...).to(fp16)), rows 2r and 2r+1 paired for v_dot2_f32_f16. The new
+    // token's row comes from vnew.
+    float pv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4_t t = *reinterpret_cast<const float4_t*>(&pw[wave][16 * pr + i]);
+      pv[i] = t[0];
+      pv[i + 1] = t[1];
+      pv[i + 2] = t[2];
+      pv[i + 3] = t[3];
+    }
+    float p_new = 0.0f;
+    if (pos_ok && npos >= c0 && npos < c0 + kChunk) {
+      const int off = npos - c0;
+      p_new = (float)(half_t)pw[wave][off];  // uniform
+      if ((off >> 4) == pr) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i == (off & 15)) pv[i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= alpha;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const half2_t pp = {(half_t)pv[2 * r], (half_t)pv[2 * r + 1]};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t a0 = vr[2 * r][j], a1 = vr[2 * r + 1][j];
+        o[2 * j] = __builtin_amdgcn_fdot2(pp, ldk::u2h2(perm_lo(a0, a1)), o[2 * j], false);
+        o[2 * j + 1] = __builtin_amdgcn_fdot2(pp, ldk::u2h2(perm_hi(a0, a1)), o[2 * j + 1], false);
+      }
+    }
+    if (p_new != 0.0f && pr == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(p_new, (float)vnew[8 * dc + e], o[e]);
+    }
+    ldk::wave_lds_sync();  // pw is rewritten by the next chunk
+    if (c0 + nw * kChunk <= pos) issue(c0 + nw * kChunk);
   }
-  ored[wave][2 * lane] = o0;
-  ored[wave][2 * lane + 1] = o1;
-  __syncthreads();
+  // ---- lanes sharing dc hold parts of the same 8 outputs: sum over pr
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = ldk::sum_lanes_strided<16>(o[e]);
+  if (pr == 0) {
+    *reinterpret_cast<float4_t*>(&ow[wave][8 * dc]) = float4_t{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<float4_t*>(&ow[wave][8 * dc + 4]) = float4_t{o[4], o[5], o[6], o[7]};
+  }
+  if (lane == 0) {
+    mw[wave] = m_run;
+    lw[wave] = l_run;
+  }
+  ldk::lds_barrier();
   if (tid < kHD) {
-    float o = 0.0f;
-    for (int i = 0; i < nw; ++i) o += ored[i][tid];
-    a.out[(int64_t)h * kHD + tid] = (half_t)(o / l);
+    float M = -__builtin_inff();
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, mw[w]);
+    float l = 0.0f, acc = 0.0f;
+    for (int w = 0; w < nw; ++w) {
+      const float f = mw[w] == -__builtin_inff() ? 0.0f : __expf(mw[w] - M);
+      l = __builtin_fmaf(lw[w], f, l);
+      acc = __builtin_fmaf(ow[w][tid], f, acc);
+    }
+    a.out[(int64_t)h * kHD + tid] = (half_t)(l > 0.0f ? acc / l : 0.0f);
   }
 }
 
@@ -139,13 +265,15 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
   if (!qkv || !pos || !inv_freq || !kt_cache || !v_cache || !out) return ldk::fail(LDK_ERR_INVALID, "decode_attention: null pointer");
   if (head_dim != kHD) return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention: head_dim=%d (only 128)", head_dim);
   if (nq <= 0 || nkv <= 0 || nq % nkv) return ldk::fail(LDK_ERR_INVALID, "decode_attention: nq=%d must be a positive multiple of nkv=%d", nq, nkv);
-  if (max_len <= 0 || max_len > kMaxWaves * 64)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention: max_len=%lld outside 1..%d", (long long)max_len, kMaxWaves * 64);
-  if (!ldk::aligned(v_cache, 4) || !ldk::aligned(pos, 8))
-    return ldk::fail(LDK_ERR_ALIGN, "decode_attention: v_cache 4-byte and pos 8-byte aligned");
+  if (max_len < 8 || max_len > kMaxLen || max_len % 8)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention: max_len=%lld must be a multiple of 8 in 8..%lld",
+                     (long long)max_len, (long long)kMaxLen);
+  if (!ldk::aligned(kt_cache, 16) || !ldk::aligned(v_cache, 16) || !ldk::aligned(pos, 8))
+    return ldk::fail(LDK_ERR_ALIGN, "decode_attention: kt_cache and v_cache 16-byte, pos 8-byte aligned");
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)kt_cache, (half_t*)v_cache, (half_t*)out,
                    nq, nkv, (int)max_len, scale};
-  const int nw = (int)std::max<int64_t>(2, (max_len + 63) / 64);  // >= 128 threads: one per dim
+  // >= 128 threads (one per dim for RoPE and the output), one wave per 64-position chunk up to 8
+  const int nw = (int)std::min<int64_t>(kMaxWaves, std::max<int64_t>(2, (max_len + kChunk - 1) / kChunk));
   (void)hipGetLastError();
   decode_attention_kernel<<<nq, nw * 64, 0, (hipStream_t)stream>>>(a);
   return ldk::check_launch("decode_attention");

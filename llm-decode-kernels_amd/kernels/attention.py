@@ -12,12 +12,15 @@ import torch
 
 from kernels import _lib
 
-MAX_LEN = 512
+MAX_LEN = 1 << 20
 HEAD_DIM = 128
 
 
 def supported(head_dim: int, max_len: int, batch: int, tokens: int) -> bool:
-    return head_dim == HEAD_DIM and max_len <= MAX_LEN and batch == 1 and tokens == 1
+    """The kernel's domain: head_dim 128, one token of one sequence, and a cache length that is a
+    multiple of 8 (its K^T rows are read 8 positions per 16-byte load)."""
+    return (head_dim == HEAD_DIM and 8 <= max_len <= MAX_LEN and max_len % 8 == 0 and batch == 1
+            and tokens == 1)
 
 
 def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tensor,

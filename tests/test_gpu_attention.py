@@ -23,7 +23,9 @@ def _rope64(x, pos, inv_freq):
 
 
 @pytest.mark.parametrize("nq,nkv,L,pos", [(12, 2, 392, 0), (12, 2, 392, 127), (12, 2, 392, 383),
-                                          (4, 4, 64, 63), (8, 1, 512, 511), (16, 2, 130, 64)])
+                                          (12, 2, 392, 391), (12, 2, 392, 320), (4, 4, 64, 63),
+                                          (8, 1, 512, 511), (16, 2, 136, 64), (12, 2, 8, 5),
+                                          (12, 2, 2048, 1500), (12, 2, 4096, 4095)])
 def test_against_float64(nq, nkv, L, pos):
     g = torch.Generator().manual_seed(pos + 7 * nq)
     hd = 128
@@ -64,8 +66,22 @@ def test_against_float64(nq, nkv, L, pos):
 
 def test_rejects_unsupported_shapes():
     qkv = torch.zeros(16 * 128, dtype=torch.float16, device="cuda")
-    kt = torch.zeros(1, 2, 128, 600, dtype=torch.float16, device="cuda")
-    vc = torch.zeros(1, 2, 600, 128, dtype=torch.float16, device="cuda")
+    kt = torch.zeros(1, 2, 128, 602, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(1, 2, 602, 128, dtype=torch.float16, device="cuda")
     inv = torch.ones(64, device="cuda")
-    with pytest.raises(RuntimeError):  # max_len 600 > 512
+    with pytest.raises(RuntimeError):  # max_len 602 is not a multiple of 8
         decode_attention(qkv, torch.tensor([0], device="cuda"), inv, kt, vc, 12, 2, 1.0)
+
+
+def test_pos_past_the_cache_writes_nothing():
+    """pos >= max_len: attention over the whole cache, the cache is left as it was."""
+    nq, nkv, L, hd = 12, 2, 64, 128
+    g = torch.Generator().manual_seed(3)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda()
+    kt = (torch.randn(1, nkv, hd, L, generator=g) * 0.7).half().cuda()
+    vc = torch.randn(1, nkv, L, hd, generator=g).half().cuda()
+    kt0, vc0 = kt.clone(), vc.clone()
+    inv = torch.ones(64, device="cuda")
+    out = decode_attention(qkv, torch.tensor([L], device="cuda"), inv, kt, vc, nq, nkv, hd ** -0.5)
+    assert torch.equal(kt, kt0) and torch.equal(vc, vc0)
+    assert torch.isfinite(out).all()

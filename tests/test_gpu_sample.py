@@ -41,6 +41,26 @@ def test_ties_take_the_lowest_index_and_nan_wins():
     assert int(pos) == 5 and int(out[4]) == 5000
 
 
+def test_signed_zeros_tie_and_negative_nan_wins():
+    x = torch.full((20000,), -1.0, dtype=torch.float32)
+    x[11] = -0.0
+    x[19000] = 0.0
+    tok, pos, out = _state()
+    greedy_step(x.cuda(), tok, pos, out)
+    assert int(tok) == 11 == int(x.argmax())
+    x[15000] = -float("nan")
+    greedy_step(x.cuda(), tok, pos, out)
+    assert int(tok) == 15000 == int(x.argmax())
+
+
+def test_unaligned_row_takes_the_scalar_path():
+    base = torch.randn(151937, dtype=torch.float16, device="cuda")
+    row = base[1:]  # 2-byte offset: not 16-byte aligned
+    tok, pos, out = _state()
+    greedy_step(row, tok, pos, out)
+    assert int(tok) == int(row.float().argmax())
+
+
 def test_pos_outside_the_log_skips_the_write():
     tok, pos, out = _state(L=4, p=4)
     greedy_step(torch.arange(10, dtype=torch.float16, device="cuda"), tok, pos, out)
