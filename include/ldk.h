@@ -114,6 +114,31 @@ int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const v
 int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n,
                      int* split_k, int* flags);
 
+/* Fused decode entries (M = 1, group_size 128). Each forms the activation row inside the W4A16
+ * kernel's x staging instead of in a kernel of its own, one launch fewer per use. Same
+ * qweight/scales/zeros/bias/out/workspace rules as ldk_w4a16_matmul.
+ *
+ * out [1, N] = rmsnorm(x (+ residual)) @ dequant(W)^T (+ bias) with x [K]: h = x (+ residual, fp16
+ * add, written to residual_out); the activation is norm_weight * fp16(h * rsqrt(mean(h^2) + eps))
+ * with the steps of ldk_rmsnorm. residual/residual_out both NULL or both set; residual_out must
+ * not alias x or residual. Replaces the pair rmsnorm (kernels/rmsnorm.py:44-68) + w4a16_matmul
+ * (kernels/w4a16.py:301-330) that the reference's OursBackend runs as norm then linear
+ * (kernels/e2e/model.py:79-97). */
+int ldk_w4a16_rmsnorm_matmul(const void* x, const void* residual, void* residual_out,
+                             const void* norm_weight, float eps, const int32_t* qweight,
+                             const void* scales, const void* zeros, const void* bias, void* out,
+                             int64_t N, int64_t K, int group_size, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
+/* out [1, N] = swiglu(gate_up) @ dequant(W)^T (+ bias) with gate_up [2K] = [gate | up]: the
+ * activation is fp16(silu(gate)) * up, bit-identical to ldk_swiglu. Replaces the pair
+ * swiglu_fused (kernels/swiglu.py:56-61) + w4a16_matmul (kernels/w4a16.py:301-330) of the
+ * reference's OursBackend act then linear (kernels/e2e/model.py:79-97). */
+int ldk_w4a16_swiglu_matmul(const void* gate_up, const int32_t* qweight, const void* scales,
+                            const void* zeros, const void* bias, void* out, int64_t N, int64_t K,
+                            int group_size, void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
 /* ----------------------------------------------------------------------------- FP8 (W8A16) */
 
 /* Per-output-channel OCP e4m3 quantization of w [N, K] (dtype F16/BF16/F32): writes wq [K, N]
@@ -161,7 +186,9 @@ int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void*
  *   inv_freq: [head_dim/2] fp32 RoPE inverse frequencies;
  *   kt_cache: fp16 [nkv][head_dim][max_len] (K transposed), v_cache: fp16 [nkv][max_len][head_dim];
  *   out:      [nq*head_dim] fp16; scale: the softmax scale (head_dim^-0.5).
- * head_dim == 128, nq % nkv == 0, max_len <= 512. Replaces the per-layer attention of the
+ * head_dim == 128, nq % nkv == 0, max_len a multiple of 8 (kt_cache and v_cache 16-byte
+ * aligned). A *pos outside 0..max_len-1 writes nothing and attends over the whole cache.
+ * Replaces the per-layer attention of the
  * reference's runner for decode steps (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into
  * the cache, scaled_dot_product_attention with the causal mask). */
 int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* kt_cache,
@@ -172,7 +199,8 @@ int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_f
 
 /* idx = argmax(logits[0:V]) (torch.argmax order: NaN largest, lowest index on ties), then
  * out[*pos] = idx when 0 <= *pos < out_len (out may be NULL), *tok = idx, *pos += 1; one launch,
- * no memset, no cross-workgroup state, so it replays safely inside a hipGraph. logits dtype
+ * no memset. Its workgroups meet in library-owned device state that the launch leaves zeroed,
+ * so it replays safely inside a hipGraph; calls on one device must be stream-ordered. logits dtype
  * LDK_F16/BF16/F32; tok, out and pos are int64 device pointers. Replaces the greedy step of
  * kernels/e2e/run.py:69-74 (argmax, out.index_copy_, tok.copy_, pos.add_). */
 int ldk_greedy_step(const void* logits, int dtype, int64_t V, int64_t* tok, int64_t* out,

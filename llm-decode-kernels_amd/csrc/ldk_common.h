@@ -41,6 +41,16 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return x * q + (x < rem ? x : rem) + b / kXcd;
 }
 
+// Buffer resource over [p, p + bytes) (gfx9 raw-buffer word 3): a raw buffer load at a byte
+// offset outside it returns zero and makes no memory request, so a load that only some lanes
+// need is issued unconditionally, with no branch for the compiler to wait at.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
+}
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ half2_t u2h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }

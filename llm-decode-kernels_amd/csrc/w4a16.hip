@@ -151,11 +151,68 @@ __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, con
 // workgroup's groups at a stride of NW * GPW groups.
 // RSH > 0 fixes log2(rows per group) at compile time (the common group size 128 has RSH = 4);
 // RSH = 0 reads it from the arguments.
-template <int LN, int NW, int RSH>
-__global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec) {
+//
+// PRO selects how the activation row is formed while it is staged (each x row of a pass is read
+// by one lane, so an elementwise prologue costs one evaluation per element per workgroup):
+//  - kProNone: x as given;
+//  - kProRms / kProRmsRes: x = rmsnorm(x (+ residual)) * weight with the rounding steps of the
+//    standalone RMSNorm kernel (h = fp16(x + r), fp32 mean of squares, w * fp16(h * rstd)).
+//    The row statistic is reduced once per workgroup (wave sums, one LDS barrier). In the
+//    EXACT variants (kProRmsX, kProRmsResX: whole tiles and one pass per wave covering the
+//    row, which every decode shape is) each wave sums the rows its pass staged anyway, so no
+//    load is added and the barrier waits only for the pass's first (x, residual) loads, not for
+//    its weight rows. The general variants also load the row (tid, tid + NT, ...) ahead of the
+//    pass, as buffer loads that read zero past the row without a branch. Workgroup 0 writes h,
+//    the updated residual stream, to res_out;
+//  - kProSwiglu: x = fp16(silu(g)) * u from a fused [g | u] row of 2K (the standalone SwiGLU
+//    kernel's steps, so the staged values are bit-identical to its output).
+enum Prologue { kProNone = 0, kProRms = 1, kProRmsRes = 2, kProSwiglu = 3, kProRmsX = 4, kProRmsResX = 5 };
+
+struct ProArgs {
+  const half_t* res;  // kProRmsRes: residual added before the norm
+  half_t* res_out;    // kProRmsRes: x + residual (written by workgroup 0)
+  const half_t* nw;   // kProRms*: norm weight [K]
+  float eps;
+};
+
+// The staged 8 activations of one packed row from the raw loads (x, second operand, norm weight).
+template <int PRO>
+__device__ __forceinline__ u32x4 pro_stage(u32x4 xr, u32x4 x2, u32x4 x3, float rs) {
+  if constexpr (PRO == kProNone) {
+    return xr;
+  } else if constexpr (PRO == kProSwiglu) {
+    const half8_t g = __builtin_bit_cast(half8_t, xr), u = __builtin_bit_cast(half8_t, x2);
+    half8_t sv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (float)g[j];
+      sv[j] = (half_t)(f / (1.0f + expf(-f)));
+    }
+    return __builtin_bit_cast(u32x4, sv * u);  // fp16 multiply
+  } else {
+    half8_t h = __builtin_bit_cast(half8_t, xr);
+    if constexpr (PRO == kProRmsRes || PRO == kProRmsResX) h = h + __builtin_bit_cast(half8_t, x2);  // fp16 add
+    half8_t o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v = (float)h[j] * rs;
+      asm volatile("" : "+v"(v));  // a -0 * rs must stay -0 (no v_fma_mix with a +0 addend)
+      o[j] = (half_t)v;
+    }
+    return __builtin_bit_cast(u32x4, __builtin_bit_cast(half8_t, x3) * o);  // fp16 multiply
+  }
+}
+
+template <int LN, int NW, int RSH, int PRO>
+__global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
   constexpr int LKW = 64 / LN, RPL = 4, RPW = RPL * LKW, CW = 4 * LN;
+  constexpr bool kExact = PRO == kProRmsX || PRO == kProRmsResX;
+  constexpr bool kRes = PRO == kProRmsRes || PRO == kProRmsResX;
+  constexpr bool kRms = kExact || PRO == kProRms || PRO == kProRmsRes;
+  constexpr int kStatV = 2;  // row vectors per thread loaded ahead of the pass (general variants)
   __shared__ __align__(16) unsigned char xrec[NW][RPW][32];
   __shared__ __align__(16) float4_t red[NW][LN];
+  __shared__ float stat[NW];
   const int rsh = RSH ? RSH : a.gsh_rows;  // log2(packed rows per group), >= 2
   const int lgsh = rsh - 2;    // log2(LG)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -174,24 +231,130 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
   // (the other waves find no pass in the loop below and leave after it).
   const bool one_wave = !whole && ge - gb <= gpw;
 
-  const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
-  const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int gp = gb + wave * gpw; gp < ge; gp += NW * gpw) {
-    const int row0 = gp << rsh;
-    const u32x4 xr = *reinterpret_cast<const u32x4*>(a.x + 8 * min(row0 + lane, R - 1));
-    const int g = min(gp + gi, ge - 1);  // clamped; such lanes are masked out below
-    const u32x2 sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
-    const u32x2 zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
+  // ---- loads of one pass, in consumption order: x row(s), scale and zero words, weight rows
+  struct Pass {
+    u32x4 xr, x2, x3;
+    u32x2 sv, zv;
     u32x4 w[RPL];
+  };
+  auto load_pass = [&](int gp, Pass& P) {
+    const int xo = 8 * min((gp << rsh) + lane, R - 1);
+    P.xr = *reinterpret_cast<const u32x4*>(a.x + xo);
+    if constexpr (kRes) P.x2 = *reinterpret_cast<const u32x4*>(pa.res + xo);
+    if constexpr (PRO == kProSwiglu) P.x2 = *reinterpret_cast<const u32x4*>(a.x + a.K + xo);
+    if constexpr (kRms) P.x3 = *reinterpret_cast<const u32x4*>(pa.nw + xo);
+    const int g = min(gp + gi, ge - 1);  // clamped; such lanes are masked out below
+    P.sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
+    P.zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
 #pragma unroll
     for (int t = 0; t < RPL; ++t) {
       const int r = (g << rsh) + sub + (t << lgsh);
-      w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
+      P.w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
     }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
+  };
+  // The general RMSNorm variants wait for the row statistic's loads before their barrier. They
+  // issue their first pass with buffer loads from every wave, with an out-of-range offset where
+  // the wave has no pass (zeros, no request): the load count is then the same on every path, so
+  // that wait covers the statistic's loads only.
+  auto load_pass_buf = [&](int gp, bool live, Pass& P) {
+    constexpr uint32_t kOut = 0x80000000u;  // past every resource below (each < 2 GiB)
+    const auto xb = ldk::buffer_rsrc(a.x, (uint32_t)a.K * 2u);
+    const auto rb = ldk::buffer_rsrc(pa.res, kRes ? (uint32_t)a.K * 2u : 0u);
+    const auto nb = ldk::buffer_rsrc(pa.nw, (uint32_t)a.K * 2u);
+    const auto sb = ldk::buffer_rsrc(a.s, (uint32_t)ng * (uint32_t)a.N * 2u);
+    const auto zb = ldk::buffer_rsrc(a.z, (uint32_t)ng * (uint32_t)a.N * 2u);
+    const auto wb = ldk::buffer_rsrc(a.qw, (uint32_t)R * (uint32_t)a.N * 4u);
+    // a dead wave ORs kOut into every offset (a VALU op; a select on the uniform flag would
+    // become a branch around the loads)
+    const uint32_t dead = ldk::vgpr_const<0>() | (live ? 0u : kOut);
+    const uint32_t xo = (16u * (uint32_t)min((gp << rsh) + lane, R - 1)) | dead;
+    P.xr = ldk::buffer_load16(xb, xo);
+    if constexpr (kRes) P.x2 = ldk::buffer_load16(rb, xo);
+    P.x3 = ldk::buffer_load16(nb, xo);
+    const int g = min(gp + gi, ge - 1);
+    const uint32_t so = (2u * (uint32_t)(g * a.N + col)) | dead;
+    P.sv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sb, so, 0, 0));
+    P.zv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(zb, so, 0, 0));
+#pragma unroll
+    for (int t = 0; t < RPL; ++t) {
+      const int r = (g << rsh) + sub + (t << lgsh);
+      const uint32_t wo = (4u * (uint32_t)(r * a.N + col)) | dead;
+      P.w[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wb, wo, 0, 2));  // nt
+    }
+  };
 
-    if (lane < RPW) store_fact_record(&xrec[wave][lane][0], xr);
+  // ---- general RMSNorm variants: row vectors tid, tid + NT, ... for the statistic, first
+  u32x4 sx[kStatV], sr[kStatV];
+  if constexpr (kRms && !kExact) {
+    const auto xb = ldk::buffer_rsrc(a.x, (uint32_t)a.K * 2u);
+    const auto rb = ldk::buffer_rsrc(pa.res, kRes ? (uint32_t)a.K * 2u : 0u);
+#pragma unroll
+    for (int i = 0; i < kStatV; ++i) {
+      const uint32_t off = 16u * (threadIdx.x + i * NW * 64);
+      sx[i] = ldk::buffer_load16(xb, off);
+      if constexpr (kRes) sr[i] = ldk::buffer_load16(rb, off);
+    }
+  }
+  int gp = gb + wave * gpw;
+  Pass P;
+  if constexpr (kExact) {
+    load_pass(gp, P);  // every wave has exactly one pass
+  } else if constexpr (kRms) {
+    load_pass_buf(gp, gp < ge, P);
+  } else {
+    if (gp < ge) load_pass(gp, P);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
+
+  float rs = 0.0f;
+  if constexpr (kRms) {
+    float ss = 0.0f;
+    const bool wr = kRes && blockIdx.x == 0;
+    if constexpr (kExact) {  // this wave's pass rows, lanes < RPW
+      if (lane < RPW) {
+        half8_t h = __builtin_bit_cast(half8_t, P.xr);
+        if constexpr (kRes) h = h + __builtin_bit_cast(half8_t, P.x2);
+        if (wr) *reinterpret_cast<half8_t*>(pa.res_out + 8 * ((gp << rsh) + lane)) = h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf((float)h[j], (float)h[j], ss);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kStatV; ++i) {  // lanes past the row hold zeros
+        half8_t h = __builtin_bit_cast(half8_t, sx[i]);
+        if constexpr (kRes) h = h + __builtin_bit_cast(half8_t, sr[i]);
+        const int t = threadIdx.x + i * NW * 64;
+        if (wr && t < R) *reinterpret_cast<half8_t*>(pa.res_out + 8 * t) = h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf((float)h[j], (float)h[j], ss);
+      }
+      for (int t = threadIdx.x + kStatV * NW * 64; t < R; t += NW * 64) {  // rows beyond kStatV per thread
+        half8_t h = *reinterpret_cast<const half8_t*>(a.x + 8 * t);
+        if constexpr (kRes) h = h + *reinterpret_cast<const half8_t*>(pa.res + 8 * t);
+        if (wr) *reinterpret_cast<half8_t*>(pa.res_out + 8 * t) = h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf((float)h[j], (float)h[j], ss);
+      }
+    }
+    ss = ldk::sum_lanes_strided<1>(ss);
+    if (lane == 0) stat[wave] = ss;
+    ldk::lds_barrier();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += stat[w];
+    rs = 1.0f / __builtin_sqrtf(tot / (float)a.K + pa.eps);
+  }
+
+  const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
+  const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (bool first = true; gp < ge; gp += NW * gpw, first = false) {
+    if (!first) {
+      if constexpr (kRms && !kExact) load_pass_buf(gp, true, P);
+      else load_pass(gp, P);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (lane < RPW) store_fact_record(&xrec[wave][lane][0], pro_stage<PRO>(P.xr, P.x2, P.x3, rs));
     ldk::wave_lds_sync();
     u32x4 xp[RPL];
     float c0 = 0.0f, xs = 0.0f;
@@ -208,7 +371,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
     for (int t = 0; t < RPL; ++t) {  // rows in arrival order
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t wc = w[t][q], v = wc >> 8;
+        const uint32_t wc = P.w[t][q], v = wc >> 8;
         tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][3]), ldk::u2h2((v & mhi) | magic), tt[q], false);
         tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][2]), ldk::u2h2((v & mlo) | magic), tt[q], false);
         tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][1]), ldk::u2h2((wc & mhi) | magic), tt[q], false);
@@ -216,7 +379,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
       }
     }
     const bool gok = gp + gi < ge;
-    const half4_t s4 = __builtin_bit_cast(half4_t, sv), z4 = __builtin_bit_cast(half4_t, zv);
+    const half4_t s4 = __builtin_bit_cast(half4_t, P.sv), z4 = __builtin_bit_cast(half4_t, P.zv);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {  // s * (sum x*q - z * sum x)
       const float v = (float)s4[q] * __builtin_fmaf(-(float)z4[q], xs, tt[q]);
@@ -681,29 +844,51 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
 }
 
 template <int LN, int NW>
-int launch_m1_t(const W4Args& a, const SplitArgs& sp, hipStream_t stream) {
-  const int64_t tiles = (a.N + 4 * LN - 1) / (4 * LN);
+int launch_m1_t(const W4Args& a, const SplitArgs& sp, int pro, const ProArgs& pa, hipStream_t stream) {
   const int out_vec = ldk::aligned(a.out, 8) ? 1 : 0;
   const unsigned grid = (unsigned)(sp.full + sp.nsplit);
+  if (pro != kProNone) {
+    // fused prologues are built for the decode tile widths and group size 128
+    if constexpr (LN == 4 || LN == 8) {
+      if (a.gsh_rows != 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues need group_size 128");
+      (void)hipGetLastError();
+      // exact: whole tiles, and one wave pass per wave covers the row
+      const int gpw = (64 / LN) >> (a.gsh_rows - 2);
+      const bool exact = sp.splits == 1 && sp.full == 0 && ((a.K >> 3) >> a.gsh_rows) == NW * gpw;
+      if (exact && pro == kProRms) pro = kProRmsX;
+      if (exact && pro == kProRmsRes) pro = kProRmsResX;
+      switch (pro) {
+        case kProRms: w4a16_m1_kernel<LN, NW, 4, kProRms><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsRes: w4a16_m1_kernel<LN, NW, 4, kProRmsRes><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsX: w4a16_m1_kernel<LN, NW, 4, kProRmsX><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsResX: w4a16_m1_kernel<LN, NW, 4, kProRmsResX><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProSwiglu: w4a16_m1_kernel<LN, NW, 4, kProSwiglu><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        default: return ldk::fail(LDK_ERR_INVALID, "w4a16: unknown prologue %d", pro);
+      }
+      return ldk::check_launch("w4a16_m1");
+    } else {
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues take block_n 16 or 32");
+    }
+  }
   (void)hipGetLastError();
   if (a.gsh_rows == 4)
-    w4a16_m1_kernel<LN, NW, 4><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec);
+    w4a16_m1_kernel<LN, NW, 4, kProNone><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa);
   else
-    w4a16_m1_kernel<LN, NW, 0><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec);
+    w4a16_m1_kernel<LN, NW, 0, kProNone><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa);
   return ldk::check_launch("w4a16_m1");
 }
 
 template <int LN>
-int launch_m1_ln(const W4Args& a, const SplitArgs& sp, int nw, hipStream_t s) {
+int launch_m1_ln(const W4Args& a, const SplitArgs& sp, int nw, int pro, const ProArgs& pa, hipStream_t s) {
   switch (nw) {
-    case 1: return launch_m1_t<LN, 1>(a, sp, s);
-    case 2: return launch_m1_t<LN, 2>(a, sp, s);
-    case 3: return launch_m1_t<LN, 3>(a, sp, s);
-    case 4: return launch_m1_t<LN, 4>(a, sp, s);
-    case 6: return launch_m1_t<LN, 6>(a, sp, s);
-    case 8: return launch_m1_t<LN, 8>(a, sp, s);
-    case 12: return launch_m1_t<LN, 12>(a, sp, s);
-    case 16: return launch_m1_t<LN, 16>(a, sp, s);
+    case 1: return launch_m1_t<LN, 1>(a, sp, pro, pa, s);
+    case 2: return launch_m1_t<LN, 2>(a, sp, pro, pa, s);
+    case 3: return launch_m1_t<LN, 3>(a, sp, pro, pa, s);
+    case 4: return launch_m1_t<LN, 4>(a, sp, pro, pa, s);
+    case 6: return launch_m1_t<LN, 6>(a, sp, pro, pa, s);
+    case 8: return launch_m1_t<LN, 8>(a, sp, pro, pa, s);
+    case 12: return launch_m1_t<LN, 12>(a, sp, pro, pa, s);
+    case 16: return launch_m1_t<LN, 16>(a, sp, pro, pa, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %d waves per workgroup not instantiated", nw);
 }
@@ -765,7 +950,8 @@ int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
   return ldk::check_launch("w4a16_mfma16");
 }
 
-int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
+int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro = kProNone,
+                const ProArgs& pa = ProArgs{}) {
   const int64_t tiles = (a.N + plan_cw(p) - 1) / plan_cw(p);
   const SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr, p.full,
                      (int)((tiles - p.full) * p.splits), div_magic(p.splits)};
@@ -779,12 +965,13 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s) {
       return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d too wide for group_size %d on the M = 1 kernel",
                        4 * p.ln, 8 << a.gsh_rows);
     switch (p.ln) {
-      case 4: return launch_m1_ln<4>(a, sp, p.nw, s);
-      case 8: return launch_m1_ln<8>(a, sp, p.nw, s);
-      case 16: return launch_m1_ln<16>(a, sp, p.nw, s);
+      case 4: return launch_m1_ln<4>(a, sp, p.nw, pro, pa, s);
+      case 8: return launch_m1_ln<8>(a, sp, p.nw, pro, pa, s);
+      case 16: return launch_m1_ln<16>(a, sp, p.nw, pro, pa, s);
     }
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
   }
+  if (pro != kProNone) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues run on the M = 1 kernel");
   if (p.kern == kMfma) {
     const bool two = p.cpw == 2;
     switch (1 << a.gsh_rows) {
@@ -885,4 +1072,50 @@ extern "C" int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweig
   if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_decode: M=%lld > 16 rows", (long long)M);
   return ldk_w4a16_matmul(x, ldx, qweight, scales, zeros, bias, out, ldo, M, N, K, group_size, 0, split_k, 0,
                           workspace, workspace_bytes, stream);
+}
+
+// Fused decode entries (M = 1): the activation row is formed inside the W4A16 kernel's x staging,
+// which removes one launch each from a decode layer (the reference runs rmsnorm and swiglu as
+// kernels of their own, kernels/e2e/model.py:79-97).
+
+extern "C" int ldk_w4a16_rmsnorm_matmul(const void* x, const void* residual, void* residual_out, const void* norm_weight,
+                                        float eps, const int32_t* qweight, const void* scales, const void* zeros,
+                                        const void* bias, void* out, int64_t N, int64_t K, int group_size,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  int gsh_rows = 0;
+  int st = validate("w4a16_rmsnorm_matmul", x, K, qweight, scales, zeros, out, N, 1, N, K, group_size, &gsh_rows);
+  if (st) return st;
+  if (!norm_weight) return ldk::fail(LDK_ERR_INVALID, "w4a16_rmsnorm_matmul: null norm_weight");
+  if ((residual == nullptr) != (residual_out == nullptr))
+    return ldk::fail(LDK_ERR_INVALID, "w4a16_rmsnorm_matmul: residual and residual_out must both be given or both be null");
+  if (residual && (residual == residual_out || x == residual_out))
+    return ldk::fail(LDK_ERR_INVALID, "w4a16_rmsnorm_matmul: residual_out must not alias x or residual");
+  if (!ldk::aligned(norm_weight, 16) || (residual && (!ldk::aligned(residual, 16) || !ldk::aligned(residual_out, 16))))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_rmsnorm_matmul: norm_weight, residual and residual_out must be 16-byte aligned");
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_rmsnorm_matmul: workspace must be a 256-byte aligned pointer");
+  Plan p = make_plan(1, N, K, gsh_rows, 0, 0, 0, workspace ? (size_t)workspace_bytes : 0);
+  if (p.full) {  // whole tiles: every workgroup then reads the whole row, which its statistic needs
+    p.full = 0;
+    p.splits = 1;
+    p.gps = (int)((K / 8) >> gsh_rows);
+  }
+  const W4Args a{(const half_t*)x, K, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                 (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K, gsh_rows};
+  const ProArgs pa{(const half_t*)residual, (half_t*)residual_out, (const half_t*)norm_weight, eps};
+  return launch_plan(a, p, workspace, (hipStream_t)stream, residual ? kProRmsRes : kProRms, pa);
+}
+
+extern "C" int ldk_w4a16_swiglu_matmul(const void* gate_up, const int32_t* qweight, const void* scales, const void* zeros,
+                                       const void* bias, void* out, int64_t N, int64_t K, int group_size,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  int gsh_rows = 0;
+  int st = validate("w4a16_swiglu_matmul", gate_up, 2 * K, qweight, scales, zeros, out, N, 1, N, K, group_size, &gsh_rows);
+  if (st) return st;
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_swiglu_matmul: workspace must be a 256-byte aligned pointer");
+  const Plan p = make_plan(1, N, K, gsh_rows, 0, 0, 0, workspace ? (size_t)workspace_bytes : 0);
+  const W4Args a{(const half_t*)gate_up, 2 * K, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                 (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K, gsh_rows};
+  return launch_plan(a, p, workspace, (hipStream_t)stream, kProSwiglu, ProArgs{});
 }

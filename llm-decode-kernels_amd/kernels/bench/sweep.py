@@ -11,7 +11,7 @@ one launch per set in one hipGraph, median of 7 samples) and reported as us, GB/
 8 TB/s HBM peak with the reference's algorithmic byte formulas. Each row also records the
 kernel configuration the library chose.
 
-    python -m kernels.bench.sweep [--only w4a16,fp8,norm,act] [--json out.json]
+    python -m kernels.bench.sweep [--only w4a16,fp8,norm,act,fused] [--json out.json]
 """
 
 from __future__ import annotations
@@ -117,7 +117,56 @@ def act_rows(Ms=(1, 16, 2048)):
     return rows
 
 
-SECTIONS = {"w4a16": w4a16_rows, "fp8": fp8_rows, "norm": norm_rows, "act": act_rows}
+def fused_rows():
+    """The decode layer's fused pairs against their two-launch compositions at M = 1: residual +
+    RMSNorm into the qkv (with bias) and gate_up projections, SwiGLU into the down projection.
+    Bytes: the projection's plus the activation side's (rmsnorm: x, residual, weight read and the
+    new residual written; swiglu: the [2I] row read)."""
+    from kernels.fused import rmsnorm_w4a16_matmul, swiglu_w4a16_matmul
+    from kernels.quant import quantize_rtn, weight_bytes
+    from kernels.rmsnorm import rmsnorm
+    from kernels.swiglu import swiglu_fused
+    from kernels.w4a16 import w4a16_matmul
+
+    rows = []
+    H, I = 1536, 8960
+    for name, N, K, bias in (("qkv", 2048, H, True), ("gate_up", 17920, H, False)):
+        w, _ = cases.w4a16_case(1, N, K, seed=2)
+        qw, s, z = quantize_rtn(w.cuda(), GS)
+        b = torch.zeros(N, dtype=torch.float16, device="cuda") if bias else None
+        x, r, wn = (t.cuda() for t in cases.rmsnorm_case(1, K, seed=1))
+        per = tensor_bytes((x, r, wn, qw, s, z)) + 2 * N + 2 * K
+        sets = [(x.clone(), r.clone(), wn.clone(), qw.clone(), s.clone(), z.clone())
+                for _ in range(n_copies(per))]
+        nbytes = weight_bytes(N, K, GS) + 2 * N + (2 * N if bias else 0) + 4 * K * 2 + 2 * K
+
+        def fused(xx, rr, ww, q, sc, zz):
+            return rmsnorm_w4a16_matmul(xx, ww, 1e-6, rr, q, sc, zz, GS, b)
+
+        def split(xx, rr, ww, q, sc, zz):
+            h, res = rmsnorm(xx, ww, 1e-6, residual=rr)
+            return w4a16_matmul(h, q, sc, zz, GS, b), res
+
+        for kind, fn in (("rms+w4a16", fused), ("rms,w4a16", split)):
+            rows.append(_row(kind, f"{name} {N}x{K}", 1, _time(fn, sets), nbytes))
+        del sets
+    w, _ = cases.w4a16_case(1, H, I, seed=2)
+    qw, s, z = quantize_rtn(w.cuda(), GS)
+    gu = cases.swiglu_case(1, I, seed=1).cuda()
+    per = tensor_bytes((gu, qw, s, z)) + 2 * H
+    sets = [(gu.clone(), qw.clone(), s.clone(), z.clone()) for _ in range(n_copies(per))]
+    nbytes = weight_bytes(H, I, GS) + 2 * H + 4 * I
+    rows.append(_row("swiglu+w4a16", f"down {H}x{I}", 1,
+                     _time(lambda g, q, sc, zz: swiglu_w4a16_matmul(g, q, sc, zz, GS), sets), nbytes))
+    rows.append(_row("swiglu,w4a16", f"down {H}x{I}", 1,
+                     _time(lambda g, q, sc, zz: w4a16_matmul(swiglu_fused(g), q, sc, zz, GS), sets),
+                     nbytes))
+    del sets
+    return rows
+
+
+SECTIONS = {"w4a16": w4a16_rows, "fp8": fp8_rows, "norm": norm_rows, "act": act_rows,
+            "fused": fused_rows}
 
 
 def main(argv=None) -> int:

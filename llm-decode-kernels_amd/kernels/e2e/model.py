@@ -71,6 +71,18 @@ class Backend:
         i = gate_up.shape[-1] // 2
         return F.silu(gate_up[..., :i]) * gate_up[..., i:]
 
+    def norm_linear(self, x, w, eps, residual, p: Linear):
+        """norm then linear, the order of the reference's layer (model.py:226-233): returns the
+        projection of the normalized row and the updated residual (None without one)."""
+        if residual is None:
+            return self.linear(self.norm(x, w, eps), p), None
+        h, res = self.norm(x, w, eps, residual=residual)
+        return self.linear(h, p), res
+
+    def act_linear(self, gate_up, p: Linear):
+        """act then linear (the MLP's down projection, model.py:233)."""
+        return self.linear(self.act(gate_up), p)
+
 
 class W4RefBackend(Backend):
     """RTN int4 weights dequantized once (bit-exact HIP dequantizer) then the fp16 GEMM: the same
@@ -118,6 +130,25 @@ class OursBackend(Backend):
 
         return swiglu_fused(gate_up)
 
+    def norm_linear(self, x, w, eps, residual, p: Linear):
+        """One launch at decode: the RMSNorm (+ residual) forms the activation inside the W4A16
+        kernel's x staging (kernels.fused)."""
+        if self.decode_kernel != "library":
+            return super().norm_linear(x, w, eps, residual, p)
+        from kernels.fused import rmsnorm_w4a16_matmul
+
+        return rmsnorm_w4a16_matmul(x, w, eps, residual, p.qweight, p.scales, p.zeros,
+                                    config.GROUP_SIZE, p.bias)
+
+    def act_linear(self, gate_up, p: Linear):
+        """One launch at decode: SwiGLU forms the down projection's activation (kernels.fused)."""
+        if self.decode_kernel != "library":
+            return super().act_linear(gate_up, p)
+        from kernels.fused import swiglu_w4a16_matmul
+
+        return swiglu_w4a16_matmul(gate_up, p.qweight, p.scales, p.zeros, config.GROUP_SIZE,
+                                   p.bias)
+
 
 class OursFP8Backend(OursBackend):
     """FP8 (OCP e4m3) weight-only linears with the same fused norm and activation
@@ -137,6 +168,9 @@ class OursFP8Backend(OursBackend):
         from kernels.fp8 import w8a16_matmul
 
         return w8a16_matmul(x, p.qweight, p.scales, bias=p.bias)
+
+    norm_linear = Backend.norm_linear  # the fused entries take W4A16 weights
+    act_linear = Backend.act_linear
 
 
 def make_backend(name: str) -> Backend:
@@ -310,10 +344,9 @@ class QwenRunner:
         residual, h = x, None
         for i, L in enumerate(self.layers):
             if h is None:
-                h = be.norm(x, L.ln1, eps)
+                qkv, _ = be.norm_linear(x, L.ln1, eps, None, L.qkv)
             else:  # the previous MLP output joins the residual inside this layer's input norm
-                h, residual = be.norm(h, L.ln1, eps, residual=residual)
-            qkv = be.linear(h, L.qkv)
+                qkv, residual = be.norm_linear(h, L.ln1, eps, residual, L.qkv)
             if fused:
                 attn = decode_attention(qkv, pos, self.inv_freq, self.kt_cache[i], self.v_cache[i],
                                         nq, nkv, hd ** -0.5)
@@ -323,11 +356,11 @@ class QwenRunner:
                 k = self._rope(k.view(B, T, nkv, hd), cos, sin)
                 attn = self._attend(i, q, k, v.view(B, T, nkv, hd), pos)
             o = be.linear(attn, L.o)
-            h, residual = be.norm(o, L.ln2, eps, residual=residual)
-            h = be.linear(be.act(be.linear(h, L.gate_up)), L.down)
-        h, _ = be.norm(h, self.final_norm, eps, residual=residual)
-        if not all_logits:
-            h = h[:, -1:]
+            gate_up, residual = be.norm_linear(o, L.ln2, eps, residual, L.gate_up)
+            h = be.act_linear(gate_up, L.down)
+        if not all_logits:  # the final norm is per row: normalize the last row only
+            h, residual = h[:, -1:], residual[:, -1:]
         if self.head_q is not None:
-            return be.linear(h, self.head_q)
+            return be.norm_linear(h, self.final_norm, eps, residual, self.head_q)[0]
+        h, _ = be.norm(h, self.final_norm, eps, residual=residual)
         return F.linear(h, self.lm_head)

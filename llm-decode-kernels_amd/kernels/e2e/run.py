@@ -103,7 +103,8 @@ def decode_speed(runner, ids, steps: int, repeats: int = 3) -> dict:
 
 def layers_only_ms(runner, M: int = 1) -> float:
     """Graph time of the swapped ops alone for one decode step (run.py:166-201): per layer the
-    qkv, o, gate_up and down projections, two fused add+norms and the activation."""
+    qkv, o, gate_up and down projections, two add+norms and the activation, through the
+    backend's norm_linear/act_linear (one launch per pair on the fused backends)."""
     be, eps = runner.backend, runner.eps
     dev = runner.embed.device
     H = runner.embed.shape[1]
@@ -113,13 +114,12 @@ def layers_only_ms(runner, M: int = 1) -> float:
     nq, hd = runner.n_heads, runner.head_dim
 
     def step():
-        h, r = be.norm(x, runner.layers[0].ln1, eps, residual=res)
+        h, r = x, res
         for L in runner.layers:
-            qkv = be.linear(h, L.qkv)
+            qkv, r = be.norm_linear(h, L.ln1, eps, r, L.qkv)
             o = be.linear(qkv[..., : nq * hd].contiguous(), L.o)
-            h, r = be.norm(o, L.ln2, eps, residual=r)
-            h = be.linear(be.act(be.linear(h, L.gate_up)), L.down)
-            h, r = be.norm(h, L.ln1, eps, residual=r)
+            gate_up, r = be.norm_linear(o, L.ln2, eps, r, L.gate_up)
+            h = be.act_linear(gate_up, L.down)
 
     for _ in range(3):
         step()

@@ -1,0 +1,95 @@
+"""Fusions on either side of the W4A16 decode GEMV (libldk_amd.so `ldk_w4a16_rmsnorm_matmul`,
+`ldk_w4a16_swiglu_matmul`).
+
+The reference's OursBackend runs a decode layer as separate kernels: rmsnorm (+ residual), then
+the W4A16 projection; swiglu, then the down projection (kernels/e2e/model.py:79-97). Here the
+activation row is formed inside the W4A16 M = 1 kernel while it stages x, so each pair is one
+launch. The staged activations follow the standalone kernels' rounding steps (`kernels.rmsnorm`,
+`kernels.swiglu`); SwiGLU's are bit-identical to them, RMSNorm's can differ from them by one fp16
+ulp, because the row's sum of squares is reduced in another order.
+
+Rows other than one (prefill) and group sizes other than 128 run the two ops back to back.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from kernels import _lib
+from kernels.rmsnorm import rmsnorm
+from kernels.swiglu import swiglu_fused
+from kernels.w4a16 import w4a16_matmul
+
+FUSED_GROUP_SIZE = 128
+
+
+def _aligned(*ts) -> bool:
+    return all(t is None or (t.is_contiguous() and t.data_ptr() % 16 == 0) for t in ts)
+
+
+def rmsnorm_w4a16_matmul(x, weight, eps, residual, qweight, scales, zeros, group_size=128,
+                         bias=None):
+    """y = w4a16_matmul(rmsnorm(x, weight, eps, residual), W) (+ bias).
+
+    Returns (y, x + residual) when a residual is given (the updated residual stream, as
+    `rmsnorm` returns it), else (y, None). x, residual: [..., K] fp16."""
+    K = x.shape[-1]
+    N = qweight.shape[1]
+    rows = x.numel() // K
+    fuse = (rows == 1 and group_size == FUSED_GROUP_SIZE and x.dtype == torch.float16
+            and weight.dtype == torch.float16 and x.is_cuda
+            and _aligned(x, weight, residual, qweight))
+    if not fuse:
+        if residual is None:
+            h, res = rmsnorm(x, weight, eps), None
+        else:
+            h, res = rmsnorm(x, weight, eps, residual=residual)
+        return w4a16_matmul(h, qweight, scales, zeros, group_size, bias), res
+    assert qweight.shape[0] * 8 == K and weight.numel() == K
+    dev = _lib.require_gpu(x, weight, residual, qweight, scales, zeros, bias,
+                           what="rmsnorm_w4a16_matmul")
+    if scales.dtype != torch.float16 or zeros.dtype != torch.float16:
+        raise ValueError("rmsnorm_w4a16_matmul: scales and zeros must be float16")
+    if residual is not None and residual.shape != x.shape:
+        raise ValueError("rmsnorm_w4a16_matmul: residual must have x's shape")
+    s, z = scales.contiguous(), zeros.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    out = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=dev)
+    res_out = None if residual is None else torch.empty_like(x)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w4a16_rmsnorm_matmul(
+            _lib.ptr(x), _lib.ptr(residual), _lib.ptr(res_out), _lib.ptr(weight), float(eps),
+            _lib.ptr(qweight), _lib.ptr(s), _lib.ptr(z), _lib.ptr(b), _lib.ptr(out), N, K,
+            group_size, ws, ws_bytes, _lib.stream(dev))
+    _lib.check(st, "rmsnorm_w4a16_matmul")
+    return out, res_out
+
+
+def swiglu_w4a16_matmul(gate_up, qweight, scales, zeros, group_size=128, bias=None):
+    """y = w4a16_matmul(swiglu_fused(gate_up), W) (+ bias); gate_up: [..., 2K] fp16."""
+    K2 = gate_up.shape[-1]
+    K = K2 // 2
+    N = qweight.shape[1]
+    rows = gate_up.numel() // K2
+    fuse = (rows == 1 and group_size == FUSED_GROUP_SIZE and gate_up.dtype == torch.float16
+            and gate_up.is_cuda and _aligned(gate_up, qweight) and K % 8 == 0)
+    if not fuse:
+        return w4a16_matmul(swiglu_fused(gate_up), qweight, scales, zeros, group_size, bias)
+    assert K2 % 2 == 0 and qweight.shape[0] * 8 == K
+    dev = _lib.require_gpu(gate_up, qweight, scales, zeros, bias, what="swiglu_w4a16_matmul")
+    if scales.dtype != torch.float16 or zeros.dtype != torch.float16:
+        raise ValueError("swiglu_w4a16_matmul: scales and zeros must be float16")
+    s, z = scales.contiguous(), zeros.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    out = torch.empty((*gate_up.shape[:-1], N), dtype=torch.float16, device=dev)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w4a16_swiglu_matmul(
+            _lib.ptr(gate_up), _lib.ptr(qweight), _lib.ptr(s), _lib.ptr(z), _lib.ptr(b),
+            _lib.ptr(out), N, K, group_size, ws, ws_bytes, _lib.stream(dev))
+    _lib.check(st, "swiglu_w4a16_matmul")
+    return out
+
+
+__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul"]

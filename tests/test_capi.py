@@ -102,6 +102,28 @@ def test_rmsnorm_residual_pairing_rejected():
     assert st == _lib.ERR_INVALID
 
 
+def test_fused_entries_validate_before_launch():
+    lib = _lib.load()
+    p, q = ctypes.c_void_p(256), ctypes.c_void_p(512)
+    # residual_out aliasing the residual
+    st, msg = _err(lib.ldk_w4a16_rmsnorm_matmul(p, q, q, p, 1e-6, p, p, p, None, p, 1536, 1536, 128,
+                                                None, 0, None))
+    assert st == _lib.ERR_INVALID and "alias" in msg
+    # residual without residual_out
+    st, _ = _err(lib.ldk_w4a16_rmsnorm_matmul(p, q, None, p, 1e-6, p, p, p, None, p, 1536, 1536,
+                                              128, None, 0, None))
+    assert st == _lib.ERR_INVALID
+    # no norm weight
+    st, _ = _err(lib.ldk_w4a16_rmsnorm_matmul(p, None, None, None, 1e-6, p, p, p, None, p, 1536,
+                                              1536, 128, None, 0, None))
+    assert st == _lib.ERR_INVALID
+    # a group size the fused kernels are not built for (64) is reported, not launched
+    st, msg = _err(lib.ldk_w4a16_swiglu_matmul(p, p, p, p, None, p, 1536, 1536, 64, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "128" in msg
+    st, _ = _err(lib.ldk_w4a16_swiglu_matmul(None, p, p, p, None, p, 1536, 1536, 128, None, 0, None))
+    assert st == _lib.ERR_INVALID
+
+
 def test_w8a16_n_multiple_of_16():
     lib = _lib.load()
     p = ctypes.c_void_p(256)

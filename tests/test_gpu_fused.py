@@ -1,0 +1,131 @@
+"""The fused decode entries (kernels.fused: ldk_w4a16_rmsnorm_matmul, ldk_w4a16_swiglu_matmul)
+against the oracle's unfused chain (kernels/reference.py:9-45: rmsnorm_ref or swiglu_ref, then
+the fp32 dequantize-then-matmul) and against the library's own two-launch composition.
+
+Bars: the north star's max-abs 2e-2 and rel-L2 1e-3 against the oracle chain; the updated
+residual bit-exact (one fp16 add); SwiGLU + matmul bit-identical to swiglu_fused then
+w4a16_matmul (same staged activations, same plan and reduction order); RMSNorm + matmul within
+a few fp16 ulps of the composition (its staged values can differ by one ulp, the row statistic
+being reduced in another order)."""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_north_star, bits16, to_np
+from kernels.bench import cases
+from kernels.fused import rmsnorm_w4a16_matmul, swiglu_w4a16_matmul
+from kernels.quant import quantize_rtn
+from kernels.rmsnorm import rmsnorm
+from kernels.swiglu import swiglu_fused
+from kernels.w4a16 import w4a16_matmul
+from oracle import quant as oq
+from oracle.reference import rmsnorm_ref, swiglu_ref, w4a16_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(N, K, seed, bias=False):
+    w, _ = cases.w4a16_case(1, N, K, seed)
+    qw, s, z = quantize_rtn(w.cuda())
+    b = (torch.randn(N, generator=cases.gen(seed + 1)) * 0.1).half() if bias else None
+    return qw, s, z, b
+
+
+def _oracle_linear(xn, qw, s, z, b):
+    return w4a16_ref(xn, to_np(qw), to_np(s), to_np(z), 128, None if b is None else b.numpy())
+
+
+# qkv (with bias), o, gate_up, a K with more than 4 row vectors per thread in small workgroups,
+# and the quantized lm_head shape
+@pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (1536, 1536, False),
+                                      (17920, 1536, False), (512, 8960, False),
+                                      (151936, 1536, False)])
+@pytest.mark.parametrize("with_res", [True, False])
+def test_rmsnorm_matmul(N, K, bias, with_res):
+    qw, s, z, b = _weights(N, K, 11, bias)
+    x, r, w = cases.rmsnorm_case(1, K, 12)
+    res = r.cuda() if with_res else None
+    y, res_out = rmsnorm_w4a16_matmul(x.cuda().view(1, 1, K), w.cuda(), 1e-6,
+                                      None if res is None else res.view(1, 1, K), qw, s, z, 128,
+                                      None if b is None else b.cuda())
+    assert y.shape == (1, 1, N) and y.dtype == torch.float16
+    if with_res:
+        xn, h = rmsnorm_ref(x.numpy(), w.numpy(), 1e-6, residual=r.numpy())
+        assert np.array_equal(bits16(res_out.view(1, K)), bits16(h))
+    else:
+        xn = rmsnorm_ref(x.numpy(), w.numpy(), 1e-6)
+        assert res_out is None
+    assert_north_star(to_np(y.view(1, N)), _oracle_linear(xn, qw, s, z, b))
+    # against the library's two launches: the staged activations agree to one fp16 ulp
+    if with_res:
+        h2, _ = rmsnorm(x.cuda(), w.cuda(), 1e-6, residual=res)
+    else:
+        h2 = rmsnorm(x.cuda(), w.cuda(), 1e-6)
+    y2 = w4a16_matmul(h2, qw, s, z, 128, None if b is None else b.cuda())
+    d = (y.view(1, N).float() - y2.float()).abs()
+    assert float(d.max()) <= 4e-3 * max(1.0, float(y2.float().abs().max())), float(d.max())
+
+
+@pytest.mark.parametrize("N,K", [(1536, 8960), (1536, 1536), (256, 8960), (4096, 2048)])
+def test_swiglu_matmul(N, K):
+    qw, s, z, b = _weights(N, K, 21, bias=(N == 256))
+    gu = cases.swiglu_case(1, K, 22)
+    y = swiglu_w4a16_matmul(gu.cuda(), qw, s, z, 128, None if b is None else b.cuda())
+    act = swiglu_ref(gu[:, :K].numpy(), gu[:, K:].numpy())
+    assert_north_star(to_np(y), _oracle_linear(act, qw, s, z, b))
+    y2 = w4a16_matmul(swiglu_fused(gu.cuda()), qw, s, z, 128, None if b is None else b.cuda())
+    assert torch.equal(y, y2)
+
+
+def test_rows_other_than_one_compose():
+    """Prefill rows run rmsnorm/swiglu then w4a16_matmul (same results as the two calls)."""
+    qw, s, z, _ = _weights(1536, 1536, 31)
+    x, r, w = cases.rmsnorm_case(5, 1536, 32)
+    y, res = rmsnorm_w4a16_matmul(x.cuda(), w.cuda(), 1e-6, r.cuda(), qw, s, z)
+    h, res2 = rmsnorm(x.cuda(), w.cuda(), 1e-6, residual=r.cuda())
+    assert torch.equal(res, res2) and torch.equal(y, w4a16_matmul(h, qw, s, z))
+    gu = cases.swiglu_case(3, 768, 33)
+    qd, sd, zd, _ = _weights(1536, 768, 34)
+    assert torch.equal(swiglu_w4a16_matmul(gu.cuda(), qd, sd, zd),
+                       w4a16_matmul(swiglu_fused(gu.cuda()), qd, sd, zd))
+
+
+def test_graph_replays_match_eager():
+    """Both fused entries captured in one graph and replayed with new inputs written between the
+    replays: every replay equals the eager result (the split-K workspace stays clean)."""
+    qw, s, z, _ = _weights(17920, 1536, 41)
+    qd, sd, zd, _ = _weights(1536, 8960, 42)
+    wn = (1 + 0.1 * torch.randn(1536, generator=cases.gen(43))).half().cuda()
+    x = torch.zeros(1, 1536, dtype=torch.float16, device="cuda")
+    r = torch.zeros_like(x)
+    y, _ = rmsnorm_w4a16_matmul(x, wn, 1e-6, r, qw, s, z)  # warm-up: allocates the workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gu, res = rmsnorm_w4a16_matmul(x, wn, 1e-6, r, qw, s, z)
+        out = swiglu_w4a16_matmul(gu, qd, sd, zd)
+    gen = torch.Generator(device="cuda").manual_seed(44)
+    for i in range(6):
+        x.copy_(torch.randn(1, 1536, device="cuda", generator=gen).half())
+        r.copy_(torch.randn(1, 1536, device="cuda", generator=gen).half())
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        gu2, res2 = rmsnorm_w4a16_matmul(x, wn, 1e-6, r, qw, s, z)
+        out2 = swiglu_w4a16_matmul(gu2, qd, sd, zd)
+        assert torch.equal(gu, gu2) and torch.equal(res, res2) and torch.equal(out, out2), i
+
+
+def test_rejects_aliased_residual_output():
+    from kernels import _lib
+
+    qw, s, z, _ = _weights(1536, 1536, 51)
+    x = torch.randn(1536, device="cuda").half()
+    w = torch.ones(1536, device="cuda").half()
+    out = torch.empty(1536, device="cuda").half()
+    ws, nb = _lib.workspace(x.device)
+    st = _lib.load().ldk_w4a16_rmsnorm_matmul(
+        _lib.ptr(x), _lib.ptr(x), _lib.ptr(x), _lib.ptr(w), 1e-6, _lib.ptr(qw), _lib.ptr(s),
+        _lib.ptr(z), None, _lib.ptr(out), 1536, 1536, 128, ws, nb, _lib.stream(x.device))
+    assert st == _lib.ERR_INVALID
