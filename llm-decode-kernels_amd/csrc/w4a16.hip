@@ -582,14 +582,26 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 
 // ------------------------------------------------------------------------------ MFMA kernel
 //
-// Lane l of a wave: c16 = l % 16 is the column inside each 16x16 tile and the A row, kb = l / 16
-// the 8-wide K block inside a 32-wide K step. The lane's 128-bit load of packed row
-// (g*rpg + 4*ks + kb) at columns n0 + 4*c16 .. +3 feeds tiles j = 0..3, whose column c16 is the
-// real column n0 + 4*c16 + j. A wave handles whole groups (rpg/4 K steps each): groups
-// gb + w, gb + w + NW, ... in rounds of CPW groups whose loads are all issued first.
-template <int KS, int CPW>  // KS: 32-wide K steps per group (group_size / 32)
-__global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs sp) {
-  constexpr int CW = 64;
+// M <= 16 rows (padded to 16) on v_mfma_f32_16x16x32_f16. A workgroup owns CW = 64 * NH output
+// columns (NH 128-byte line halves of the packed rows: 128 columns on wide shapes, 140 workgroups
+// for gate_up, one per CU, instead of 280 that put two 64-column tiles on 24 CUs) and a range of
+// quantization groups; its waves (up to 16 at 64 columns, 8 at 128) take groups round-robin, CPW
+// groups per pass with every load of the pass in flight.
+//
+// Lane l = (c16 = l % 16, kb = l / 16). For 32-row K step ks of group g it loads packed row
+// g*rpg + 4*ks + kb at columns n0 + 64h + 4*c16 .. +3 (one 16-byte load per half h): each of the 4
+// words is exactly one lane's B operand (8 consecutive K of one column), so word j feeds MFMA
+// tile (h, j), whose column c16 is the real column n0 + 64h + 4*c16 + j. The A operand is x row
+// c16 in the matching nibble-pair order (x_pairs), zeros past M.
+//
+// FACTORED on the matrix cores: B is the magic-decoded 1024 + q (one v_and_or_b32 per pair, no
+// subtraction), and one more MFMA per K step against an all-ones B gives sum(x) of each output
+// row in the same fragment layout. A group then adds s * (sum x*(1024+q) - (1024+z) * sum x) =
+// s * sum x*(q - z) to the fp32 accumulator: 4 VALU ops per 8 weights plus a per-group epilogue,
+// against 12 for dequantizing every weight to fp16 first.
+template <int NH, int KS, int CPW>  // KS: 32-wide K steps per group (group_size / 32)
+__global__ __launch_bounds__(NH == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args a, SplitArgs sp) {
+  constexpr int CW = 64 * NH, NT = 4 * NH;  // columns, 16-column MFMA tiles
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
   extern __shared__ __align__(16) unsigned char smem[];
   const int rpg = 4 * KS;
@@ -602,81 +614,98 @@ __global__ __launch_bounds__(1024) void w4a16_mfma16_kernel(W4Args a, SplitArgs 
   ldk::pin_sgpr(a.qw);
   const TileWork tw = map_block(sp, ng);
   const int n0 = tw.tile * CW;
-  const int col = min(n0 + 4 * c16, a.N - 4);
+  int col[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) col[h] = min(n0 + 64 * h + 4 * c16, a.N - 4);  // clamped: tail lanes store nothing
   const int gb = tw.gb, ge = tw.ge;
   const int xrow = min(c16, a.M - 1);
   const bool xok = c16 < a.M;
   const int mrows = min(a.M, 16);
-  float* red = reinterpret_cast<float*>(smem);  // [NW][mrows * 64]
+  float* red = reinterpret_cast<float*>(smem);  // [NW][mrows][CW]
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>();
-  float4_t acc[4];
+  const half8v ones = {(half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f,
+                       (half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f};
+  float4_t acc[NT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int g0 = gb + wave; g0 < ge; g0 += NW * CPW) {
-    // loads in consumption order, group by group: zero point, per K step the A fragment and the
-    // weight word row, then the scale (used after the group's MFMAs)
-    u32x2 zv[CPW], sv[CPW];
-    u32x4 ar[CPW][KS], w[CPW][KS];
+    // loads in consumption order, group by group: per K step the A fragment and the weight
+    // words of each half, then the zero points and scales (used after the group's MFMAs)
+    u32x2 zv[CPW][NH], sv[CPW][NH];
+    u32x4 ar[CPW][KS], w[CPW][KS][NH];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       const int g = min(g0 + NW * c, ge - 1);
-      zv[c] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int r = g * rpg + 4 * ks + kb;
         ar[c][ks] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)xrow * a.ldx + 8 * r);
-        w[c][ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col));
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          w[c][ks][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col[h]));
       }
-      sv[c] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        zv[c][h] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col[h]);
+        sv[c][h] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col[h]);
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the round is in flight before the first wait
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       if (g0 + NW * c >= ge) break;  // uniform
-      const half4_t z4 = __builtin_bit_cast(half4_t, zv[c]);
-      float4_t tmp[4];
+      float4_t tmp[NT], sx = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) tmp[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int j = 0; j < NT; ++j) tmp[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         u32x4 ap = x_pairs(ar[c][ks]);
         if (!xok) ap = u32x4{0u, 0u, 0u, 0u};
         const half8v A = __builtin_bit_cast(half8v, ap);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t wc = w[c][ks][j];
-          const half_t zb1 = -((half_t)1024.0f + z4[j]);
-          const half2_t zb = {zb1, zb1};
-          u32x4 b;
-          b[0] = ldk::h22u(ldk::u2h2((wc & mlo) | magic) + zb);          // (q0, q4) - z
-          b[1] = ldk::h22u(ldk::u2h2(((wc >> 4) & mlo) | magic) + zb);   // (q1, q5) - z
-          b[2] = ldk::h22u(ldk::u2h2(((wc >> 8) & mlo) | magic) + zb);   // (q2, q6) - z
-          b[3] = ldk::h22u(ldk::u2h2(((wc >> 12) & mlo) | magic) + zb);  // (q3, q7) - z
-          tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), tmp[j], 0, 0, 0);
+        for (int h = 0; h < NH; ++h) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t wc = w[c][ks][h][j];
+            u32x4 bq;
+            bq[0] = (wc & mlo) | magic;          // 1024 + (q0, q4)
+            bq[1] = ((wc >> 4) & mlo) | magic;   // 1024 + (q1, q5)
+            bq[2] = ((wc >> 8) & mlo) | magic;   // 1024 + (q2, q6)
+            bq[3] = ((wc >> 12) & mlo) | magic;  // 1024 + (q3, q7)
+            tmp[4 * h + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, bq), tmp[4 * h + j], 0, 0, 0);
+          }
         }
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ones, sx, 0, 0, 0);
       }
-      const half4_t s4 = __builtin_bit_cast(half4_t, sv[c]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float sj = (float)s4[j];
+      for (int h = 0; h < NH; ++h) {
+        const half4_t z4 = __builtin_bit_cast(half4_t, zv[c][h]), s4 = __builtin_bit_cast(half4_t, sv[c][h]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(sj, tmp[j][i], acc[j][i]);
+        for (int j = 0; j < 4; ++j) {
+          const float zz = 1024.0f + (float)z4[j], sj = (float)s4[j];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[4 * h + j][i] = __builtin_fmaf(sj, __builtin_fmaf(-zz, sx[i], tmp[4 * h + j][i]), acc[4 * h + j][i]);
+        }
       }
     }
   }
 
-  // tile j, element i of lane l: row 4*kb + i, column 4*c16 + j of the workgroup's 64 columns.
-  // Rows >= M are all zero and not stored; each lane writes 4 consecutive columns per row.
+  // tile (h, j), element i of lane l: row 4*kb + i, column 64h + 4*c16 + j of the workgroup's CW.
+  // Rows >= M are all zero and not stored; each lane writes 4 consecutive columns per half.
   const int n = mrows * CW;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * kb + i;
-    if (row < mrows)
-      *reinterpret_cast<float4_t*>(red + (size_t)wave * n + row * CW + 4 * c16) =
-          float4_t{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+    if (row < mrows) {
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+        *reinterpret_cast<float4_t*>(red + (size_t)wave * n + row * CW + 64 * h + 4 * c16) =
+            float4_t{acc[4 * h][i], acc[4 * h + 1][i], acc[4 * h + 2][i], acc[4 * h + 3][i]};
+    }
   }
   __syncthreads();
   finish_tile(red, n, NW, tw, sp, [&](int o, float v) {
@@ -694,7 +723,8 @@ enum Kern { kM1 = 0, kValu = 1, kMfma = 2 };
 
 struct Plan {
   Kern kern;
-  int mt, ln, rpl, cpw;  // row tile, lanes along N, rows per lane, chunks per wave and round
+  int mt, ln, rpl, cpw;  // row tile, lanes along N (MFMA: 16 * 64-column halves), rows per lane,
+                         // chunks (MFMA: groups) per wave and pass
   int nw, splits, gps;
   int full;  // M = 1 kernel: leading tiles run whole while the rest split (0: all tiles alike)
 };
@@ -726,17 +756,17 @@ int gemv_pxw(const Plan& p) { return (p.cpw * p.rpl * p.mt + p.ln - 1) / p.ln; }
 
 size_t plan_lds_bytes(const Plan& p, int64_t M) {
   if (p.kern == kM1) return 0;  // static LDS
-  if (p.kern == kMfma) return (size_t)p.nw * std::min<int64_t>(M, 16) * 64 * 4;
+  if (p.kern == kMfma) return (size_t)p.nw * std::min<int64_t>(M, 16) * (4 * p.ln) * 4;
   return (size_t)p.nw * 64 * gemv_pxw(p) * 16 + (size_t)p.nw * p.mt * 4 * p.ln * 4;
 }
 
-int plan_cw(const Plan& p) { return p.kern == kMfma ? 64 : 4 * p.ln; }
+int plan_cw(const Plan& p) { return 4 * p.ln; }
 
 size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
   if (p.splits <= 1) return 0;
   const int cw = plan_cw(p);
   const int64_t tiles = (N + cw - 1) / cw - p.full;
-  const int64_t n = p.kern == kMfma ? std::min<int64_t>(M, 16) * 64 : (int64_t)p.mt * cw;
+  const int64_t n = p.kern == kMfma ? std::min<int64_t>(M, 16) * cw : (int64_t)p.mt * cw;
   return (size_t)tiles * n * 8;
 }
 
@@ -760,16 +790,18 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const int rpg = 1 << gsh_rows;
   const int64_t ng = (K / 8) >> gsh_rows;
   const int64_t wbytes = N * K / 2;
-  // MFMA from 5 rows (3 on shapes of > 4 MB): its B operand costs 11 VALU ops per 8 weights for
+  // MFMA from 5 rows (3 on shapes of > 4 MB): its B operand costs 4 VALU ops per 8 weights for
   // all 16 rows, the VALU kernel's dequantize-then-dot grows by 4 dot2 per 8 weights per row.
   // A block_n only the VALU kernels take (16 or 32) keeps M <= 8 on the VALU path.
-  const bool mfma_auto = M > 8 || ((M > 4 || (M > 2 && wbytes > (4 << 20))) && (block_n == 0 || block_n == 64));
+  // EXACT keeps M <= 8 on the VALU kernels, which dequantize every weight as dequantize_ref does.
+  const bool mfma_auto =
+      M > 8 || (!(flags & LDK_EXACT) && (M > 4 || (M > 2 && wbytes > (4 << 20))) && (block_n == 0 || block_n >= 64));
   const bool mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
   const bool m1 = !mfma && M == 1 && !(flags & LDK_EXACT);
   p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
   p.mt = mfma ? 16 : round_mt(M);
-  if (mfma) {
-    p.ln = 16;
+  if (mfma) {  // 128 columns on shapes wide enough to fill the CUs with them, else 64
+    p.ln = block_n == 64 ? 16 : block_n == 128 ? 32 : (N >= 128 * 128 ? 32 : 16);
   } else if (block_n) {
     p.ln = block_n / 4;
   } else if (m1) {  // small shapes are latency-bound: more, narrower workgroups
@@ -790,7 +822,11 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const int gw = mfma ? 1 : lkw / (rpg / p.rpl);
   const int64_t tiles = (N + cw - 1) / cw;
   int64_t splits = split_k > 0 ? split_k : 1;
-  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20))  // M = 1: about one workgroup per CU
+  // narrow shapes that move more than a couple of MB split K across workgroups (M = 1: about one
+  // workgroup per CU). Multi-row splits carry M outputs per column through returning atomics,
+  // so small shapes keep whole tiles and split K over the waves of a workgroup instead (q/o at
+  // M = 16: 5.9 us whole, 25 us split twelve ways).
+  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20))
     splits = m1 ? std::max<int64_t>(2, 256 / tiles) : (192 + tiles - 1) / tiles;
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
@@ -833,11 +869,16 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     for (int c : {1, 2, 4})
       if (chunks <= 16 * c) { cpw = c; break; }
   }
-  if (mfma) {
+  if (mfma) {  // groups per wave and pass: all in one pass where registers allow (<= 16 waves at
+              // 64 columns, <= 8 at 128)
+    const int wmax = p.ln == 16 ? 16 : 8;
+    if (!cpw_from_flags(flags)) cpw = chunks > wmax ? 2 : 1;
     cpw = std::min(cpw, rpg <= 16 ? 2 : 1);
-  } else {
-    while (cpw > 1 && !gemv_shape_ok(p.mt, p.ln, p.rpl, cpw)) cpw >>= 1;
+    p.cpw = cpw;
+    p.nw = (int)std::min<int64_t>(wmax, (chunks + cpw - 1) / cpw);
+    return p;
   }
+  while (cpw > 1 && !gemv_shape_ok(p.mt, p.ln, p.rpl, cpw)) cpw >>= 1;
   p.cpw = cpw;
   p.nw = (int)std::min<int64_t>(16, (chunks + cpw - 1) / cpw);
   return p;
@@ -939,15 +980,27 @@ int launch_gemv_ln(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t l
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
 }
 
-template <int KS, int CPW>
+template <int NH, int KS, int CPW>
 int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipStream_t s) {
-  auto kern = w4a16_mfma16_kernel<KS, CPW>;
+  auto kern = w4a16_mfma_kernel<NH, KS, CPW>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
   (void)hipGetLastError();
   kern<<<(unsigned)(sp.full + sp.nsplit), nw * 64, lds, s>>>(a, sp);
-  return ldk::check_launch("w4a16_mfma16");
+  return ldk::check_launch("w4a16_mfma");
+}
+
+template <int NH>
+int launch_mfma_nh(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
+  const bool two = p.cpw == 2;
+  switch (1 << a.gsh_rows) {
+    case 4: return two ? launch_mfma_t<NH, 1, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 1, 1>(a, sp, p.nw, lds, s);
+    case 8: return two ? launch_mfma_t<NH, 2, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 2, 1>(a, sp, p.nw, lds, s);
+    case 16: return two ? launch_mfma_t<NH, 4, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 4, 1>(a, sp, p.nw, lds, s);
+    case 32: return launch_mfma_t<NH, 8, 1>(a, sp, p.nw, lds, s);
+  }
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
 }
 
 int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro = kProNone,
@@ -972,16 +1025,7 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
   }
   if (pro != kProNone) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues run on the M = 1 kernel");
-  if (p.kern == kMfma) {
-    const bool two = p.cpw == 2;
-    switch (1 << a.gsh_rows) {
-      case 4: return two ? launch_mfma_t<1, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<1, 1>(a, sp, p.nw, lds, s);
-      case 8: return two ? launch_mfma_t<2, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<2, 1>(a, sp, p.nw, lds, s);
-      case 16: return two ? launch_mfma_t<4, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<4, 1>(a, sp, p.nw, lds, s);
-      case 32: return launch_mfma_t<8, 1>(a, sp, p.nw, lds, s);
-    }
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
-  }
+  if (p.kern == kMfma) return p.ln == 16 ? launch_mfma_nh<1>(a, sp, p, lds, s) : launch_mfma_nh<2>(a, sp, p, lds, s);
   switch (p.mt) {
     case 1: return launch_gemv_ln<1>(a, sp, p, lds, s);
     case 2: return launch_gemv_ln<2>(a, sp, p, lds, s);
@@ -1016,7 +1060,7 @@ int validate(const char* fn, const void* x, int64_t ldx, const int32_t* qw, cons
 
 int plan_flags(const Plan& p) {
   const int cpw_code = p.kern == kValu ? (p.cpw == 1 ? 1 : p.cpw == 2 ? 2 : 3) : 0;
-  return (p.kern == kMfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.kern == kM1 ? LDK_FACTORED : LDK_EXACT) |
+  return (p.kern == kMfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.kern == kValu ? LDK_EXACT : LDK_FACTORED) |
          (cpw_code << 4);
 }
 
@@ -1048,17 +1092,22 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: unknown flags 0x%x", flags);
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: FACTORED and EXACT are exclusive");
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: VALU and MFMA paths are exclusive");
-  if ((flags & LDK_FACTORED) && M > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED is the M = 1 kernel");
-  if ((flags & LDK_FACTORED) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED runs on the VALU kernel");
+  if ((flags & LDK_FACTORED) && M > 1 && !(flags & LDK_PATH_MFMA))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED with more than one row is the MFMA kernel (LDK_PATH_MFMA)");
+  if ((flags & LDK_EXACT) && (flags & LDK_PATH_MFMA))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel computes the factored form; EXACT runs on the VALU kernels (M <= 8)");
   if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the VALU kernel takes M <= 8");
-  if (block_n && block_n != 16 && block_n != 32 && block_n != 64)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=%d must be 16, 32 or 64", block_n);
+  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=%d must be 16, 32, 64 or 128 (MFMA)", block_n);
+  if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && !(M > 4 || (M > 2 && N * K / 2 > (4 << 20))))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=128 is the MFMA kernel's tile (M > 4 or the MFMA flag)");
   if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d must be >= 0", split_k);
   if (split_k > kMaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: split_k=%d above %d", split_k, kMaxSplits);
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul: workspace must be a 256-byte aligned pointer");
   const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
-  if (p.kern == kMfma && block_n && block_n != 64) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n=64");
+  if (p.kern == kMfma && block_n && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n 64 or 128");
   if (split_k > 1 && p.splits == 1 && (K / group_size) > 1)
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,

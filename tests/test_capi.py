@@ -95,6 +95,16 @@ def test_factored_needs_one_row():
     assert st == _lib.ERR_UNSUPPORTED
 
 
+def test_exact_is_not_the_mfma_kernel():
+    """The MFMA kernel computes the factored form: EXACT with the MFMA path is refused, and a
+    FACTORED multi-row call needs the MFMA path."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, msg = _err(lib.ldk_w4a16_matmul(p, 256, p, p, p, None, p, 64, 16, 64, 256, 128, 0, 0,
+                                        _lib.EXACT | _lib.PATH_MFMA, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "factored" in msg
+
+
 def test_rmsnorm_residual_pairing_rejected():
     lib = _lib.load()
     p = ctypes.c_void_p(256)
@@ -139,7 +149,7 @@ def test_config_query():
     assert fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU
     st = _lib.load().ldk_w4a16_config(16, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
-    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 64
+    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 128
 
 
 def test_workspace_size():

@@ -128,6 +128,20 @@ def test_split_k_large_partials():
     assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(ref) + 0.5)
 
 
+@pytest.mark.parametrize("M,N", [(16, 17920), (9, 17920), (4, 17920), (16, 2048), (3, 4100),
+                                 (16, 260)])
+@pytest.mark.parametrize("block_n", [64, 128])
+def test_mfma_tile_widths(M, N, block_n):
+    """The MFMA kernel's 64- and 128-column tiles (two 16-byte line halves per lane, eight MFMA
+    column tiles), including column tails that end inside a tile."""
+    _run(M, N, 1536, config={"MFMA": True, "block_n": block_n})
+
+
+def test_mfma_split_k_with_128_columns():
+    _run(16, 1536, 8960, config={"MFMA": True, "block_n": 128, "split_k": 5})
+    _run(7, 512, 8960, config={"MFMA": True, "block_n": 128, "split_k": 14}, bias=True)
+
+
 @pytest.mark.parametrize("M", [1, 4, 9, 16])
 def test_mfma_and_valu_paths_agree_with_reference(M):
     if M <= 8:
