@@ -34,8 +34,13 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
   const int tid = threadIdx.x, NT = blockDim.x;
   const int nchunk = a.N / VEC;
   const half_t* x = a.x + (int64_t)row * a.ldx;
-  hv_t h[CPT];
+  hv_t h[CPT], wv[CPT];
   float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {  // the weight goes out with the row, before the barrier
+    const int c = min(tid + i * NT, nchunk - 1);  // clamped, unconditional: no branch to wait at
+    wv[i] = *reinterpret_cast<const hv_t*>(a.w + c * VEC);
+  }
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + i * NT;
@@ -64,7 +69,6 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + i * NT;
     if (c < nchunk) {
-      const hv_t wv = *reinterpret_cast<const hv_t*>(a.w + c * VEC);
       hv_t o;
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
@@ -72,7 +76,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
         asm volatile("" : "+v"(v));  // a -0 * rs must stay -0 (no v_fma_mix with a +0 addend)
         o[j] = (half_t)v;
       }
-      *reinterpret_cast<hv_t*>(a.out + (int64_t)row * a.ldo + c * VEC) = wv * o;  // fp16 multiply
+      *reinterpret_cast<hv_t*>(a.out + (int64_t)row * a.ldo + c * VEC) = wv[i] * o;  // fp16 multiply
     }
   }
 }

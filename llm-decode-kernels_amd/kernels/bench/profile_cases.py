@@ -1,0 +1,153 @@
+"""Counter workload: launches each hot-path kernel on the benchmark configurations so that one
+rocprofv3 run per counter set covers all of them, plus a 64 MiB elementwise pass (torch.neg on
+fp16) that calibrates the byte counters: it reads and writes exactly 65536 KiB per dispatch.
+
+Every case rotates over input sets sized to 4x the 256 MB MALL (as the sweep does), so each
+launch reads its weights from HBM. Cases run one after another, `--reps` launches each.
+
+    rocprofv3 --kernel-trace --stats -d OUT -o prof -- python3 -m kernels.bench.profile_cases
+    rocprofv3 --pmc FETCH_SIZE -d OUT -o prof -- python3 -m kernels.bench.profile_cases
+    rocprofv3 --pmc WRITE_SIZE -d OUT -o prof -- python3 -m kernels.bench.profile_cases
+    rocprofv3 --pmc VALUBusy MfmaUtil -d OUT -o prof -- python3 -m kernels.bench.profile_cases
+    python3 -m kernels.bench.counters OUT        # one table per kernel and grid
+
+`--cases` picks a subset by name (comma-separated).
+"""
+
+from __future__ import annotations
+
+import argparse
+
+import torch
+
+from kernels.bench import cases
+from kernels.bench.harness import n_copies, tensor_bytes
+
+GS = 128
+
+
+def _rotate(fn, sets, reps):
+    for i in range(reps):
+        fn(*sets[i % len(sets)])
+
+
+def case_w4a16(M, N, K, reps):
+    from kernels.quant import quantize_rtn
+    from kernels.w4a16 import w4a16_matmul
+
+    w, _ = cases.w4a16_case(1, N, K, seed=2)
+    qw, s, z = quantize_rtn(w.cuda(), GS)
+    x = cases.activations(M, K, cases.gen(2)).cuda()
+    sets = [(x.clone(), qw.clone(), s.clone(), z.clone())
+            for _ in range(n_copies(tensor_bytes((x, qw, s, z))))]
+    _rotate(lambda xx, q, sc, zz: w4a16_matmul(xx, q, sc, zz, GS), sets, reps)
+
+
+def case_fp8(M, N, K, reps):
+    from kernels.fp8 import quantize_fp8, w8a16_matmul
+
+    w, _ = cases.w4a16_case(1, N, K, seed=3)
+    wq, sc = quantize_fp8(w.cuda())
+    x = cases.activations(M, K, cases.gen(3)).cuda()
+    sets = [(x.clone(), wq.clone(), sc.clone()) for _ in range(n_copies(tensor_bytes((x, wq, sc))))]
+    _rotate(lambda xx, q, ss: w8a16_matmul(xx, q, ss), sets, reps)
+
+
+def case_rms_w4a16(N, K, reps, bias):
+    from kernels.fused import rmsnorm_w4a16_matmul
+    from kernels.quant import quantize_rtn
+
+    w, _ = cases.w4a16_case(1, N, K, seed=2)
+    qw, s, z = quantize_rtn(w.cuda(), GS)
+    b = torch.zeros(N, dtype=torch.float16, device="cuda") if bias else None
+    x, r, wn = (t.cuda() for t in cases.rmsnorm_case(1, K, seed=1))
+    sets = [(x.clone(), r.clone(), qw.clone(), s.clone(), z.clone())
+            for _ in range(n_copies(tensor_bytes((x, r, qw, s, z))))]
+    _rotate(lambda xx, rr, q, sc, zz: rmsnorm_w4a16_matmul(xx, wn, 1e-6, rr, q, sc, zz, GS, b),
+            sets, reps)
+
+
+def case_swiglu_w4a16(N, I, reps):
+    from kernels.fused import swiglu_w4a16_matmul
+    from kernels.quant import quantize_rtn
+
+    w, _ = cases.w4a16_case(1, N, I, seed=2)
+    qw, s, z = quantize_rtn(w.cuda(), GS)
+    gu = cases.swiglu_case(1, I, seed=1).cuda()
+    sets = [(gu.clone(), qw.clone(), s.clone(), z.clone())
+            for _ in range(n_copies(tensor_bytes((gu, qw, s, z))))]
+    _rotate(lambda g, q, sc, zz: swiglu_w4a16_matmul(g, q, sc, zz, GS), sets, reps)
+
+
+def case_attention(reps, L=392, pos=300):
+    from kernels.attention import decode_attention
+
+    g = cases.gen(5)
+    nq, nkv, hd = 12, 2, 128
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda()
+    kt = torch.randn(1, nkv, hd, L, generator=g).half().cuda()
+    vc = torch.randn(1, nkv, L, hd, generator=g).half().cuda()
+    inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    p = torch.tensor([pos], device="cuda")
+    sets = [(kt.clone(), vc.clone()) for _ in range(n_copies(tensor_bytes((kt, vc))))]
+    _rotate(lambda k, v: decode_attention(qkv, p, inv, k, v, nq, nkv, hd ** -0.5), sets, reps)
+
+
+def case_rmsnorm(M, N, reps):
+    from kernels.rmsnorm import rmsnorm
+
+    x, r, w = (t.cuda() for t in cases.rmsnorm_case(M, N, seed=1))
+    sets = [(x.clone(), r.clone()) for _ in range(n_copies(tensor_bytes((x, r)) * 2))]
+    _rotate(lambda xx, rr: rmsnorm(xx, w, 1e-6, residual=rr), sets, reps)
+
+
+def case_swiglu(M, I, reps):
+    from kernels.swiglu import swiglu_fused
+
+    gu = cases.swiglu_case(M, I, seed=1).cuda()
+    sets = [(gu.clone(),) for _ in range(n_copies(tensor_bytes(gu) * 3 // 2))]
+    _rotate(swiglu_fused, sets, reps)
+
+
+def case_copy(reps):
+    """torch.neg over 64 MiB of fp16: reads and writes exactly 65536 KiB per dispatch, under a
+    kernel name nothing else in the workload uses (the weight clones run rocclr's copy kernel)."""
+    a = torch.randn(32 * 2**20, dtype=torch.float16, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        torch.neg(a, out=b)
+
+
+CASES = {
+    "calib_neg64MiB": lambda r: case_copy(r),
+    "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
+    "w4a16_down_m1": lambda r: case_w4a16(1, 1536, 8960, r),
+    "w4a16_gate_up_m4": lambda r: case_w4a16(4, 17920, 1536, r),
+    "w4a16_gate_up_m16": lambda r: case_w4a16(16, 17920, 1536, r),
+    "w4a16_down_m16": lambda r: case_w4a16(16, 1536, 8960, r),
+    "fp8_gate_up_m1": lambda r: case_fp8(1, 17920, 1536, r),
+    "fp8_gate_up_m16": lambda r: case_fp8(16, 17920, 1536, r),
+    "rms_qkv_m1": lambda r: case_rms_w4a16(2048, 1536, r, True),
+    "rms_gate_up_m1": lambda r: case_rms_w4a16(17920, 1536, r, False),
+    "swiglu_down_m1": lambda r: case_swiglu_w4a16(1536, 8960, r),
+    "attention_l392": lambda r: case_attention(r),
+    "rmsnorm_res_m2048": lambda r: case_rmsnorm(2048, 1536, r),
+    "swiglu_m2048": lambda r: case_swiglu(2048, 8960, r),
+}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reps", type=int, default=40)
+    ap.add_argument("--cases", default=",".join(CASES))
+    args = ap.parse_args(argv)
+    torch.cuda.init()
+    for name in args.cases.split(","):
+        CASES[name](args.reps)
+        torch.cuda.synchronize()
+        print(f"case {name}: {args.reps} launches", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
