@@ -582,7 +582,9 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 
 // ------------------------------------------------------------------------------ MFMA kernel
 //
-// M <= 16 rows (padded to 16) on v_mfma_f32_16x16x32_f16. A workgroup owns CW = 64 * NH output
+// Rows in blocks of 16 * MT (MT = 1 for decode, padded to 16; MT = 2 for M > 16, one block per
+// grid row, the decoded weights of a K step serving both 16-row tiles; the other blocks re-read
+// the weights from the MALL) on v_mfma_f32_16x16x32_f16. A workgroup owns CW = 64 * NH output
 // columns (NH 128-byte line halves of the packed rows: 128 columns on wide shapes, 140 workgroups
 // for gate_up, one per CU, instead of 280 that put two 64-column tiles on 24 CUs) and a range of
 // quantization groups; its waves (up to 16 at 64 columns, 8 at 128) take groups round-robin, CPW
@@ -599,8 +601,8 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 // row in the same fragment layout. A group then adds s * (sum x*(1024+q) - (1024+z) * sum x) =
 // s * sum x*(q - z) to the fp32 accumulator: 4 VALU ops per 8 weights plus a per-group epilogue,
 // against 12 for dequantizing every weight to fp16 first.
-template <int NH, int KS, int CPW>  // KS: 32-wide K steps per group (group_size / 32)
-__global__ __launch_bounds__(NH == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args a, SplitArgs sp) {
+template <int NH, int KS, int CPW, int MT>  // KS: 32-wide K steps per group; MT: 16-row tiles
+__global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args a, SplitArgs sp) {
   constexpr int CW = 64 * NH, NT = 4 * NH;  // columns, 16-column MFMA tiles
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
   extern __shared__ __align__(16) unsigned char smem[];
@@ -614,35 +616,45 @@ __global__ __launch_bounds__(NH == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args
   ldk::pin_sgpr(a.qw);
   const TileWork tw = map_block(sp, ng);
   const int n0 = tw.tile * CW;
+  const int m0 = blockIdx.y * 16 * MT;  // first row of this workgroup's row block
   int col[NH];
 #pragma unroll
   for (int h = 0; h < NH; ++h) col[h] = min(n0 + 64 * h + 4 * c16, a.N - 4);  // clamped: tail lanes store nothing
   const int gb = tw.gb, ge = tw.ge;
-  const int xrow = min(c16, a.M - 1);
-  const bool xok = c16 < a.M;
-  const int mrows = min(a.M, 16);
+  int xrow[MT];
+  bool xok[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    xrow[t] = min(m0 + 16 * t + c16, a.M - 1);
+    xok[t] = m0 + 16 * t + c16 < a.M;
+  }
+  const int mrows = min(a.M - m0, 16 * MT);
   float* red = reinterpret_cast<float*>(smem);  // [NW][mrows][CW]
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>();
   const half8v ones = {(half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f,
                        (half_t)1.0f, (half_t)1.0f, (half_t)1.0f, (half_t)1.0f};
-  float4_t acc[NT];
+  float4_t acc[MT][NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[t][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int g0 = gb + wave; g0 < ge; g0 += NW * CPW) {
-    // loads in consumption order, group by group: per K step the A fragment and the weight
+    // loads in consumption order, group by group: per K step the A fragments and the weight
     // words of each half, then the zero points and scales (used after the group's MFMAs)
     u32x2 zv[CPW][NH], sv[CPW][NH];
-    u32x4 ar[CPW][KS], w[CPW][KS][NH];
+    u32x4 ar[CPW][KS][MT], w[CPW][KS][NH];
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       const int g = min(g0 + NW * c, ge - 1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int r = g * rpg + 4 * ks + kb;
-        ar[c][ks] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)xrow * a.ldx + 8 * r);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          ar[c][ks][t] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)xrow[t] * a.ldx + 8 * r);
 #pragma unroll
         for (int h = 0; h < NH; ++h)
           w[c][ks][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col[h]));
@@ -657,28 +669,37 @@ __global__ __launch_bounds__(NH == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       if (g0 + NW * c >= ge) break;  // uniform
-      float4_t tmp[NT], sx = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      float4_t tmp[MT][NT], sx[MT];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) tmp[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int t = 0; t < MT; ++t) {
+        sx[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < NT; ++j) tmp[t][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        u32x4 ap = x_pairs(ar[c][ks]);
-        if (!xok) ap = u32x4{0u, 0u, 0u, 0u};
-        const half8v A = __builtin_bit_cast(half8v, ap);
+        u32x4 bq[NT];  // decoded once, used by every row tile
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const uint32_t wc = w[c][ks][h][j];
-            u32x4 bq;
-            bq[0] = (wc & mlo) | magic;          // 1024 + (q0, q4)
-            bq[1] = ((wc >> 4) & mlo) | magic;   // 1024 + (q1, q5)
-            bq[2] = ((wc >> 8) & mlo) | magic;   // 1024 + (q2, q6)
-            bq[3] = ((wc >> 12) & mlo) | magic;  // 1024 + (q3, q7)
-            tmp[4 * h + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, bq), tmp[4 * h + j], 0, 0, 0);
+            bq[4 * h + j][0] = (wc & mlo) | magic;          // 1024 + (q0, q4)
+            bq[4 * h + j][1] = ((wc >> 4) & mlo) | magic;   // 1024 + (q1, q5)
+            bq[4 * h + j][2] = ((wc >> 8) & mlo) | magic;   // 1024 + (q2, q6)
+            bq[4 * h + j][3] = ((wc >> 12) & mlo) | magic;  // 1024 + (q3, q7)
           }
         }
-        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ones, sx, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          u32x4 ap = x_pairs(ar[c][ks][t]);
+          if (!xok[t]) ap = u32x4{0u, 0u, 0u, 0u};
+          const half8v A = __builtin_bit_cast(half8v, ap);
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            tmp[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, bq[j]), tmp[t][j], 0, 0, 0);
+          sx[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ones, sx[t], 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int h = 0; h < NH; ++h) {
@@ -687,24 +708,31 @@ __global__ __launch_bounds__(NH == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args
         for (int j = 0; j < 4; ++j) {
           const float zz = 1024.0f + (float)z4[j], sj = (float)s4[j];
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[4 * h + j][i] = __builtin_fmaf(sj, __builtin_fmaf(-zz, sx[i], tmp[4 * h + j][i]), acc[4 * h + j][i]);
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[t][4 * h + j][i] =
+                  __builtin_fmaf(sj, __builtin_fmaf(-zz, sx[t][i], tmp[t][4 * h + j][i]), acc[t][4 * h + j][i]);
         }
       }
     }
   }
 
-  // tile (h, j), element i of lane l: row 4*kb + i, column 64h + 4*c16 + j of the workgroup's CW.
-  // Rows >= M are all zero and not stored; each lane writes 4 consecutive columns per half.
+  // tile (t, h, j), element i of lane l: row 16t + 4*kb + i of the block, column 64h + 4*c16 + j
+  // of the workgroup's CW. Rows past M are all zero and not stored; each lane writes 4
+  // consecutive columns per half.
   const int n = mrows * CW;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * kb + i;
-    if (row < mrows) {
+  for (int t = 0; t < MT; ++t) {
 #pragma unroll
-      for (int h = 0; h < NH; ++h)
-        *reinterpret_cast<float4_t*>(red + (size_t)wave * n + row * CW + 64 * h + 4 * c16) =
-            float4_t{acc[4 * h][i], acc[4 * h + 1][i], acc[4 * h + 2][i], acc[4 * h + 3][i]};
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * t + 4 * kb + i;
+      if (row < mrows) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+          *reinterpret_cast<float4_t*>(red + (size_t)wave * n + row * CW + 64 * h + 4 * c16) =
+              float4_t{acc[t][4 * h][i], acc[t][4 * h + 1][i], acc[t][4 * h + 2][i], acc[t][4 * h + 3][i]};
+      }
     }
   }
   __syncthreads();
@@ -712,7 +740,7 @@ __global__ __launch_bounds__(NH == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args
     const int m = o / CW, nn = n0 + (o - m * CW);
     if (nn < a.N) {
       if (a.bias) v += (float)a.bias[nn];
-      a.out[(int64_t)m * a.ldo + nn] = (half_t)v;
+      a.out[(int64_t)(m0 + m) * a.ldo + nn] = (half_t)v;
     }
   });
 }
@@ -726,7 +754,8 @@ struct Plan {
   int mt, ln, rpl, cpw;  // row tile, lanes along N (MFMA: 16 * 64-column halves), rows per lane,
                          // chunks (MFMA: groups) per wave and pass
   int nw, splits, gps;
-  int full;  // M = 1 kernel: leading tiles run whole while the rest split (0: all tiles alike)
+  int full;   // M = 1 kernel: leading tiles run whole while the rest split (0: all tiles alike)
+  int mtile;  // MFMA kernel: 16-row tiles per workgroup (1, or 2 when M > 16)
 };
 
 int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
@@ -756,7 +785,7 @@ int gemv_pxw(const Plan& p) { return (p.cpw * p.rpl * p.mt + p.ln - 1) / p.ln; }
 
 size_t plan_lds_bytes(const Plan& p, int64_t M) {
   if (p.kern == kM1) return 0;  // static LDS
-  if (p.kern == kMfma) return (size_t)p.nw * std::min<int64_t>(M, 16) * (4 * p.ln) * 4;
+  if (p.kern == kMfma) return (size_t)p.nw * std::min<int64_t>(M, 16 * p.mtile) * (4 * p.ln) * 4;
   return (size_t)p.nw * 64 * gemv_pxw(p) * 16 + (size_t)p.nw * p.mt * 4 * p.ln * 4;
 }
 
@@ -800,8 +829,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const bool m1 = !mfma && M == 1 && !(flags & LDK_EXACT);
   p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
   p.mt = mfma ? 16 : round_mt(M);
-  if (mfma) {  // 128 columns on shapes wide enough to fill the CUs with them, else 64
-    p.ln = block_n == 64 ? 16 : block_n == 128 ? 32 : (N >= 128 * 128 ? 32 : 16);
+  p.mtile = mfma && M > 16 ? 2 : 1;
+  if (mfma) {  // 128 columns on shapes wide enough to fill the CUs with them, else 64 (and 64 for
+              // 32-row blocks of group-256 weights, whose 128-column variant runs out of registers)
+    p.ln = block_n == 64 ? 16 : block_n == 128 ? 32 : (N >= 128 * 128 && !(M > 16 && rpg > 16) ? 32 : 16);
   } else if (block_n) {
     p.ln = block_n / 4;
   } else if (m1) {  // small shapes are latency-bound: more, narrower workgroups
@@ -826,8 +857,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // workgroup per CU). Multi-row splits carry M outputs per column through returning atomics,
   // so small shapes keep whole tiles and split K over the waves of a workgroup instead (q/o at
   // M = 16: 5.9 us whole, 25 us split twelve ways).
-  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20))
+  if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20) && M <= 16)
     splits = m1 ? std::max<int64_t>(2, 256 / tiles) : (192 + tiles - 1) / tiles;
+  if (M > 16) splits = 1;  // row blocks fill the grid; a K split would carry every row through atomics
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
   p.splits = (int)((ng + p.gps - 1) / p.gps);
@@ -871,9 +903,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   }
   if (mfma) {  // groups per wave and pass: all in one pass where registers allow (<= 16 waves at
               // 64 columns, <= 8 at 128)
-    const int wmax = p.ln == 16 ? 16 : 8;
+    const int wmax = p.ln == 16 && p.mtile == 1 ? 16 : 8;
     if (!cpw_from_flags(flags)) cpw = chunks > wmax ? 2 : 1;
-    cpw = std::min(cpw, rpg <= 16 ? 2 : 1);
+    cpw = std::min(cpw, rpg <= 16 && p.mtile == 1 ? 2 : 1);
     p.cpw = cpw;
     p.nw = (int)std::min<int64_t>(wmax, (chunks + cpw - 1) / cpw);
     return p;
@@ -980,25 +1012,39 @@ int launch_gemv_ln(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t l
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
 }
 
-template <int NH, int KS, int CPW>
+template <int NH, int KS, int CPW, int MT>
 int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipStream_t s) {
-  auto kern = w4a16_mfma_kernel<NH, KS, CPW>;
+  auto kern = w4a16_mfma_kernel<NH, KS, CPW, MT>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
+  const int64_t mblocks = (a.M + 16 * MT - 1) / (16 * MT);
+  if (mblocks > 65535) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: M=%d needs more than 65535 row blocks", a.M);
+  if (MT > 1 && sp.splits > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: row blocks of 32 take no K split");
   (void)hipGetLastError();
-  kern<<<(unsigned)(sp.full + sp.nsplit), nw * 64, lds, s>>>(a, sp);
+  kern<<<dim3((unsigned)(sp.full + sp.nsplit), (unsigned)mblocks), nw * 64, lds, s>>>(a, sp);
   return ldk::check_launch("w4a16_mfma");
 }
 
 template <int NH>
 int launch_mfma_nh(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
   const bool two = p.cpw == 2;
+  if (p.mtile == 2) {
+    switch (1 << a.gsh_rows) {
+      case 4: return launch_mfma_t<NH, 1, 1, 2>(a, sp, p.nw, lds, s);
+      case 8: return launch_mfma_t<NH, 2, 1, 2>(a, sp, p.nw, lds, s);
+      case 16: return launch_mfma_t<NH, 4, 1, 2>(a, sp, p.nw, lds, s);
+      case 32:
+        if constexpr (NH == 1) return launch_mfma_t<NH, 8, 1, 2>(a, sp, p.nw, lds, s);
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group_size 256 with M > 16 takes block_n=64");
+    }
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
+  }
   switch (1 << a.gsh_rows) {
-    case 4: return two ? launch_mfma_t<NH, 1, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 1, 1>(a, sp, p.nw, lds, s);
-    case 8: return two ? launch_mfma_t<NH, 2, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 2, 1>(a, sp, p.nw, lds, s);
-    case 16: return two ? launch_mfma_t<NH, 4, 2>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 4, 1>(a, sp, p.nw, lds, s);
-    case 32: return launch_mfma_t<NH, 8, 1>(a, sp, p.nw, lds, s);
+    case 4: return two ? launch_mfma_t<NH, 1, 2, 1>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 1, 1, 1>(a, sp, p.nw, lds, s);
+    case 8: return two ? launch_mfma_t<NH, 2, 2, 1>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 2, 1, 1>(a, sp, p.nw, lds, s);
+    case 16: return two ? launch_mfma_t<NH, 4, 2, 1>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 4, 1, 1>(a, sp, p.nw, lds, s);
+    case 32: return launch_mfma_t<NH, 8, 1, 1>(a, sp, p.nw, lds, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
 }
@@ -1070,7 +1116,7 @@ extern "C" int64_t ldk_workspace_bytes(void) { return (int64_t)32 << 20; }
 
 extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n, int* split_k, int* flags) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_config: sizes must be positive");
-  if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_config: only the decode path (M <= 16) has a table");
+
   const int gsh = log2_exact(group_size);
   if (gsh < 5 || gsh > 8 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "w4a16_config: bad group_size %d", group_size);
   const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
@@ -1087,7 +1133,7 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   int gsh_rows = 0;
   int st = validate("w4a16_matmul", x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
   if (st) return st;
-  if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: M=%lld > 16 (prefill GEMM not built yet)", (long long)M);
+  if (M > 65535LL * 32) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: M=%lld too large", (long long)M);
   if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_CPW_MASK))
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: unknown flags 0x%x", flags);
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: FACTORED and EXACT are exclusive");
@@ -1108,7 +1154,7 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
   if (p.kern == kMfma && block_n && block_n != 64 && block_n != 128)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n 64 or 128");
-  if (split_k > 1 && p.splits == 1 && (K / group_size) > 1)
+  if (split_k > 1 && p.splits == 1 && (K / group_size) > 1 && M <= 16)
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
                  (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, gsh_rows};

@@ -14,9 +14,13 @@ libldk_amd.so whose tile and K-split come from the library's per-shape table:
   the MFMA kernel where the table gives it the shape); M > 8 runs the MFMA kernel, which computes
   the same factored form on the matrix cores.
 
-Prefill shapes (M > 16) dequantize the weight once with the bit-exact HIP dequantizer and run
-one hipBLASLt/rocBLAS fp16 GEMM through torch (the reference runs its Triton tensor-core GEMM
-there, w4a16.py:264-268).
+Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268): up to
+PREFILL_NATIVE_MAX_M rows run the MFMA kernel in 32-row blocks over the packed weights (each
+block decodes the weights once for its two 16-row tiles; the other blocks re-read them from the
+MALL). Measured on MI355X against dequantize-once + hipBLASLt, it is faster at every Qwen2.5-1.5B
+shape up to 256 rows and slower beyond, so more rows dequantize the weight once with the
+bit-exact HIP dequantizer and run one hipBLASLt fp16 GEMM through torch. `config={"prefill":
+"native" | "dequant"}` forces either.
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
 `GEMV` (force the VALU decode kernel, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
@@ -37,6 +41,10 @@ from kernels import _lib
 from kernels.quant import PACK, dequantize
 
 _decode_choice: dict[tuple, str] = {}  # (m_key, N, K, bias) -> chosen configuration, for export
+
+# Rows up to which the hand-written MFMA kernel (32-row blocks over the packed weights) runs;
+# more rows dequantize once and run the library fp16 GEMM.
+PREFILL_NATIVE_MAX_M = 256
 
 
 def _next_pow2(n: int) -> int:
@@ -91,12 +99,13 @@ def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=No
     s = scales if scales.is_contiguous() else scales.contiguous()
     z = zeros if zeros.is_contiguous() else zeros.contiguous()
     b = None if bias is None else bias.to(torch.float16).contiguous()
-    if M <= 16:
+    prefill = (config or {}).get("prefill")
+    if M <= 16 or (prefill != "dequant" and (prefill == "native" or M <= PREFILL_NATIVE_MAX_M)):
         block_n, split_k, flags = _flags_from_config(config, M)
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
         key = (min(_next_pow2(M), 16), N, K, bias is not None)
-        if key not in _decode_choice:
+        if M <= 16 and key not in _decode_choice:
             _decode_choice[key] = config_for(M, N, K, group_size)
     else:
         w = dequantize(qw, s, z, group_size)

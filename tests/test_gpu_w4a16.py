@@ -238,6 +238,41 @@ def test_decode_entry(M):
     _run(M, 1536, 1536, entry=w4a16_decode_hip)
 
 
+# ------------------------------------------------------------- prefill rows (M > 16)
+@pytest.mark.parametrize("M", [17, 32, 33, 100, 128, 256])
+@pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (17920, 1536, False),
+                                      (1536, 8960, False), (96, 384, True)])
+def test_prefill_native_rows(M, N, K, bias):
+    """The MFMA kernel in 32-row blocks (the reference's prefill path, w4a16.py:264-268 and
+    tests/test_w4a16.py:93-97): row tails inside a block, bias, every Qwen width class."""
+    _run(M, N, K, bias=bias, config={"prefill": "native"})
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256])
+def test_prefill_native_group_sizes(gs):
+    _run(48, 4096, 2048, gs=gs, config={"prefill": "native"})
+    _run(40, 17920, 1024, gs=gs, config={"prefill": "native"})
+
+
+def test_prefill_paths_agree():
+    """Above the native threshold the wrapper dequantizes once and runs the library GEMM; both
+    paths meet the bar on the same inputs."""
+    for path in ("native", "dequant"):
+        _run(300, 2048, 1536, config={"prefill": path})
+
+
+def test_prefill_one_hot_rows_reproduce_dequantized_weight():
+    """x = e_k rows (k = 0, 7, 130, ...): row m of the output is column k of dequant(W), exact."""
+    N, K = 17920, 1536
+    _, qw, s, z, _ = _make(1, N, K, 5)
+    ks = [0, 7, 130, 511, 1024, 1535] * 6  # 36 rows, two row blocks
+    x = np.zeros((len(ks), K), dtype=np.float16)
+    x[np.arange(len(ks)), ks] = 1.0
+    out = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z), config={"prefill": "native"})
+    deq = dequantize_ref(qw, s, z)
+    assert np.array_equal(bits16(out), bits16(deq[:, ks].T))
+
+
 def test_decode_entry_rejects_17_rows():
     """As the reference's CUDA entry (tests/test_w4a16_cuda.py:43-45)."""
     with pytest.raises(RuntimeError):
