@@ -91,7 +91,8 @@ int64_t ldk_workspace_bytes(void);
 /* out [M, N] = x [M, K] @ dequant(qweight, scales, zeros)^T (+ bias [N]), fp32 accumulation,
  * fp16 output. Replaces kernels/w4a16.py:301-330 (w4a16_matmul) and its launch paths
  * w4a16.py:214-279. group_size a power of two in 32..256 dividing K; N % 4 == 0; x, qweight
- * 16-byte aligned with ldx % 8 == 0; scales, zeros 8-byte aligned. M <= 16.
+ * 16-byte aligned with ldx % 8 == 0; scales, zeros 8-byte aligned. M > 16 (prefill) runs the
+ * MFMA kernel in 32-row blocks without a cross-workgroup split (split_k is ignored there).
  *   block_n: output columns per workgroup, 16/32/64 (0 = table),
  *   split_k: workgroups splitting K per column tile (0 = table; > 1 needs the workspace),
  *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_VALU / LDK_PATH_MFMA, LDK_CPW_* (0 = table),
@@ -155,8 +156,8 @@ int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, void* out, 
 
 /* out [M, N] = x [M, K] @ (e4m3(wq) * scale)^T (+ bias), fp32 accumulation, fp16 out.
  * wq [K, N] e4m3fn, scale [N] fp16. Replaces kernels/fp8.py:200-223 (w8a16_matmul) and its
- * kernels fp8.py:42-127. N % 16 == 0 and 16-byte aligned wq; M <= 16; block_n, split_k, flags
- * and the workspace as for ldk_w4a16_matmul. */
+ * kernels fp8.py:42-127. N % 16 == 0 and 16-byte aligned wq; block_n, split_k, flags and the
+ * workspace as for ldk_w4a16_matmul. M > 16 (prefill) runs the MFMA kernel in 16-row blocks. */
 int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale,
                      const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
                      int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,

@@ -261,7 +261,8 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 
 // ------------------------------------------------------------------------ W8A16 MFMA kernel
 //
-// M <= 16 rows (padded to 16) on v_mfma_f32_16x16x32_f16, for M >= 8 where the VALU kernel's
+// Rows in blocks of 16 (padded; grid z walks the blocks, which re-read the weights from the
+// MALL) on v_mfma_f32_16x16x32_f16, for M >= 3 where the VALU kernel's
 // fp32 FMAs (16 x M per 16 weights) bound it. Lane l = (c16 = l % 16, kb = l / 16) of a wave:
 //  * B operand: for each 32-row K step it loads rows k0 + 8 kb + i (i < 8) at columns
 //    n0 + 8 c16 .. +7, one 8-byte load per row (16 lanes cover a 128-byte line of a row);
@@ -282,12 +283,13 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
   const int tile = blockIdx.x, split = blockIdx.y;
+  const int m0 = blockIdx.z * 16;  // row block (rows past 16 re-read the weights from the MALL)
   const int n0 = tile * CW;
   const int col = min(n0 + 8 * c16, a.N - 8);  // clamped: tail lanes load valid memory, store nothing
   const int rb = split * sp.kps, re = min(a.K, rb + sp.kps);
   const int nks = (re - rb + 31) / 32;  // K steps of this workgroup
-  const bool xrow_ok = c16 < a.M;
-  const half_t* xrow = a.x + (int64_t)min(c16, a.M - 1) * a.ldx;
+  const bool xrow_ok = m0 + c16 < a.M;
+  const half_t* xrow = a.x + (int64_t)min(m0 + c16, a.M - 1) * a.ldx;
 
   float4_t acc[8];
 #pragma unroll
@@ -355,7 +357,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
     *reinterpret_cast<float4_t*>(rrow + 4) = float4_t{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
   }
   ldk::lds_barrier();
-  const int mrows = min(a.M, 16);
+  const int mrows = min(a.M - m0, 16);
   for (int o = tid; o < mrows * CW; o += NW * 64) {
     const int m = o / CW, c = o - m * CW;
     const int n = n0 + c;
@@ -366,12 +368,12 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
     v *= (float)a.scale[n];
     if (sp.splits == 1) {
       if (a.bias) v += (float)a.bias[n];
-      a.out[(int64_t)m * a.ldo + n] = (half_t)v;
+      a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)v;
     } else {
       float tot;
-      if (ldk::splitk_add(sp.acc + (size_t)tile * 16 * CW + o, sp.splits, v, &tot)) {
+      if (ldk::splitk_add(sp.acc + ((size_t)blockIdx.z * gridDim.x + tile) * 16 * CW + o, sp.splits, v, &tot)) {
         if (a.bias) tot += (float)a.bias[n];
-        a.out[(int64_t)m * a.ldo + n] = (half_t)tot;
+        a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)tot;
       }
     }
   }
@@ -405,7 +407,7 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t w
   const int64_t sps = (steps + splits - 1) / splits;  // K steps per split
   p.kps = (int)(sps * 32);
   p.splits = (int)((steps + sps - 1) / sps);
-  if (p.splits > 1 && tiles * 16 * 128 * 8 > ws_bytes) {
+  if (p.splits > 1 && ((M + 15) / 16) * tiles * 16 * 128 * 8 > ws_bytes) {
     p.splits = 1;
     p.kps = (int)(steps * 32);
   }
@@ -417,7 +419,7 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t w
 template <int KSW>
 int launch_w8_mfma_t(const W8Args& a, const W8Split& sp, hipStream_t s) {
   constexpr int NW = kW8MfmaWaves;
-  const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)sp.splits, 1);
+  const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)sp.splits, (unsigned)((a.M + 15) / 16));
   const size_t lds = (size_t)NW * 16 * 128 * 4;
   (void)hipGetLastError();
   w8a16_mfma_kernel<NW, KSW><<<grid, NW * 64, lds, s>>>(a, sp);
@@ -548,7 +550,8 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
                                 void* workspace, int64_t workspace_bytes, void* stream) {
   if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: null pointer");
   if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: M, N, K must be positive");
-  if (M > 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld > 16 (prefill GEMM not built yet)", (long long)M);
+  if (M > 65535LL * 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld too large", (long long)M);
+  if (M > 16 && (flags & LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the VALU kernel takes M <= 16");
   if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N=%lld must be a multiple of 16", (long long)N);
   if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: K=%lld must be a multiple of 8", (long long)K);
   if (ldx < K || ldo < N) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: row stride smaller than K/N");
@@ -565,7 +568,7 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   // MFMA from 3 rows (the VALU kernel's fp32 FMAs grow with M; measured at M = 4: 17.4 us VALU,
   // 9.5 us MFMA at M = 8 on gate_up); block_n other than 128 keeps the
   // VALU kernel, which has the narrower tiles.
-  const bool mfma = (flags & LDK_PATH_MFMA) || (M >= 3 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
+  const bool mfma = M > 16 || (flags & LDK_PATH_MFMA) || (M >= 3 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
   if (mfma && block_n && block_n != 128) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the MFMA kernel uses block_n=128");
   const int64_t wsb = workspace ? workspace_bytes : 0;
   const W8Plan p = mfma ? make_w8_mfma_plan(M, N, K, split_k, wsb) : make_w8_plan(M, N, K, block_n, split_k, wsb);

@@ -4,8 +4,11 @@ Drop-in for the reference's `kernels/fp8.py`: weights are float8 e4m3fn with one
 channel, stored [K, N] (N contiguous). gfx950 decodes OCP e4m3 natively (v_cvt_pk_f32_fp8), so
 the weight bytes go straight from a 128-bit load to fp32 FMAs; the scale is applied once after
 the K reduction (fp8.py:120). Quantize/dequantize run HIP kernels that reproduce the reference
-bit for bit. Decode shapes (M <= 16) run the wave64 HIP GEMV with an in-workgroup split-K;
-M > 16 dequantizes once and runs a torch fp16 GEMM.
+bit for bit. Decode shapes run the wave64 VALU GEMV with an in-workgroup split-K at M <= 2 and
+the MFMA kernel (in-register byte transpose, exact e4m3 -> fp16) from 3 rows.
+Prefill rows (M > 16) run the MFMA kernel in 16-row blocks up to PREFILL_NATIVE_MAX_M rows
+(`config={"prefill": "native" | "dequant"}` forces a path); more rows dequantize once and run a
+torch fp16 GEMM.
 """
 
 from __future__ import annotations
@@ -47,6 +50,11 @@ def dequantize_fp8(wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# Rows up to which the MFMA kernel (16-row blocks over the e4m3 weights) runs; more rows
+# dequantize once and run the library fp16 GEMM.
+PREFILL_NATIVE_MAX_M = 256
+
+
 def fp8_bytes(N: int, K: int) -> int:
     """Weight bytes plus fp16 scales (fp8.py:38-39)."""
     return N * K + N * 2
@@ -69,8 +77,9 @@ def w8a16_matmul(x, wq, scale, bias=None, config=None):
     q = wq if wq.is_contiguous() else wq.contiguous()
     s = scale.contiguous()
     b = None if bias is None else bias.to(torch.float16).contiguous()
-    if M <= 16:
-        cfg = config or {}
+    cfg = config or {}
+    prefill = cfg.get("prefill")
+    if M <= 16 or (prefill != "dequant" and (prefill == "native" or M <= PREFILL_NATIVE_MAX_M)):
         flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
         if cfg.get("MFMA"):
             flags |= _lib.PATH_MFMA

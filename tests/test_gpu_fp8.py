@@ -104,6 +104,19 @@ def test_mfma_split_k(split_k):
     _run(8, 512, 8960, bias=True, config={"MFMA": True, "split_k": split_k})
 
 
+@pytest.mark.parametrize("M", [17, 33, 100, 256])
+@pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (1536, 8960, False), (48, 96, True)])
+def test_prefill_native_rows(M, N, K, bias):
+    """Prefill rows on the MFMA kernel in 16-row blocks (grid z), row tails inside a block, the
+    split-K words of each block kept apart (down splits K), bias."""
+    _run(M, N, K, bias=bias, config={"prefill": "native"})
+
+
+def test_prefill_paths_agree():
+    for path in ("native", "dequant"):
+        _run(300, 2048, 1536, config={"prefill": path})
+
+
 def test_mfma_one_hot_rows_exact():
     """x row m = e_{3m}: the MFMA path returns e4m3(wq[3m, n]) * scale exactly (one product,
     one rounding), so the in-register byte transpose and the decode are checked bit for bit."""
