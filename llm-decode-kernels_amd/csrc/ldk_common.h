@@ -1,5 +1,5 @@
 // Shared device/host helpers for the gfx950 decode kernels: status reporting for the C ABI,
-// packed fp16 types, the XCD-aware workgroup remap and the wave64 cross-lane reductions.
+// packed fp16 types, buffer-load helpers and the wave64 cross-lane reductions.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -30,16 +30,6 @@ __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (re
 
 // ---------------------------------------------------------------------------------- device side
 namespace ldk {
-
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on XCD b % 8), and
-// each XCD has its own L2. This bijection renumbers workgroups so that logical tiles t and t+1
-// (which share cache lines and scale rows) run on the same XCD.
-__device__ __forceinline__ int xcd_remap(int b, int n) {
-  constexpr int kXcd = 8;
-  const int q = n / kXcd, rem = n % kXcd;
-  const int x = b % kXcd;
-  return x * q + (x < rem ? x : rem) + b / kXcd;
-}
 
 // Buffer resource over [p, p + bytes) (gfx9 raw-buffer word 3): a raw buffer load at a byte
 // offset outside it returns zero and makes no memory request, so a load that only some lanes
