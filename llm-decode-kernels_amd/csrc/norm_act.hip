@@ -4,7 +4,8 @@
 // kernels/swiglu.py:14-61. Both keep the reference's fp16 rounding steps (kernels/reference.py:9-24):
 //   rmsnorm: h = fp16(x + r) (written as the new residual); var = sum(h^2) / N in fp32;
 //            out = w * fp16(h * (1 / sqrt(var + eps)))  (fp16 multiply, one rounding)
-//   swiglu:  out = fp16(g / (1 + exp(-g))) * u        (silu in fp32, fp16 multiply)
+//   swiglu:  out = fp16(g * rcp(1 + exp(-g))) * u     (silu in fp32 with the hardware reciprocal,
+//            1 ulp, as the reference's Triton kernel divides approximately; fp16 multiply)
 // Both are pure streaming kernels: every element is read once and written once, 16 bytes per lane.
 #include "ldk_common.h"
 
@@ -105,7 +106,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
     const float f = (float)g[j];
-    s[j] = (half_t)(f / (1.0f + expf(-f)));
+    s[j] = (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
   }
   *reinterpret_cast<hv_t*>(a.out + row * a.ldo + c) = s * u;  // fp16 multiply
 }

@@ -186,7 +186,7 @@ __device__ __forceinline__ u32x4 pro_stage(u32x4 xr, u32x4 x2, u32x4 x3, float r
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float f = (float)g[j];
-      sv[j] = (half_t)(f / (1.0f + expf(-f)));
+      sv[j] = (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
     }
     return __builtin_bit_cast(u32x4, sv * u);  // fp16 multiply
   } else {
