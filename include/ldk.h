@@ -39,8 +39,8 @@ enum ldk_dtype { LDK_F16 = 0, LDK_BF16 = 1, LDK_F32 = 2 };
 
 /* Flags for the matmul entry points (`flags`). Zero = let the library choose. */
 enum ldk_flags {
-  LDK_FACTORED = 1,  /* W4A16: s * sum x*(q - z) per group (w4a16.py:116-119, FACTORED): the M = 1
-                        VALU kernel, and always the MFMA kernel */
+  LDK_FACTORED = 1,  /* W4A16: s * sum x*(q - z) per group (w4a16.py:116-119, FACTORED): the
+                        VALU kernel for M <= 2, and always the MFMA kernel */
   LDK_EXACT = 2,     /* W4A16: dequantize each weight to fp16 exactly as dequantize_ref first (the
                         VALU kernels, M <= 8; not with LDK_PATH_MFMA) */
   LDK_PATH_VALU = 4, /* force the wave64 VALU (dot2) skinny kernel */

@@ -154,20 +154,31 @@ constexpr float kFixClamp = 1048576.0f;           // 2^20
 constexpr int64_t kFixPoison = int64_t(1) << 50;  // > 32 * 2^44, the largest legal sum
 constexpr int64_t kFixPoisonSeen = int64_t(3) << 48;
 
-// Adds partial p of one output to its accumulator word. Returns true in the one contribution that
-// completes the count; *total then holds the reduced value and the word is back to zero.
-__device__ __forceinline__ bool splitk_add(uint64_t* word, int splits, float p, float* total) {
+// The two halves of splitk_add, for a caller with several outputs per lane: issue every add first
+// (their round trips overlap), then finish each with the word it returned.
+__device__ __forceinline__ uint64_t splitk_inc(float p) {
   const int64_t v = __builtin_isfinite(p)
                         ? (int64_t)__builtin_rintf(__builtin_fminf(__builtin_fmaxf(p, -kFixClamp), kFixClamp) * kFixScale)
                         : kFixPoison;
-  const uint64_t inc = ((uint64_t)v << 8) + 1u;
-  const uint64_t old = __hip_atomic_fetch_add(word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return ((uint64_t)v << 8) + 1u;
+}
+__device__ __forceinline__ uint64_t splitk_issue(uint64_t* word, uint64_t inc) {
+  return __hip_atomic_fetch_add(word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool splitk_finish(uint64_t* word, int splits, uint64_t old, uint64_t inc, float* total) {
   if ((int)(old & 0xffu) != splits - 1) return false;
   const int64_t tot = (int64_t)(old + inc) >> 8;
   const bool poisoned = tot >= kFixPoisonSeen || tot <= -kFixPoisonSeen;
   *total = poisoned ? __builtin_nanf("") : (float)tot * (1.0f / kFixScale);
   __hip_atomic_store(word, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
+}
+
+// Adds partial p of one output to its accumulator word. Returns true in the one contribution that
+// completes the count; *total then holds the reduced value and the word is back to zero.
+__device__ __forceinline__ bool splitk_add(uint64_t* word, int splits, float p, float* total) {
+  const uint64_t inc = splitk_inc(p);
+  return splitk_finish(word, splits, splitk_issue(word, inc), inc, total);
 }
 
 template <typename Part, typename Store>

@@ -28,15 +28,16 @@
 // (0x6400) is exactly the fp16 value 1024 + q, so one v_and_or_b32 per pair turns packed nibbles
 // into fp16 pairs (q_i, q_{i+4}); x is staged as the matching pairs (x_i, x_{i+4}).
 //
-//  - M = 1 kernel (FACTORED): s * (sum x*q - z * sum x) per group, the reference's FACTORED
-//    identity (kernels/w4a16.py:116-119). Nibbles 1/3/5/7 are masked in place as 16*q and meet x
-//    pairs pre-scaled by 1/16; one v_dot2_f32_f16 chain per column runs over the lane's four rows
-//    of a group, starting at -1024*(offset-weighted sum of x): 9 VALU ops per 8 weights. All tile
-//    parameters are compile-time, so the epilogue is straight-line code.
+//  - M = 1 kernel (FACTORED, M <= 2): s * (sum x*q - z * sum x) per group, the reference's
+//    FACTORED identity (kernels/w4a16.py:116-119). Nibbles 1/3/5/7 are masked in place as 16*q
+//    and meet x pairs pre-scaled by 1/16; one v_dot2_f32_f16 chain per column and row runs over
+//    the lane's four rows of a group, starting at -1024*(offset-weighted sum of x): 5 + 4M VALU
+//    ops per 8 weights (the nibble pairs are decoded once for both rows). All tile parameters are
+//    compile-time, so the epilogue is straight-line code.
 //  - VALU kernel (M <= 8, EXACT): ((1024+q) - (1024+z)) * s in packed fp16 is exactly the
 //    reference's dequantized weight (one RNE rounding, kernels/reference.py:35), then dot2 with
-//    each x row. Also the M = 1 path when exact dequantization is requested.
-//  - MFMA kernel (larger M): an int32 word holds 8 consecutive K of one column, which is exactly
+//    each x row. The path when exact dequantization is requested.
+//  - MFMA kernel (from 3 rows): an int32 word holds 8 consecutive K of one column, which is exactly
 //    one lane's B operand of v_mfma_f32_16x16x32_f16. A lane's 128-bit load feeds four 16x16
 //    tiles; B = (q - z) exactly in fp16, A = x rows permuted to the nibble-pair order, the fp32
 //    tile of one group is scaled by s once.
@@ -203,15 +204,29 @@ __device__ __forceinline__ u32x4 pro_stage(u32x4 xr, u32x4 x2, u32x4 x3, float r
   }
 }
 
-template <int LN, int NW, int RSH, int PRO>
-__global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
+// Static LDS of the M = 1 kernel: x records [NW][MR][RPW] of 32 bytes, wave partials [NW][MR][LN]
+// float4 and the statistic slots. Instantiations are limited to 48 KiB so that three workgroups
+// fit a CU.
+constexpr int m1_lds_bytes(int ln, int nw, int mr) { return nw * mr * (256 / ln) * 32 + nw * mr * ln * 16 + nw * 4; }
+constexpr bool m1_lds_ok(int ln, int nw, int mr) { return m1_lds_bytes(ln, nw, mr) <= 48 * 1024; }
+
+// The one-row 32-column kernel is held to 7 waves per SIMD (<= 72 VGPRs): the gate_up grid
+// averages 3.1 six-wave workgroups per CU, and at 6 waves per SIMD a CU's fourth workgroup does
+// not fit and runs as a tail (measured 5.17 -> 5.80 us at 73 VGPRs).
+template <int LN, int NW, int RSH, int PRO, int MR>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LN == 8 && NW <= 8 && PRO == kProNone ? 7 : 1)))
+void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
+  static_assert(MR == 1 || PRO == kProNone, "fused prologues take one row");
   constexpr int LKW = 64 / LN, RPL = 4, RPW = RPL * LKW, CW = 4 * LN;
+  // x records of a pass: MR rows x RPW packed rows, XL per lane (record r = lane + 64 i is row
+  // r / RPW, packed row r % RPW of the pass)
+  constexpr int XREC = MR * RPW, XL = (XREC + 63) / 64;
   constexpr bool kExact = PRO == kProRmsX || PRO == kProRmsResX;
   constexpr bool kRes = PRO == kProRmsRes || PRO == kProRmsResX;
   constexpr bool kRms = kExact || PRO == kProRms || PRO == kProRmsRes;
   constexpr int kStatV = 2;  // row vectors per thread loaded ahead of the pass (general variants)
-  __shared__ __align__(16) unsigned char xrec[NW][RPW][32];
-  __shared__ __align__(16) float4_t red[NW][LN];
+  __shared__ __align__(16) unsigned char xrec[NW][MR][RPW][32];
+  __shared__ __align__(16) float4_t red[NW][MR][LN];
   __shared__ float stat[NW];
   const int rsh = RSH ? RSH : a.gsh_rows;  // log2(packed rows per group), >= 2
   const int lgsh = rsh - 2;    // log2(LG)
@@ -233,13 +248,21 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
 
   // ---- loads of one pass, in consumption order: x row(s), scale and zero words, weight rows
   struct Pass {
-    u32x4 xr, x2, x3;
+    u32x4 xr[XL], x2, x3;
     u32x2 sv, zv;
     u32x4 w[RPL];
   };
   auto load_pass = [&](int gp, Pass& P) {
     const int xo = 8 * min((gp << rsh) + lane, R - 1);
-    P.xr = *reinterpret_cast<const u32x4*>(a.x + xo);
+    if constexpr (MR == 1) {
+      P.xr[0] = *reinterpret_cast<const u32x4*>(a.x + xo);
+    } else {
+#pragma unroll
+      for (int i = 0; i < XL; ++i) {  // rows past M repeat the last row; their outputs are not stored
+        const int r = lane + 64 * i, m = min(r / RPW, a.M - 1);
+        P.xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)m * a.ldx + 8 * min((gp << rsh) + r % RPW, R - 1));
+      }
+    }
     if constexpr (kRes) P.x2 = *reinterpret_cast<const u32x4*>(pa.res + xo);
     if constexpr (PRO == kProSwiglu) P.x2 = *reinterpret_cast<const u32x4*>(a.x + a.K + xo);
     if constexpr (kRms) P.x3 = *reinterpret_cast<const u32x4*>(pa.nw + xo);
@@ -268,7 +291,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
     // become a branch around the loads)
     const uint32_t dead = ldk::vgpr_const<0>() | (live ? 0u : kOut);
     const uint32_t xo = (16u * (uint32_t)min((gp << rsh) + lane, R - 1)) | dead;
-    P.xr = ldk::buffer_load16(xb, xo);
+    P.xr[0] = ldk::buffer_load16(xb, xo);
     if constexpr (kRes) P.x2 = ldk::buffer_load16(rb, xo);
     P.x3 = ldk::buffer_load16(nb, xo);
     const int g = min(gp + gi, ge - 1);
@@ -312,7 +335,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
     const bool wr = kRes && blockIdx.x == 0;
     if constexpr (kExact) {  // this wave's pass rows, lanes < RPW
       if (lane < RPW) {
-        half8_t h = __builtin_bit_cast(half8_t, P.xr);
+        half8_t h = __builtin_bit_cast(half8_t, P.xr[0]);
         if constexpr (kRes) h = h + __builtin_bit_cast(half8_t, P.x2);
         if (wr) *reinterpret_cast<half8_t*>(pa.res_out + 8 * ((gp << rsh) + lane)) = h;
 #pragma unroll
@@ -347,93 +370,214 @@ __global__ __launch_bounds__(NW * 64) void w4a16_m1_kernel(W4Args a, SplitArgs s
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();  // v_and_or_b32 operands (see sgpr_const)
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[MR][4];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[m][q] = 0.0f;
   for (bool first = true; gp < ge; gp += NW * gpw, first = false) {
     if (!first) {
       if constexpr (kRms && !kExact) load_pass_buf(gp, true, P);
       else load_pass(gp, P);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (lane < RPW) store_fact_record(&xrec[wave][lane][0], pro_stage<PRO>(P.xr, P.x2, P.x3, rs));
-    ldk::wave_lds_sync();
-    u32x4 xp[RPL];
-    float c0 = 0.0f, xs = 0.0f;
+    if constexpr (MR == 1) {
+      if (lane < RPW) store_fact_record(&xrec[wave][0][lane][0], pro_stage<PRO>(P.xr[0], P.x2, P.x3, rs));
+    } else {
 #pragma unroll
-    for (int t = 0; t < RPL; ++t) {
-      const int rr = (gi << rsh) + sub + (t << lgsh);
-      xp[t] = *reinterpret_cast<const u32x4*>(&xrec[wave][rr][0]);
-      const float2_t k = *reinterpret_cast<const float2_t*>(&xrec[wave][rr][16]);
-      c0 += k[0];
-      xs += k[1];
+      for (int i = 0; i < XL; ++i) {
+        const int r = lane + 64 * i;
+        if (r < XREC) store_fact_record(&xrec[wave][r / RPW][r % RPW][0], P.xr[i]);
+      }
     }
-    float tt[4] = {c0, c0, c0, c0};
+    ldk::wave_lds_sync();
+    // one row: every record read up front; more rows: a packed row's records when it is used
+    // (registers: the kernel is held to 72 VGPRs)
+    u32x4 xp[MR][RPL];
+    float c0[MR], xs[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      c0[m] = 0.0f;
+      xs[m] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < RPL; ++t) {
+        const int rr = (gi << rsh) + sub + (t << lgsh);
+        if constexpr (MR == 1) xp[m][t] = *reinterpret_cast<const u32x4*>(&xrec[wave][m][rr][0]);
+        const float2_t k = *reinterpret_cast<const float2_t*>(&xrec[wave][m][rr][16]);
+        c0[m] += k[0];
+        xs[m] += k[1];
+      }
+    }
+    float tt[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tt[m][q] = c0[m];
 #pragma unroll
     for (int t = 0; t < RPL; ++t) {  // rows in arrival order
+      if constexpr (MR > 1) {
+        const int rr = (gi << rsh) + sub + (t << lgsh);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+        for (int m = 0; m < MR; ++m) xp[m][t] = *reinterpret_cast<const u32x4*>(&xrec[wave][m][rr][0]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // the decoded nibble pairs are common to all rows
         const uint32_t wc = P.w[t][q], v = wc >> 8;
-        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][3]), ldk::u2h2((v & mhi) | magic), tt[q], false);
-        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][2]), ldk::u2h2((v & mlo) | magic), tt[q], false);
-        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][1]), ldk::u2h2((wc & mhi) | magic), tt[q], false);
-        tt[q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[t][0]), ldk::u2h2((wc & mlo) | magic), tt[q], false);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          tt[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][t][3]), ldk::u2h2((v & mhi) | magic), tt[m][q], false);
+          tt[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][t][2]), ldk::u2h2((v & mlo) | magic), tt[m][q], false);
+          tt[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][t][1]), ldk::u2h2((wc & mhi) | magic), tt[m][q], false);
+          tt[m][q] = __builtin_amdgcn_fdot2(ldk::u2h2(xp[m][t][0]), ldk::u2h2((wc & mlo) | magic), tt[m][q], false);
+        }
       }
     }
     const bool gok = gp + gi < ge;
     const half4_t s4 = __builtin_bit_cast(half4_t, P.sv), z4 = __builtin_bit_cast(half4_t, P.zv);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {  // s * (sum x*q - z * sum x)
-      const float v = (float)s4[q] * __builtin_fmaf(-(float)z4[q], xs, tt[q]);
-      acc[q] += gok ? v : 0.0f;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float v = (float)s4[q] * __builtin_fmaf(-(float)z4[q], xs[m], tt[m][q]);
+        acc[m][q] += gok ? v : 0.0f;
+      }
     }
     ldk::wave_lds_sync();  // the next pass rewrites this wave's records
   }
 
   // ---- reduction: lanes sharing ln within the wave, then the NW waves through LDS
+  if constexpr (MR == 1) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) acc[q] = ldk::sum_lanes_strided<LN>(acc[q]);
+    for (int q = 0; q < 4; ++q) acc[0][q] = ldk::sum_lanes_strided<LN>(acc[0][q]);
+    if (one_wave) {
+      if (wave != 0) return;
+      // lane l < CW owns output n0 + l: element l % 4 of the lanes holding columns 4(l/4)..
+      const int src = (lane >> 2) % LN, e = lane & 3;
+      const float e0 = __shfl(acc[0][0], src), e1 = __shfl(acc[0][1], src);
+      const float e2 = __shfl(acc[0][2], src), e3 = __shfl(acc[0][3], src);
+      const float v = e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3;
+      const int c = n0 + lane;
+      float tot;
+      if (lane < CW && c < a.N && ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
+        if (a.bias) tot += (float)a.bias[c];
+        a.out[c] = (half_t)tot;
+      }
+      return;
+    }
+    if (lane < LN) red[wave][0][lane] = float4_t{acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+    __syncthreads();
+    if (wave != 0) return;
+    if (whole || sp.splits == 1) {
+      const int c = n0 + 4 * lane;
+      if (lane >= LN || c >= a.N) return;
+      float4_t v = red[0][0][lane];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) v += red[i][0][lane];
+      if (a.bias) v += float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
+      const half4_t o{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+      if (out_vec) {
+        *reinterpret_cast<half4_t*>(a.out + c) = o;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a.out[c + q] = o[q];
+      }
+    } else {
+      // one output per lane, so the CW returning atomics of the tile are in flight together
+      const int c = n0 + lane;
+      if (lane >= CW || c >= a.N) return;
+      const float* rf = reinterpret_cast<const float*>(&red[0][0][0]);
+      float v = rf[lane];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) v += rf[i * CW + lane];
+      float tot;
+      if (ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
+        if (a.bias) tot += (float)a.bias[c];
+        a.out[c] = (half_t)tot;
+      }
+    }
+    return;
+  }
+  // ---- several rows: the split-K words of a split tile are [MR][CW] (row m, column n0 + l)
+  const int mrows = min(MR, a.M);
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[m][q] = ldk::sum_lanes_strided<LN>(acc[m][q]);
+  uint64_t* const words = whole ? nullptr : sp.acc + (size_t)(tile - sp.full) * MR * CW;
   if (one_wave) {
     if (wave != 0) return;
     // lane l < CW owns output n0 + l: element l % 4 of the lanes holding columns 4(l/4)..
     const int src = (lane >> 2) % LN, e = lane & 3;
-    const float e0 = __shfl(acc[0], src), e1 = __shfl(acc[1], src), e2 = __shfl(acc[2], src), e3 = __shfl(acc[3], src);
-    const float v = e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3;
     const int c = n0 + lane;
-    float tot;
-    if (lane < CW && c < a.N && ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
-      if (a.bias) tot += (float)a.bias[c];
-      a.out[c] = (half_t)tot;
+    uint64_t inc[MR], old[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float e0 = __shfl(acc[m][0], src), e1 = __shfl(acc[m][1], src);
+      const float e2 = __shfl(acc[m][2], src), e3 = __shfl(acc[m][3], src);
+      inc[m] = ldk::splitk_inc(e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3);
+    }
+    if (lane >= CW || c >= a.N) return;
+#pragma unroll
+    for (int m = 0; m < MR; ++m)  // every add in flight before the first result is used
+      if (m < mrows) old[m] = ldk::splitk_issue(words + m * CW + lane, inc[m]);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float tot;
+      if (m < mrows && ldk::splitk_finish(words + m * CW + lane, sp.splits, old[m], inc[m], &tot)) {
+        if (a.bias) tot += (float)a.bias[c];
+        a.out[(int64_t)m * a.ldo + c] = (half_t)tot;
+      }
     }
     return;
   }
-  if (lane < LN) red[wave][lane] = float4_t{acc[0], acc[1], acc[2], acc[3]};
+  if (lane < LN) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[wave][m][lane] = float4_t{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+  }
   __syncthreads();
   if (wave != 0) return;
   if (whole || sp.splits == 1) {
-    const int c = n0 + 4 * lane;
-    if (lane >= LN || c >= a.N) return;
-    float4_t v = red[0][lane];
+    // lane l: row l / LN, columns n0 + 4 (l % LN) .. +3
 #pragma unroll
-    for (int i = 1; i < NW; ++i) v += red[i][lane];
-    if (a.bias) v += float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
-    const half4_t o{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-    if (out_vec) {
-      *reinterpret_cast<half4_t*>(a.out + c) = o;
-    } else {
+    for (int l0 = 0; l0 < MR * LN; l0 += 64) {
+      const int l = l0 + lane, m = l / LN, j = l % LN;
+      const int c = n0 + 4 * j;
+      if (l >= MR * LN || m >= mrows || c >= a.N) continue;
+      float4_t v = red[0][m][j];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a.out[c + q] = o[q];
+      for (int i = 1; i < NW; ++i) v += red[i][m][j];
+      if (a.bias) v += float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
+      const half4_t o{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+      half_t* dst = a.out + (int64_t)m * a.ldo + c;
+      if (out_vec) {
+        *reinterpret_cast<half4_t*>(dst) = o;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[q] = o[q];
+      }
     }
   } else {
-    // one output per lane, so the CW returning atomics of the tile are in flight together
+    // one output per lane and row, so the CW returning atomics of a row are in flight together
     const int c = n0 + lane;
     if (lane >= CW || c >= a.N) return;
-    const float* rf = reinterpret_cast<const float*>(&red[0][0]);
-    float v = rf[lane];
+    uint64_t inc[MR], old[MR];
 #pragma unroll
-    for (int i = 1; i < NW; ++i) v += rf[i * CW + lane];
-    float tot;
-    if (ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
-      if (a.bias) tot += (float)a.bias[c];
-      a.out[c] = (half_t)tot;
+    for (int m = 0; m < MR; ++m) {
+      float v = reinterpret_cast<const float*>(&red[0][m][0])[lane];
+#pragma unroll
+      for (int i = 1; i < NW; ++i) v += reinterpret_cast<const float*>(&red[i][m][0])[lane];
+      inc[m] = ldk::splitk_inc(v);
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < mrows) old[m] = ldk::splitk_issue(words + m * CW + lane, inc[m]);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float tot;
+      if (m < mrows && ldk::splitk_finish(words + m * CW + lane, sp.splits, old[m], inc[m], &tot)) {
+        if (a.bias) tot += (float)a.bias[c];
+        a.out[(int64_t)m * a.ldo + c] = (half_t)tot;
+      }
     }
   }
 }
@@ -630,6 +774,13 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
   }
   const int mrows = min(a.M - m0, 16 * MT);
   float* red = reinterpret_cast<float*>(smem);  // [NW][mrows][CW]
+  // A rows past M are buffer loads past the end of the resource: zeros, and no memory request,
+  // so a decode block of M < 16 rows moves only its M rows of x
+  // (the resource spans this block's rows; the launcher keeps it below 2 GiB)
+  const auto xb = ldk::buffer_rsrc(a.x + (int64_t)m0 * a.ldx, (uint32_t)((int64_t)(mrows - 1) * a.ldx * 2 + a.K * 2));
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xoff[t] = xok[t] ? (uint32_t)((int64_t)(xrow[t] - m0) * a.ldx * 2) : 0x80000000u;
 
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>();
@@ -653,8 +804,7 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
       for (int ks = 0; ks < KS; ++ks) {
         const int r = g * rpg + 4 * ks + kb;
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-          ar[c][ks][t] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)xrow[t] * a.ldx + 8 * r);
+        for (int t = 0; t < MT; ++t) ar[c][ks][t] = ldk::buffer_load16(xb, xoff[t] + 16u * (uint32_t)r);
 #pragma unroll
         for (int h = 0; h < NH; ++h)
           w[c][ks][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col[h]));
@@ -692,8 +842,7 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
         }
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          u32x4 ap = x_pairs(ar[c][ks][t]);
-          if (!xok[t]) ap = u32x4{0u, 0u, 0u, 0u};
+          const u32x4 ap = x_pairs(ar[c][ks][t]);  // zeros past M
           const half8v A = __builtin_bit_cast(half8v, ap);
 #pragma unroll
           for (int j = 0; j < NT; ++j)
@@ -781,6 +930,13 @@ int m1_round_nw(int64_t want) {
   return 16;
 }
 
+// Most waves per workgroup the M = 1 kernel is instantiated for at this tile width and row count.
+int m1_max_waves(int ln, int mr) {
+  for (int i = (int)(sizeof(kM1Waves) / sizeof(kM1Waves[0])) - 1; i > 0; --i)
+    if (m1_lds_ok(ln, kM1Waves[i], mr)) return kM1Waves[i];
+  return 1;
+}
+
 int gemv_pxw(const Plan& p) { return (p.cpw * p.rpl * p.mt + p.ln - 1) / p.ln; }
 
 size_t plan_lds_bytes(const Plan& p, int64_t M) {
@@ -819,14 +975,14 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const int rpg = 1 << gsh_rows;
   const int64_t ng = (K / 8) >> gsh_rows;
   const int64_t wbytes = N * K / 2;
-  // MFMA from 5 rows (3 on shapes of > 4 MB): its B operand costs 4 VALU ops per 8 weights for
-  // all 16 rows, the VALU kernel's dequantize-then-dot grows by 4 dot2 per 8 weights per row.
-  // A block_n only the VALU kernels take (16 or 32) keeps M <= 8 on the VALU path.
-  // EXACT keeps M <= 8 on the VALU kernels, which dequantize every weight as dequantize_ref does.
-  const bool mfma_auto =
-      M > 8 || (!(flags & LDK_EXACT) && (M > 4 || (M > 2 && wbytes > (4 << 20))) && (block_n == 0 || block_n >= 64));
+  // M = 1 and 2 run the factored VALU kernel (5 + 4M VALU ops per 8 weights, issued once the
+  // pass's loads land: with 4 rows that compute alone outlasts the loads), from 3 rows the MFMA
+  // kernel (4 VALU ops per 8 weights for all 16 rows of its B operand). A block_n only the VALU
+  // kernels take (16 or 32) keeps M <= 8 on the VALU path. EXACT keeps M <= 8 on the VALU
+  // kernels, which dequantize every weight as dequantize_ref does.
+  const bool mfma_auto = M > 8 || (!(flags & LDK_EXACT) && M > 2 && (block_n == 0 || block_n >= 64));
   const bool mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
-  const bool m1 = !mfma && M == 1 && !(flags & LDK_EXACT);
+  const bool m1 = !mfma && !(flags & LDK_EXACT) && M <= 2;  // the factored VALU kernel
   p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
   p.mt = mfma ? 16 : round_mt(M);
   p.mtile = mfma && M > 16 ? 2 : 1;
@@ -891,7 +1047,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const int64_t chunks = ((p.full ? ng : p.gps) + gw - 1) / gw;  // wave passes of the largest workgroup
   if (m1) {
     p.cpw = 1;
-    p.nw = m1_round_nw(std::min<int64_t>(16, chunks));
+    p.nw = m1_round_nw(std::min<int64_t>(m1_max_waves(p.ln, p.mt), chunks));
     return p;
   }
   // chunks per wave and round: the smallest that fits all chunks in one round of <= 16 waves
@@ -916,9 +1072,26 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   return p;
 }
 
+template <int LN, int NW, int MR>
+int launch_m1_rows(const W4Args& a, const SplitArgs& sp, int out_vec, hipStream_t stream) {
+  if constexpr (m1_lds_ok(LN, NW, MR)) {
+    const unsigned grid = (unsigned)(sp.full + sp.nsplit);
+    ProArgs pa{};
+    (void)hipGetLastError();
+    if (a.gsh_rows == 4)
+      w4a16_m1_kernel<LN, NW, 4, kProNone, MR><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa);
+    else
+      w4a16_m1_kernel<LN, NW, 0, kProNone, MR><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa);
+    return ldk::check_launch("w4a16_m1");
+  } else {
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %d rows on %d waves of block_n %d exceed the LDS budget", MR, NW,
+                     4 * LN);
+  }
+}
+
 template <int LN, int NW>
-int launch_m1_t(const W4Args& a, const SplitArgs& sp, int pro, const ProArgs& pa, hipStream_t stream) {
-  const int out_vec = ldk::aligned(a.out, 8) ? 1 : 0;
+int launch_m1_t(const W4Args& a, const SplitArgs& sp, int mr, int pro, const ProArgs& pa, hipStream_t stream) {
+  const int out_vec = ldk::aligned(a.out, 8) && (a.M == 1 || a.ldo % 4 == 0) ? 1 : 0;
   const unsigned grid = (unsigned)(sp.full + sp.nsplit);
   if (pro != kProNone) {
     // fused prologues are built for the decode tile widths and group size 128
@@ -931,11 +1104,11 @@ int launch_m1_t(const W4Args& a, const SplitArgs& sp, int pro, const ProArgs& pa
       if (exact && pro == kProRms) pro = kProRmsX;
       if (exact && pro == kProRmsRes) pro = kProRmsResX;
       switch (pro) {
-        case kProRms: w4a16_m1_kernel<LN, NW, 4, kProRms><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
-        case kProRmsRes: w4a16_m1_kernel<LN, NW, 4, kProRmsRes><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
-        case kProRmsX: w4a16_m1_kernel<LN, NW, 4, kProRmsX><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
-        case kProRmsResX: w4a16_m1_kernel<LN, NW, 4, kProRmsResX><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
-        case kProSwiglu: w4a16_m1_kernel<LN, NW, 4, kProSwiglu><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRms: w4a16_m1_kernel<LN, NW, 4, kProRms, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsRes: w4a16_m1_kernel<LN, NW, 4, kProRmsRes, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsX: w4a16_m1_kernel<LN, NW, 4, kProRmsX, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsResX: w4a16_m1_kernel<LN, NW, 4, kProRmsResX, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProSwiglu: w4a16_m1_kernel<LN, NW, 4, kProSwiglu, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         default: return ldk::fail(LDK_ERR_INVALID, "w4a16: unknown prologue %d", pro);
       }
       return ldk::check_launch("w4a16_m1");
@@ -943,25 +1116,24 @@ int launch_m1_t(const W4Args& a, const SplitArgs& sp, int pro, const ProArgs& pa
       return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues take block_n 16 or 32");
     }
   }
-  (void)hipGetLastError();
-  if (a.gsh_rows == 4)
-    w4a16_m1_kernel<LN, NW, 4, kProNone><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa);
-  else
-    w4a16_m1_kernel<LN, NW, 0, kProNone><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa);
-  return ldk::check_launch("w4a16_m1");
+  switch (mr) {
+    case 1: return launch_m1_rows<LN, NW, 1>(a, sp, out_vec, stream);
+    case 2: return launch_m1_rows<LN, NW, 2>(a, sp, out_vec, stream);
+  }
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: row tile %d not instantiated for the factored VALU kernel", mr);
 }
 
 template <int LN>
-int launch_m1_ln(const W4Args& a, const SplitArgs& sp, int nw, int pro, const ProArgs& pa, hipStream_t s) {
+int launch_m1_ln(const W4Args& a, const SplitArgs& sp, int nw, int mr, int pro, const ProArgs& pa, hipStream_t s) {
   switch (nw) {
-    case 1: return launch_m1_t<LN, 1>(a, sp, pro, pa, s);
-    case 2: return launch_m1_t<LN, 2>(a, sp, pro, pa, s);
-    case 3: return launch_m1_t<LN, 3>(a, sp, pro, pa, s);
-    case 4: return launch_m1_t<LN, 4>(a, sp, pro, pa, s);
-    case 6: return launch_m1_t<LN, 6>(a, sp, pro, pa, s);
-    case 8: return launch_m1_t<LN, 8>(a, sp, pro, pa, s);
-    case 12: return launch_m1_t<LN, 12>(a, sp, pro, pa, s);
-    case 16: return launch_m1_t<LN, 16>(a, sp, pro, pa, s);
+    case 1: return launch_m1_t<LN, 1>(a, sp, mr, pro, pa, s);
+    case 2: return launch_m1_t<LN, 2>(a, sp, mr, pro, pa, s);
+    case 3: return launch_m1_t<LN, 3>(a, sp, mr, pro, pa, s);
+    case 4: return launch_m1_t<LN, 4>(a, sp, mr, pro, pa, s);
+    case 6: return launch_m1_t<LN, 6>(a, sp, mr, pro, pa, s);
+    case 8: return launch_m1_t<LN, 8>(a, sp, mr, pro, pa, s);
+    case 12: return launch_m1_t<LN, 12>(a, sp, mr, pro, pa, s);
+    case 16: return launch_m1_t<LN, 16>(a, sp, mr, pro, pa, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %d waves per workgroup not instantiated", nw);
 }
@@ -1021,6 +1193,8 @@ int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
   const int64_t mblocks = (a.M + 16 * MT - 1) / (16 * MT);
   if (mblocks > 65535) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: M=%d needs more than 65535 row blocks", a.M);
   if (MT > 1 && sp.splits > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: row blocks of 32 take no K split");
+  if ((int64_t)(16 * MT - 1) * a.ldx * 2 + (int64_t)a.K * 2 >= (int64_t(1) << 31))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: a row block of x spans 2 GiB or more (ldx=%lld)", (long long)a.ldx);
   (void)hipGetLastError();
   kern<<<dim3((unsigned)(sp.full + sp.nsplit), (unsigned)mblocks), nw * 64, lds, s>>>(a, sp);
   return ldk::check_launch("w4a16_mfma");
@@ -1064,9 +1238,9 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro
       return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d too wide for group_size %d on the M = 1 kernel",
                        4 * p.ln, 8 << a.gsh_rows);
     switch (p.ln) {
-      case 4: return launch_m1_ln<4>(a, sp, p.nw, pro, pa, s);
-      case 8: return launch_m1_ln<8>(a, sp, p.nw, pro, pa, s);
-      case 16: return launch_m1_ln<16>(a, sp, p.nw, pro, pa, s);
+      case 4: return launch_m1_ln<4>(a, sp, p.nw, p.mt, pro, pa, s);
+      case 8: return launch_m1_ln<8>(a, sp, p.nw, p.mt, pro, pa, s);
+      case 16: return launch_m1_ln<16>(a, sp, p.nw, p.mt, pro, pa, s);
     }
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
   }
@@ -1138,15 +1312,15 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: unknown flags 0x%x", flags);
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: FACTORED and EXACT are exclusive");
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: VALU and MFMA paths are exclusive");
-  if ((flags & LDK_FACTORED) && M > 1 && !(flags & LDK_PATH_MFMA))
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED with more than one row is the MFMA kernel (LDK_PATH_MFMA)");
+  if ((flags & LDK_FACTORED) && (flags & LDK_PATH_VALU) && M > 2)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED on the VALU kernel takes M <= 2; more rows run it on the MFMA kernel");
   if ((flags & LDK_EXACT) && (flags & LDK_PATH_MFMA))
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel computes the factored form; EXACT runs on the VALU kernels (M <= 8)");
   if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the VALU kernel takes M <= 8");
   if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=%d must be 16, 32, 64 or 128 (MFMA)", block_n);
-  if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && !(M > 4 || (M > 2 && N * K / 2 > (4 << 20))))
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=128 is the MFMA kernel's tile (M > 4 or the MFMA flag)");
+  if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && (M <= 2 || (flags & (LDK_EXACT | LDK_PATH_VALU))))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=128 is the MFMA kernel's tile (M > 2 or the MFMA flag)");
   if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d must be >= 0", split_k);
   if (split_k > kMaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: split_k=%d above %d", split_k, kMaxSplits);
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))

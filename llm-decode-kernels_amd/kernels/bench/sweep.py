@@ -46,7 +46,7 @@ def _row(kind, shape, M, ms, nbytes, extra=None) -> dict:
     return r
 
 
-def w4a16_rows(Ms=(1, 4, 16)):
+def w4a16_rows(Ms=(1, 2, 4, 8, 16)):
     from kernels.quant import quantize_rtn, weight_bytes
     from kernels.w4a16 import config_for, w4a16_matmul
 

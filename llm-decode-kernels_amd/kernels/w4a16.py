@@ -9,10 +9,10 @@ libldk_amd.so whose tile and K-split come from the library's per-shape table:
   shapes with many bytes (the down projection) also split K across workgroups that meet in a
   per-device workspace, all within the one launch, so there is no zero-fill or cast launch (the
   reference's split paths add two elementwise launches, w4a16.py:218-219,272-275);
-- M = 1 uses the FACTORED inner loop s * (sum x*q - z * sum x) (w4a16.py:116-119); 2 <= M <= 8
-  dequantizes each weight exactly as dequantize_ref and accumulates with v_dot2_f32_f16 (or runs
-  the MFMA kernel where the table gives it the shape); M > 8 runs the MFMA kernel, which computes
-  the same factored form on the matrix cores.
+- M = 1 and M = 2 use the FACTORED inner loop s * (sum x*q - z * sum x) (w4a16.py:116-119) on
+  the VALU, each packed word decoded once for both rows; from 3 rows the MFMA kernel computes the
+  same factored form on the matrix cores. `config={"FACTORED": False}` (EXACT, M <= 8) instead
+  dequantizes each weight exactly as dequantize_ref and accumulates with v_dot2_f32_f16.
 
 Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268): up to
 PREFILL_NATIVE_MAX_M rows run the MFMA kernel in 32-row blocks over the packed weights (each
@@ -23,8 +23,9 @@ bit-exact HIP dequantizer and run one hipBLASLt fp16 GEMM through torch. `config
 "native" | "dequant"}` forces either.
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
-`GEMV` (force the VALU decode kernel, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
-(True: factored M=1 loop; False: exact dequantize-then-dot on the VALU kernels, M <= 8),
+`GEMV` (force the VALU decode kernels, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
+(True: the factored loop, on the VALU kernel for M <= 2; False: exact dequantize-then-dot on the
+VALU kernels, M <= 8),
 `block_n` (columns per workgroup: 16, 32 or 64; 64 or 128 on the MFMA kernel), `split_k`
 (workgroups splitting K per column tile) and `chunks_per_wave` (1, 2 or 4: load chunks a wave
 keeps in flight per round). Triton tile keys (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, GROUP_M)
@@ -60,7 +61,7 @@ def _flags_from_config(config: dict | None, M: int) -> tuple[int, int, int]:
     if config.get("MFMA"):
         flags |= _lib.PATH_MFMA
     if "FACTORED" in config:
-        if config["FACTORED"] and M == 1:
+        if config["FACTORED"] and (M <= 2 or not config.get("GEMV")):
             flags |= _lib.FACTORED
         elif not config["FACTORED"]:
             flags |= _lib.EXACT

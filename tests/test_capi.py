@@ -87,17 +87,18 @@ def test_misaligned_pointer_rejected():
     assert st == _lib.ERR_ALIGN
 
 
-def test_factored_needs_one_row():
+def test_factored_valu_takes_two_rows():
+    """The factored VALU kernel takes M <= 2; more rows run the factored form on the MFMA kernel,
+    so FACTORED with the VALU path is refused from 3 rows (before any launch)."""
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    st, _ = _err(lib.ldk_w4a16_matmul(p, 256, p, p, p, None, p, 64, 2, 64, 256, 128, 0, 0,
-                                      _lib.FACTORED, None, 0, None))
-    assert st == _lib.ERR_UNSUPPORTED
+    st, msg = _err(lib.ldk_w4a16_matmul(p, 256, p, p, p, None, p, 64, 3, 64, 256, 128, 0, 0,
+                                        _lib.FACTORED | _lib.PATH_VALU, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "M <= 2" in msg
 
 
 def test_exact_is_not_the_mfma_kernel():
-    """The MFMA kernel computes the factored form: EXACT with the MFMA path is refused, and a
-    FACTORED multi-row call needs the MFMA path."""
+    """The MFMA kernel computes the factored form: EXACT with the MFMA path is refused."""
     lib = _lib.load()
     p = ctypes.c_void_p(256)
     st, msg = _err(lib.ldk_w4a16_matmul(p, 256, p, p, p, None, p, 64, 16, 64, 256, 128, 0, 0,
@@ -150,6 +151,13 @@ def test_config_query():
     st = _lib.load().ldk_w4a16_config(16, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
     assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 128
+    # two rows: the factored VALU kernel; from three rows the MFMA kernel, also on small shapes
+    st = _lib.load().ldk_w4a16_config(2, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
+                                      ctypes.byref(fl))
+    assert st == 0 and fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU and bn.value == 32
+    st = _lib.load().ldk_w4a16_config(3, 1536, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
+                                      ctypes.byref(fl))
+    assert st == 0 and fl.value & _lib.PATH_MFMA
 
 
 def test_workspace_size():

@@ -59,6 +59,7 @@ def test_block_n_variants(block_n):
 def test_split_k_variants(split_k):
     """Cross-workgroup split of K (partials meet in the workspace; the last workgroup reduces)."""
     _run(1, 1536, 1536, config={"block_n": 32, "split_k": split_k})
+    _run(2, 1536, 1536, config={"split_k": split_k})
     _run(3, 1536, 1536, config={"split_k": split_k})
     _run(16, 1536, 1536, config={"split_k": split_k})
 
@@ -203,6 +204,35 @@ def test_one_hot_rows_reproduce_dequantized_weight(factored):
         assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, k0:k0 + 16].T))), k0
 
 
+def test_two_rows_factored_paths():
+    """M = 2 runs the factored VALU kernel with two x rows per pass: whole tiles, the gate_up
+    hybrid (one-wave split pieces), the down projection's LDS-reduced split, bias, strided rows."""
+    _run(2, 17920, 1536, bias=True)
+    _run(2, 1536, 8960, bias=True)
+    _run(2, 2048, 1536, bias=True)
+    for bn in (16, 32, 64):
+        _run(2, 1000, 1024, config={"block_n": bn})
+    x, qw, s, z, _ = _make(2, 256, 512, 4)
+    big = torch.zeros(2, 1024, dtype=torch.float16, device="cuda")
+    big[:, :512] = dev(x)
+    assert_north_star(w4a16_matmul(big[:, :512], dev(qw), dev(s), dev(z)), w4a16_ref(x, qw, s, z))
+
+
+@pytest.mark.parametrize("N,K", [(256, 512), (1536, 8960)])
+def test_two_rows_one_hot_reproduce_dequantized_weight(N, K):
+    """Two rows e_j, e_k: both output rows are exact columns of dequant(W), through whole tiles
+    (256 x 512) and the cross-workgroup split (1536 x 8960)."""
+    _, qw, s, z, _ = _make(1, N, K, 9)
+    deq = dequantize_ref(qw, s, z, 128)
+    qwd, sd, zd = dev(qw), dev(s), dev(z)
+    for j, k in ((0, 1), (7, K - 1), (K // 2 + 3, 129), (K - 8, 8)):
+        x = torch.zeros(2, K, dtype=torch.float16, device="cuda")
+        x[0, j] = 1.0
+        x[1, k] = 1.0
+        got = w4a16_matmul(x, qwd, sd, zd).cpu().numpy()
+        assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, [j, k]].T))), (j, k)
+
+
 def test_one_hot_multi_row():
     """M = 16 rows, row m = e_m: the exact path returns dequantized weights too."""
     N, K = 128, 256
@@ -221,7 +251,7 @@ def test_config0_headline():
     assert e["rel_l2"] < 1e-3
 
 
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 2, 4, 16])
 @pytest.mark.parametrize("name,N,K", cases.QWEN_LINEARS)
 def test_config2_qwen_shapes(name, N, K, M):
     _run(M, N, K, seed=2)
