@@ -190,7 +190,10 @@ int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void*
  *   kt_cache: fp16 [nkv][head_dim][max_len] (K transposed), v_cache: fp16 [nkv][max_len][head_dim];
  *   out:      [nq*head_dim] fp16; scale: the softmax scale (head_dim^-0.5).
  * head_dim == 128, nq % nkv == 0, max_len a multiple of 8 (kt_cache and v_cache 16-byte
- * aligned). A *pos outside 0..max_len-1 writes nothing and attends over the whole cache.
+ * aligned). A *pos >= max_len writes nothing and attends over the whole cache; a negative *pos
+ * writes nothing and returns zeros. Caches of more than 512 positions are split into up to 32
+ * position ranges per head whose partials meet in library-owned device state that each launch
+ * leaves zeroed (graph replay is safe); calls on one device must be stream-ordered.
  * Replaces the per-layer attention of the
  * reference's runner for decode steps (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into
  * the cache, scaled_dot_product_attention with the causal mask). */

@@ -9,10 +9,17 @@
 // the cache keeps K transposed, kt [nkv][128][max_len], and V as v [nkv][max_len][128]; out
 // [nq*128] fp16. max_len is a multiple of 8 (16-byte rows of 8 positions).
 //
-// Work split. One workgroup per query head (kv head h / (nq/nkv)), up to 8 waves. Wave w takes
-// the 64-position chunks w, w + nw, ... that hold live positions (<= pos). A chunk is 16 KB of K
+// Work split (flash-decoding). The cache positions are cut into `nsplit` ranges of S = 64 * cps
+// positions (at most 32 ranges of at least 8 chunks each: one range up to max_len 512), and the
+// grid is one workgroup per (query head, range): kv head h / (nq/nkv), up to 8 waves, wave w taking
+// the chunks w, w + nw, ... of its range that hold live positions (<= pos). A chunk is 16 KB of K
 // and 16 KB of V, and a wave issues all 32 of its 16-byte loads per lane before the first wait,
 // so the whole chunk is one memory round trip (a per-position loop would be 64 dependent ones).
+// One head's cache thus streams through as many CUs as it has ranges instead of one CU. Ranges
+// past pos exit at once. While pos lies in the first range, that workgroup writes the output
+// itself; otherwise every live range publishes its partial (running max m, sum l, unnormalised
+// output o[128]) to library-owned device memory and counts itself in with one agent-scope atomic,
+// and the last to arrive merges the partials, writes the output and re-zeroes the counter.
 //  - Scores: lane (pg = lane % 8, dg = lane / 8) loads K^T rows dg + 8i (i < 16), positions
 //    8pg .. 8pg+7 of the chunk, and sums q[d] * K[d][p] over its 16 rows for its 8 positions;
 //    lanes sharing pg are summed with DPP/permlane (stride 8).
@@ -21,8 +28,9 @@
 //  - Output: lane (dc = lane % 16, pr = lane / 16) loads V rows 16pr + i (i < 16), dims
 //    8dc .. 8dc+7, weighted by the chunk's softmax numerators (passed through LDS); lanes sharing
 //    dc are summed with permlane swaps (stride 16).
-// The cache at `pos` is stale while the first workgroup of the group writes the new k/v, so the
-// score at pos is recomputed from the roped k in LDS and the V row at pos is replaced by the new v.
+// The cache at `pos` is stale while the range holding pos (first head of the group) writes the new
+// k/v, so the score at pos is recomputed from the roped k in LDS and the V row at pos is replaced
+// by the new v. Calls on one device must be stream-ordered (the partials and counters are shared).
 //
 // Numerics: RoPE as the reference's fp16 torch ops (cos/sin of pos * inv_freq in fp32 rounded to
 // fp16, q*cos and rotate_half(q)*sin each rounded to fp16, their sum rounded); scores from the
@@ -39,6 +47,20 @@ constexpr int kHD = 128;
 constexpr int kMaxWaves = 8;
 constexpr int kChunk = 64;  // positions per wave pass
 constexpr int64_t kMaxLen = 1 << 20;
+constexpr int kMaxSplits = 32;  // position ranges per head
+constexpr int kMaxHeads = 64;   // query heads that can split (more heads run one range each)
+// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt and lgkmcnt unconstrained
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+constexpr int kMinChunksPerSplit = 8;  // a range keeps >= 8 chunks (512 positions) of work
+// Partials of the ranges of a launch in progress: {m, l} per [head][range], o per
+// [head][dim][range] (a dim's partials of every range are contiguous for the merge), and per head
+// the number of ranges that have published theirs (0 between launches).
+__device__ float g_ml[kMaxHeads][kMaxSplits][2];
+__device__ __align__(16) float g_o[kMaxHeads][kHD][kMaxSplits];
+__device__ uint32_t g_arrive[kMaxHeads];
+// buffer-load cache policy: sc1, read at the device coherence point (as agent-scope atomic loads)
+constexpr int kCoherent = 16;
 
 struct AttnArgs {
   const half_t* qkv;
@@ -48,17 +70,19 @@ struct AttnArgs {
   half_t* v;              // [nkv][max_len][128]
   half_t* out;            // [nq*128]
   int nq, nkv, max_len;
+  int cps;                // 64-position chunks per range (gridDim.y ranges)
   float scale;
 };
 
-// fp16 RoPE of element d of a 128-vector x (rotate_half pairs d with d +- 64).
-__device__ __forceinline__ half_t rope_elem(const half_t* x, int d, float ang) {
+// fp16 RoPE of the pair (x[d], x[d + 64]) of a 128-vector, d < 64 (rotate_half pairs d with
+// d + 64): returns (x[d] c - x[d+64] s, x[d+64] c + x[d] s) with the reference's fp16 roundings.
+__device__ __forceinline__ void rope_pair(const half_t* x, int d, float ang, half_t* lo, half_t* hi) {
   const half_t c = (half_t)cosf(ang), s = (half_t)sinf(ang);
-  const half_t xd = x[d];
-  const half_t rh = d < 64 ? (half_t)(-(float)x[d + 64]) : x[d - 64];
-  const half_t a = (half_t)((float)xd * (float)c);
-  const half_t b = (half_t)((float)rh * (float)s);
-  return (half_t)((float)a + (float)b);
+  const half_t x0 = x[d], x1 = x[d + 64];
+  const half_t a0 = (half_t)((float)x0 * (float)c), b0 = (half_t)(-(float)x1 * (float)s);
+  const half_t a1 = (half_t)((float)x1 * (float)c), b1 = (half_t)((float)x0 * (float)s);
+  *lo = (half_t)((float)a0 + (float)b0);
+  *hi = (half_t)((float)a1 + (float)b1);
 }
 
 __device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (lo16(a), lo16(b))
@@ -88,7 +112,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
   __shared__ __align__(16) float pw[kMaxWaves][kChunk];  // softmax numerators of a wave's chunk
   __shared__ __align__(16) float ow[kMaxWaves][kHD];     // per-wave unnormalized outputs
   __shared__ float mw[kMaxWaves], lw[kMaxWaves];
-  const int h = blockIdx.x;
+  __shared__ int last_flag;
+  const int h = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
   const int g = a.nq / a.nkv, kvh = h / g;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int L = a.max_len;
@@ -96,6 +121,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
   const bool pos_ok = pos_in >= 0 && pos_in < L;  // else: attend over the cache, write nothing
   const int pos = pos_ok ? (int)pos_in : pos_in < 0 ? -1 : L - 1;  // last live position
   const int npos = (int)pos_in;
+  // ranges [s0, s0 + S) holding live positions; the first one is live even with none (pos < 0)
+  const int S = a.cps * kChunk, s0 = split * S;
+  const int nlive = pos < 0 ? 1 : pos / S + 1;
+  if (split >= nlive) return;  // uniform over the workgroup
+  const int cend = min(s0 + S, pos + 1);  // chunk starts c0 < cend have live positions
   const half_t* q = a.qkv + (int64_t)h * kHD;
   const half_t* kx = a.qkv + (int64_t)a.nq * kHD + (int64_t)kvh * kHD;
   const half_t* vx = kx + (int64_t)a.nkv * kHD;
@@ -106,7 +136,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
   const int dc = lane & 15, pr = lane >> 4;   // output lanes
 
   // ---- first chunk's loads go out before the RoPE work, so both latencies overlap
-  int c0 = wave * kChunk;
+  int c0 = s0 + wave * kChunk;
   u32x4 kr[16], vr[16];
   auto issue = [&](int base) {
     const int p8 = min(base + 8 * pg, L - 8);
@@ -119,19 +149,27 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
       vr[i] = *reinterpret_cast<const u32x4*>(vc + (int64_t)p * kHD + 8 * dc);
     }
   };
-  if (c0 <= pos) issue(c0);
+  if (c0 < cend) issue(c0);
 
-  // ---- RoPE (q, new k), stage the new k/v, write them to the cache (first head of the group)
-  if (tid < kHD) {
-    const float ang = (float)pos_in * a.inv_freq[tid & 63];
-    qs[tid] = (float)rope_elem(q, tid, ang);
-    const half_t k1 = rope_elem(kx, tid, ang);
-    const half_t v1 = vx[tid];
-    knew[tid] = k1;
-    vnew[tid] = v1;
-    if (h % g == 0 && pos_ok) {
-      kt[(int64_t)tid * L + npos] = k1;
-      vc[(int64_t)npos * kHD + tid] = v1;
+  // ---- RoPE (q, new k) on dims (d, d + 64), stage the new k/v; the range holding pos writes them
+  // to the cache (first head of the group)
+  if (tid < 64) {
+    const float ang = (float)pos_in * a.inv_freq[tid];
+    half_t lo, hi;
+    rope_pair(q, tid, ang, &lo, &hi);
+    qs[tid] = (float)lo;
+    qs[tid + 64] = (float)hi;
+    rope_pair(kx, tid, ang, &lo, &hi);
+    knew[tid] = lo;
+    knew[tid + 64] = hi;
+    const half_t v0 = vx[tid], v1 = vx[tid + 64];
+    vnew[tid] = v0;
+    vnew[tid + 64] = v1;
+    if (h % g == 0 && pos_ok && npos >= s0 && npos < s0 + S) {
+      kt[(int64_t)tid * L + npos] = lo;
+      kt[(int64_t)(tid + 64) * L + npos] = hi;
+      vc[(int64_t)npos * kHD + tid] = v0;
+      vc[(int64_t)npos * kHD + tid + 64] = v1;
     }
   }
   ldk::lds_barrier();
@@ -151,7 +189,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.0f;
 
-  for (; c0 <= pos; c0 += nw * kChunk) {
+  for (; c0 < cend; c0 += nw * kChunk) {
     // ---- partial scores for positions c0 + 8pg + j over rows dg + 8i: rows 2r and 2r+1 are
     // paired with v_perm_b32 and meet the q pair in one v_dot2_f32_f16
     float s[8];
@@ -230,7 +268,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
       for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(p_new, (float)vnew[8 * dc + e], o[e]);
     }
     ldk::wave_lds_sync();  // pw is rewritten by the next chunk
-    if (c0 + nw * kChunk <= pos) issue(c0 + nw * kChunk);
+    if (c0 + nw * kChunk < cend) issue(c0 + nw * kChunk);
   }
   // ---- lanes sharing dc hold parts of the same 8 outputs: sum over pr
 #pragma unroll
@@ -244,17 +282,79 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
     lw[wave] = l_run;
   }
   ldk::lds_barrier();
-  if (tid < kHD) {
-    float M = -__builtin_inff();
+  // ---- merge the waves of this range: threads < 64 take dims d and d + 64
+  float M = -__builtin_inff(), l = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
+  if (tid < 64) {
     for (int w = 0; w < nw; ++w) M = fmaxf(M, mw[w]);
-    float l = 0.0f, acc = 0.0f;
     for (int w = 0; w < nw; ++w) {
       const float f = mw[w] == -__builtin_inff() ? 0.0f : __expf(mw[w] - M);
       l = __builtin_fmaf(lw[w], f, l);
-      acc = __builtin_fmaf(ow[w][tid], f, acc);
+      acc0 = __builtin_fmaf(ow[w][tid], f, acc0);
+      acc1 = __builtin_fmaf(ow[w][tid + 64], f, acc1);
     }
-    a.out[(int64_t)h * kHD + tid] = (half_t)(l > 0.0f ? acc / l : 0.0f);
   }
+  half_t* out = a.out + (int64_t)h * kHD;
+  if (nlive == 1) {  // the only live range: final output
+    if (tid < 64) {
+      out[tid] = (half_t)(l > 0.0f ? acc0 / l : 0.0f);
+      out[tid + 64] = (half_t)(l > 0.0f ? acc1 / l : 0.0f);
+    }
+    return;
+  }
+  // ---- publish this range's partial, count in; the last range to arrive merges them all.
+  // The partials move only through accesses performed at the device coherence point (sc1:
+  // agent-scope atomic stores, buffer loads with sc1). All stores are wave 0's, which waits for
+  // their completion (s_waitcnt vmcnt(0)) before its thread 0 bumps the counter, and the reads are
+  // issued after the counter's value has returned, so the counter needs no release/acquire of its
+  // own: those write back and invalidate the XCD's whole L2 in every workgroup.
+  if (tid < 64) {
+    __hip_atomic_store(&g_o[h][tid][split], acc0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&g_o[h][tid + 64][split], acc1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      __hip_atomic_store(&g_ml[h][split][0], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&g_ml[h][split][1], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this wave's partial stores have completed
+      const uint32_t before = __hip_atomic_fetch_add(&g_arrive[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = before == (uint32_t)(nlive - 1);
+    }
+  }
+  __syncthreads();
+  if (!last_flag || tid >= 64) return;
+  // ---- merge (wave 0 of the last range): lane r < nlive holds range r's (m, l); every lane then
+  // reads the 32 range partials of its dims d and d + 64 with 16-byte loads, all in flight at once
+  const int r = min(lane, nlive - 1);
+  const float mr = __hip_atomic_load(&g_ml[h][r][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float lr = __hip_atomic_load(&g_ml[h][r][1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const auto ob = ldk::buffer_rsrc(&g_o[h][0][0], (uint32_t)sizeof(g_o[0]));
+  u32x4 ov[2][kMaxSplits / 4];
+#pragma unroll
+  for (int k = 0; k < kMaxSplits / 4; ++k) {
+    ov[0][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ob, (uint32_t)((tid * kMaxSplits + 4 * k) * 4), 0, kCoherent));
+    ov[1][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ob, (uint32_t)(((tid + 64) * kMaxSplits + 4 * k) * 4), 0, kCoherent));
+  }
+  float Mg = lane < nlive ? mr : -__builtin_inff();
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) Mg = fmaxf(Mg, __shfl_xor(Mg, off));
+  const float fr = lane < nlive ? __expf(mr - Mg) : 0.0f;  // weight of range `lane`
+  float lg = lr * fr;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lg += __shfl_xor(lg, off);
+  float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kMaxSplits / 4; ++k) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = 4 * k + e;
+      const float f = __shfl(fr, rr);  // 0 past the live ranges, whose stale words are skipped
+      if (rr < nlive) {
+        o0 = __builtin_fmaf(ldk::u2f(ov[0][k][e]), f, o0);
+        o1 = __builtin_fmaf(ldk::u2f(ov[1][k][e]), f, o1);
+      }
+    }
+  }
+  out[tid] = (half_t)(lg > 0.0f ? o0 / lg : 0.0f);
+  out[tid + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
+  if (tid == 0) __hip_atomic_store(&g_arrive[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -270,11 +370,18 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
                      (long long)max_len, (long long)kMaxLen);
   if (!ldk::aligned(kt_cache, 16) || !ldk::aligned(v_cache, 16) || !ldk::aligned(pos, 8))
     return ldk::fail(LDK_ERR_ALIGN, "decode_attention: kt_cache and v_cache 16-byte, pos 8-byte aligned");
+  // position ranges: at most kMaxSplits of at least kMinChunksPerSplit whole 64-position chunks
+  // (one range per head when the heads exceed the partials' capacity); one wave per chunk of a
+  // range, up to 8. A split costs about three memory round trips to merge, so caches of up to
+  // 512 positions run one range (measured at max_len 256: 6.3 us one range, 8.3 us four).
+  const int64_t nchunks = (max_len + kChunk - 1) / kChunk;
+  const int64_t cps = nq <= kMaxHeads ? std::max<int64_t>(kMinChunksPerSplit, (nchunks + kMaxSplits - 1) / kMaxSplits)
+                                      : nchunks;
+  const int nsplit = (int)((nchunks + cps - 1) / cps);
+  const int nw = (int)std::min<int64_t>(kMaxWaves, cps);
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)kt_cache, (half_t*)v_cache, (half_t*)out,
-                   nq, nkv, (int)max_len, scale};
-  // >= 128 threads (one per dim for RoPE and the output), one wave per 64-position chunk up to 8
-  const int nw = (int)std::min<int64_t>(kMaxWaves, std::max<int64_t>(2, (max_len + kChunk - 1) / kChunk));
+                   nq, nkv, (int)max_len, (int)cps, scale};
   (void)hipGetLastError();
-  decode_attention_kernel<<<nq, nw * 64, 0, (hipStream_t)stream>>>(a);
+  decode_attention_kernel<<<dim3(nq, nsplit), nw * 64, 0, (hipStream_t)stream>>>(a);
   return ldk::check_launch("decode_attention");
 }

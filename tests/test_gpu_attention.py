@@ -25,8 +25,15 @@ def _rope64(x, pos, inv_freq):
 @pytest.mark.parametrize("nq,nkv,L,pos", [(12, 2, 392, 0), (12, 2, 392, 127), (12, 2, 392, 383),
                                           (12, 2, 392, 391), (12, 2, 392, 320), (4, 4, 64, 63),
                                           (8, 1, 512, 511), (16, 2, 136, 64), (12, 2, 8, 5),
-                                          (12, 2, 2048, 1500), (12, 2, 4096, 4095)])
+                                          (12, 2, 2048, 1500), (12, 2, 4096, 4095),
+                                          (72, 8, 256, 200), (64, 8, 2048, 2047),
+                                          (12, 2, 2112, 2111), (12, 2, 40000, 39999),
+                                          (12, 2, 40000, 700)])
 def test_against_float64(nq, nkv, L, pos):
+    """Cache lengths cover one position range (up to 512 positions), several ranges of 8 chunks
+    with a short last one (2048, 2112: 4 and 5 ranges, 4096: 8), 32 ranges of 20 chunks with
+    8 waves looping (40000), pos in the first range of a split cache (40000, 700), and more
+    heads than can split (72)."""
     g = torch.Generator().manual_seed(pos + 7 * nq)
     hd = 128
     qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half()
@@ -85,3 +92,58 @@ def test_pos_past_the_cache_writes_nothing():
     out = decode_attention(qkv, torch.tensor([L], device="cuda"), inv, kt, vc, nq, nkv, hd ** -0.5)
     assert torch.equal(kt, kt0) and torch.equal(vc, vc0)
     assert torch.isfinite(out).all()
+
+
+def _reference(qkv, kt_now, vc_now, nq, nkv, pos, inv_freq):
+    hd = 128
+    x = qkv.double().cpu().numpy()
+    q = _rope64(x[: nq * hd].reshape(nq, hd), pos, inv_freq.cpu().numpy())
+    K = kt_now[0].transpose(0, 2, 1)[:, : pos + 1]
+    V = vc_now[0][:, : pos + 1]
+    gq = nq // nkv
+    ref = np.zeros((nq, hd))
+    for h in range(nq):
+        s = K[h // gq] @ q[h] / math.sqrt(hd)
+        p = np.exp(s - s.max())
+        ref[h] = (p / p.sum()) @ V[h // gq]
+    return ref
+
+
+@pytest.mark.parametrize("L,steps", [(512, 301), (1536, 1100)])
+def test_decode_sequence_two_layers(L, steps):
+    """Decode steps over two layers' caches, as the runner issues them: every step writes its
+    k/v and attends over 0..pos. A 1536-position cache has three 512-position ranges, so from
+    pos 512 on a head's ranges meet through the shared partials and arrival counters, which each
+    launch must leave zeroed for the next."""
+    nq, nkv, hd = 12, 2, 128
+    g = torch.Generator().manual_seed(11)
+    inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    caches = [((torch.randn(1, nkv, hd, L, generator=g) * 0.7).half().cuda(),
+               torch.randn(1, nkv, L, hd, generator=g).half().cuda()) for _ in range(2)]
+    pos_t = torch.zeros(1, dtype=torch.int64, device="cuda")
+    edges = (63, 64, 65, 127, 128, 511, 512, 513, 1023, 1024, 1025, steps - 1)
+    for pos in range(steps):
+        pos_t.fill_(pos)
+        for li, (kt, vc) in enumerate(caches):
+            qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda()
+            out = decode_attention(qkv, pos_t, inv, kt, vc, nq, nkv, hd ** -0.5)
+            if pos % 50 == 0 or pos in edges:
+                ref = _reference(qkv, kt.cpu().double().numpy(), vc.cpu().double().numpy(), nq, nkv,
+                                 pos, inv)
+                got = out.view(nq, hd).cpu().double().numpy()
+                assert np.abs(got - ref).max() <= 2e-2, (pos, li)
+                assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2e-3, (pos, li)
+
+
+def test_negative_pos_attends_nothing():
+    """pos < 0: no live position, the output is zero and the cache is left as it was."""
+    nq, nkv, L, hd = 12, 2, 256, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda()
+    kt = torch.randn(1, nkv, hd, L, generator=g).half().cuda()
+    vc = torch.randn(1, nkv, L, hd, generator=g).half().cuda()
+    kt0, vc0 = kt.clone(), vc.clone()
+    out = decode_attention(qkv, torch.tensor([-1], device="cuda"), torch.ones(64, device="cuda"),
+                           kt, vc, nq, nkv, hd ** -0.5)
+    assert torch.equal(kt, kt0) and torch.equal(vc, vc0)
+    assert torch.count_nonzero(out) == 0
