@@ -745,9 +745,13 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 // row in the same fragment layout. A group then adds s * (sum x*(1024+q) - (1024+z) * sum x) =
 // s * sum x*(q - z) to the fp32 accumulator: 4 VALU ops per 8 weights plus a per-group epilogue,
 // against 12 for dequantizing every weight to fp16 first.
-template <int NH, int KS, int CPW, int MT>  // KS: 32-wide K steps per group; MT: 16-row tiles
+// NWD: packed words per lane and load, 4 (16-byte loads, 64-column halves) or 2 (8-byte loads,
+// 32-column tiles: the M = 1 kernel's 128-byte tile, whose grid fills every CU on wide shapes).
+template <int NH, int KS, int CPW, int MT, int NWD>  // KS: 32-wide K steps per group; MT: 16-row tiles
 __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_kernel(W4Args a, SplitArgs sp) {
-  constexpr int CW = 64 * NH, NT = 4 * NH;  // columns, 16-column MFMA tiles
+  static_assert(NWD == 2 || NWD == 4, "4 or 2 words per lane");
+  constexpr int HW = 16 * NWD;                 // columns of one load across the 16 column lanes
+  constexpr int CW = HW * NH, NT = NWD * NH;   // columns, 16-column MFMA tiles
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
   extern __shared__ __align__(16) unsigned char smem[];
   const int rpg = 4 * KS;
@@ -763,7 +767,7 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
   const int m0 = blockIdx.y * 16 * MT;  // first row of this workgroup's row block
   int col[NH];
 #pragma unroll
-  for (int h = 0; h < NH; ++h) col[h] = min(n0 + 64 * h + 4 * c16, a.N - 4);  // clamped: tail lanes store nothing
+  for (int h = 0; h < NH; ++h) col[h] = min(n0 + HW * h + NWD * c16, a.N - NWD);  // clamped: tail lanes store nothing
   const int gb = tw.gb, ge = tw.ge;
   int xrow[MT];
   bool xok[MT];
@@ -806,13 +810,25 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 #pragma unroll
         for (int t = 0; t < MT; ++t) ar[c][ks][t] = ldk::buffer_load16(xb, xoff[t] + 16u * (uint32_t)r);
 #pragma unroll
-        for (int h = 0; h < NH; ++h)
-          w[c][ks][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw + (int64_t)r * a.N + col[h]));
+        for (int h = 0; h < NH; ++h) {
+          const uint32_t* wp = a.qw + (int64_t)r * a.N + col[h];
+          if constexpr (NWD == 4) {
+            w[c][ks][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp));
+          } else {
+            const u32x2 w2 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wp));
+            w[c][ks][h] = u32x4{w2[0], w2[1], 0u, 0u};
+          }
+        }
       }
 #pragma unroll
       for (int h = 0; h < NH; ++h) {
-        zv[c][h] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col[h]);
-        sv[c][h] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col[h]);
+        if constexpr (NWD == 4) {
+          zv[c][h] = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col[h]);
+          sv[c][h] = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col[h]);
+        } else {
+          zv[c][h] = u32x2{*reinterpret_cast<const uint32_t*>(a.z + (int64_t)g * a.N + col[h]), 0u};
+          sv[c][h] = u32x2{*reinterpret_cast<const uint32_t*>(a.s + (int64_t)g * a.N + col[h]), 0u};
+        }
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
@@ -832,12 +848,12 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < NWD; ++j) {
             const uint32_t wc = w[c][ks][h][j];
-            bq[4 * h + j][0] = (wc & mlo) | magic;          // 1024 + (q0, q4)
-            bq[4 * h + j][1] = ((wc >> 4) & mlo) | magic;   // 1024 + (q1, q5)
-            bq[4 * h + j][2] = ((wc >> 8) & mlo) | magic;   // 1024 + (q2, q6)
-            bq[4 * h + j][3] = ((wc >> 12) & mlo) | magic;  // 1024 + (q3, q7)
+            bq[NWD * h + j][0] = (wc & mlo) | magic;          // 1024 + (q0, q4)
+            bq[NWD * h + j][1] = ((wc >> 4) & mlo) | magic;   // 1024 + (q1, q5)
+            bq[NWD * h + j][2] = ((wc >> 8) & mlo) | magic;   // 1024 + (q2, q6)
+            bq[NWD * h + j][3] = ((wc >> 12) & mlo) | magic;  // 1024 + (q3, q7)
           }
         }
 #pragma unroll
@@ -854,21 +870,21 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
       for (int h = 0; h < NH; ++h) {
         const half4_t z4 = __builtin_bit_cast(half4_t, zv[c][h]), s4 = __builtin_bit_cast(half4_t, sv[c][h]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NWD; ++j) {
           const float zz = 1024.0f + (float)z4[j], sj = (float)s4[j];
 #pragma unroll
           for (int t = 0; t < MT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              acc[t][4 * h + j][i] =
-                  __builtin_fmaf(sj, __builtin_fmaf(-zz, sx[t][i], tmp[t][4 * h + j][i]), acc[t][4 * h + j][i]);
+              acc[t][NWD * h + j][i] =
+                  __builtin_fmaf(sj, __builtin_fmaf(-zz, sx[t][i], tmp[t][NWD * h + j][i]), acc[t][NWD * h + j][i]);
         }
       }
     }
   }
 
-  // tile (t, h, j), element i of lane l: row 16t + 4*kb + i of the block, column 64h + 4*c16 + j
-  // of the workgroup's CW. Rows past M are all zero and not stored; each lane writes 4
+  // tile (t, h, j), element i of lane l: row 16t + 4*kb + i of the block, column HW*h + NWD*c16 + j
+  // of the workgroup's CW. Rows past M are all zero and not stored; each lane writes NWD
   // consecutive columns per half.
   const int n = mrows * CW;
 #pragma unroll
@@ -878,9 +894,14 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
       const int row = 16 * t + 4 * kb + i;
       if (row < mrows) {
 #pragma unroll
-        for (int h = 0; h < NH; ++h)
-          *reinterpret_cast<float4_t*>(red + (size_t)wave * n + row * CW + 64 * h + 4 * c16) =
-              float4_t{acc[t][4 * h][i], acc[t][4 * h + 1][i], acc[t][4 * h + 2][i], acc[t][4 * h + 3][i]};
+        for (int h = 0; h < NH; ++h) {
+          float* dst = red + (size_t)wave * n + row * CW + HW * h + NWD * c16;
+          if constexpr (NWD == 4)
+            *reinterpret_cast<float4_t*>(dst) =
+                float4_t{acc[t][4 * h][i], acc[t][4 * h + 1][i], acc[t][4 * h + 2][i], acc[t][4 * h + 3][i]};
+          else
+            *reinterpret_cast<float2_t*>(dst) = float2_t{acc[t][2 * h][i], acc[t][2 * h + 1][i]};
+        }
       }
     }
   }
@@ -987,8 +1008,13 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   p.mt = mfma ? 16 : round_mt(M);
   p.mtile = mfma && M > 16 ? 2 : 1;
   if (mfma) {  // 128 columns on shapes wide enough to fill the CUs with them, else 64 (and 64 for
-              // 32-row blocks of group-256 weights, whose 128-column variant runs out of registers)
-    p.ln = block_n == 64 ? 16 : block_n == 128 ? 32 : (N >= 128 * 128 && !(M > 16 && rpg > 16) ? 32 : 16);
+              // 32-row blocks of group-256 weights, whose 128-column variant runs out of registers);
+              // decode rows on shapes of <= 2 MB take 32 columns (q/o/k/v at M = 8: 4.7 -> 4.4 us)
+    p.ln = block_n == 32    ? 8
+           : block_n == 64  ? 16
+           : block_n == 128 ? 32
+           : (M <= 16 && wbytes <= (2 << 20)) ? 8
+           : (N >= 128 * 128 && !(M > 16 && rpg > 16) ? 32 : 16);
   } else if (block_n) {
     p.ln = block_n / 4;
   } else if (m1) {  // small shapes are latency-bound: more, narrower workgroups
@@ -1184,9 +1210,9 @@ int launch_gemv_ln(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t l
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
 }
 
-template <int NH, int KS, int CPW, int MT>
+template <int NH, int KS, int CPW, int MT, int NWD>
 int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipStream_t s) {
-  auto kern = w4a16_mfma_kernel<NH, KS, CPW, MT>;
+  auto kern = w4a16_mfma_kernel<NH, KS, CPW, MT, NWD>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
@@ -1200,25 +1226,25 @@ int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
   return ldk::check_launch("w4a16_mfma");
 }
 
-template <int NH>
+template <int NH, int NWD>
 int launch_mfma_nh(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t lds, hipStream_t s) {
   const bool two = p.cpw == 2;
   if (p.mtile == 2) {
     switch (1 << a.gsh_rows) {
-      case 4: return launch_mfma_t<NH, 1, 1, 2>(a, sp, p.nw, lds, s);
-      case 8: return launch_mfma_t<NH, 2, 1, 2>(a, sp, p.nw, lds, s);
-      case 16: return launch_mfma_t<NH, 4, 1, 2>(a, sp, p.nw, lds, s);
+      case 4: return launch_mfma_t<NH, 1, 1, 2, NWD>(a, sp, p.nw, lds, s);
+      case 8: return launch_mfma_t<NH, 2, 1, 2, NWD>(a, sp, p.nw, lds, s);
+      case 16: return launch_mfma_t<NH, 4, 1, 2, NWD>(a, sp, p.nw, lds, s);
       case 32:
-        if constexpr (NH == 1) return launch_mfma_t<NH, 8, 1, 2>(a, sp, p.nw, lds, s);
+        if constexpr (NH == 1) return launch_mfma_t<NH, 8, 1, 2, NWD>(a, sp, p.nw, lds, s);
         return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group_size 256 with M > 16 takes block_n=64");
     }
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
   }
   switch (1 << a.gsh_rows) {
-    case 4: return two ? launch_mfma_t<NH, 1, 2, 1>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 1, 1, 1>(a, sp, p.nw, lds, s);
-    case 8: return two ? launch_mfma_t<NH, 2, 2, 1>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 2, 1, 1>(a, sp, p.nw, lds, s);
-    case 16: return two ? launch_mfma_t<NH, 4, 2, 1>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 4, 1, 1>(a, sp, p.nw, lds, s);
-    case 32: return launch_mfma_t<NH, 8, 1, 1>(a, sp, p.nw, lds, s);
+    case 4: return two ? launch_mfma_t<NH, 1, 2, 1, NWD>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 1, 1, 1, NWD>(a, sp, p.nw, lds, s);
+    case 8: return two ? launch_mfma_t<NH, 2, 2, 1, NWD>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 2, 1, 1, NWD>(a, sp, p.nw, lds, s);
+    case 16: return two ? launch_mfma_t<NH, 4, 2, 1, NWD>(a, sp, p.nw, lds, s) : launch_mfma_t<NH, 4, 1, 1, NWD>(a, sp, p.nw, lds, s);
+    case 32: return launch_mfma_t<NH, 8, 1, 1, NWD>(a, sp, p.nw, lds, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: group size not supported by the MFMA kernel");
 }
@@ -1245,7 +1271,10 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
   }
   if (pro != kProNone) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues run on the M = 1 kernel");
-  if (p.kern == kMfma) return p.ln == 16 ? launch_mfma_nh<1>(a, sp, p, lds, s) : launch_mfma_nh<2>(a, sp, p, lds, s);
+  if (p.kern == kMfma) {
+    if (p.ln == 8) return launch_mfma_nh<1, 2>(a, sp, p, lds, s);  // 32-column tiles
+    return p.ln == 16 ? launch_mfma_nh<1, 4>(a, sp, p, lds, s) : launch_mfma_nh<2, 4>(a, sp, p, lds, s);
+  }
   switch (p.mt) {
     case 1: return launch_gemv_ln<1>(a, sp, p, lds, s);
     case 2: return launch_gemv_ln<2>(a, sp, p, lds, s);
@@ -1326,8 +1355,8 @@ extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweig
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul: workspace must be a 256-byte aligned pointer");
   const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
-  if (p.kern == kMfma && block_n && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n 64 or 128");
+  if (p.kern == kMfma && block_n && block_n != 32 && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n 32, 64 or 128");
   if (split_k > 1 && p.splits == 1 && (K / group_size) > 1 && M <= 16)
     return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,

@@ -131,11 +131,20 @@ def test_split_k_large_partials():
 
 @pytest.mark.parametrize("M,N", [(16, 17920), (9, 17920), (4, 17920), (16, 2048), (3, 4100),
                                  (16, 260)])
-@pytest.mark.parametrize("block_n", [64, 128])
+@pytest.mark.parametrize("block_n", [32, 64, 128])
 def test_mfma_tile_widths(M, N, block_n):
-    """The MFMA kernel's 64- and 128-column tiles (two 16-byte line halves per lane, eight MFMA
-    column tiles), including column tails that end inside a tile."""
+    """The MFMA kernel's 32-column tiles (8-byte loads, two MFMA column tiles per lane), 64- and
+    128-column tiles (one or two 16-byte line halves per lane, four or eight MFMA column tiles),
+    including column tails that end inside a tile."""
     _run(M, N, 1536, config={"MFMA": True, "block_n": block_n})
+
+
+def test_mfma_32_column_tiles_split_and_prefill():
+    """32-column MFMA tiles with the cross-workgroup K split (down projection) and in 32-row
+    prefill blocks, with bias."""
+    _run(8, 1536, 8960, bias=True, config={"MFMA": True, "block_n": 32})
+    _run(16, 1536, 8960, config={"MFMA": True, "block_n": 32, "split_k": 7})
+    _run(40, 2048, 1536, bias=True, config={"MFMA": True, "block_n": 32})
 
 
 def test_mfma_split_k_with_128_columns():
