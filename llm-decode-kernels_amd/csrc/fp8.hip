@@ -11,7 +11,8 @@
 // GEMV layout (M <= 16): like the W4A16 skinny kernel, a workgroup owns CW = 16*LN columns and
 // all of K; each lane owns 16 adjacent columns, so one 128-bit load = one K row of 16 weights;
 // LK = NW*64/LN lanes split K and are reduced in-workgroup (DPP/permlane, then LDS). x is staged
-// in LDS as fp16. The per-channel scale is applied once after the K reduction (fp8.py:120).
+// in LDS as fp16 by the wave that uses it (no workgroup barrier before the FMAs). The
+// per-channel scale is applied once after the K reduction (fp8.py:120).
 #include <algorithm>
 
 #include "ldk_common.h"
@@ -154,7 +155,11 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
   constexpr int CW = 16 * LN;
   constexpr int LKW = 64 / LN;
   constexpr int RPP = LKW * NW * RPL;  // K rows per pass
-  __shared__ __align__(16) half_t xs[RPP][MT];
+  constexpr int RPW = LKW * RPL;       // K rows of a pass one wave uses
+  constexpr int XPL = (RPW * MT + 63) / 64;  // x values a lane stages per pass
+  // x is staged per wave (only the rows the wave uses, so no workgroup barrier): slot lk + j*LKW
+  // holds row wave*LKW + lk + j*LKW*NW of the pass
+  __shared__ __align__(16) half_t xs[NW][MT][RPW];
   __shared__ __align__(16) float red[NW][MT][CW];
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.wq);
@@ -174,38 +179,34 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
     for (int j = 0; j < 16; ++j) acc[m][j] = 0.0f;
 
   for (int p0 = rb; p0 < re; p0 += RPP) {
+    // loads in consumption order: this wave's x values, then the weight rows (clamped, branch
+    // free; rows past re and x rows past M are zeroed when staged)
+    half_t xl[XPL];
+#pragma unroll
+    for (int i = 0; i < XPL; ++i) {
+      const int e = lane + 64 * i, m = min(e / RPW, MT - 1), rr = e % RPW;
+      const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
+      xl[i] = a.x[(int64_t)min(m0 + m, a.M - 1) * a.ldx + min(k, a.K - 1)];
+    }
     u32x4 w[RPL];
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
       const int r = min(p0 + lrow + j * LKW * NW, re - 1);  // clamped; such rows meet zero x
       w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.wq + (int64_t)r * a.N + col));
     }
-    __builtin_amdgcn_sched_barrier(0);  // every weight load of the pass is in flight first
-    // stage x[m0 .. m0+MT)[p0 .. p0+RPP) as [row][m]; rows past re and m past M are zeros
-    if (p0 != rb) ldk::lds_barrier();  // the previous pass is done reading xs
-    for (int i = tid; i < RPP * MT; i += NW * 64) {
-      const int m = i / RPP, r = i - m * RPP;
-      const int k = p0 + r;
-      half_t v = (half_t)0.0f;
-      if (m0 + m < a.M && k < re) v = a.x[(int64_t)(m0 + m) * a.ldx + k];
-      xs[r][m] = v;
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight first
+#pragma unroll
+    for (int i = 0; i < XPL; ++i) {
+      const int e = lane + 64 * i, m = e / RPW, rr = e % RPW;
+      const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
+      if (e < RPW * MT) xs[wave][m][rr] = (m0 + m < a.M && k < re) ? xl[i] : (half_t)0.0f;
     }
-    ldk::lds_barrier();
+    ldk::wave_lds_sync();
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
-      const int rl = lrow + j * LKW * NW;
       float xv[MT];
-      if constexpr (MT == 4) {
-        const half4_t h = *reinterpret_cast<const half4_t*>(&xs[rl][0]);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) xv[m] = (float)h[m];
-      } else if constexpr (MT == 2) {
-        const half2_t h = *reinterpret_cast<const half2_t*>(&xs[rl][0]);
-        xv[0] = (float)h[0];
-        xv[1] = (float)h[1];
-      } else {
-        xv[0] = (float)xs[rl][0];
-      }
+      for (int m = 0; m < MT; ++m) xv[m] = (float)xs[wave][m][lk + j * LKW];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[j][d], false);
@@ -219,6 +220,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
         }
       }
     }
+    ldk::wave_lds_sync();  // the next pass rewrites this wave's x slots
   }
 
   // ---- reduction: the LKW lanes of a wave sharing ln (DPP/permlane), then the NW waves (LDS)
