@@ -43,7 +43,9 @@ def _cpu_model() -> str:
 def cpu_baseline(w16, x, seconds: float = 15.0) -> dict:
     """The oracle's restatement of the reference CPU path (kernels/reference.py:39-45: unpack and
     dequantize every call, then the fp32 matmul), single-threaded, on a bounded sample of calls:
-    3 warm-up calls, then timed calls until ~`seconds` of CPU work (at most 7, median)."""
+    3 warm-up calls, then timed calls until ~`seconds` of CPU work (at most 7, median). Beside it,
+    the dequantize-once variant (the reference's W4RefBackend, e2e/model.py:62-67): the fp32
+    matmul alone over weights dequantized beforehand."""
     from threadpoolctl import threadpool_limits
 
     from oracle import quant as oq
@@ -64,15 +66,31 @@ def cpu_baseline(w16, x, seconds: float = 15.0) -> dict:
             t0 = time.perf_counter()
             w4a16_ref(xn, qw, s, z, GS)
             times.append(time.perf_counter() - t0)
+        # dequantize once (as the reference's W4RefBackend, model.py:62-67), then fp32 matmuls
+        from oracle.reference import dequantize_ref
+
+        w32 = dequantize_ref(qw, s, z, GS).astype("float32")
+        x32 = xn.astype("float32")
+        once = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            _ = x32 @ w32.T
+            once.append(time.perf_counter() - t0)
     from kernels.quant import weight_bytes
 
     sec = statistics.median(times)
     nbytes = weight_bytes(N, K, GS) + 2 * M * K + 2 * M * N
+    sec_once = statistics.median(once[3:])
     return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{len(times)} timed calls (+{1 + warm} warm-up) of oracle w4a16_ref on "
                       f"config 0 (dequantize each call + fp32 matmul), median "
                       f"{sec * 1e3:.1f} ms/call, 1 thread of {os.cpu_count()} "
-                      f"({_cpu_model()})"}
+                      f"({_cpu_model()})",
+            "dequant_once": {"value": round(nbytes / sec_once / 1e9, 3), "unit": "GB/s",
+                             "sample": f"weights dequantized once to fp32 outside the timing, "
+                                       f"then 7 timed fp32 matmuls (+3 warm-up), median "
+                                       f"{sec_once * 1e3:.2f} ms/call, 1 thread (same "
+                                       f"algorithmic bytes as the int4 path)"}}
 
 
 def e2e_leg(steps: int) -> dict:
