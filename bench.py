@@ -210,7 +210,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbps / PEAK_GBPS, 4),
                      "traffic": measured_traffic(kcfg), "bytes_per_launch": nbytes,
-                     "kernel": "w4a16_m1_kernel<8, 6, 4, 0>",
+                     "kernel": "w4a16_m1_kernel<8, 6, 4, 0, 1>",
                      "timing": "HIP events on the graph-replay stream over all timed launches"},
     }
     timer.close()
