@@ -163,6 +163,16 @@ int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* 
                      int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
                      void* stream);
 
+/* out [1, N] = (silu(g) * u) @ dequant_fp8(wq) (+ bias) for one row gate_up = [g | u] of 2K fp16
+ * values: the activation is formed inside the W8A16 GEMV's x staging with the steps of
+ * ldk_swiglu (bit-identical staged values), one launch instead of two. Same wq/scale/bias/
+ * out/workspace rules as ldk_w8a16_matmul. Replaces the pair swiglu_fused (kernels/swiglu.py:56)
+ * + w8a16_matmul (kernels/fp8.py:200) that the reference's OursFP8Backend runs as act then linear
+ * (kernels/e2e/model.py:100-118). */
+int ldk_w8a16_swiglu_matmul(const void* gate_up, const uint8_t* wq, const void* scale,
+                            const void* bias, void* out, int64_t N, int64_t K, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------- RMSNorm and SwiGLU */
 
 /* Per row of x [M, N]: h = x (+ residual, fp16 add, written to res_out); out = weight * fp16(

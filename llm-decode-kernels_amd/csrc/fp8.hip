@@ -150,8 +150,12 @@ struct W8Split {
 // 3 * 2^48 = 48 * 2^44, so up to 40 legal partials can never look poisoned.
 constexpr int kW8MaxSplits = 40;
 
-template <int MT, int LN, int NW, int RPL>
+// PRO = 1: the x row is [g | u] of 2K values and the activation silu(g) * u is formed while it is
+// staged (one row; the steps of the standalone SwiGLU kernel, so the staged values are
+// bit-identical to its output).
+template <int MT, int LN, int NW, int RPL, int PRO>
 __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split sp) {
+  static_assert(PRO == 0 || MT == 1, "the SwiGLU prologue takes one row");
   constexpr int CW = 16 * LN;
   constexpr int LKW = 64 / LN;
   constexpr int RPP = LKW * NW * RPL;  // K rows per pass
@@ -181,12 +185,14 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
   for (int p0 = rb; p0 < re; p0 += RPP) {
     // loads in consumption order: this wave's x values, then the weight rows (clamped, branch
     // free; rows past re and x rows past M are zeroed when staged)
-    half_t xl[XPL];
+    half_t xl[XPL], xu[XPL];
 #pragma unroll
     for (int i = 0; i < XPL; ++i) {
       const int e = lane + 64 * i, m = min(e / RPW, MT - 1), rr = e % RPW;
       const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
-      xl[i] = a.x[(int64_t)min(m0 + m, a.M - 1) * a.ldx + min(k, a.K - 1)];
+      const int64_t xo = (int64_t)min(m0 + m, a.M - 1) * a.ldx + min(k, a.K - 1);
+      xl[i] = a.x[xo];
+      if constexpr (PRO == 1) xu[i] = a.x[xo + a.K];
     }
     u32x4 w[RPL];
 #pragma unroll
@@ -199,7 +205,9 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
     for (int i = 0; i < XPL; ++i) {
       const int e = lane + 64 * i, m = e / RPW, rr = e % RPW;
       const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
-      if (e < RPW * MT) xs[wave][m][rr] = (m0 + m < a.M && k < re) ? xl[i] : (half_t)0.0f;
+      half_t v = xl[i];
+      if constexpr (PRO == 1) v = ldk::silu_f16(xl[i]) * xu[i];  // fp16 multiply
+      if (e < RPW * MT) xs[wave][m][rr] = (m0 + m < a.M && k < re) ? v : (half_t)0.0f;
     }
     ldk::wave_lds_sync();
 #pragma unroll
@@ -476,40 +484,44 @@ W8Plan make_w8_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, i
   return p;
 }
 
-template <int MT, int LN, int NW, int RPL>
+template <int MT, int LN, int NW, int RPL, int PRO>
 int launch_w8_t(const W8Args& a, const W8Split& sp, int mblocks, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 16 * LN - 1) / (16 * LN)), (unsigned)sp.splits, (unsigned)mblocks);
   (void)hipGetLastError();
-  w8a16_gemv_kernel<MT, LN, NW, RPL><<<grid, NW * 64, 0, s>>>(a, sp);
+  w8a16_gemv_kernel<MT, LN, NW, RPL, PRO><<<grid, NW * 64, 0, s>>>(a, sp);
   return ldk::check_launch("w8a16_gemv");
 }
 
-template <int MT, int LN>
+template <int MT, int LN, int PRO>
 int launch_w8_rpl(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
   switch (p.rpl) {
-    case 2: return launch_w8_t<MT, LN, 4, 2>(a, sp, p.mblocks, s);
-    case 4: return launch_w8_t<MT, LN, 4, 4>(a, sp, p.mblocks, s);
-    case 8: return launch_w8_t<MT, LN, 4, 8>(a, sp, p.mblocks, s);
+    case 2: return launch_w8_t<MT, LN, 4, 2, PRO>(a, sp, p.mblocks, s);
+    case 4: return launch_w8_t<MT, LN, 4, 4, PRO>(a, sp, p.mblocks, s);
+    case 8: return launch_w8_t<MT, LN, 4, 8, PRO>(a, sp, p.mblocks, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d rows per lane not instantiated", p.rpl);
 }
 
-template <int MT>
+template <int MT, int PRO>
 int launch_w8_ln(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
   switch (p.ln) {
-    case 1: return launch_w8_rpl<MT, 1>(a, sp, p, s);
-    case 2: return launch_w8_rpl<MT, 2>(a, sp, p, s);
-    case 4: return launch_w8_rpl<MT, 4>(a, sp, p, s);
-    case 8: return launch_w8_rpl<MT, 8>(a, sp, p, s);
+    case 1: return launch_w8_rpl<MT, 1, PRO>(a, sp, p, s);
+    case 2: return launch_w8_rpl<MT, 2, PRO>(a, sp, p, s);
+    case 4: return launch_w8_rpl<MT, 4, PRO>(a, sp, p, s);
+    case 8: return launch_w8_rpl<MT, 8, PRO>(a, sp, p, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: block_n=%d not supported (16, 32, 64 or 128)", 16 * p.ln);
 }
 
-int launch_w8(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+int launch_w8(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s, int pro = 0) {
+  if (pro) {
+    if (p.mt != 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: the SwiGLU prologue takes one row");
+    return launch_w8_ln<1, 1>(a, sp, p, s);
+  }
   switch (p.mt) {
-    case 1: return launch_w8_ln<1>(a, sp, p, s);
-    case 2: return launch_w8_ln<2>(a, sp, p, s);
-    case 4: return launch_w8_ln<4>(a, sp, p, s);
+    case 1: return launch_w8_ln<1, 0>(a, sp, p, s);
+    case 2: return launch_w8_ln<2, 0>(a, sp, p, s);
+    case 4: return launch_w8_ln<4, 0>(a, sp, p, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: row block %d not instantiated", p.mt);
 }
@@ -579,4 +591,25 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   const W8Args a{(const half_t*)x, ldx, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K};
   const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
   return p.mfma ? launch_w8_mfma(a, sp, p, (hipStream_t)stream) : launch_w8(a, sp, p, (hipStream_t)stream);
+}
+
+// Fused decode entry (one row): the down projection's activation silu(g) * u is formed inside
+// the W8A16 GEMV's x staging, one launch fewer per decode layer (the reference's
+// OursFP8Backend runs swiglu and the FP8 linear as two, kernels/e2e/model.py:100-118).
+extern "C" int ldk_w8a16_swiglu_matmul(const void* gate_up, const uint8_t* wq, const void* scale, const void* bias,
+                                       void* out, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  if (!gate_up || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_swiglu_matmul: null pointer");
+  if (N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_swiglu_matmul: N, K must be positive");
+  if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_swiglu_matmul: N=%lld must be a multiple of 16", (long long)N);
+  if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_swiglu_matmul: K=%lld must be a multiple of 8", (long long)K);
+  if (!ldk::aligned(gate_up, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
+    return ldk::fail(LDK_ERR_ALIGN, "w8a16_swiglu_matmul: wq must be 16-byte aligned");
+  if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_swiglu_matmul: N or K too large");
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w8a16_swiglu_matmul: workspace must be a 256-byte aligned pointer");
+  const W8Plan p = make_w8_plan(1, N, K, 0, 0, workspace ? workspace_bytes : 0);
+  const W8Args a{(const half_t*)gate_up, 2 * K, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K};
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
+  return launch_w8(a, sp, p, (hipStream_t)stream, 1);
 }

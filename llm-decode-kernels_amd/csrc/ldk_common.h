@@ -41,6 +41,13 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
 }
 
+// SwiGLU's activation of one gate value with the steps of the standalone SwiGLU kernel: silu in
+// fp32 with the hardware reciprocal, rounded to fp16 (the caller multiplies by u in fp16).
+__device__ __forceinline__ half_t silu_f16(half_t g) {
+  const float f = (float)g;
+  return (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
+}
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ half2_t u2h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }

@@ -169,8 +169,14 @@ class OursFP8Backend(OursBackend):
 
         return w8a16_matmul(x, p.qweight, p.scales, bias=p.bias)
 
-    norm_linear = Backend.norm_linear  # the fused entries take W4A16 weights
-    act_linear = Backend.act_linear
+    norm_linear = Backend.norm_linear  # the fused RMSNorm entry takes W4A16 weights
+
+    def act_linear(self, gate_up, p: Linear):
+        """One launch at decode: SwiGLU forms the FP8 down projection's activation
+        (kernels.fused.swiglu_w8a16_matmul)."""
+        from kernels.fused import swiglu_w8a16_matmul
+
+        return swiglu_w8a16_matmul(gate_up, p.qweight, p.scales, bias=p.bias)
 
 
 def make_backend(name: str) -> Backend:

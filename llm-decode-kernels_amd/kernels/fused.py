@@ -1,5 +1,5 @@
-"""Fusions on either side of the W4A16 decode GEMV (libldk_amd.so `ldk_w4a16_rmsnorm_matmul`,
-`ldk_w4a16_swiglu_matmul`).
+"""Fusions on either side of the decode GEMVs (libldk_amd.so `ldk_w4a16_rmsnorm_matmul`,
+`ldk_w4a16_swiglu_matmul`, `ldk_w8a16_swiglu_matmul`).
 
 The reference's OursBackend runs a decode layer as separate kernels: rmsnorm (+ residual), then
 the W4A16 projection; swiglu, then the down projection (kernels/e2e/model.py:79-97). Here the
@@ -92,4 +92,33 @@ def swiglu_w4a16_matmul(gate_up, qweight, scales, zeros, group_size=128, bias=No
     return out
 
 
-__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul"]
+def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
+    """y = w8a16_matmul(swiglu_fused(gate_up), wq, scale) (+ bias); gate_up: [..., 2K] fp16,
+    wq: [K, N] float8_e4m3fn, scale: [N] fp16. One row runs one launch (ldk_w8a16_swiglu_matmul),
+    more rows the two ops back to back."""
+    from kernels.fp8 import FP8, w8a16_matmul
+
+    K2 = gate_up.shape[-1]
+    K = K2 // 2
+    N = wq.shape[1]
+    rows = gate_up.numel() // K2
+    fuse = (rows == 1 and gate_up.dtype == torch.float16 and gate_up.is_cuda and K2 % 2 == 0
+            and K % 8 == 0 and N % 16 == 0 and wq.dtype == FP8 and scale.dtype == torch.float16
+            and _aligned(gate_up, wq))
+    if not fuse:
+        return w8a16_matmul(swiglu_fused(gate_up), wq, scale, bias=bias)
+    assert wq.shape[0] == K and scale.numel() == N
+    dev = _lib.require_gpu(gate_up, wq, scale, bias, what="swiglu_w8a16_matmul")
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    sc = scale.contiguous()
+    out = torch.empty((*gate_up.shape[:-1], N), dtype=torch.float16, device=dev)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w8a16_swiglu_matmul(
+            _lib.ptr(gate_up), _lib.ptr(wq), _lib.ptr(sc), _lib.ptr(b), _lib.ptr(out), N, K, ws,
+            ws_bytes, _lib.stream(dev))
+    _lib.check(st, "swiglu_w8a16_matmul")
+    return out
+
+
+__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "swiglu_w8a16_matmul"]

@@ -106,6 +106,17 @@ def test_exact_is_not_the_mfma_kernel():
     assert st == _lib.ERR_UNSUPPORTED and "factored" in msg
 
 
+def test_w8a16_swiglu_validates_before_launch():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    st, msg = _err(lib.ldk_w8a16_swiglu_matmul(p, p, p, None, p, 40, 256, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "multiple of 16" in msg
+    st, _ = _err(lib.ldk_w8a16_swiglu_matmul(p, p, p, None, p, 64, 100, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED
+    st, _ = _err(lib.ldk_w8a16_swiglu_matmul(p, ctypes.c_void_p(264), p, None, p, 64, 256, None, 0, None))
+    assert st == _lib.ERR_ALIGN
+
+
 def test_rmsnorm_residual_pairing_rejected():
     lib = _lib.load()
     p = ctypes.c_void_p(256)

@@ -112,6 +112,12 @@ def test_prefill_native_rows(M, N, K, bias):
     _run(M, N, K, bias=bias, config={"prefill": "native"})
 
 
+@pytest.mark.parametrize("M", [1, 4, 16, 512])
+def test_reference_rows(M):
+    """The reference's autotuned rows (test_fp8.py slow cases: M in {1, 4, 16, 512})."""
+    _run(M, 1536, 1536, bias=True)
+
+
 def test_prefill_paths_agree():
     for path in ("native", "dequant"):
         _run(300, 2048, 1536, config={"prefill": path})

@@ -1,5 +1,5 @@
-"""The fused decode entries (kernels.fused: ldk_w4a16_rmsnorm_matmul, ldk_w4a16_swiglu_matmul)
-against the oracle's unfused chain (kernels/reference.py:9-45: rmsnorm_ref or swiglu_ref, then
+"""The fused decode entries (kernels.fused: ldk_w4a16_rmsnorm_matmul, ldk_w4a16_swiglu_matmul,
+ldk_w8a16_swiglu_matmul) against the oracle's unfused chain (kernels/reference.py:9-45: rmsnorm_ref or swiglu_ref, then
 the fp32 dequantize-then-matmul) and against the library's own two-launch composition.
 
 Bars: the north star's max-abs 2e-2 and rel-L2 1e-3 against the oracle chain; the updated
@@ -14,11 +14,13 @@ import torch
 
 from _util import assert_north_star, bits16, to_np
 from kernels.bench import cases
-from kernels.fused import rmsnorm_w4a16_matmul, swiglu_w4a16_matmul
+from kernels.fp8 import FP8, quantize_fp8, w8a16_matmul
+from kernels.fused import rmsnorm_w4a16_matmul, swiglu_w4a16_matmul, swiglu_w8a16_matmul
 from kernels.quant import quantize_rtn
 from kernels.rmsnorm import rmsnorm
 from kernels.swiglu import swiglu_fused
 from kernels.w4a16 import w4a16_matmul
+from oracle import fp8 as of
 from oracle import quant as oq
 from oracle.reference import rmsnorm_ref, swiglu_ref, w4a16_ref
 
@@ -76,6 +78,29 @@ def test_swiglu_matmul(N, K):
     assert_north_star(to_np(y), _oracle_linear(act, qw, s, z, b))
     y2 = w4a16_matmul(swiglu_fused(gu.cuda()), qw, s, z, 128, None if b is None else b.cuda())
     assert torch.equal(y, y2)
+
+
+# FP8 down projection shapes: the e2e down (K split 35 ways), small K, bias, a wide N
+@pytest.mark.parametrize("N,K,bias", [(1536, 8960, False), (256, 1536, True), (2048, 768, False),
+                                      (17920, 1536, True)])
+def test_swiglu_w8a16_matmul(N, K, bias):
+    w, _ = cases.w4a16_case(1, N, K, 41)
+    wq, sc = quantize_fp8(w.cuda())
+    b = (torch.randn(N, generator=cases.gen(42)) * 0.1).half().cuda() if bias else None
+    gu = cases.swiglu_case(1, K, 43)
+    y = swiglu_w8a16_matmul(gu.cuda(), wq, sc, bias=b)
+    act = swiglu_ref(gu[:, :K].numpy(), gu[:, K:].numpy())
+    ref = of.w8a16_ref(act, to_np(wq.view(torch.uint8)), to_np(sc), None if b is None else to_np(b))
+    assert_north_star(to_np(y), ref)
+    # same staged activations, same plan and reduction order as the two launches
+    assert torch.equal(y, w8a16_matmul(swiglu_fused(gu.cuda()), wq, sc, bias=b))
+
+
+def test_swiglu_w8a16_rows_other_than_one_compose():
+    w, _ = cases.w4a16_case(1, 512, 768, 44)
+    wq, sc = quantize_fp8(w.cuda())
+    gu = cases.swiglu_case(3, 768, 45).cuda()
+    assert torch.equal(swiglu_w8a16_matmul(gu, wq, sc), w8a16_matmul(swiglu_fused(gu), wq, sc))
 
 
 def test_rows_other_than_one_compose():

@@ -176,6 +176,16 @@ def test_all_decode_rows(M):
 def test_odd_n_and_bias():
     _run(5, 1000, 1024, bias=True)
     _run(1, 132, 256, bias=True)
+    for M in (1, 2, 4, 16):  # the reference's odd N = 200 with bias (test_w4a16.py slow cases)
+        _run(M, 200, 1536, bias=True)
+
+
+@pytest.mark.parametrize("M", [33, 128, 2048])
+@pytest.mark.parametrize("N,K", [(1536, 1536), (256, 1536)])
+def test_prefill_reference_rows(M, N, K):
+    """The reference's prefill rows (test_w4a16.py slow cases: M in {33, 128, 2048}): the native
+    MFMA blocks up to 256 rows, dequantize + hipBLASLt beyond."""
+    _run(M, N, K, bias=True)
 
 
 def test_3d_input():
