@@ -173,6 +173,19 @@ int ldk_w8a16_swiglu_matmul(const void* gate_up, const uint8_t* wq, const void* 
                             const void* bias, void* out, int64_t N, int64_t K, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
+/* out [1, N] = rmsnorm(x (+ residual)) @ dequant_fp8(wq) (+ bias) for one row x [K]: the
+ * activation norm_weight * fp16(h * rsqrt(mean(h^2) + eps)), h = x (+ residual, fp16 add, written
+ * to residual_out), is formed inside the W8A16 GEMV's x staging with the steps of ldk_rmsnorm
+ * (the row statistic is reduced in another order, so a staged value can differ from ldk_rmsnorm's
+ * by one fp16 ulp). residual/residual_out both NULL or both set; residual_out must not alias x
+ * or residual; x, norm_weight, residual, residual_out and wq 16-byte aligned. Replaces the pair
+ * rmsnorm (kernels/rmsnorm.py:44-68) + w8a16_matmul (kernels/fp8.py:200) that the reference's
+ * OursFP8Backend runs as norm then linear (kernels/e2e/model.py:79-118). */
+int ldk_w8a16_rmsnorm_matmul(const void* x, const void* residual, void* residual_out,
+                             const void* norm_weight, float eps, const uint8_t* wq,
+                             const void* scale, const void* bias, void* out, int64_t N, int64_t K,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------- RMSNorm and SwiGLU */
 
 /* Per row of x [M, N]: h = x (+ residual, fp16 add, written to res_out); out = weight * fp16(

@@ -138,6 +138,12 @@ struct W8Args {
   half_t* out;
   int64_t ldo;
   int M, N, K;
+  // RMSNorm prologue (PRO 2, 3): residual added before the norm, x + residual written by the
+  // first workgroup, norm weight [K], eps
+  const half_t* res;
+  half_t* res_out;
+  const half_t* nw;
+  float eps;
 };
 
 struct W8Split {
@@ -150,12 +156,20 @@ struct W8Split {
 // 3 * 2^48 = 48 * 2^44, so up to 40 legal partials can never look poisoned.
 constexpr int kW8MaxSplits = 40;
 
-// PRO = 1: the x row is [g | u] of 2K values and the activation silu(g) * u is formed while it is
-// staged (one row; the steps of the standalone SwiGLU kernel, so the staged values are
-// bit-identical to its output).
+// Prologues (one row) that form the activation while it is staged, with the steps of the
+// standalone kernels:
+//  PRO = 1: the x row is [g | u] of 2K values, activation silu(g) * u (bit-identical to the
+//           SwiGLU kernel's output);
+//  PRO = 2, 3: RMSNorm of x (PRO 3: of x + residual, written to res_out by the first workgroup)
+//           times the norm weight. Each workgroup stages only its K range, so it reduces the
+//           row statistic over the whole row itself: its first row vectors are loaded ahead of
+//           the pass (one LDS barrier, which waits for those loads only). The statistic's order
+//           differs from the RMSNorm kernel's, so a staged value can differ from its output by
+//           one fp16 ulp.
 template <int MT, int LN, int NW, int RPL, int PRO>
 __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split sp) {
-  static_assert(PRO == 0 || MT == 1, "the SwiGLU prologue takes one row");
+  static_assert(PRO == 0 || MT == 1, "the prologues take one row");
+  constexpr bool kRms = PRO == 2 || PRO == 3, kRes = PRO == 3;
   constexpr int CW = 16 * LN;
   constexpr int LKW = 64 / LN;
   constexpr int RPP = LKW * NW * RPL;  // K rows per pass
@@ -165,6 +179,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
   // holds row wave*LKW + lk + j*LKW*NW of the pass
   __shared__ __align__(16) half_t xs[NW][MT][RPW];
   __shared__ __align__(16) float red[NW][MT][CW];
+  __shared__ float stat[NW];
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.wq);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -182,10 +197,19 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[m][j] = 0.0f;
 
+  // RMSNorm prologue: this thread's first row vector for the statistic, issued ahead of the pass
+  // (buffer loads read zeros past the row)
+  u32x4 sx0{}, sr0{};
+  if constexpr (kRms) {
+    sx0 = ldk::buffer_load16(ldk::buffer_rsrc(a.x, (uint32_t)a.K * 2u), 16u * tid);
+    if constexpr (kRes) sr0 = ldk::buffer_load16(ldk::buffer_rsrc(a.res, (uint32_t)a.K * 2u), 16u * tid);
+  }
+  float rs = 0.0f;
+
   for (int p0 = rb; p0 < re; p0 += RPP) {
     // loads in consumption order: this wave's x values, then the weight rows (clamped, branch
     // free; rows past re and x rows past M are zeroed when staged)
-    half_t xl[XPL], xu[XPL];
+    half_t xl[XPL], xu[XPL], xn[XPL];
 #pragma unroll
     for (int i = 0; i < XPL; ++i) {
       const int e = lane + 64 * i, m = min(e / RPW, MT - 1), rr = e % RPW;
@@ -193,6 +217,8 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
       const int64_t xo = (int64_t)min(m0 + m, a.M - 1) * a.ldx + min(k, a.K - 1);
       xl[i] = a.x[xo];
       if constexpr (PRO == 1) xu[i] = a.x[xo + a.K];
+      if constexpr (kRes) xu[i] = a.res[xo];
+      if constexpr (kRms) xn[i] = a.nw[xo];
     }
     u32x4 w[RPL];
 #pragma unroll
@@ -201,12 +227,41 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
       w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.wq + (int64_t)r * a.N + col));
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight first
+    if constexpr (kRms) {
+      if (p0 == rb) {  // the row statistic, once (uniform)
+        const int nv = a.K >> 3;
+        const bool wr = kRes && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+        float ss = 0.0f;
+        auto add = [&](u32x4 xv, u32x4 rv, int t) {
+          half8_t h = __builtin_bit_cast(half8_t, xv);
+          if constexpr (kRes) h = h + __builtin_bit_cast(half8_t, rv);  // fp16 add
+          if (wr && t < nv) *reinterpret_cast<half8_t*>(a.res_out + 8 * t) = h;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss = __builtin_fmaf((float)h[j], (float)h[j], ss);
+        };
+        add(sx0, sr0, tid);
+        for (int t = tid + NW * 64; t < nv; t += NW * 64) {  // rows of more than NW*64 vectors
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + 8 * t);
+          u32x4 rv{};
+          if constexpr (kRes) rv = *reinterpret_cast<const u32x4*>(a.res + 8 * t);
+          add(xv, rv, t);
+        }
+        ss = ldk::sum_lanes_strided<1>(ss);
+        if (lane == 0) stat[wave] = ss;
+        ldk::lds_barrier();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot += stat[w];
+        rs = 1.0f / __builtin_sqrtf(tot / (float)a.K + a.eps);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < XPL; ++i) {
       const int e = lane + 64 * i, m = e / RPW, rr = e % RPW;
       const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
       half_t v = xl[i];
       if constexpr (PRO == 1) v = ldk::silu_f16(xl[i]) * xu[i];  // fp16 multiply
+      if constexpr (kRms) v = ldk::rms_f16(kRes ? xl[i] + xu[i] : xl[i], rs, xn[i]);
       if (e < RPW * MT) xs[wave][m][rr] = (m0 + m < a.M && k < re) ? v : (half_t)0.0f;
     }
     ldk::wave_lds_sync();
@@ -515,8 +570,13 @@ int launch_w8_ln(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_
 
 int launch_w8(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s, int pro = 0) {
   if (pro) {
-    if (p.mt != 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: the SwiGLU prologue takes one row");
-    return launch_w8_ln<1, 1>(a, sp, p, s);
+    if (p.mt != 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: the prologues take one row");
+    switch (pro) {
+      case 1: return launch_w8_ln<1, 1>(a, sp, p, s);
+      case 2: return launch_w8_ln<1, 2>(a, sp, p, s);
+      case 3: return launch_w8_ln<1, 3>(a, sp, p, s);
+    }
+    return ldk::fail(LDK_ERR_INVALID, "w8a16: unknown prologue %d", pro);
   }
   switch (p.mt) {
     case 1: return launch_w8_ln<1, 0>(a, sp, p, s);
@@ -612,4 +672,31 @@ extern "C" int ldk_w8a16_swiglu_matmul(const void* gate_up, const uint8_t* wq, c
   const W8Args a{(const half_t*)gate_up, 2 * K, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K};
   const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
   return launch_w8(a, sp, p, (hipStream_t)stream, 1);
+}
+
+// Fused decode entry (one row): RMSNorm (+ residual) forms the activation inside the W8A16 GEMV's
+// x staging, one launch fewer per use (the reference's OursFP8Backend runs rmsnorm and the FP8
+// linear as two, kernels/e2e/model.py:79-118).
+extern "C" int ldk_w8a16_rmsnorm_matmul(const void* x, const void* residual, void* residual_out, const void* norm_weight,
+                                        float eps, const uint8_t* wq, const void* scale, const void* bias, void* out,
+                                        int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!x || !norm_weight || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_rmsnorm_matmul: null pointer");
+  if ((residual == nullptr) != (residual_out == nullptr))
+    return ldk::fail(LDK_ERR_INVALID, "w8a16_rmsnorm_matmul: residual and residual_out must both be given or both be null");
+  if (residual && (residual == residual_out || x == residual_out))
+    return ldk::fail(LDK_ERR_INVALID, "w8a16_rmsnorm_matmul: residual_out must not alias x or residual");
+  if (N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_rmsnorm_matmul: N, K must be positive");
+  if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_rmsnorm_matmul: N=%lld must be a multiple of 16", (long long)N);
+  if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_rmsnorm_matmul: K=%lld must be a multiple of 8", (long long)K);
+  if (!ldk::aligned(x, 16) || !ldk::aligned(norm_weight, 16) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2) ||
+      (residual && (!ldk::aligned(residual, 16) || !ldk::aligned(residual_out, 16))))
+    return ldk::fail(LDK_ERR_ALIGN, "w8a16_rmsnorm_matmul: x, norm_weight, residual, residual_out and wq must be 16-byte aligned");
+  if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_rmsnorm_matmul: N or K too large");
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w8a16_rmsnorm_matmul: workspace must be a 256-byte aligned pointer");
+  const W8Plan p = make_w8_plan(1, N, K, 0, 0, workspace ? workspace_bytes : 0);
+  const W8Args a{(const half_t*)x,  K,      wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K,
+                 (const half_t*)residual, (half_t*)residual_out, (const half_t*)norm_weight, eps};
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
+  return launch_w8(a, sp, p, (hipStream_t)stream, residual ? 3 : 2);
 }

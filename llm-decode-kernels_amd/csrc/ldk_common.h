@@ -48,6 +48,14 @@ __device__ __forceinline__ half_t silu_f16(half_t g) {
   return (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
 }
 
+// RMSNorm's staged value of one element with the steps of the standalone RMSNorm kernel:
+// w * fp16(h * rs), the product rounded to fp16 once and the weight applied as an fp16 multiply.
+__device__ __forceinline__ half_t rms_f16(half_t h, float rs, half_t w) {
+  float v = (float)h * rs;
+  asm volatile("" : "+v"(v));  // a -0 * rs must stay -0 (no v_fma_mix with a +0 addend)
+  return w * (half_t)v;
+}
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ half2_t u2h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }

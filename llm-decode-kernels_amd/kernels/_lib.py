@@ -53,6 +53,8 @@ SIGNATURES = {
     "ldk_fp8_quantize": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
     "ldk_fp8_dequant": [_vp, _vp, _i32, _vp, _i64, _i64, _vp],
     "ldk_w8a16_swiglu_matmul": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp],
+    "ldk_w8a16_rmsnorm_matmul": [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _vp,
+                                 _i64, _vp],
     "ldk_w8a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
                          _vp, _i64, _vp],
     "ldk_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _f32, _vp],

@@ -169,7 +169,12 @@ class OursFP8Backend(OursBackend):
 
         return w8a16_matmul(x, p.qweight, p.scales, bias=p.bias)
 
-    norm_linear = Backend.norm_linear  # the fused RMSNorm entry takes W4A16 weights
+    def norm_linear(self, x, w, eps, residual, p: Linear):
+        """One launch at decode: the RMSNorm (+ residual) forms the FP8 projection's activation
+        (kernels.fused.rmsnorm_w8a16_matmul)."""
+        from kernels.fused import rmsnorm_w8a16_matmul
+
+        return rmsnorm_w8a16_matmul(x, w, eps, residual, p.qweight, p.scales, bias=p.bias)
 
     def act_linear(self, gate_up, p: Linear):
         """One launch at decode: SwiGLU forms the FP8 down projection's activation

@@ -1,5 +1,5 @@
 """Fusions on either side of the decode GEMVs (libldk_amd.so `ldk_w4a16_rmsnorm_matmul`,
-`ldk_w4a16_swiglu_matmul`, `ldk_w8a16_swiglu_matmul`).
+`ldk_w4a16_swiglu_matmul`, `ldk_w8a16_rmsnorm_matmul`, `ldk_w8a16_swiglu_matmul`).
 
 The reference's OursBackend runs a decode layer as separate kernels: rmsnorm (+ residual), then
 the W4A16 projection; swiglu, then the down projection (kernels/e2e/model.py:79-97). Here the
@@ -121,4 +121,42 @@ def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
     return out
 
 
-__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "swiglu_w8a16_matmul"]
+def rmsnorm_w8a16_matmul(x, weight, eps, residual, wq, scale, bias=None):
+    """y = w8a16_matmul(rmsnorm(x, weight, eps, residual), wq, scale) (+ bias).
+
+    Returns (y, x + residual) when a residual is given, else (y, None). One row runs one launch
+    (ldk_w8a16_rmsnorm_matmul), more rows the two ops back to back."""
+    from kernels.fp8 import FP8, w8a16_matmul
+
+    K = x.shape[-1]
+    N = wq.shape[1]
+    rows = x.numel() // K
+    fuse = (rows == 1 and x.dtype == torch.float16 and weight.dtype == torch.float16 and x.is_cuda
+            and K % 8 == 0 and N % 16 == 0 and wq.dtype == FP8 and scale.dtype == torch.float16
+            and _aligned(x, weight, residual, wq))
+    if not fuse:
+        if residual is None:
+            h, res = rmsnorm(x, weight, eps), None
+        else:
+            h, res = rmsnorm(x, weight, eps, residual=residual)
+        return w8a16_matmul(h, wq, scale, bias=bias), res
+    assert wq.shape[0] == K and weight.numel() == K and scale.numel() == N
+    dev = _lib.require_gpu(x, weight, residual, wq, scale, bias, what="rmsnorm_w8a16_matmul")
+    if residual is not None and residual.shape != x.shape:
+        raise ValueError("rmsnorm_w8a16_matmul: residual must have x's shape")
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    sc = scale.contiguous()
+    out = torch.empty((*x.shape[:-1], N), dtype=torch.float16, device=dev)
+    res_out = None if residual is None else torch.empty_like(x)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w8a16_rmsnorm_matmul(
+            _lib.ptr(x), _lib.ptr(residual), _lib.ptr(res_out), _lib.ptr(weight), float(eps),
+            _lib.ptr(wq), _lib.ptr(sc), _lib.ptr(b), _lib.ptr(out), N, K, ws, ws_bytes,
+            _lib.stream(dev))
+    _lib.check(st, "rmsnorm_w8a16_matmul")
+    return out, res_out
+
+
+__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "rmsnorm_w8a16_matmul",
+           "swiglu_w8a16_matmul"]

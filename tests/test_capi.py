@@ -117,6 +117,23 @@ def test_w8a16_swiglu_validates_before_launch():
     assert st == _lib.ERR_ALIGN
 
 
+def test_w8a16_rmsnorm_validates_before_launch():
+    lib = _lib.load()
+    p, q = ctypes.c_void_p(256), ctypes.c_void_p(512)
+    st, msg = _err(lib.ldk_w8a16_rmsnorm_matmul(p, q, q, p, 1e-6, p, p, None, p, 64, 256, None, 0,
+                                                None))
+    assert st == _lib.ERR_INVALID and "alias" in msg
+    st, _ = _err(lib.ldk_w8a16_rmsnorm_matmul(p, q, None, p, 1e-6, p, p, None, p, 64, 256, None, 0,
+                                              None))
+    assert st == _lib.ERR_INVALID
+    st, _ = _err(lib.ldk_w8a16_rmsnorm_matmul(ctypes.c_void_p(258), None, None, p, 1e-6, p, p, None,
+                                              p, 64, 256, None, 0, None))
+    assert st == _lib.ERR_ALIGN
+    st, _ = _err(lib.ldk_w8a16_rmsnorm_matmul(p, None, None, p, 1e-6, p, p, None, p, 40, 256, None,
+                                              0, None))
+    assert st == _lib.ERR_UNSUPPORTED
+
+
 def test_rmsnorm_residual_pairing_rejected():
     lib = _lib.load()
     p = ctypes.c_void_p(256)

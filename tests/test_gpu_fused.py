@@ -1,5 +1,5 @@
 """The fused decode entries (kernels.fused: ldk_w4a16_rmsnorm_matmul, ldk_w4a16_swiglu_matmul,
-ldk_w8a16_swiglu_matmul) against the oracle's unfused chain (kernels/reference.py:9-45: rmsnorm_ref or swiglu_ref, then
+ldk_w8a16_rmsnorm_matmul, ldk_w8a16_swiglu_matmul) against the oracle's unfused chain (kernels/reference.py:9-45: rmsnorm_ref or swiglu_ref, then
 the fp32 dequantize-then-matmul) and against the library's own two-launch composition.
 
 Bars: the north star's max-abs 2e-2 and rel-L2 1e-3 against the oracle chain; the updated
@@ -15,7 +15,8 @@ import torch
 from _util import assert_north_star, bits16, to_np
 from kernels.bench import cases
 from kernels.fp8 import FP8, quantize_fp8, w8a16_matmul
-from kernels.fused import rmsnorm_w4a16_matmul, swiglu_w4a16_matmul, swiglu_w8a16_matmul
+from kernels.fused import (rmsnorm_w4a16_matmul, rmsnorm_w8a16_matmul, swiglu_w4a16_matmul,
+                           swiglu_w8a16_matmul)
 from kernels.quant import quantize_rtn
 from kernels.rmsnorm import rmsnorm
 from kernels.swiglu import swiglu_fused
@@ -94,6 +95,33 @@ def test_swiglu_w8a16_matmul(N, K, bias):
     assert_north_star(to_np(y), ref)
     # same staged activations, same plan and reduction order as the two launches
     assert torch.equal(y, w8a16_matmul(swiglu_fused(gu.cuda()), wq, sc, bias=b))
+
+
+# FP8 qkv (bias), o, gate_up, a K of more than 256 row vectors (the statistic's extra loop), the
+# e4m3 lm_head
+@pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (1536, 1536, False), (17920, 1536, False),
+                                      (512, 4096, False), (151936, 1536, False)])
+@pytest.mark.parametrize("with_res", [True, False])
+def test_rmsnorm_w8a16_matmul(N, K, bias, with_res):
+    w, _ = cases.w4a16_case(1, N, K, 51)
+    wq, sc = quantize_fp8(w.cuda())
+    b = (torch.randn(N, generator=cases.gen(52)) * 0.1).half().cuda() if bias else None
+    x, r, wn = cases.rmsnorm_case(1, K, 53)
+    r_arg = r.cuda() if with_res else None
+    y, res = rmsnorm_w8a16_matmul(x.cuda(), wn.cuda(), 1e-6, r_arg, wq, sc, bias=b)
+    if with_res:
+        xn, h = rmsnorm_ref(x.numpy(), wn.numpy(), 1e-6, residual=r.numpy())
+        assert np.array_equal(bits16(res), bits16(h))  # x + residual, one fp16 add
+    else:
+        xn = rmsnorm_ref(x.numpy(), wn.numpy(), 1e-6)
+        assert res is None
+    ref = of.w8a16_ref(xn, to_np(wq.view(torch.uint8)), to_np(sc), None if b is None else to_np(b))
+    assert_north_star(to_np(y), ref)
+    # the two-launch composition, within a few fp16 ulps (statistic reduced in another order)
+    h2 = rmsnorm(x.cuda(), wn.cuda(), 1e-6, residual=r_arg)
+    y2 = w8a16_matmul(h2[0] if with_res else h2, wq, sc, bias=b)
+    d = (y.float() - y2.float()).abs()
+    assert float(d.max()) <= 4e-3 * max(1.0, float(y2.float().abs().max())), float(d.max())
 
 
 def test_swiglu_w8a16_rows_other_than_one_compose():
