@@ -224,6 +224,30 @@ int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_f
                          void* v_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
                          float scale, void* stream);
 
+/* Residual + RMSNorm carried across the two projections around it (decode, one row), as a pair
+ * of launches that replaces linear + rmsnorm(x, residual) + linear of the reference's layer
+ * (kernels/e2e/model.py:79-97, 226-233: o_proj, post_attention_layernorm, gate_up). Group size
+ * 128. No counterpart entry exists in the reference; it is this build's fusion of its pair.
+ *
+ * ldk_w4a16_matmul_residual_stats: h_out [N] = fp16(fp16(x @ dequant(W)^T (+ bias)) + residual)
+ * (the linear's fp16 output, then the norm's fp16 residual add) and row_stats[t] = the sum of
+ * h^2 over column tile t, for ldk_w4a16_row_stats_count(N, K, group_size) tiles (at most 256).
+ * h_out may alias residual (an in-place residual update), not x; residual and h_out 8-byte
+ * aligned. ldk_w4a16_rmsnorm_stats_matmul: out [N] = rmsnorm(h) @ dequant(W)^T (+ bias) with the
+ * statistic summed from those nstats partials; the activation norm_weight * fp16(h * rsqrt(
+ * mean(h^2) + eps)) as ldk_rmsnorm forms it (the statistic's order differs, so a staged value can
+ * differ from ldk_rmsnorm's by one fp16 ulp). norm_weight 16-byte aligned. */
+int64_t ldk_w4a16_row_stats_count(int64_t N, int64_t K, int group_size); /* < 0: -ldk_status */
+int ldk_w4a16_matmul_residual_stats(const void* x, const void* residual, void* h_out, float* row_stats,
+                                    const int32_t* qweight, const void* scales, const void* zeros,
+                                    const void* bias, int64_t N, int64_t K, int group_size,
+                                    void* workspace, int64_t workspace_bytes, void* stream);
+int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int nstats,
+                                   const void* norm_weight, float eps, const int32_t* qweight,
+                                   const void* scales, const void* zeros, const void* bias,
+                                   void* out, int64_t N, int64_t K, int group_size,
+                                   void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------- greedy decode bookkeeping */
 
 /* idx = argmax(logits[0:V]) (torch.argmax order: NaN largest, lowest index on ties), then

@@ -183,20 +183,34 @@ __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, con
 //    pass, as buffer loads that read zero past the row without a branch. Workgroup 0 writes h,
 //    the updated residual stream, to res_out;
 //  - kProSwiglu: x = fp16(silu(g)) * u from a fused [g | u] row of 2K (the standalone SwiGLU
-//    kernel's steps, so the staged values are bit-identical to its output).
-enum Prologue { kProNone = 0, kProRms = 1, kProRmsRes = 2, kProSwiglu = 3, kProRmsX = 4, kProRmsResX = 5 };
+//    kernel's steps, so the staged values are bit-identical to its output);
+//  - kProRmsPre: x = rmsnorm(h) * weight where the row statistic comes from the per-tile partial
+//    sums of squares that the kEpiResStat launch producing h wrote: every wave sums them itself
+//    (a fixed lane order, so every workgroup gets the same bits), with no barrier and no row
+//    loads beyond its own staged rows.
+// and one epilogue, for the projection that feeds a residual + RMSNorm:
+//  - kEpiResStat (whole tiles, x as given): h = fp16(y + residual) with y the fp16 output (the
+//    reference's linear, then the norm's residual add), stored as the output, and the tile's
+//    sum of h^2 stored to stats[tile].
+enum Prologue {
+  kProNone = 0, kProRms = 1, kProRmsRes = 2, kProSwiglu = 3, kProRmsX = 4, kProRmsResX = 5,
+  kProRmsPre = 6, kEpiResStat = 7
+};
+constexpr int kMaxRowStats = 256;  // per-tile partials a kProRmsPre launch reads
 
 struct ProArgs {
-  const half_t* res;  // kProRmsRes: residual added before the norm
+  const half_t* res;  // kProRmsRes, kEpiResStat: residual added before the norm
   half_t* res_out;    // kProRmsRes: x + residual (written by workgroup 0)
   const half_t* nw;   // kProRms*: norm weight [K]
   float eps;
+  float* stats;       // kEpiResStat: per-tile sums of h^2 (written); kProRmsPre: read
+  int nstats;
 };
 
 // The staged 8 activations of one packed row from the raw loads (x, second operand, norm weight).
 template <int PRO>
 __device__ __forceinline__ u32x4 pro_stage(u32x4 xr, u32x4 x2, u32x4 x3, float rs) {
-  if constexpr (PRO == kProNone) {
+  if constexpr (PRO == kProNone || PRO == kEpiResStat) {
     return xr;
   } else if constexpr (PRO == kProSwiglu) {
     const half8_t g = __builtin_bit_cast(half8_t, xr), u = __builtin_bit_cast(half8_t, x2);
@@ -231,7 +245,7 @@ constexpr bool m1_lds_ok(int ln, int nw, int mr) { return m1_lds_bytes(ln, nw, m
 // averages 3.1 six-wave workgroups per CU, and at 6 waves per SIMD a CU's fourth workgroup does
 // not fit and runs as a tail (measured 5.17 -> 5.80 us at 73 VGPRs).
 template <int LN, int NW, int RSH, int PRO, int MR>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LN == 8 && NW <= 8 && PRO == kProNone ? 7 : 1)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(LN == 8 && NW <= 8 && (PRO == kProNone || PRO == kProRmsPre) ? 7 : 1)))
 void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
   static_assert(MR == 1 || PRO == kProNone, "fused prologues take one row");
   constexpr int LKW = 64 / LN, RPL = 4, RPW = RPL * LKW, CW = 4 * LN;
@@ -241,6 +255,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
   constexpr bool kExact = PRO == kProRmsX || PRO == kProRmsResX;
   constexpr bool kRes = PRO == kProRmsRes || PRO == kProRmsResX;
   constexpr bool kRms = kExact || PRO == kProRms || PRO == kProRmsRes;
+  constexpr bool kPre = PRO == kProRmsPre, kEpi = PRO == kEpiResStat;
   constexpr int kStatV = 2;  // row vectors per thread loaded ahead of the pass (general variants)
   __shared__ __align__(16) unsigned char xrec[NW][MR][RPW][32];
   __shared__ __align__(16) float4_t red[NW][MR][LN];
@@ -282,7 +297,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
     }
     if constexpr (kRes) P.x2 = *reinterpret_cast<const u32x4*>(pa.res + xo);
     if constexpr (PRO == kProSwiglu) P.x2 = *reinterpret_cast<const u32x4*>(a.x + a.K + xo);
-    if constexpr (kRms) P.x3 = *reinterpret_cast<const u32x4*>(pa.nw + xo);
+    if constexpr (kRms || kPre) P.x3 = *reinterpret_cast<const u32x4*>(pa.nw + xo);
     const int g = min(gp + gi, ge - 1);  // clamped; such lanes are masked out below
     P.sv = *reinterpret_cast<const u32x2*>(a.s + (int64_t)g * a.N + col);
     P.zv = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + col);
@@ -335,11 +350,19 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
       if constexpr (kRes) sr[i] = ldk::buffer_load16(rb, off);
     }
   }
+  // ---- kProRmsPre: the per-tile partial sums of squares, ahead of the pass (zeros past nstats)
+  float pst[kMaxRowStats / 64];
+  if constexpr (kPre) {
+    const auto sb = ldk::buffer_rsrc(pa.stats, (uint32_t)pa.nstats * 4u);
+#pragma unroll
+    for (int i = 0; i < kMaxRowStats / 64; ++i)
+      pst[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sb, 4u * (uint32_t)(lane + 64 * i), 0, 0));
+  }
   int gp = gb + wave * gpw;
   Pass P;
   if constexpr (kExact) {
     load_pass(gp, P);  // every wave has exactly one pass
-  } else if constexpr (kRms) {
+  } else if constexpr (kRms || kPre) {  // branch free: the statistic's wait covers its loads only
     load_pass_buf(gp, gp < ge, P);
   } else {
     if (gp < ge) load_pass(gp, P);
@@ -347,6 +370,13 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
   __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
 
   float rs = 0.0f;
+  if constexpr (kPre) {  // same lanes, same order in every wave and workgroup
+    float ss = pst[0];
+#pragma unroll
+    for (int i = 1; i < kMaxRowStats / 64; ++i) ss += pst[i];
+    ss = ldk::sum_lanes_strided<1>(ss);
+    rs = 1.0f / __builtin_sqrtf(ss / (float)a.K + pa.eps);
+  }
   if constexpr (kRms) {
     float ss = 0.0f;
     const bool wr = kRes && blockIdx.x == 0;
@@ -394,7 +424,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
     for (int q = 0; q < 4; ++q) acc[m][q] = 0.0f;
   for (bool first = true; gp < ge; gp += NW * gpw, first = false) {
     if (!first) {
-      if constexpr (kRms && !kExact) load_pass_buf(gp, true, P);
+      if constexpr ((kRms && !kExact) || kPre) load_pass_buf(gp, true, P);
       else load_pass(gp, P);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -486,6 +516,23 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
     if (wave != 0) return;
     if (whole || sp.splits == 1) {
       const int c = n0 + 4 * lane;
+      if constexpr (kEpi) {  // h = fp16(y + residual) stored, the tile's sum of h^2 published
+        float ps = 0.0f;
+        if (lane < LN && c < a.N) {
+          float4_t v = red[0][0][lane];
+#pragma unroll
+          for (int i = 1; i < NW; ++i) v += red[i][0][lane];
+          if (a.bias) v += float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
+          const half4_t y{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+          const half4_t h = y + *reinterpret_cast<const half4_t*>(pa.res + c);  // fp16 add
+          *reinterpret_cast<half4_t*>(a.out + c) = h;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ps = __builtin_fmaf((float)h[q], (float)h[q], ps);
+        }
+        ps = ldk::sum_lanes_strided<1>(ps);
+        if (lane == 0) pa.stats[tile] = ps;
+        return;
+      }
       if (lane >= LN || c >= a.N) return;
       float4_t v = red[0][0][lane];
 #pragma unroll
@@ -1152,6 +1199,8 @@ int launch_m1_t(const W4Args& a, const SplitArgs& sp, int mr, int pro, const Pro
         case kProRmsX: w4a16_m1_kernel<LN, NW, 4, kProRmsX, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         case kProRmsResX: w4a16_m1_kernel<LN, NW, 4, kProRmsResX, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         case kProSwiglu: w4a16_m1_kernel<LN, NW, 4, kProSwiglu, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProRmsPre: w4a16_m1_kernel<LN, NW, 4, kProRmsPre, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kEpiResStat: w4a16_m1_kernel<LN, NW, 4, kEpiResStat, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         default: return ldk::fail(LDK_ERR_INVALID, "w4a16: unknown prologue %d", pro);
       }
       return ldk::check_launch("w4a16_m1");
@@ -1433,4 +1482,78 @@ extern "C" int ldk_w4a16_swiglu_matmul(const void* gate_up, const int32_t* qweig
   const W4Args a{(const half_t*)gate_up, 2 * K, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
                  (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K, gsh_rows};
   return launch_plan(a, p, workspace, (hipStream_t)stream, kProSwiglu, ProArgs{});
+}
+
+// Residual + RMSNorm split across the two projections around it (decode, one row). The first
+// launch (the o projection of a layer) computes h = fp16(y + residual), the new residual stream,
+// for its columns and publishes one partial sum of h^2 per column tile; the second (gate_up)
+// forms rmsnorm(h) * weight while it stages h, summing those partials instead of reducing the
+// row itself (no barrier, no extra row loads, and its balanced grid). The pair replaces
+// linear + rmsnorm(x, residual) + linear of the reference's layer (kernels/e2e/model.py:79-97,
+// 226-233). The first launch runs whole column tiles (each tile's columns end in one workgroup).
+
+namespace {
+Plan residual_stats_plan(int64_t N, int64_t K, int gsh_rows, size_t ws) {
+  Plan p = make_plan(1, N, K, gsh_rows, 0, 0, 0, ws);
+  p.full = 0;
+  p.splits = 1;
+  p.gps = (int)((K / 8) >> gsh_rows);
+  const int gw = (64 / p.ln) >> (gsh_rows - 2);
+  p.nw = m1_round_nw(std::min<int64_t>(m1_max_waves(p.ln, 1), (p.gps + gw - 1) / gw));
+  return p;
+}
+}  // namespace
+
+extern "C" int64_t ldk_w4a16_row_stats_count(int64_t N, int64_t K, int group_size) {
+  const int gsh = log2_exact(group_size);
+  if (N <= 0 || K <= 0 || gsh < 5 || gsh > 8 || K % group_size)
+    return -(int64_t)ldk::fail(LDK_ERR_INVALID, "w4a16_row_stats_count: bad shape N=%lld K=%lld group_size=%d",
+                               (long long)N, (long long)K, group_size);
+  const Plan p = residual_stats_plan(N, K, gsh - 3, (size_t)ldk_workspace_bytes());
+  return (N + plan_cw(p) - 1) / plan_cw(p);
+}
+
+extern "C" int ldk_w4a16_matmul_residual_stats(const void* x, const void* residual, void* h_out, float* row_stats,
+                                               const int32_t* qweight, const void* scales, const void* zeros,
+                                               const void* bias, int64_t N, int64_t K, int group_size, void* workspace,
+                                               int64_t workspace_bytes, void* stream) {
+  int gsh_rows = 0;
+  int st = validate("w4a16_matmul_residual_stats", x, K, qweight, scales, zeros, h_out, N, 1, N, K, group_size, &gsh_rows);
+  if (st) return st;
+  if (!residual || !row_stats) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul_residual_stats: null residual or row_stats");
+  if (h_out == x) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul_residual_stats: h_out must not alias x");
+  if (!ldk::aligned(residual, 8) || !ldk::aligned(h_out, 8) || !ldk::aligned(row_stats, 4))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul_residual_stats: residual and h_out 8-byte, row_stats 4-byte aligned");
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul_residual_stats: workspace must be a 256-byte aligned pointer");
+  const Plan p = residual_stats_plan(N, K, gsh_rows, workspace ? (size_t)workspace_bytes : 0);
+  const int64_t tiles = (N + plan_cw(p) - 1) / plan_cw(p);
+  if (tiles > kMaxRowStats)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul_residual_stats: %lld column tiles exceed %d partials",
+                     (long long)tiles, kMaxRowStats);
+  const W4Args a{(const half_t*)x, K, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                 (const half_t*)bias, (half_t*)h_out, N, 1, (int)N, (int)K, gsh_rows};
+  const ProArgs pa{(const half_t*)residual, nullptr, nullptr, 0.0f, row_stats, (int)tiles};
+  return launch_plan(a, p, workspace, (hipStream_t)stream, kEpiResStat, pa);
+}
+
+extern "C" int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int nstats, const void* norm_weight,
+                                              float eps, const int32_t* qweight, const void* scales, const void* zeros,
+                                              const void* bias, void* out, int64_t N, int64_t K, int group_size,
+                                              void* workspace, int64_t workspace_bytes, void* stream) {
+  int gsh_rows = 0;
+  int st = validate("w4a16_rmsnorm_stats_matmul", h, K, qweight, scales, zeros, out, N, 1, N, K, group_size, &gsh_rows);
+  if (st) return st;
+  if (!row_stats || !norm_weight) return ldk::fail(LDK_ERR_INVALID, "w4a16_rmsnorm_stats_matmul: null row_stats or norm_weight");
+  if (nstats <= 0 || nstats > kMaxRowStats)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_rmsnorm_stats_matmul: nstats=%d outside 1..%d", nstats, kMaxRowStats);
+  if (!ldk::aligned(norm_weight, 16) || !ldk::aligned(row_stats, 4))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_rmsnorm_stats_matmul: norm_weight 16-byte, row_stats 4-byte aligned");
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "w4a16_rmsnorm_stats_matmul: workspace must be a 256-byte aligned pointer");
+  const Plan p = make_plan(1, N, K, gsh_rows, 0, 0, 0, workspace ? (size_t)workspace_bytes : 0);
+  const W4Args a{(const half_t*)h, K, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                 (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K, gsh_rows};
+  const ProArgs pa{nullptr, nullptr, (const half_t*)norm_weight, eps, const_cast<float*>(row_stats), nstats};
+  return launch_plan(a, p, workspace, (hipStream_t)stream, kProRmsPre, pa);
 }

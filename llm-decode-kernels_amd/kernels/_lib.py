@@ -53,6 +53,11 @@ SIGNATURES = {
     "ldk_fp8_quantize": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
     "ldk_fp8_dequant": [_vp, _vp, _i32, _vp, _i64, _i64, _vp],
     "ldk_w8a16_swiglu_matmul": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp],
+    "ldk_w4a16_row_stats_count": [_i64, _i64, _i32],
+    "ldk_w4a16_matmul_residual_stats": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32,
+                                        _vp, _i64, _vp],
+    "ldk_w4a16_rmsnorm_stats_matmul": [_vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64,
+                                       _i64, _i32, _vp, _i64, _vp],
     "ldk_w8a16_rmsnorm_matmul": [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _vp,
                                  _i64, _vp],
     "ldk_w8a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
@@ -86,7 +91,8 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = {"ldk_last_error": ctypes.c_char_p,
-                              "ldk_workspace_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
+                              "ldk_workspace_bytes": ctypes.c_int64,
+                              "ldk_w4a16_row_stats_count": ctypes.c_int64}.get(name, ctypes.c_int)
             _lib = lib
     return _lib
 

@@ -83,6 +83,11 @@ class Backend:
         """act then linear (the MLP's down projection, model.py:233)."""
         return self.linear(self.act(gate_up), p)
 
+    def linear_norm_linear(self, x, p1: Linear, residual, w, eps, p2: Linear):
+        """linear, then norm (+ residual) then linear: the attention output projection, the
+        post-attention norm and gate_up (model.py:226-233). Returns (y2, new residual)."""
+        return self.norm_linear(self.linear(x, p1), w, eps, residual, p2)
+
 
 class W4RefBackend(Backend):
     """RTN int4 weights dequantized once (bit-exact HIP dequantizer) then the fp16 GEMM: the same
@@ -140,6 +145,18 @@ class OursBackend(Backend):
         return rmsnorm_w4a16_matmul(x, w, eps, residual, p.qweight, p.scales, p.zeros,
                                     config.GROUP_SIZE, p.bias)
 
+    def linear_norm_linear(self, x, p1: Linear, residual, w, eps, p2: Linear):
+        """Two launches at decode: the first projection's epilogue adds the residual and
+        publishes the row's partial sums of squares, the second forms the norm while it stages
+        its input (kernels.fused.linear_rmsnorm_w4a16_matmul)."""
+        if self.decode_kernel != "library":
+            return super().linear_norm_linear(x, p1, residual, w, eps, p2)
+        from kernels.fused import linear_rmsnorm_w4a16_matmul
+
+        return linear_rmsnorm_w4a16_matmul(x, p1.qweight, p1.scales, p1.zeros, p1.bias, residual,
+                                           w, eps, p2.qweight, p2.scales, p2.zeros, p2.bias,
+                                           config.GROUP_SIZE)
+
     def act_linear(self, gate_up, p: Linear):
         """One launch at decode: SwiGLU forms the down projection's activation (kernels.fused)."""
         if self.decode_kernel != "library":
@@ -175,6 +192,8 @@ class OursFP8Backend(OursBackend):
         from kernels.fused import rmsnorm_w8a16_matmul
 
         return rmsnorm_w8a16_matmul(x, w, eps, residual, p.qweight, p.scales, bias=p.bias)
+
+    linear_norm_linear = Backend.linear_norm_linear  # the residual-statistics pair is W4A16
 
     def act_linear(self, gate_up, p: Linear):
         """One launch at decode: SwiGLU forms the FP8 down projection's activation
@@ -366,8 +385,7 @@ class QwenRunner:
                 q = self._rope(q.view(B, T, nq, hd), cos, sin)
                 k = self._rope(k.view(B, T, nkv, hd), cos, sin)
                 attn = self._attend(i, q, k, v.view(B, T, nkv, hd), pos)
-            o = be.linear(attn, L.o)
-            gate_up, residual = be.norm_linear(o, L.ln2, eps, residual, L.gate_up)
+            gate_up, residual = be.linear_norm_linear(attn, L.o, residual, L.ln2, eps, L.gate_up)
             h = be.act_linear(gate_up, L.down)
         if not all_logits:  # the final norm is per row: normalize the last row only
             h, residual = h[:, -1:], residual[:, -1:]

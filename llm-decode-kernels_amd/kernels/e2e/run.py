@@ -104,7 +104,7 @@ def decode_speed(runner, ids, steps: int, repeats: int = 3) -> dict:
 def layers_only_ms(runner, M: int = 1) -> float:
     """Graph time of the swapped ops alone for one decode step (run.py:166-201): per layer the
     qkv, o, gate_up and down projections, two add+norms and the activation, through the
-    backend's norm_linear/act_linear (one launch per pair on the fused backends)."""
+    backend's norm_linear/linear_norm_linear/act_linear (fused launches on the fused backends)."""
     be, eps = runner.backend, runner.eps
     dev = runner.embed.device
     H = runner.embed.shape[1]
@@ -117,8 +117,8 @@ def layers_only_ms(runner, M: int = 1) -> float:
         h, r = x, res
         for L in runner.layers:
             qkv, r = be.norm_linear(h, L.ln1, eps, r, L.qkv)
-            o = be.linear(qkv[..., : nq * hd].contiguous(), L.o)
-            gate_up, r = be.norm_linear(o, L.ln2, eps, r, L.gate_up)
+            gate_up, r = be.linear_norm_linear(qkv[..., : nq * hd].contiguous(), L.o, r, L.ln2,
+                                               eps, L.gate_up)
             h = be.act_linear(gate_up, L.down)
 
     for _ in range(3):

@@ -1,5 +1,6 @@
 """Fusions on either side of the decode GEMVs (libldk_amd.so `ldk_w4a16_rmsnorm_matmul`,
-`ldk_w4a16_swiglu_matmul`, `ldk_w8a16_rmsnorm_matmul`, `ldk_w8a16_swiglu_matmul`).
+`ldk_w4a16_swiglu_matmul`, `ldk_w4a16_matmul_residual_stats` + `ldk_w4a16_rmsnorm_stats_matmul`,
+`ldk_w8a16_rmsnorm_matmul`, `ldk_w8a16_swiglu_matmul`).
 
 The reference's OursBackend runs a decode layer as separate kernels: rmsnorm (+ residual), then
 the W4A16 projection; swiglu, then the down projection (kernels/e2e/model.py:79-97). Here the
@@ -92,6 +93,57 @@ def swiglu_w4a16_matmul(gate_up, qweight, scales, zeros, group_size=128, bias=No
     return out
 
 
+def linear_rmsnorm_w4a16_matmul(x, qweight1, scales1, zeros1, bias1, residual, weight, eps,
+                                qweight2, scales2, zeros2, bias2=None, group_size=128):
+    """The pair linear -> rmsnorm(+ residual) -> linear of a decoder layer (o_proj,
+    post_attention_layernorm, gate_up: kernels/e2e/model.py:226-233 of the reference).
+
+    Returns (y2, h) with h = linear1(x) + residual, the updated residual stream, and
+    y2 = linear2(rmsnorm(h) * weight). One row runs two launches
+    (ldk_w4a16_matmul_residual_stats, ldk_w4a16_rmsnorm_stats_matmul): the residual add and the
+    row's per-tile sums of squares come out of the first projection's epilogue, so the second
+    one forms the norm in its x staging without reducing the row itself. Other rows run
+    w4a16_matmul then rmsnorm_w4a16_matmul."""
+    K1 = x.shape[-1]
+    N1 = qweight1.shape[1]
+    rows = x.numel() // K1
+    fuse = (rows == 1 and group_size == FUSED_GROUP_SIZE and x.dtype == torch.float16 and x.is_cuda
+            and residual is not None and residual.dtype == torch.float16
+            and residual.numel() == N1 and weight.dtype == torch.float16
+            and _aligned(x, residual, weight, qweight1, qweight2))
+    nstats = int(_lib.load().ldk_w4a16_row_stats_count(N1, K1, group_size)) if fuse else 0
+    if not fuse or not 0 < nstats <= 256:
+        y1 = w4a16_matmul(x, qweight1, scales1, zeros1, group_size, bias1)
+        return rmsnorm_w4a16_matmul(y1, weight, eps, residual, qweight2, scales2, zeros2,
+                                    group_size, bias2)
+    K2, N2 = N1, qweight2.shape[1]
+    assert qweight1.shape[0] * 8 == K1 and qweight2.shape[0] * 8 == K2 and weight.numel() == K2
+    dev = _lib.require_gpu(x, residual, weight, qweight1, scales1, zeros1, bias1, qweight2,
+                           scales2, zeros2, bias2, what="linear_rmsnorm_w4a16_matmul")
+    for t in (scales1, zeros1, scales2, zeros2):
+        if t.dtype != torch.float16:
+            raise ValueError("linear_rmsnorm_w4a16_matmul: scales and zeros must be float16")
+    b1 = None if bias1 is None else bias1.to(torch.float16).contiguous()
+    b2 = None if bias2 is None else bias2.to(torch.float16).contiguous()
+    h = torch.empty((*x.shape[:-1], N1), dtype=torch.float16, device=dev)
+    stats = torch.empty(nstats, dtype=torch.float32, device=dev)
+    y2 = torch.empty((*x.shape[:-1], N2), dtype=torch.float16, device=dev)
+    lib = _lib.load()
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = lib.ldk_w4a16_matmul_residual_stats(
+            _lib.ptr(x), _lib.ptr(residual), _lib.ptr(h), _lib.ptr(stats), _lib.ptr(qweight1),
+            _lib.ptr(scales1.contiguous()), _lib.ptr(zeros1.contiguous()), _lib.ptr(b1), N1, K1,
+            group_size, ws, ws_bytes, _lib.stream(dev))
+        _lib.check(st, "linear_rmsnorm_w4a16_matmul")
+        st = lib.ldk_w4a16_rmsnorm_stats_matmul(
+            _lib.ptr(h), _lib.ptr(stats), nstats, _lib.ptr(weight), float(eps), _lib.ptr(qweight2),
+            _lib.ptr(scales2.contiguous()), _lib.ptr(zeros2.contiguous()), _lib.ptr(b2),
+            _lib.ptr(y2), N2, K2, group_size, ws, ws_bytes, _lib.stream(dev))
+        _lib.check(st, "linear_rmsnorm_w4a16_matmul")
+    return y2, h
+
+
 def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
     """y = w8a16_matmul(swiglu_fused(gate_up), wq, scale) (+ bias); gate_up: [..., 2K] fp16,
     wq: [K, N] float8_e4m3fn, scale: [N] fp16. One row runs one launch (ldk_w8a16_swiglu_matmul),
@@ -158,5 +210,5 @@ def rmsnorm_w8a16_matmul(x, weight, eps, residual, wq, scale, bias=None):
     return out, res_out
 
 
-__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "rmsnorm_w8a16_matmul",
-           "swiglu_w8a16_matmul"]
+__all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "linear_rmsnorm_w4a16_matmul",
+           "rmsnorm_w8a16_matmul", "swiglu_w8a16_matmul"]

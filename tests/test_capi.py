@@ -134,6 +134,24 @@ def test_w8a16_rmsnorm_validates_before_launch():
     assert st == _lib.ERR_UNSUPPORTED
 
 
+def test_residual_stats_pair_validation():
+    lib = _lib.load()
+    p, q = ctypes.c_void_p(256), ctypes.c_void_p(4096)
+    assert lib.ldk_w4a16_row_stats_count(1536, 1536, 128) == 96
+    assert lib.ldk_w4a16_row_stats_count(1536, 1000, 128) < 0
+    # h_out aliasing x
+    st, msg = _err(lib.ldk_w4a16_matmul_residual_stats(p, q, p, q, p, p, p, None, 1536, 1536, 128,
+                                                       None, 0, None))
+    assert st == _lib.ERR_INVALID and "alias" in msg
+    # more tiles than partials
+    st, _ = _err(lib.ldk_w4a16_matmul_residual_stats(p, q, q, q, p, p, p, None, 16384, 1536, 128,
+                                                     None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED
+    st, _ = _err(lib.ldk_w4a16_rmsnorm_stats_matmul(p, q, 0, p, 1e-6, p, p, p, None, p, 2048, 1536,
+                                                    128, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED
+
+
 def test_rmsnorm_residual_pairing_rejected():
     lib = _lib.load()
     p = ctypes.c_void_p(256)

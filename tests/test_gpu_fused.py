@@ -15,8 +15,8 @@ import torch
 from _util import assert_north_star, bits16, to_np
 from kernels.bench import cases
 from kernels.fp8 import FP8, quantize_fp8, w8a16_matmul
-from kernels.fused import (rmsnorm_w4a16_matmul, rmsnorm_w8a16_matmul, swiglu_w4a16_matmul,
-                           swiglu_w8a16_matmul)
+from kernels.fused import (linear_rmsnorm_w4a16_matmul, rmsnorm_w4a16_matmul,
+                           rmsnorm_w8a16_matmul, swiglu_w4a16_matmul, swiglu_w8a16_matmul)
 from kernels.quant import quantize_rtn
 from kernels.rmsnorm import rmsnorm
 from kernels.swiglu import swiglu_fused
@@ -129,6 +129,30 @@ def test_swiglu_w8a16_rows_other_than_one_compose():
     wq, sc = quantize_fp8(w.cuda())
     gu = cases.swiglu_case(3, 768, 45).cuda()
     assert torch.equal(swiglu_w8a16_matmul(gu, wq, sc), w8a16_matmul(swiglu_fused(gu), wq, sc))
+
+
+# (o projection N1 x K1) -> norm -> (N2 x N1): the Qwen2.5-1.5B pair into gate_up and into a
+# biased qkv-like projection; a wide first projection (more than 256 tiles) takes the composition
+@pytest.mark.parametrize("N1,K1,N2,bias2", [(1536, 1536, 17920, False), (1536, 1536, 2048, True),
+                                            (1536, 2048, 8960, False), (16384, 1536, 256, False)])
+def test_linear_rmsnorm_pair(N1, K1, N2, bias2):
+    qw1, s1, z1, b1 = _weights(N1, K1, 61, bias=True)
+    qw2, s2, z2, b2 = _weights(N2, N1, 62, bias=bias2)
+    b1, b2 = b1.cuda(), (None if b2 is None else b2.cuda())
+    x = cases.activations(1, K1, cases.gen(63))
+    _, r, wn = cases.rmsnorm_case(1, N1, 64)
+    y2, h = linear_rmsnorm_w4a16_matmul(x.cuda(), qw1, s1, z1, b1, r.cuda(), wn.cuda(), 1e-6,
+                                        qw2, s2, z2, b2)
+    # h: the first projection's fp16 output plus the residual, bit for bit as the composition
+    y1 = w4a16_matmul(x.cuda(), qw1, s1, z1, 128, b1)
+    h_ref = y1 + r.cuda()
+    assert torch.equal(h.view(1, N1), h_ref.view(1, N1))
+    # y2 against the oracle chain (north star) and the two-launch fused norm (a few fp16 ulps)
+    xn = rmsnorm_ref(to_np(h_ref), wn.numpy(), 1e-6)
+    assert_north_star(to_np(y2), _oracle_linear(xn, qw2, s2, z2, None if b2 is None else b2.cpu()))
+    y2c, _ = rmsnorm_w4a16_matmul(y1, wn.cuda(), 1e-6, r.cuda(), qw2, s2, z2, 128, b2)
+    d = (y2.float() - y2c.float()).abs()
+    assert float(d.max()) <= 4e-3 * max(1.0, float(y2c.float().abs().max())), float(d.max())
 
 
 def test_rows_other_than_one_compose():
