@@ -71,6 +71,8 @@ struct AttnArgs {
   half_t* out;            // [nq*128]
   int nq, nkv, max_len;
   int cps;                // 64-position chunks per range (gridDim.y ranges)
+  int xcd_group;          // 1: gridDim.x = 8 * (nq / nkv); workgroup x takes query head j of kv head
+                          // x % 8 (j = x / 8), and exits at once for x % 8 >= nkv
   float scale;
 };
 
@@ -113,7 +115,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void decode_attention_kernel(AttnAr
   __shared__ __align__(16) float ow[kMaxWaves][kHD];     // per-wave unnormalized outputs
   __shared__ float mw[kMaxWaves], lw[kMaxWaves];
   __shared__ int last_flag;
-  const int h = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
+  // The query heads of one kv head read the same K and V: placing them on one XCD (workgroups
+  // are dispatched to the 8 XCDs round-robin) lets its L2 serve the group from one fetch
+  // (max_len 384: 8.3 -> 8.0 us at pos 300).
+  const int gq = a.nq / a.nkv;
+  if (a.xcd_group && (int)(blockIdx.x % 8) >= a.nkv) return;
+  const int h = a.xcd_group ? (int)(blockIdx.x % 8) * gq + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  const int split = blockIdx.y, nsplit = gridDim.y;
   const int g = a.nq / a.nkv, kvh = h / g;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int L = a.max_len;
@@ -380,8 +388,8 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
   const int nsplit = (int)((nchunks + cps - 1) / cps);
   const int nw = (int)std::min<int64_t>(kMaxWaves, cps);
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)kt_cache, (half_t*)v_cache, (half_t*)out,
-                   nq, nkv, (int)max_len, (int)cps, scale};
+                   nq, nkv, (int)max_len, (int)cps, nkv <= 8 ? 1 : 0, scale};
   (void)hipGetLastError();
-  decode_attention_kernel<<<dim3(nq, nsplit), nw * 64, 0, (hipStream_t)stream>>>(a);
+  decode_attention_kernel<<<dim3(nkv <= 8 ? 8 * (nq / nkv) : nq, nsplit), nw * 64, 0, (hipStream_t)stream>>>(a);
   return ldk::check_launch("decode_attention");
 }
