@@ -79,6 +79,46 @@ def case_swiglu_w4a16(N, I, reps):
     _rotate(lambda g, q, sc, zz: swiglu_w4a16_matmul(g, q, sc, zz, GS), sets, reps)
 
 
+def case_linear_rms_pair(reps):
+    """o projection (residual add and per-tile sums of squares in its epilogue) into gate_up
+    (RMSNorm formed in its staging from those sums), at the Qwen2.5-1.5B shapes."""
+    from kernels.fused import linear_rmsnorm_w4a16_matmul
+    from kernels.quant import quantize_rtn
+
+    H, I2 = 1536, 17920
+    w1, _ = cases.w4a16_case(1, H, H, seed=2)
+    w2, _ = cases.w4a16_case(1, I2, H, seed=3)
+    q1, s1, z1 = quantize_rtn(w1.cuda(), GS)
+    q2, s2, z2 = quantize_rtn(w2.cuda(), GS)
+    x, r, wn = (t.cuda() for t in cases.rmsnorm_case(1, H, seed=1))
+    sets = [(q1.clone(), s1.clone(), z1.clone(), q2.clone(), s2.clone(), z2.clone())
+            for _ in range(n_copies(tensor_bytes((q1, s1, z1, q2, s2, z2))))]
+    _rotate(lambda a, b, c, d, e, f: linear_rmsnorm_w4a16_matmul(
+        x, a, b, c, None, r, wn, 1e-6, d, e, f, None, GS), sets, reps)
+
+
+def case_rms_fp8(N, K, reps):
+    from kernels.fp8 import quantize_fp8
+    from kernels.fused import rmsnorm_w8a16_matmul
+
+    w, _ = cases.w4a16_case(1, N, K, seed=3)
+    wq, sc = quantize_fp8(w.cuda())
+    x, r, wn = (t.cuda() for t in cases.rmsnorm_case(1, K, seed=1))
+    sets = [(wq.clone(), sc.clone()) for _ in range(n_copies(tensor_bytes((wq, sc))))]
+    _rotate(lambda q, ss: rmsnorm_w8a16_matmul(x, wn, 1e-6, r, q, ss), sets, reps)
+
+
+def case_swiglu_fp8(N, I, reps):
+    from kernels.fp8 import quantize_fp8
+    from kernels.fused import swiglu_w8a16_matmul
+
+    w, _ = cases.w4a16_case(1, N, I, seed=3)
+    wq, sc = quantize_fp8(w.cuda())
+    gu = cases.swiglu_case(1, I, seed=1).cuda()
+    sets = [(wq.clone(), sc.clone()) for _ in range(n_copies(tensor_bytes((wq, sc))))]
+    _rotate(lambda q, ss: swiglu_w8a16_matmul(gu, q, ss), sets, reps)
+
+
 def case_attention(reps, L=392, pos=300):
     from kernels.attention import decode_attention
 
@@ -122,6 +162,7 @@ CASES = {
     "calib_neg64MiB": lambda r: case_copy(r),
     "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
     "w4a16_down_m1": lambda r: case_w4a16(1, 1536, 8960, r),
+    "w4a16_gate_up_m2": lambda r: case_w4a16(2, 17920, 1536, r),
     "w4a16_gate_up_m4": lambda r: case_w4a16(4, 17920, 1536, r),
     "w4a16_gate_up_m16": lambda r: case_w4a16(16, 17920, 1536, r),
     "w4a16_down_m16": lambda r: case_w4a16(16, 1536, 8960, r),
@@ -130,7 +171,11 @@ CASES = {
     "rms_qkv_m1": lambda r: case_rms_w4a16(2048, 1536, r, True),
     "rms_gate_up_m1": lambda r: case_rms_w4a16(17920, 1536, r, False),
     "swiglu_down_m1": lambda r: case_swiglu_w4a16(1536, 8960, r),
+    "o_rms_gate_up_pair_m1": lambda r: case_linear_rms_pair(r),
+    "fp8_rms_gate_up_m1": lambda r: case_rms_fp8(17920, 1536, r),
+    "fp8_swiglu_down_m1": lambda r: case_swiglu_fp8(1536, 8960, r),
     "attention_l392": lambda r: case_attention(r),
+    "attention_l4096": lambda r: case_attention(r, L=4096, pos=4000),
     "rmsnorm_res_m2048": lambda r: case_rmsnorm(2048, 1536, r),
     "swiglu_m2048": lambda r: case_swiglu(2048, 8960, r),
 }
