@@ -210,18 +210,22 @@ int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void*
  *   qkv:      [nq*head_dim + 2*nkv*head_dim] fp16, the qkv projection output (bias added);
  *   pos:      int64 device scalar, the new token's position (< max_len);
  *   inv_freq: [head_dim/2] fp32 RoPE inverse frequencies;
- *   kt_cache: fp16 [nkv][head_dim][max_len] (K transposed), v_cache: fp16 [nkv][max_len][head_dim];
+ *   k_cache:  fp16 K tiles, per kv head [max_len/32][2][4][16][32]: chunk c, row half hb, dim
+ *             step s, row i, column e hold K[32c + 8(i/4) + 4hb + i%4][32s + e];
+ *   vt_cache: fp16 V^T tiles, per kv head [max_len/32][8][16][32]: step t, dim block b, row r,
+ *             column e hold V[32t + e][16b + r];
  *   out:      [nq*head_dim] fp16; scale: the softmax scale (head_dim^-0.5).
- * head_dim == 128, nq % nkv == 0, max_len a multiple of 8 (kt_cache and v_cache 16-byte
+ * head_dim == 128, nq % nkv == 0, max_len a multiple of 32 (k_cache and vt_cache 16-byte
  * aligned). A *pos >= max_len writes nothing and attends over the whole cache; a negative *pos
  * writes nothing and returns zeros. Caches of more than 512 positions are split into up to 32
- * position ranges per head whose partials meet in library-owned device state that each launch
- * leaves zeroed (graph replay is safe); calls on one device must be stream-ordered.
+ * position ranges per head tile whose partials meet in library-owned device state that each
+ * launch leaves zeroed (graph replay is safe); calls on one device must be stream-ordered.
  * Replaces the per-layer attention of the
  * reference's runner for decode steps (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into
- * the cache, scaled_dot_product_attention with the causal mask). */
-int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* kt_cache,
-                         void* v_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
+ * the cache, scaled_dot_product_attention with the causal mask; the reference's cache is
+ * [batch][kv][max_len][head_dim] for both K and V). */
+int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
+                         void* vt_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
                          float scale, void* stream);
 
 /* Residual + RMSNorm carried across the two projections around it (decode, one row), as a pair

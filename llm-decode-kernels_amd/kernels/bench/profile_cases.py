@@ -119,17 +119,17 @@ def case_swiglu_fp8(N, I, reps):
     _rotate(lambda q, ss: swiglu_w8a16_matmul(gu, q, ss), sets, reps)
 
 
-def case_attention(reps, L=392, pos=300):
-    from kernels.attention import decode_attention
+def case_attention(reps, L=416, pos=300):
+    from kernels.attention import decode_attention, k_cache_shape, vt_cache_shape
 
     g = cases.gen(5)
     nq, nkv, hd = 12, 2, 128
     qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda()
-    kt = torch.randn(1, nkv, hd, L, generator=g).half().cuda()
-    vc = torch.randn(1, nkv, L, hd, generator=g).half().cuda()
+    kc = torch.randn((1,) + k_cache_shape(nkv, L), generator=g).half().cuda()
+    vt = torch.randn((1,) + vt_cache_shape(nkv, L), generator=g).half().cuda()
     inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
     p = torch.tensor([pos], device="cuda")
-    sets = [(kt.clone(), vc.clone()) for _ in range(n_copies(tensor_bytes((kt, vc))))]
+    sets = [(kc.clone(), vt.clone()) for _ in range(n_copies(tensor_bytes((kc, vt))))]
     _rotate(lambda k, v: decode_attention(qkv, p, inv, k, v, nq, nkv, hd ** -0.5), sets, reps)
 
 
@@ -174,7 +174,7 @@ CASES = {
     "o_rms_gate_up_pair_m1": lambda r: case_linear_rms_pair(r),
     "fp8_rms_gate_up_m1": lambda r: case_rms_fp8(17920, 1536, r),
     "fp8_swiglu_down_m1": lambda r: case_swiglu_fp8(1536, 8960, r),
-    "attention_l392": lambda r: case_attention(r),
+    "attention_l416": lambda r: case_attention(r),
     "attention_l4096": lambda r: case_attention(r, L=4096, pos=4000),
     "rmsnorm_res_m2048": lambda r: case_rmsnorm(2048, 1536, r),
     "swiglu_m2048": lambda r: case_swiglu(2048, 8960, r),

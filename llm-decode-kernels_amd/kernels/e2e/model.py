@@ -8,12 +8,13 @@ Same public surface as the reference's kernels/e2e/model.py (`Linear`, `Backend`
   embedding, RoPE, attention and the tied fp16 lm_head are the same torch code on both sides, as
   in the reference (model.py:1-12). q/k/v and gate/up are concatenated into one projection each
   (model.py:168-191).
-- The KV cache keeps K transposed, [layers, batch, kv_heads, head_dim, max_len], and V as
-  [layers, batch, kv_heads, max_len, head_dim], so both attention products are plain batched
-  matmuls over contiguous operands (no transposed right operand). Grouped-query attention folds
-  the query heads of one KV head into the row dimension: scores [B, kv, group*T, max_len].
+- The KV cache is kept in the fused decode attention's tiled operand order (K tiles and V^T
+  tiles, kernels/attention.py), max_len a multiple of 32. The torch path (prompt steps) writes
+  it with kernels.attention.write_kv and reads K and V back in the reference's [.., max_len,
+  head_dim] order; grouped-query attention folds the query heads of one KV head into the row
+  dimension: scores [B, kv, group*T, max_len].
 - Every step is capturable in a hipGraph: positions are device tensors, the cache is written
-  with index_copy_, the causal mask is built from the positions inside the graph.
+  by index on device, the causal mask is built from the positions inside the graph.
 
 The model comes from a Hugging Face Qwen2 module object (as in the reference) or from
 `random_qwen2`, which builds the Qwen2.5-1.5B architecture with Hugging Face's initialisation
@@ -306,13 +307,19 @@ class QwenRunner:
                 gate_up=lin(mlp.gate_proj, mlp.up_proj), down=lin(mlp.down_proj),
             ))
         L, dt = len(self.layers), self.embed.dtype
-        self.kt_cache = torch.zeros((L, batch, self.n_kv, d, max_len), device=dev, dtype=dt)
-        self.v_cache = torch.zeros((L, batch, self.n_kv, max_len, d), device=dev, dtype=dt)
+        # K and V^T in the fused attention kernel's tiled operand order (kernels/attention.py);
+        # the torch path reads and writes them through the same layout helpers
+        from kernels import attention as fa
+
+        if max_len % fa.CHUNK:
+            raise ValueError(f"max_len={max_len} must be a multiple of {fa.CHUNK}")
+        if d % 32:
+            raise ValueError(f"head_dim={d} must be a multiple of 32")
+        self.k_cache = torch.zeros((L, batch) + fa.k_cache_shape(self.n_kv, max_len, d), device=dev, dtype=dt)
+        self.vt_cache = torch.zeros((L, batch) + fa.vt_cache_shape(self.n_kv, max_len, d), device=dev, dtype=dt)
         self.keys = torch.arange(max_len, device=dev)
         self.fused_attention = False
         if attention == "fused" and dev.type == "cuda":
-            from kernels import attention as fa
-
             self.fused_attention = fa.supported(d, max_len, batch, 1)
         elif attention not in ("fused", "torch"):
             raise ValueError(f"attention={attention!r}: 'fused' or 'torch'")
@@ -332,7 +339,7 @@ class QwenRunner:
         return {"linear_layers": layers, "embed": nbytes(self.embed), "lm_head_read": head,
                 "lm_head_quantized": self.head_q is not None,
                 "lm_head_shared_with_embed": self.lm_head.data_ptr() == self.embed.data_ptr(),
-                "kv_cache": nbytes(self.kt_cache) + nbytes(self.v_cache)}
+                "kv_cache": nbytes(self.k_cache) + nbytes(self.vt_cache)}
 
     def _rope(self, x, cos, sin):
         half = self.head_dim // 2
@@ -344,15 +351,18 @@ class QwenRunner:
         B, T = q.shape[:2]
         nkv, hd = self.n_kv, self.head_dim
         g = self.n_heads // nkv
-        self.kt_cache[i].index_copy_(3, pos, k.permute(0, 2, 3, 1))
-        self.v_cache[i].index_copy_(2, pos, v.transpose(1, 2))
+        from kernels import attention as fa
+
+        fa.write_kv(self.k_cache[i], self.vt_cache[i], pos, k.transpose(1, 2), v.transpose(1, 2))
+        kc = fa.k_from_tiles(self.k_cache[i])  # [B, nkv, max_len, hd]
+        vc = fa.v_from_tiles(self.vt_cache[i])
         # rows ordered (query head within the group, token): [B, nkv, g*T, hd]
         qg = q.view(B, T, nkv, g, hd).permute(0, 2, 3, 1, 4).reshape(B, nkv, g * T, hd)
-        scores = torch.matmul(qg, self.kt_cache[i]).float() * (hd ** -0.5)
+        scores = torch.matmul(qg, kc.transpose(-1, -2).contiguous()).float() * (hd ** -0.5)
         allowed = self.keys[None, :] <= pos[:, None]  # [T, max_len]
         scores = scores.masked_fill(~allowed.repeat(g, 1), float("-inf"))
         p = torch.softmax(scores, dim=-1).to(q.dtype)
-        out = torch.matmul(p, self.v_cache[i])  # [B, nkv, g*T, hd]
+        out = torch.matmul(p, vc)  # [B, nkv, g*T, hd]
         return out.view(B, nkv, g, T, hd).permute(0, 3, 1, 2, 4).reshape(B, T, nkv * g * hd)
 
     @torch.no_grad()
@@ -378,7 +388,7 @@ class QwenRunner:
             else:  # the previous MLP output joins the residual inside this layer's input norm
                 qkv, residual = be.norm_linear(h, L.ln1, eps, residual, L.qkv)
             if fused:
-                attn = decode_attention(qkv, pos, self.inv_freq, self.kt_cache[i], self.v_cache[i],
+                attn = decode_attention(qkv, pos, self.inv_freq, self.k_cache[i], self.vt_cache[i],
                                         nq, nkv, hd ** -0.5)
             else:
                 q, k, v = qkv.split([nq * hd, nkv * hd, nkv * hd], dim=-1)

@@ -149,7 +149,7 @@ def run(params: dict) -> dict:
     hf = random_qwen2(seed=seed)
     g = torch.Generator(device="cuda").manual_seed(seed)
     ids = torch.randint(0, hf.config.vocab_size, (1, prompt_len), device="cuda", generator=g)
-    max_len = prompt_len + steps + 8
+    max_len = -(-(prompt_len + steps + 8) // 32) * 32  # the cache tiles hold 32 positions
     result = {"model": "Qwen2.5-1.5B architecture, random init (HF init, seed %d)" % seed,
               "prompt_len": prompt_len, "decode_steps": steps, "max_len": max_len,
               "backends": {}}
