@@ -117,6 +117,15 @@ __device__ __forceinline__ float max_xor32(float v) {
   return fmaxf(ldk::u2f(p[0]), ldk::u2f(p[1]));
 }
 
+// Maximum over the 64 lanes, in every lane (row rotations, then the permlane swaps).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, ldk::row_ror<1>(v));
+  v = fmaxf(v, ldk::row_ror<2>(v));
+  v = fmaxf(v, ldk::row_ror<4>(v));
+  v = fmaxf(v, ldk::row_ror<8>(v));
+  return max_xor32(max_xor16(v));
+}
+
 __device__ __forceinline__ float4_t mfma16(u32x4 a, u32x4 b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
 }
@@ -411,20 +420,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
       ov[0][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ob, (uint32_t)((lane * kMaxSplits + 4 * k) * 4), 0, kCoherent));
       ov[1][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ob, (uint32_t)(((lane + 64) * kMaxSplits + 4 * k) * 4), 0, kCoherent));
     }
-    float Mg = lane < nlive ? mr : -__builtin_inff();
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) Mg = fmaxf(Mg, __shfl_xor(Mg, off));
+    const float Mg = wave_max(lane < nlive ? mr : -__builtin_inff());
     const float fr = lane < nlive ? __expf(mr - Mg) : 0.0f;  // weight of range `lane`
-    float lg = lr * fr;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lg += __shfl_xor(lg, off);
+    const float lg = ldk::sum_lanes_strided<1>(lr * fr);
     float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
     for (int k = 0; k < kMaxSplits / 4; ++k) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int rr = 4 * k + e;
-        const float f = __shfl(fr, rr);  // 0 past the live ranges, whose stale words are skipped
+        // range rr's weight, read into a scalar register (0 past the live ranges, whose stale
+        // words are skipped)
+        const float f = ldk::u2f(__builtin_amdgcn_readlane(ldk::f2u(fr), rr));
         if (rr < nlive) {
           o0 = __builtin_fmaf(ldk::u2f(ov[0][k][e]), f, o0);
           o1 = __builtin_fmaf(ldk::u2f(ov[1][k][e]), f, o1);
