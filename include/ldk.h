@@ -218,8 +218,9 @@ int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void*
  * head_dim == 128, nq % nkv == 0, max_len a multiple of 32 (k_cache and vt_cache 16-byte
  * aligned). A *pos >= max_len writes nothing and attends over the whole cache; a negative *pos
  * writes nothing and returns zeros. Caches of more than 512 positions are split into up to 32
- * position ranges per head tile whose partials meet in library-owned device state that each
- * launch leaves zeroed (graph replay is safe); calls on one device must be stream-ordered.
+ * position ranges whose partials go through library-owned device memory to a second launch on
+ * the same stream that merges them (graph capture is safe); calls on one device must be
+ * stream-ordered.
  * Replaces the per-layer attention of the
  * reference's runner for decode steps (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into
  * the cache, scaled_dot_product_attention with the causal mask; the reference's cache is

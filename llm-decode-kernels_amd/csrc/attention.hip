@@ -19,7 +19,7 @@
 // for every GQA shape up to 16 heads per kv head), so each K and V byte of a head is read once
 // per launch, and its products run on the matrix cores (v_mfma_f32_16x16x32_f16, the 16 heads are
 // the tile's columns). Caches of more than 512 positions are cut into up to 32 position ranges
-// with one workgroup per (head tile, range).
+// of at least 128 positions, with one workgroup per (head tile, range).
 //  - Wave w takes the 32-position chunks w, w + 8, ... of its range, two at a time, and loads
 //    each chunk's 8 K tiles and 8 V^T tiles (16 KB, all live) before its first use. The RoPE
 //    needs no barrier: each lane ropes exactly the q and k dims of its own MFMA operands from
@@ -34,10 +34,11 @@
 //  - The waves' (m, l, O) meet once through LDS at the end.
 // The cache at pos is stale while the workgroup holding pos writes the new k/v, so the score at
 // pos is taken from q . k_new and the V^T registers at pos are replaced by v_new. With several
-// ranges, every range publishes its partial (running max m, sum l, unnormalised output o[128] per
-// head) to library-owned device memory and counts itself in with one agent-scope atomic; the last
-// to arrive merges the partials, writes the output and re-zeroes the counter. Calls on one device
-// must be stream-ordered.
+// ranges, every range stores its partial (running max m, sum l, unnormalised output o[128] per
+// head) to library-owned device memory, and a second launch on the same stream merges them: the
+// kernel boundary orders the stores before the loads, which a last-arriver merge inside the range
+// kernel pays for with three device-coherent round trips (partial stores, a counter atomic,
+// partial loads). Calls on one device must be stream-ordered (the partials are shared).
 //
 // Numerics: RoPE as the reference's fp16 torch ops (cos/sin of pos * inv_freq in fp32 rounded to
 // fp16, q*cos and rotate_half(q)*sin each rounded to fp16, their sum rounded); scores from the
@@ -57,8 +58,6 @@ constexpr int kBlock = 512;  // positions per softmax block: 16 chunks, two per 
 constexpr int64_t kMaxLen = 1 << 20;
 constexpr int kMaxSplits = 32;  // position ranges per head tile
 constexpr int kMaxHeads = 128;  // query heads that can split (more run one range per tile)
-// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt and lgkmcnt unconstrained
-constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr uint32_t kDead = 0x80000000u;  // buffer offset past every resource: the load returns 0
 constexpr int kTileHalves = 512;         // halves per 1 KB cache tile
 
@@ -72,15 +71,11 @@ __device__ __forceinline__ int vt_offset(int d, int p) {
   return ((p >> 5) * 8 + (d >> 4)) * kTileHalves + (d & 15) * 32 + (p & 31);
 }
 
-// Partials of the ranges of a launch in progress: {m, l} per [head][range], o per
-// [head][dim][range] (a dim's partials of every range are contiguous for the merge), and per head
-// tile (indexed by its first head) the number of ranges that have published theirs (0 between
-// launches).
+// Partials of the ranges of a launch in progress: {m, l} per [head][range] and o per
+// [head][dim][range] (a dim's partials of every range are contiguous for the merge), written by
+// the range kernel and read by the merge launch after it on the same stream.
 __device__ float g_ml[kMaxHeads][kMaxSplits][2];
 __device__ __align__(16) float g_o[kMaxHeads][kHD][kMaxSplits];
-__device__ uint32_t g_arrive[kMaxHeads];
-// buffer-load cache policy: sc1, read at the device coherence point (as agent-scope atomic loads)
-constexpr int kCoherent = 16;
 
 struct AttnArgs {
   const half_t* qkv;
@@ -91,8 +86,7 @@ struct AttnArgs {
   half_t* out;            // [nq*128]
   int nq, nkv, max_len;
   int ntile;              // workgroups per kv head along x: ceil((nq / nkv) / 16) head tiles
-  int rlen;               // positions per range (gridDim.y ranges): a multiple of 32 up to 512,
-                          // or a multiple of 512
+  int rlen;               // positions per range (gridDim.y ranges), a multiple of 32
   float scale;
 };
 
@@ -140,7 +134,6 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   __shared__ __align__(16) half_t cs[kWaves][2][64];      // RoPE cos, sin by dim, per wave
   __shared__ float mw[kWaves][kTile], lw[kWaves][kTile];  // per-wave max and sum per head
   __shared__ __align__(16) float ow[kWaves][kTile][kHD];  // per-wave unnormalised outputs
-  __shared__ int last_flag;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, no waterfalls
   const int c16 = lane & 15, kb = lane >> 4;
@@ -383,65 +376,56 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     }
     if (single) {
       a.out[(int64_t)(hbase + j) * kHD + d] = (half_t)(l > 0.0f ? acc / l : 0.0f);
-    } else {
-      // publish this range's partial: stores performed at the device coherence point (sc1)
-      __hip_atomic_store(&g_o[hbase + j][d][split], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {  // this range's partial, for the merge launch that follows on the stream
+      g_o[hbase + j][d][split] = acc;
       if (d == 0) {
-        __hip_atomic_store(&g_ml[hbase + j][split][0], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&g_ml[hbase + j][split][1], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        g_ml[hbase + j][split][0] = M;
+        g_ml[hbase + j][split][1] = l;
       }
     }
   }
-  if (single) return;
-  // ---- count in; the last range to arrive merges them all. Every wave waits for the completion
-  // of its partial stores (s_waitcnt vmcnt(0)) before the barrier after which thread 0 bumps the
-  // counter, and the reads are issued after the counter's value has returned, so the counter needs
-  // no release/acquire of its own: those write back and invalidate the XCD's whole L2.
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  ldk::lds_barrier();
-  if (tid == 0) {
-    const uint32_t before = __hip_atomic_fetch_add(&g_arrive[hbase], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = before == (uint32_t)(nlive - 1);
+}
+
+// The ranges' partials of one query head (one wave per head, launched after the ranges on the
+// same stream, so their stores are visible): lane r < nlive holds range r's (m, l); every lane
+// reads the 32 range partials of its dims d and d + 64 with 16-byte loads, all in flight at once.
+// With a single live range the range kernel has written the output and this returns at once.
+__global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_p, half_t* out, int L, int rlen) {
+  const int64_t pos_in = *pos_p;
+  const bool pos_ok = pos_in >= 0 && pos_in < L;
+  const int pos = pos_ok ? (int)pos_in : pos_in < 0 ? -1 : L - 1;
+  const int nlive = pos < 0 ? 1 : pos / rlen + 1;
+  if (nlive == 1) return;
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const int r = min(lane, nlive - 1);
+  const float mr = g_ml[h][r][0], lr = g_ml[h][r][1];
+  const auto ob = ldk::buffer_rsrc(&g_o[h][0][0], (uint32_t)sizeof(g_o[0]));
+  u32x4 ov[2][kMaxSplits / 4];
+#pragma unroll
+  for (int k = 0; k < kMaxSplits / 4; ++k) {
+    ov[0][k] = ldk::buffer_load16(ob, (uint32_t)((lane * kMaxSplits + 4 * k) * 4));
+    ov[1][k] = ldk::buffer_load16(ob, (uint32_t)(((lane + 64) * kMaxSplits + 4 * k) * 4));
   }
-  ldk::lds_barrier();
-  if (!last_flag) return;
-  // ---- merge (the last range): wave w takes heads w, w + 8 of the tile; lane r < nlive holds
-  // range r's (m, l), and every lane reads the 32 range partials of its dims d and d + 64 with
-  // 16-byte loads, all in flight at once
-  for (int jh = wave; jh < nh; jh += kWaves) {
-    const int h = hbase + jh;
-    const int r = min(lane, nlive - 1);
-    const float mr = __hip_atomic_load(&g_ml[h][r][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float lr = __hip_atomic_load(&g_ml[h][r][1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const auto ob = ldk::buffer_rsrc(&g_o[h][0][0], (uint32_t)sizeof(g_o[0]));
-    u32x4 ov[2][kMaxSplits / 4];
+  const float Mg = wave_max(lane < nlive ? mr : -__builtin_inff());
+  const float fr = lane < nlive ? __expf(mr - Mg) : 0.0f;  // weight of range `lane`
+  const float lg = ldk::sum_lanes_strided<1>(lr * fr);
+  float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxSplits / 4; ++k) {
-      ov[0][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ob, (uint32_t)((lane * kMaxSplits + 4 * k) * 4), 0, kCoherent));
-      ov[1][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ob, (uint32_t)(((lane + 64) * kMaxSplits + 4 * k) * 4), 0, kCoherent));
-    }
-    const float Mg = wave_max(lane < nlive ? mr : -__builtin_inff());
-    const float fr = lane < nlive ? __expf(mr - Mg) : 0.0f;  // weight of range `lane`
-    const float lg = ldk::sum_lanes_strided<1>(lr * fr);
-    float o0 = 0.0f, o1 = 0.0f;
+  for (int k = 0; k < kMaxSplits / 4; ++k) {
 #pragma unroll
-    for (int k = 0; k < kMaxSplits / 4; ++k) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rr = 4 * k + e;
-        // range rr's weight, read into a scalar register (0 past the live ranges, whose stale
-        // words are skipped)
-        const float f = ldk::u2f(__builtin_amdgcn_readlane(ldk::f2u(fr), rr));
-        if (rr < nlive) {
-          o0 = __builtin_fmaf(ldk::u2f(ov[0][k][e]), f, o0);
-          o1 = __builtin_fmaf(ldk::u2f(ov[1][k][e]), f, o1);
-        }
+    for (int e = 0; e < 4; ++e) {
+      const int rr = 4 * k + e;
+      // range rr's weight, read into a scalar register (0 past the live ranges, whose stale words
+      // are skipped)
+      const float f = ldk::u2f(__builtin_amdgcn_readlane(ldk::f2u(fr), rr));
+      if (rr < nlive) {
+        o0 = __builtin_fmaf(ldk::u2f(ov[0][k][e]), f, o0);
+        o1 = __builtin_fmaf(ldk::u2f(ov[1][k][e]), f, o1);
       }
     }
-    a.out[(int64_t)h * kHD + lane] = (half_t)(lg > 0.0f ? o0 / lg : 0.0f);
-    a.out[(int64_t)h * kHD + lane + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
   }
-  if (tid == 0) __hip_atomic_store(&g_arrive[hbase], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  out[(int64_t)h * kHD + lane] = (half_t)(lg > 0.0f ? o0 / lg : 0.0f);
+  out[(int64_t)h * kHD + lane + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
 }
 
 }  // namespace
@@ -457,22 +441,27 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
                      (long long)max_len, (long long)kMaxLen);
   if (!ldk::aligned(k_cache, 16) || !ldk::aligned(vt_cache, 16) || !ldk::aligned(pos, 8))
     return ldk::fail(LDK_ERR_ALIGN, "decode_attention: k_cache and vt_cache 16-byte, pos 8-byte aligned");
-  // Position ranges: a cache of up to one block runs one range; longer ones at most kMaxSplits
-  // ranges of whole blocks (one range per head tile when the heads exceed the partials'
-  // capacity). A split costs about three memory round trips to merge.
+  // Position ranges: a cache of up to 512 positions runs one range (splitting it costs more in
+  // the merge launch than it saves: 384 at pos 300 runs 7.9 us whole, 8.9 us in 128-position
+  // ranges); longer ones at most kMaxSplits ranges of at least 128 positions (4096 at pos 4000:
+  // 9.5 us, 10.3 with 256-position ranges, 12.5 with 512). Caches with more heads than the
+  // partials hold run one range per head tile.
   const int64_t nblocks = (max_len + kBlock - 1) / kBlock;
+  const int64_t nchunk = max_len / kChunk;
   int64_t rlen;
   if (nblocks == 1)
     rlen = max_len;
   else if (nq > kMaxHeads)
-    rlen = nblocks * kBlock;
+    rlen = max_len;
   else
-    rlen = (nblocks + kMaxSplits - 1) / kMaxSplits * kBlock;
+    rlen = std::max<int64_t>(128, (nchunk + kMaxSplits - 1) / kMaxSplits * kChunk);
   const int nsplit = (int)((max_len + rlen - 1) / rlen);
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, (half_t*)out,
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale};
   (void)hipGetLastError();
   decode_attention_kernel<<<dim3(nkv * ntile, nsplit), kWaves * 64, 0, (hipStream_t)stream>>>(a);
+  if (nsplit > 1)
+    attention_merge_kernel<<<nq, 64, 0, (hipStream_t)stream>>>(pos, (half_t*)out, (int)max_len, (int)rlen);
   return ldk::check_launch("decode_attention");
 }

@@ -40,12 +40,12 @@ def _caches(g, nkv, L, hd=128):
                                           (144, 8, 1536, 1100), (14, 2, 8192, 6000)])
 def test_against_float64(nq, nkv, L, pos):
     """Cache lengths cover one position range (up to 512 positions) with pos at chunk edges,
-    several 512-position ranges with a short last one (2048, 2144: 4 and 5 ranges, 4096: 8),
-    32 ranges of three 512-position passes each (40000), pos in the first range of a split
-    cache (40000, 700), more query heads per kv head than one 16-head tile (40/2: two tiles,
-    36/1: three tiles over three ranges), a full tile (16/1), seven heads per kv head (14/2),
-    and more heads than can split (72 heads in one range; 144 heads: one range of three
-    passes per tile)."""
+    128-position ranges with a short last one (2048: 16, 2144: 17; 4096: 32), 32 ranges of
+    1280 positions that each wave takes in three passes (40000), pos in the first range of a
+    split cache (40000, 700), more query heads per kv head than one 16-head tile (40/2: two
+    tiles, 36/1: three tiles over nine ranges), a full tile (16/1), seven heads per kv head
+    (14/2), and more heads than the range partials hold (72 heads in one range; 144 heads: one
+    range of 1536 positions per tile)."""
     g = torch.Generator().manual_seed(pos + 7 * nq)
     hd = 128
     qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half()
@@ -132,15 +132,15 @@ def _reference(qkv, k_tiles, vt_tiles, nq, nkv, pos, inv_freq):
 @pytest.mark.parametrize("L,steps", [(512, 301), (1536, 1100)])
 def test_decode_sequence_two_layers(L, steps):
     """Decode steps over two layers' caches, as the runner issues them: every step writes its
-    k/v and attends over 0..pos. A 1536-position cache has three 512-position ranges, so from
-    pos 512 on a head tile's ranges meet through the shared partials and arrival counters, which
-    each launch must leave zeroed for the next."""
+    k/v and attends over 0..pos. A 1536-position cache has twelve 128-position ranges, so from
+    pos 128 on a head's ranges meet through the shared partials in the merge launch, which must
+    skip the stale partials of ranges that earlier steps left behind."""
     nq, nkv, hd = 12, 2, 128
     g = torch.Generator().manual_seed(11)
     inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
     caches = [_caches(g, nkv, L)[2:] for _ in range(2)]
     pos_t = torch.zeros(1, dtype=torch.int64, device="cuda")
-    edges = (63, 64, 65, 127, 128, 511, 512, 513, 1023, 1024, 1025, steps - 1)
+    edges = (63, 64, 65, 127, 128, 129, 255, 256, 511, 512, 513, 1023, 1024, 1025, steps - 1)
     for pos in range(steps):
         pos_t.fill_(pos)
         for li, (kc, vt) in enumerate(caches):
