@@ -72,10 +72,10 @@ __device__ __forceinline__ int vt_offset(int d, int p) {
 }
 
 // Partials of the ranges of a launch in progress: {m, l} per [head][range] and o per
-// [head][dim][range] (a dim's partials of every range are contiguous for the merge), written by
-// the range kernel and read by the merge launch after it on the same stream.
+// [head][range][dim] (a range writes whole lines), written by the range kernel and read by the
+// merge launch after it on the same stream.
 __device__ float g_ml[kMaxHeads][kMaxSplits][2];
-__device__ __align__(16) float g_o[kMaxHeads][kHD][kMaxSplits];
+__device__ __align__(16) float g_o[kMaxHeads][kMaxSplits][kHD];
 
 struct AttnArgs {
   const half_t* qkv;
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     if (single) {
       a.out[(int64_t)(hbase + j) * kHD + d] = (half_t)(l > 0.0f ? acc / l : 0.0f);
     } else {  // this range's partial, for the merge launch that follows on the stream
-      g_o[hbase + j][d][split] = acc;
+      g_o[hbase + j][split][d] = acc;
       if (d == 0) {
         g_ml[hbase + j][split][0] = M;
         g_ml[hbase + j][split][1] = l;
@@ -387,9 +387,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
 }
 
 // The ranges' partials of one query head (one wave per head, launched after the ranges on the
-// same stream, so their stores are visible): lane r < nlive holds range r's (m, l); every lane
-// reads the 32 range partials of its dims d and d + 64 with 16-byte loads, all in flight at once.
-// With a single live range the range kernel has written the output and this returns at once.
+// same stream, so their stores are visible): lane r < nlive holds range r's (m, l); lane d reads
+// dims d and d + 64 of every live range's partial (coalesced dword loads, all in flight at once,
+// zero past the live ranges). With a single live range the range kernel has written the output
+// and this returns at once.
 __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_p, half_t* out, int L, int rlen) {
   const int64_t pos_in = *pos_p;
   const bool pos_ok = pos_in >= 0 && pos_in < L;
@@ -400,29 +401,23 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
   const int r = min(lane, nlive - 1);
   const float mr = g_ml[h][r][0], lr = g_ml[h][r][1];
   const auto ob = ldk::buffer_rsrc(&g_o[h][0][0], (uint32_t)sizeof(g_o[0]));
-  u32x4 ov[2][kMaxSplits / 4];
+  float ov0[kMaxSplits], ov1[kMaxSplits];
 #pragma unroll
-  for (int k = 0; k < kMaxSplits / 4; ++k) {
-    ov[0][k] = ldk::buffer_load16(ob, (uint32_t)((lane * kMaxSplits + 4 * k) * 4));
-    ov[1][k] = ldk::buffer_load16(ob, (uint32_t)(((lane + 64) * kMaxSplits + 4 * k) * 4));
+  for (int k = 0; k < kMaxSplits; ++k) {
+    const uint32_t off = (uint32_t)((k * kHD + lane) * 4) | (k < nlive ? 0u : kDead);
+    ov0[k] = ldk::u2f(__builtin_amdgcn_raw_buffer_load_b32(ob, off, 0, 0));
+    ov1[k] = ldk::u2f(__builtin_amdgcn_raw_buffer_load_b32(ob, off + 256, 0, 0));
   }
   const float Mg = wave_max(lane < nlive ? mr : -__builtin_inff());
   const float fr = lane < nlive ? __expf(mr - Mg) : 0.0f;  // weight of range `lane`
   const float lg = ldk::sum_lanes_strided<1>(lr * fr);
   float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-  for (int k = 0; k < kMaxSplits / 4; ++k) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int rr = 4 * k + e;
-      // range rr's weight, read into a scalar register (0 past the live ranges, whose stale words
-      // are skipped)
-      const float f = ldk::u2f(__builtin_amdgcn_readlane(ldk::f2u(fr), rr));
-      if (rr < nlive) {
-        o0 = __builtin_fmaf(ldk::u2f(ov[0][k][e]), f, o0);
-        o1 = __builtin_fmaf(ldk::u2f(ov[1][k][e]), f, o1);
-      }
-    }
+  for (int k = 0; k < kMaxSplits; ++k) {
+    // range k's weight, read into a scalar register (0 past the live ranges, whose loads read 0)
+    const float f = ldk::u2f(__builtin_amdgcn_readlane(ldk::f2u(fr), k));
+    o0 = __builtin_fmaf(ov0[k], f, o0);
+    o1 = __builtin_fmaf(ov1[k], f, o1);
   }
   out[(int64_t)h * kHD + lane] = (half_t)(lg > 0.0f ? o0 / lg : 0.0f);
   out[(int64_t)h * kHD + lane + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
