@@ -264,6 +264,15 @@ int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int ns
 int ldk_greedy_step(const void* logits, int dtype, int64_t V, int64_t* tok, int64_t* out,
                     int64_t out_len, int64_t* pos, void* stream);
 
+/* ------------------------------------------------------------------ fp16 lm_head (one row) */
+
+/* y[n] = fp16(sum_k w[n*ldw + k] * x[k]) for n < N: the tied fp16 lm_head of the decode step,
+ * `F.linear(h, self.lm_head)` at one row (kernels/e2e/model.py:253). x fp16 [K], w fp16 [N, ldw]
+ * row-major, y fp16 [N]; fp32 accumulation, one rounding. K and ldw multiples of 8, K <= 2048,
+ * x and w 16-byte aligned. rows_per_wave: 0 (library choice), 4 or 8. */
+int ldk_f16_gemv(const void* x, const void* w, int64_t ldw, void* y, int64_t N, int64_t K,
+                 int rows_per_wave, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

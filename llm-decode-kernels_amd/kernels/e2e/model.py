@@ -89,6 +89,10 @@ class Backend:
         post-attention norm and gate_up (model.py:226-233). Returns (y2, new residual)."""
         return self.norm_linear(self.linear(x, p1), w, eps, residual, p2)
 
+    def head(self, h, weight):
+        """The tied fp16 lm_head, `F.linear(h, self.lm_head)` (model.py:253)."""
+        return F.linear(h, weight)
+
 
 class W4RefBackend(Backend):
     """RTN int4 weights dequantized once (bit-exact HIP dequantizer) then the fp16 GEMM: the same
@@ -166,6 +170,17 @@ class OursBackend(Backend):
 
         return swiglu_w4a16_matmul(gate_up, p.qweight, p.scales, p.zeros, config.GROUP_SIZE,
                                    p.bias)
+
+    def head(self, h, weight):
+        """The fp16 table at one decode row through this build's fp16 GEMV (kernels.head): the
+        same bytes as the library GEMM, streamed once. Prefill rows keep the library GEMM."""
+        if self.decode_kernel != "library":
+            return super().head(h, weight)
+        from kernels import head as head_mod
+
+        if head_mod.applies(h, weight):
+            return head_mod.lm_head(h, weight)
+        return F.linear(h, weight)
 
 
 class OursFP8Backend(OursBackend):
@@ -402,4 +417,4 @@ class QwenRunner:
         if self.head_q is not None:
             return be.norm_linear(h, self.final_norm, eps, residual, self.head_q)[0]
         h, _ = be.norm(h, self.final_norm, eps, residual=residual)
-        return F.linear(h, self.lm_head)
+        return be.head(h, self.lm_head)
