@@ -273,6 +273,14 @@ int ldk_greedy_step(const void* logits, int dtype, int64_t V, int64_t* tok, int6
 int ldk_f16_gemv(const void* x, const void* w, int64_t ldw, void* y, int64_t N, int64_t K,
                  int rows_per_wave, void* stream);
 
+/* ldk_f16_gemv on x = rmsnorm(h (+ residual)) * norm_weight, formed in the kernel's x staging:
+ * the final `self.norm(h, residual)` and the head of kernels/e2e/model.py:250-253 in one launch
+ * (the norm's steps are rmsnorm_ref's, kernels/reference.py:9-19; h + residual is not written
+ * back). residual may be NULL; h, residual and norm_weight are fp16 [K], 16-byte aligned. */
+int ldk_f16_rmsnorm_gemv(const void* h, const void* residual, const void* norm_weight, float eps,
+                         const void* w, int64_t ldw, void* y, int64_t N, int64_t K,
+                         int rows_per_wave, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

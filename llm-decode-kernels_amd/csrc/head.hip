@@ -20,18 +20,35 @@ namespace {
 
 constexpr int kWaves = 4;
 
-template <int KJ, int RPW, bool FULL>
+// Optional prologue (NORM): x = rmsnorm(h (+ residual)) * norm_weight, the reference's final
+// `self.norm(h, residual)` before the head (kernels/e2e/model.py:250-253) with the standalone
+// RMSNorm kernel's rounding steps. A wave's KJ chunks per lane cover the whole row, so every wave
+// forms the row statistic from its own loads (DPP + permlane reduction, no LDS, no barrier) and
+// stages its x in registers; the h + residual sum is not written back (the head is its last use).
+struct NormArgs {
+  const half_t* res;  // residual row or null
+  const half_t* nw;   // norm weight [K]
+  float eps;
+};
+
+template <int KJ, int RPW, bool FULL, bool NORM>
 __global__ __launch_bounds__(kWaves * 64) void f16_gemv_kernel(const half_t* __restrict__ x,
                                                                const half_t* __restrict__ w, int64_t ldw,
-                                                               half_t* __restrict__ y, int64_t N, int KC) {
+                                                               half_t* __restrict__ y, int64_t N, int KC,
+                                                               NormArgs na) {
   const int lane = threadIdx.x & 63;
   const int64_t row0 = ((int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * RPW;
   if (row0 >= N) return;  // uniform per wave
-  u32x4 xv[KJ];
+  u32x4 xv[KJ], rv[KJ], nv[KJ];
 #pragma unroll
   for (int j = 0; j < KJ; ++j) {
     const int c = lane + 64 * j;
-    xv[j] = (FULL || c < KC) ? *reinterpret_cast<const u32x4*>(x + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    const bool in = FULL || c < KC;
+    xv[j] = in ? *reinterpret_cast<const u32x4*>(x + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (NORM) {
+      rv[j] = in && na.res ? *reinterpret_cast<const u32x4*>(na.res + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+      nv[j] = in ? *reinterpret_cast<const u32x4*>(na.nw + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
   u32x4 wv[RPW][KJ];
 #pragma unroll
@@ -43,6 +60,27 @@ __global__ __launch_bounds__(kWaves * 64) void f16_gemv_kernel(const half_t* __r
       const int c = lane + 64 * j;
       wv[r][j] = (FULL || c < KC) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 8 * c))
                                   : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  if constexpr (NORM) {
+    half8_t hv[KJ];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {  // chunks past K are zeros and add nothing
+      hv[j] = __builtin_bit_cast(half8_t, xv[j]);
+      if (na.res) hv[j] = hv[j] + __builtin_bit_cast(half8_t, rv[j]);  // fp16 add
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)hv[j][e], (float)hv[j][e], ss);
+    }
+    ss = ldk::sum_lanes_strided<1>(ss);
+    const float rs = 1.0f / __builtin_sqrtf(ss / (float)(8 * KC) + na.eps);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const half8_t wn = __builtin_bit_cast(half8_t, nv[j]);
+      half8_t o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = ldk::rms_f16(hv[j][e], rs, wn[e]);
+      xv[j] = __builtin_bit_cast(u32x4, o);
     }
   }
   float acc[RPW];
@@ -64,33 +102,35 @@ __global__ __launch_bounds__(kWaves * 64) void f16_gemv_kernel(const half_t* __r
   if (lane < RPW && row0 + lane < N) y[row0 + lane] = (half_t)mine;
 }
 
-template <int KJ, int RPW>
-int launch_rpw(const half_t* x, const half_t* w, int64_t ldw, half_t* y, int64_t N, int KC, hipStream_t s) {
+template <int KJ, int RPW, bool NORM>
+int launch_rpw(const half_t* x, const half_t* w, int64_t ldw, half_t* y, int64_t N, int KC, const NormArgs& na,
+               hipStream_t s) {
   const int64_t waves = (N + RPW - 1) / RPW;
   const int64_t blocks = (waves + kWaves - 1) / kWaves;
   (void)hipGetLastError();
   if (KC == 64 * KJ)
-    f16_gemv_kernel<KJ, RPW, true><<<(unsigned)blocks, kWaves * 64, 0, s>>>(x, w, ldw, y, N, KC);
+    f16_gemv_kernel<KJ, RPW, true, NORM><<<(unsigned)blocks, kWaves * 64, 0, s>>>(x, w, ldw, y, N, KC, na);
   else
-    f16_gemv_kernel<KJ, RPW, false><<<(unsigned)blocks, kWaves * 64, 0, s>>>(x, w, ldw, y, N, KC);
+    f16_gemv_kernel<KJ, RPW, false, NORM><<<(unsigned)blocks, kWaves * 64, 0, s>>>(x, w, ldw, y, N, KC, na);
   return ldk::check_launch("f16_gemv");
 }
 
-template <int KJ>
-int launch_kj(const half_t* x, const half_t* w, int64_t ldw, half_t* y, int64_t N, int KC, int rpw, hipStream_t s) {
-  return rpw == 4 ? launch_rpw<KJ, 4>(x, w, ldw, y, N, KC, s) : launch_rpw<KJ, 8>(x, w, ldw, y, N, KC, s);
+template <int KJ, bool NORM>
+int launch_kj(const half_t* x, const half_t* w, int64_t ldw, half_t* y, int64_t N, int KC, int rpw, const NormArgs& na,
+              hipStream_t s) {
+  return rpw == 4 ? launch_rpw<KJ, 4, NORM>(x, w, ldw, y, N, KC, na, s) : launch_rpw<KJ, 8, NORM>(x, w, ldw, y, N, KC, na, s);
 }
 
-}  // namespace
-
-extern "C" int ldk_f16_gemv(const void* x, const void* w, int64_t ldw, void* y, int64_t N, int64_t K,
-                            int rows_per_wave, void* stream) {
-  if (!x || !w || !y) return ldk::fail(LDK_ERR_INVALID, "f16_gemv: null pointer");
+// Shared argument checks and dispatch of both entry points.
+int f16_gemv(const void* x, const NormArgs* na, const void* w, int64_t ldw, void* y, int64_t N, int64_t K,
+             int rows_per_wave, void* stream) {
+  if (!x || !w || !y || (na && !na->nw)) return ldk::fail(LDK_ERR_INVALID, "f16_gemv: null pointer");
   if (N <= 0 || K <= 0 || ldw < K) return ldk::fail(LDK_ERR_INVALID, "f16_gemv: N=%lld K=%lld ldw=%lld", (long long)N, (long long)K, (long long)ldw);
   if (rows_per_wave != 0 && rows_per_wave != 4 && rows_per_wave != 8)
     return ldk::fail(LDK_ERR_INVALID, "f16_gemv: rows_per_wave=%d (0, 4 or 8)", rows_per_wave);
-  if (K % 8 != 0 || ldw % 8 != 0 || !ldk::aligned(x, 16) || !ldk::aligned(w, 16))
-    return ldk::fail(LDK_ERR_ALIGN, "f16_gemv: K and ldw must be multiples of 8, x and w 16-byte aligned");
+  if (K % 8 != 0 || ldw % 8 != 0 || !ldk::aligned(x, 16) || !ldk::aligned(w, 16) ||
+      (na && (!ldk::aligned(na->nw, 16) || (na->res && !ldk::aligned(na->res, 16)))))
+    return ldk::fail(LDK_ERR_ALIGN, "f16_gemv: K and ldw must be multiples of 8; x, residual, norm weight and w 16-byte aligned");
   if (!ldk::aligned(y, 2)) return ldk::fail(LDK_ERR_ALIGN, "f16_gemv: y must be 2-byte aligned");
   if (K > 2048) return ldk::fail(LDK_ERR_UNSUPPORTED, "f16_gemv: K=%lld > 2048", (long long)K);
   if ((N + 7) / 8 > (int64_t)kWaves * 0x7fffffff) return ldk::fail(LDK_ERR_UNSUPPORTED, "f16_gemv: N=%lld", (long long)N);
@@ -99,10 +139,33 @@ extern "C" int ldk_f16_gemv(const void* x, const void* w, int64_t ldw, void* y, 
   const half_t *xp = (const half_t*)x, *wp = (const half_t*)w;
   half_t* yp = (half_t*)y;
   hipStream_t s = (hipStream_t)stream;
-  switch (KJ) {
-    case 1: return launch_kj<1>(xp, wp, ldw, yp, N, KC, rpw, s);
-    case 2: return launch_kj<2>(xp, wp, ldw, yp, N, KC, rpw, s);
-    case 3: return launch_kj<3>(xp, wp, ldw, yp, N, KC, rpw, s);
-    default: return launch_kj<4>(xp, wp, ldw, yp, N, KC, rpw, s);
+  const NormArgs a = na ? *na : NormArgs{nullptr, nullptr, 0.0f};
+  if (na) {
+    switch (KJ) {
+      case 1: return launch_kj<1, true>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+      case 2: return launch_kj<2, true>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+      case 3: return launch_kj<3, true>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+      default: return launch_kj<4, true>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+    }
   }
+  switch (KJ) {
+    case 1: return launch_kj<1, false>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+    case 2: return launch_kj<2, false>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+    case 3: return launch_kj<3, false>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+    default: return launch_kj<4, false>(xp, wp, ldw, yp, N, KC, rpw, a, s);
+  }
+}
+
+}  // namespace
+
+extern "C" int ldk_f16_gemv(const void* x, const void* w, int64_t ldw, void* y, int64_t N, int64_t K,
+                            int rows_per_wave, void* stream) {
+  return f16_gemv(x, nullptr, w, ldw, y, N, K, rows_per_wave, stream);
+}
+
+extern "C" int ldk_f16_rmsnorm_gemv(const void* h, const void* residual, const void* norm_weight, float eps,
+                                    const void* w, int64_t ldw, void* y, int64_t N, int64_t K, int rows_per_wave,
+                                    void* stream) {
+  const NormArgs na{(const half_t*)residual, (const half_t*)norm_weight, eps};
+  return f16_gemv(h, &na, w, ldw, y, N, K, rows_per_wave, stream);
 }

@@ -66,6 +66,7 @@ SIGNATURES = {
     "ldk_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
     "ldk_greedy_step": [_vp, _i32, _i64, _vp, _vp, _i64, _vp, _vp],
     "ldk_f16_gemv": [_vp, _vp, _i64, _vp, _i64, _i64, _i32, _vp],
+    "ldk_f16_rmsnorm_gemv": [_vp, _vp, _vp, _f32, _vp, _i64, _vp, _i64, _i64, _i32, _vp],
     "ldk_decode_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _f32, _vp],
 }
 

@@ -93,6 +93,11 @@ class Backend:
         """The tied fp16 lm_head, `F.linear(h, self.lm_head)` (model.py:253)."""
         return F.linear(h, weight)
 
+    def norm_head(self, h, w, eps, residual, weight):
+        """The final norm, then the fp16 head (model.py:250-253)."""
+        h, _ = self.norm(h, w, eps, residual=residual)
+        return self.head(h, weight)
+
 
 class W4RefBackend(Backend):
     """RTN int4 weights dequantized once (bit-exact HIP dequantizer) then the fp16 GEMM: the same
@@ -181,6 +186,16 @@ class OursBackend(Backend):
         if head_mod.applies(h, weight):
             return head_mod.lm_head(h, weight)
         return F.linear(h, weight)
+
+    def norm_head(self, h, w, eps, residual, weight):
+        """One launch at decode: the final RMSNorm (+ residual) forms the head GEMV's x."""
+        if self.decode_kernel != "library":
+            return super().norm_head(h, w, eps, residual, weight)
+        from kernels import head as head_mod
+
+        if head_mod.applies(h, weight) and (residual is None or residual.numel() == h.numel()):
+            return head_mod.lm_head(h, weight, norm_weight=w, eps=eps, residual=residual)
+        return super().norm_head(h, w, eps, residual, weight)
 
 
 class OursFP8Backend(OursBackend):
@@ -416,5 +431,4 @@ class QwenRunner:
             h, residual = h[:, -1:], residual[:, -1:]
         if self.head_q is not None:
             return be.norm_linear(h, self.final_norm, eps, residual, self.head_q)[0]
-        h, _ = be.norm(h, self.final_norm, eps, residual=residual)
-        return be.head(h, self.lm_head)
+        return be.norm_head(h, self.final_norm, eps, residual, self.lm_head)

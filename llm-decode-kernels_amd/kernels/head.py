@@ -24,9 +24,20 @@ def applies(h: torch.Tensor, weight: torch.Tensor) -> bool:
             and weight.data_ptr() % 16 == 0)
 
 
-def lm_head(h: torch.Tensor, weight: torch.Tensor, rows_per_wave: int = 0) -> torch.Tensor:
+def _row(t: torch.Tensor, K: int, name: str) -> torch.Tensor:
+    if t.numel() != K or t.dtype != torch.float16:
+        raise ValueError(f"lm_head: {name} must be one fp16 row of {K}, got {tuple(t.shape)} {t.dtype}")
+    r = t.reshape(K)
+    return r if r.stride(0) == 1 and r.data_ptr() % 16 == 0 else r.contiguous()
+
+
+def lm_head(h: torch.Tensor, weight: torch.Tensor, rows_per_wave: int = 0,
+            norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+            residual: torch.Tensor | None = None) -> torch.Tensor:
     """h: fp16 [..., K] holding one row; weight: fp16 [N, K] (row stride a multiple of 8).
-    Returns fp16 [..., N] like F.linear(h, weight)."""
+    Returns fp16 [..., N] like F.linear(h, weight). With norm_weight, the row is first
+    `rmsnorm(h, norm_weight, eps, residual)` (kernels/reference.py:9-19) inside the same launch:
+    the final norm and the head of the runner (kernels/e2e/model.py:250-253)."""
     K = h.shape[-1]
     if h.numel() != K:
         raise ValueError(f"lm_head: one row expected, got shape {tuple(h.shape)}")
@@ -35,14 +46,21 @@ def lm_head(h: torch.Tensor, weight: torch.Tensor, rows_per_wave: int = 0) -> to
                          f"{tuple(weight.shape)} strides {weight.stride()}")
     if h.dtype != torch.float16 or weight.dtype != torch.float16:
         raise ValueError(f"lm_head: fp16 operands expected, got {h.dtype} and {weight.dtype}")
-    x = h.reshape(K)
-    if x.stride(0) != 1 or x.data_ptr() % 16:
-        x = x.contiguous()
-    dev = _lib.require_gpu(x, weight, what="lm_head")
+    x = _row(h, K, "h")
+    nw = None if norm_weight is None else _row(norm_weight, K, "norm_weight")
+    res = None if residual is None else _row(residual, K, "residual")
+    if res is not None and nw is None:
+        raise ValueError("lm_head: a residual needs norm_weight")
+    dev = _lib.require_gpu(x, weight, nw, res, what="lm_head")
     N = weight.shape[0]
     y = torch.empty(*h.shape[:-1], N, dtype=torch.float16, device=dev)
     with _lib.device_guard(dev):
-        st = _lib.load().ldk_f16_gemv(_lib.ptr(x), _lib.ptr(weight), weight.stride(0), _lib.ptr(y),
-                                      N, K, rows_per_wave, _lib.stream(dev))
+        if nw is None:
+            st = _lib.load().ldk_f16_gemv(_lib.ptr(x), _lib.ptr(weight), weight.stride(0), _lib.ptr(y),
+                                          N, K, rows_per_wave, _lib.stream(dev))
+        else:
+            st = _lib.load().ldk_f16_rmsnorm_gemv(_lib.ptr(x), _lib.ptr(res), _lib.ptr(nw), float(eps),
+                                                  _lib.ptr(weight), weight.stride(0), _lib.ptr(y), N, K,
+                                                  rows_per_wave, _lib.stream(dev))
     _lib.check(st, "lm_head")
     return y

@@ -107,3 +107,44 @@ def test_rejects_what_it_does_not_cover():
     with pytest.raises(ValueError):
         lm_head(torch.zeros(1, 16, dtype=torch.float16, device="cuda"),
                 torch.zeros(4, 16, dtype=torch.float16, device="cuda"), rows_per_wave=3)
+
+
+@pytest.mark.parametrize("with_res", [False, True])
+@pytest.mark.parametrize("N,K,rpw", [(1001, 1536, 0), (4099, 520, 8), (65, 2048, 4), (151936, 1536, 0)])
+def test_fused_rmsnorm_head(N, K, rpw, with_res):
+    """x = rmsnorm(h (+ residual)) * w formed inside the head launch, against the oracle's
+    rmsnorm_ref (numpy, the reference's rounding steps) followed by a float64 product. The
+    staged x may differ from the oracle's by an fp16 ulp where the row statistic's fp32 sum order
+    tips a rounding, so the bar is the north star's fp16-output bound."""
+    from oracle.reference import rmsnorm_ref
+
+    g = torch.Generator().manual_seed(N + K + with_res)
+    w = (torch.randn(N, K, generator=g) * 0.02).half()
+    h = torch.randn(1, 1, K, generator=g).half()
+    res = torch.randn(1, 1, K, generator=g).half() if with_res else None
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).half()
+    xn = rmsnorm_ref(h.numpy(), nw.numpy(), 1e-6, residual=None if res is None else res.numpy())
+    xn = xn[0] if with_res else xn
+    ref = (w.double() @ torch.from_numpy(np.ascontiguousarray(xn)).reshape(K).double()).reshape(1, 1, N)
+    out = lm_head(h.cuda(), w.contiguous().cuda(), rows_per_wave=rpw, norm_weight=nw.cuda(), eps=1e-6,
+                  residual=None if res is None else res.cuda())
+    assert out.shape == (1, 1, N) and out.dtype == torch.float16
+    assert_north_star(out.float().cpu().double().numpy(), ref.numpy())
+    # the fused launch equals the unfused pair (standalone RMSNorm kernel, then the head) to fp16
+    # output tolerance
+    from kernels.rmsnorm import rmsnorm
+
+    xr = rmsnorm(h.cuda(), nw.cuda(), 1e-6, None if res is None else res.cuda())
+    xr = xr[0] if with_res else xr
+    two = lm_head(xr, w.contiguous().cuda(), rows_per_wave=rpw)
+    d = (out.float() - two.float()).abs().max().item()
+    assert d <= 2e-2, d
+
+
+def test_fused_rmsnorm_head_rejects():
+    w = torch.zeros(16, 16, dtype=torch.float16, device="cuda")
+    h = torch.zeros(1, 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        lm_head(h, w, residual=h)  # residual without a norm weight
+    with pytest.raises(ValueError):
+        lm_head(h, w, norm_weight=torch.zeros(8, dtype=torch.float16, device="cuda"))
