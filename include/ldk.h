@@ -83,9 +83,11 @@ int ldk_w4a16_dequant(const int32_t* qweight, const void* scales, const void* ze
 
 /* Size of the split-K workspace the matmul entry points can use (bytes). The caller allocates
  * it once per device, zero-filled, 256-byte aligned, and passes it to every call. It holds one
- * 64-bit fixed-point accumulator per output of a split launch; the kernels leave every word
- * zero again by the end of each launch, so it never needs re-clearing (also under graph replay).
- * Calls that share one workspace must be ordered (same stream or synchronized). */
+ * 64-bit fixed-point accumulator per output of a split launch and, after them, one fp32 side
+ * slot per output and split for partials outside the fixed-point range (|p| >= 2^21, inf, NaN);
+ * the kernels leave every word and slot zero again by the end of each launch, so it never needs
+ * re-clearing (also under graph replay). Calls that share one workspace must be ordered (same
+ * stream or synchronized). */
 int64_t ldk_workspace_bytes(void);
 
 /* out [M, N] = x [M, K] @ dequant(qweight, scales, zeros)^T (+ bias [N]), fp32 accumulation,
@@ -116,6 +118,14 @@ int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const v
  * kernels/cuda/w4a16_cuda.py:29-42 (_pick_split), which are exported by w4a16.py:333-355. */
 int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n,
                      int* split_k, int* flags);
+
+/* Writes into buf (buf_len bytes, NUL-terminated) the name of the kernel instantiation that
+ * ldk_w4a16_matmul runs for (M, N, K, group_size) with all-zero tuning arguments and a workspace
+ * of ldk_workspace_bytes(), in the form the profiler lists it, e.g.
+ * "w4a16_m1_kernel<8, 6, 4, 0, 1>". For reports that must name the kernel they measured. No
+ * counterpart in the reference (its kernels are Triton programs named by their autotuner). */
+int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_size, char* buf,
+                          int64_t buf_len);
 
 /* Fused decode entries (M = 1, group_size 128). Each forms the activation row inside the W4A16
  * kernel's x staging instead of in a kernel of its own, one launch fewer per use. Same

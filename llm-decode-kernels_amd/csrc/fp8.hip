@@ -150,11 +150,16 @@ struct W8Split {
   int splits;     // workgroups per column tile along K (gridDim.y)
   int kps;        // K rows per split, a multiple of 8
   uint64_t* acc;  // [tiles][mblocks][MT * CW] fixed-point accumulators (splits > 1)
+  float* side;    // their fp32 side slots (ldk::SplitK), zero between launches
 };
 
-// Fixed-point split-K: a partial is clamped to 2^44 in magnitude and the poison threshold is
-// 3 * 2^48 = 48 * 2^44, so up to 40 legal partials can never look poisoned.
+// Workgroups splitting one column tile (the accumulators count up to ldk::kFixMaxSplits).
 constexpr int kW8MaxSplits = 40;
+static_assert(kW8MaxSplits <= ldk::kFixMaxSplits, "split count field");
+
+__device__ __forceinline__ ldk::SplitK w8_split_ctx(const W8Split& sp) {
+  return ldk::SplitK{sp.acc, sp.side, sp.splits, (int)blockIdx.y};
+}
 
 // Prologues (one row) that form the activation while it is staged, with the steps of the
 // standalone kernels:
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
       // every (m, n) word of the tile takes part, rows past M too, so each word is re-zeroed
       float tot;
       uint64_t* word = sp.acc + ((size_t)tile * nblk + mb) * (MT * CW) + o;
-      if (ldk::splitk_add(word, sp.splits, v, &tot) && m0 + m < a.M) {
+      if (ldk::splitk_add(w8_split_ctx(sp), word, v, &tot) && m0 + m < a.M) {
         if (a.bias) tot += (float)a.bias[n];
         a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)tot;
       }
@@ -436,7 +441,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
       a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)v;
     } else {
       float tot;
-      if (ldk::splitk_add(sp.acc + ((size_t)blockIdx.z * gridDim.x + tile) * 16 * CW + o, sp.splits, v, &tot)) {
+      if (ldk::splitk_add(w8_split_ctx(sp), sp.acc + ((size_t)blockIdx.z * gridDim.x + tile) * 16 * CW + o, v, &tot)) {
         if (a.bias) tot += (float)a.bias[n];
         a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)tot;
       }
@@ -447,6 +452,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
 struct W8Plan {
   int mt, ln, nw, rpl;
   int splits, kps, mblocks;
+  int64_t words;  // split-K accumulator words (one per output of every tile and row block)
   bool mfma;
   int ksw;  // MFMA kernel: 32-row K steps per wave and pass
 };
@@ -472,7 +478,8 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t w
   const int64_t sps = (steps + splits - 1) / splits;  // K steps per split
   p.kps = (int)(sps * 32);
   p.splits = (int)((steps + sps - 1) / sps);
-  if (p.splits > 1 && ((M + 15) / 16) * tiles * 16 * 128 * 8 > ws_bytes) {
+  p.words = ((M + 15) / 16) * tiles * 16 * 128;
+  if (p.splits > 1 && (int64_t)ldk::splitk_bytes(p.words, p.splits) > ws_bytes) {
     p.splits = 1;
     p.kps = (int)(steps * 32);
   }
@@ -531,7 +538,8 @@ W8Plan make_w8_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, i
   kps = (kps + 7) / 8 * 8;
   p.kps = (int)kps;
   p.splits = (int)((K + kps - 1) / kps);
-  const int64_t need = p.splits > 1 ? tiles * p.mblocks * p.mt * 16 * p.ln * 8 : 0;
+  p.words = tiles * p.mblocks * p.mt * 16 * p.ln;
+  const int64_t need = p.splits > 1 ? (int64_t)ldk::splitk_bytes(p.words, p.splits) : 0;
   if (need > ws_bytes) {  // no room for the partials: whole K per workgroup
     p.splits = 1;
     p.kps = (int)((K + 7) / 8 * 8);
@@ -649,7 +657,8 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   if (split_k > 1 && p.splits == 1)
     return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W8Args a{(const half_t*)x, ldx, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K};
-  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr,
+                   p.splits > 1 ? ldk::splitk_side(workspace, p.words) : nullptr};
   return p.mfma ? launch_w8_mfma(a, sp, p, (hipStream_t)stream) : launch_w8(a, sp, p, (hipStream_t)stream);
 }
 
@@ -670,7 +679,8 @@ extern "C" int ldk_w8a16_swiglu_matmul(const void* gate_up, const uint8_t* wq, c
     return ldk::fail(LDK_ERR_ALIGN, "w8a16_swiglu_matmul: workspace must be a 256-byte aligned pointer");
   const W8Plan p = make_w8_plan(1, N, K, 0, 0, workspace ? workspace_bytes : 0);
   const W8Args a{(const half_t*)gate_up, 2 * K, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K};
-  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr,
+                   p.splits > 1 ? ldk::splitk_side(workspace, p.words) : nullptr};
   return launch_w8(a, sp, p, (hipStream_t)stream, 1);
 }
 
@@ -697,6 +707,7 @@ extern "C" int ldk_w8a16_rmsnorm_matmul(const void* x, const void* residual, voi
   const W8Plan p = make_w8_plan(1, N, K, 0, 0, workspace ? workspace_bytes : 0);
   const W8Args a{(const half_t*)x,  K,      wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K,
                  (const half_t*)residual, (half_t*)residual_out, (const half_t*)norm_weight, eps};
-  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr};
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr,
+                   p.splits > 1 ? ldk::splitk_side(workspace, p.words) : nullptr};
   return launch_w8(a, sp, p, (hipStream_t)stream, residual ? 3 : 2);
 }

@@ -155,53 +155,88 @@ __device__ __forceinline__ float sum_waves(const float* p, int stride, int n) {
 
 // Cross-workgroup split-K reduction in one memory round trip. The `splits` workgroups of one
 // output tile each hold a partial p(o) for o < n (fp32, already reduced inside the workgroup).
-// Each adds it to a 64-bit word per output with one agent-scope atomic add: bits [63:8] carry
-// the sum of round(p * 2^24) in two's complement (fixed point, 2^-24 resolution), bits [7:0]
-// count the contributions. The add returns the previous word, so the workgroup whose add brings
-// the count to `splits` holds the complete sum: it stores the output and writes the word back to
-// zero, leaving the workspace zeroed for the next launch (no clearing launch, no counters, no
-// barrier, no waiting on other workgroups). Integer addition is associative, so the result does
-// not depend on arrival order (deterministic). Partials are clamped to +-2^20 (an fp16 output
-// saturates at 65504); a non-finite partial poisons the sum and the output becomes NaN.
-// Requires splits <= 32 and a zero-filled `acc` of n words for this tile.
-constexpr float kFixScale = 16777216.0f;          // 2^24
-constexpr float kFixClamp = 1048576.0f;           // 2^20
-constexpr int64_t kFixPoison = int64_t(1) << 50;  // > 32 * 2^44, the largest legal sum
-constexpr int64_t kFixPoisonSeen = int64_t(3) << 48;
+// Each adds it to a 64-bit word per output with one agent-scope atomic add:
+//   bits [5:0]   arrivals,
+//   bits [11:6]  arrivals whose partial took the side path (below),
+//   bits [63:12] the sum of round(p * 2^24) in two's complement (fixed point, 2^-24 resolution:
+//                the spacing of the smallest fp16 subnormals).
+// The add returns the previous word, so the workgroup whose add brings the arrival count to
+// `splits` holds the complete sum: it stores the output and writes the word back to zero,
+// leaving the workspace zeroed for the next launch (no clearing launch, no barrier, no waiting
+// on other workgroups). Integer addition is associative, so the result does not depend on
+// arrival order (deterministic).
+//
+// Side path. A partial with |p| >= 2^21, or a non-finite one, does not fit the fixed-point sum
+// (up to 63 partials of |p| < 2^21 keep |sum| < 2^51). Such a partial is stored as fp32 to its
+// own slot side[(word - words) * splits + split] (zero-filled, like the words), made visible at
+// agent scope by a release fence before the atomic add, and counted in bits [11:6]. The finishing
+// workgroup, seeing a non-zero side count, acquires, adds every slot of the word in split order
+// to the fixed-point sum in fp32 and zeroes them. So partials that cancel beyond the fixed-point
+// range (+3e6 and -3e6 + 10) give the fp32 sum, and inf/NaN partials propagate as in fp32
+// arithmetic. The fast path costs one compare.
+constexpr float kFixScale = 16777216.0f;  // 2^24
+constexpr float kFixRange = 2097152.0f;   // 2^21: partials below this in magnitude stay fixed point
+constexpr int kFixMaxSplits = 63;         // arrival count field
 
+struct SplitK {
+  uint64_t* words;  // first accumulator word of the launch
+  float* side;      // [words][splits] fp32 side slots, zero between launches
+  int splits;       // workgroups meeting in each word
+  int split;        // this workgroup's index among them
+};
+
+// The increment for partial p of `word` (stores p to its side slot when it takes the side path).
+__device__ __forceinline__ uint64_t splitk_inc(const SplitK& k, const uint64_t* word, float p) {
+  if (__builtin_fabsf(p) < kFixRange) return ((uint64_t)(int64_t)__builtin_rintf(p * kFixScale) << 12) + 1u;
+  k.side[(size_t)(word - k.words) * k.splits + k.split] = p;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  return (uint64_t(1) << 6) + 1u;
+}
 // The two halves of splitk_add, for a caller with several outputs per lane: issue every add first
 // (their round trips overlap), then finish each with the word it returned.
-__device__ __forceinline__ uint64_t splitk_inc(float p) {
-  const int64_t v = __builtin_isfinite(p)
-                        ? (int64_t)__builtin_rintf(__builtin_fminf(__builtin_fmaxf(p, -kFixClamp), kFixClamp) * kFixScale)
-                        : kFixPoison;
-  return ((uint64_t)v << 8) + 1u;
-}
 __device__ __forceinline__ uint64_t splitk_issue(uint64_t* word, uint64_t inc) {
   return __hip_atomic_fetch_add(word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool splitk_finish(uint64_t* word, int splits, uint64_t old, uint64_t inc, float* total) {
-  if ((int)(old & 0xffu) != splits - 1) return false;
-  const int64_t tot = (int64_t)(old + inc) >> 8;
-  const bool poisoned = tot >= kFixPoisonSeen || tot <= -kFixPoisonSeen;
-  *total = poisoned ? __builtin_nanf("") : (float)tot * (1.0f / kFixScale);
+__device__ __forceinline__ bool splitk_finish(const SplitK& k, uint64_t* word, uint64_t old, uint64_t inc, float* total) {
+  const uint64_t now = old + inc;
+  if ((int)(now & 63u) != k.splits) return false;
+  float t = (float)((int64_t)now >> 12) * (1.0f / kFixScale);
+  if (now & (uint64_t(63) << 6)) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    float* slot = k.side + (size_t)(word - k.words) * k.splits;
+    for (int i = 0; i < k.splits; ++i) {
+      t += __hip_atomic_load(slot + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      slot[i] = 0.0f;
+    }
+  }
   __hip_atomic_store(word, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  *total = t;
   return true;
 }
 
 // Adds partial p of one output to its accumulator word. Returns true in the one contribution that
 // completes the count; *total then holds the reduced value and the word is back to zero.
-__device__ __forceinline__ bool splitk_add(uint64_t* word, int splits, float p, float* total) {
-  const uint64_t inc = splitk_inc(p);
-  return splitk_finish(word, splits, splitk_issue(word, inc), inc, total);
+__device__ __forceinline__ bool splitk_add(const SplitK& k, uint64_t* word, float p, float* total) {
+  const uint64_t inc = splitk_inc(k, word, p);
+  return splitk_finish(k, word, splitk_issue(word, inc), inc, total);
 }
 
 template <typename Part, typename Store>
-__device__ __forceinline__ void splitk_accumulate(uint64_t* acc, int splits, int n, Part part, Store store) {
+__device__ __forceinline__ void splitk_accumulate(const SplitK& k, uint64_t* acc, int n, Part part, Store store) {
   for (int o = threadIdx.x; o < n; o += blockDim.x) {
     float tot;
-    if (splitk_add(acc + o, splits, part(o), &tot)) store(o, tot);
+    if (splitk_add(k, acc + o, part(o), &tot)) store(o, tot);
   }
+}
+
+// Bytes of workspace a launch with `words` accumulator words split `splits` ways needs: the words,
+// then (at the next 256-byte boundary) their fp32 side slots.
+inline size_t splitk_bytes(int64_t words, int splits) {
+  return (((size_t)words * 8 + 255) & ~size_t(255)) + (size_t)words * splits * 4;
+}
+// The side slots of a launch whose words start at `ws`.
+inline float* splitk_side(void* ws, int64_t words) {
+  return reinterpret_cast<float*>(static_cast<char*>(ws) + (((size_t)words * 8 + 255) & ~size_t(255)));
 }
 
 }  // namespace ldk

@@ -44,6 +44,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 
 #include "ldk_common.h"
@@ -51,7 +52,7 @@
 namespace {
 
 constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024.0 in both halves
-constexpr int kMaxSplits = 32;            // arrival count field of the split-K accumulators
+constexpr int kMaxSplits = 32;            // workgroups splitting one column tile (<= ldk::kFixMaxSplits)
 
 struct W4Args {
   const half_t* x;
@@ -73,6 +74,7 @@ struct SplitArgs {
                   // tiles [full, tiles) come first in dispatch order
   int nsplit;       // number of those split workgroups
   uint64_t smagic;  // ceil(2^32 / splits): b / splits == (b * smagic) >> 32 for b, splits < 2^16
+  float* side;      // fp32 side slots of the accumulators (ldk::SplitK), zero between launches
 };
 
 // ceil(2^32 / d) for 1 <= d < 2^16: floor(n / d) == (n * magic) >> 32 for every n < 2^16.
@@ -81,8 +83,15 @@ inline uint64_t div_magic(uint32_t d) { return ((uint64_t(1) << 32) + d - 1) / d
 // Work of one workgroup: a column tile and its range of quantization groups [gb, ge).
 struct TileWork {
   int tile, gb, ge;
+  int split;   // index among the workgroups splitting the tile's groups
   bool whole;  // all groups of the tile: the result is stored directly, no split-K reduction
 };
+
+// The split-K context of a workgroup (ldk::SplitK): the launch's words, their side slots, and its
+// index among the tile's splits.
+__device__ __forceinline__ ldk::SplitK split_ctx(const SplitArgs& sp, const TileWork& tw) {
+  return ldk::SplitK{sp.acc, sp.side, sp.splits, tw.split};
+}
 
 // Dispatch order: the split workgroups of tiles [full, tiles) first (splits per tile), then the
 // whole tiles [0, full). Requests are served roughly in issue order, so the split workgroups'
@@ -107,6 +116,7 @@ __device__ __forceinline__ TileWork map_block(const SplitArgs& sp, int ng) {
   TileWork w;
   w.tile = in_split ? sp.full + q : bid - sp.nsplit;
   const int split = in_split ? bid - q * sp.splits : 0;
+  w.split = split;
   w.whole = !in_split || sp.splits == 1;
   if constexpr (G > 1) {
     // the whole-tile range: [0, full) after the split workgroups, or every tile without splits
@@ -156,7 +166,7 @@ __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, con
   if (tw.whole) {
     for (int o = threadIdx.x; o < n; o += blockDim.x) store(o, part(o));
   } else {
-    ldk::splitk_accumulate(sp.acc + (size_t)(tw.tile - sp.full) * n, sp.splits, n, part, store);
+    ldk::splitk_accumulate(split_ctx(sp, tw), sp.acc + (size_t)(tw.tile - sp.full) * n, n, part, store);
   }
 }
 
@@ -505,7 +515,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
       const float v = e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3;
       const int c = n0 + lane;
       float tot;
-      if (lane < CW && c < a.N && ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
+      if (lane < CW && c < a.N && ldk::splitk_add(split_ctx(sp, tw), sp.acc + (size_t)(tile - sp.full) * CW + lane, v, &tot)) {
         if (a.bias) tot += (float)a.bias[c];
         a.out[c] = (half_t)tot;
       }
@@ -554,7 +564,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
 #pragma unroll
       for (int i = 1; i < NW; ++i) v += rf[i * CW + lane];
       float tot;
-      if (ldk::splitk_add(sp.acc + (size_t)(tile - sp.full) * CW + lane, sp.splits, v, &tot)) {
+      if (ldk::splitk_add(split_ctx(sp, tw), sp.acc + (size_t)(tile - sp.full) * CW + lane, v, &tot)) {
         if (a.bias) tot += (float)a.bias[c];
         a.out[c] = (half_t)tot;
       }
@@ -578,7 +588,9 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
     for (int m = 0; m < MR; ++m) {
       const float e0 = __shfl(acc[m][0], src), e1 = __shfl(acc[m][1], src);
       const float e2 = __shfl(acc[m][2], src), e3 = __shfl(acc[m][3], src);
-      inc[m] = ldk::splitk_inc(e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3);
+      inc[m] = 0;
+      if (lane < CW && c < a.N && m < mrows)
+        inc[m] = ldk::splitk_inc(split_ctx(sp, tw), words + m * CW + lane, e == 0 ? e0 : e == 1 ? e1 : e == 2 ? e2 : e3);
     }
     if (lane >= CW || c >= a.N) return;
 #pragma unroll
@@ -587,7 +599,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       float tot;
-      if (m < mrows && ldk::splitk_finish(words + m * CW + lane, sp.splits, old[m], inc[m], &tot)) {
+      if (m < mrows && ldk::splitk_finish(split_ctx(sp, tw), words + m * CW + lane, old[m], inc[m], &tot)) {
         if (a.bias) tot += (float)a.bias[c];
         a.out[(int64_t)m * a.ldo + c] = (half_t)tot;
       }
@@ -630,7 +642,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
       float v = reinterpret_cast<const float*>(&red[0][m][0])[lane];
 #pragma unroll
       for (int i = 1; i < NW; ++i) v += reinterpret_cast<const float*>(&red[i][m][0])[lane];
-      inc[m] = ldk::splitk_inc(v);
+      inc[m] = m < mrows ? ldk::splitk_inc(split_ctx(sp, tw), words + m * CW + lane, v) : 0;
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m)
@@ -638,7 +650,7 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       float tot;
-      if (m < mrows && ldk::splitk_finish(words + m * CW + lane, sp.splits, old[m], inc[m], &tot)) {
+      if (m < mrows && ldk::splitk_finish(split_ctx(sp, tw), words + m * CW + lane, old[m], inc[m], &tot)) {
         if (a.bias) tot += (float)a.bias[c];
         a.out[(int64_t)m * a.ldo + c] = (half_t)tot;
       }
@@ -1032,12 +1044,16 @@ size_t plan_lds_bytes(const Plan& p, int64_t M) {
 
 int plan_cw(const Plan& p) { return 4 * p.ln; }
 
-size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
-  if (p.splits <= 1) return 0;
+// Accumulator words of a split launch: one per output of every split tile.
+int64_t split_words(const Plan& p, int64_t M, int64_t N) {
   const int cw = plan_cw(p);
   const int64_t tiles = (N + cw - 1) / cw - p.full;
   const int64_t n = p.kern == kMfma ? std::min<int64_t>(M, 16) * cw : (int64_t)p.mt * cw;
-  return (size_t)tiles * n * 8;
+  return tiles * n;
+}
+
+size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
+  return p.splits <= 1 ? 0 : ldk::splitk_bytes(split_words(p, M, N), p.splits);
 }
 
 int cpw_from_flags(int flags) {
@@ -1318,8 +1334,10 @@ int launch_mfma_nh(const W4Args& a, const SplitArgs& sp, const Plan& p, size_t l
 int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro = kProNone,
                 const ProArgs& pa = ProArgs{}) {
   const int64_t tiles = (a.N + plan_cw(p) - 1) / plan_cw(p);
-  const SplitArgs sp{p.splits, p.gps, p.splits > 1 ? static_cast<uint64_t*>(ws) : nullptr, p.full,
-                     (int)((tiles - p.full) * p.splits), div_magic(p.splits)};
+  const bool split = p.splits > 1;
+  const SplitArgs sp{p.splits, p.gps, split ? static_cast<uint64_t*>(ws) : nullptr, p.full,
+                     (int)((tiles - p.full) * p.splits), div_magic(p.splits),
+                     split ? ldk::splitk_side(ws, split_words(p, a.M, a.N)) : nullptr};
   if (sp.full + (int64_t)sp.nsplit >= 65536)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %lld workgroups exceed the grid mapping limit", (long long)(sp.full + (int64_t)sp.nsplit));
   const size_t lds = plan_lds_bytes(p, a.M);
@@ -1393,6 +1411,30 @@ extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size,
   if (split_k) *split_k = p.splits;
   if (flags) *flags = plan_flags(p);
   return LDK_OK;
+}
+
+// Name of the kernel instantiation launch_plan runs for a plan, as the profiler lists it.
+static int plan_kernel_name(const Plan& p, int gsh_rows, char* buf, size_t len) {
+  const int rpg = 1 << gsh_rows;
+  int n = 0;
+  if (p.kern == kM1) {
+    n = snprintf(buf, len, "w4a16_m1_kernel<%d, %d, %d, 0, %d>", p.ln, p.nw, gsh_rows == 4 ? 4 : 0, p.mt);
+  } else if (p.kern == kValu) {
+    n = snprintf(buf, len, "w4a16_gemv_kernel<%d, %d, %d, %d>", p.mt, p.ln, p.rpl, p.cpw);
+  } else {
+    const int nh = p.ln == 32 ? 2 : 1, nwd = p.ln == 8 ? 2 : 4, ks = rpg / 4;
+    const int cpw = p.mtile == 2 ? 1 : (p.cpw == 2 && rpg <= 16 ? 2 : 1);
+    n = snprintf(buf, len, "w4a16_mfma_kernel<%d, %d, %d, %d, %d>", nh, ks, cpw, p.mtile, nwd);
+  }
+  return n < 0 || (size_t)n >= len ? ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: buffer of %zu bytes too small", len) : LDK_OK;
+}
+
+extern "C" int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_size, char* buf, int64_t buf_len) {
+  if (M <= 0 || N <= 0 || K <= 0 || !buf || buf_len <= 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: bad arguments");
+  const int gsh = log2_exact(group_size);
+  if (gsh < 5 || gsh > 8 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: bad group_size %d", group_size);
+  const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
+  return plan_kernel_name(p, gsh - 3, buf, (size_t)buf_len);
 }
 
 extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweight, const void* scales, const void* zeros,

@@ -47,6 +47,7 @@ SIGNATURES = {
     "ldk_w4a16_decode": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
                          _vp, _i64, _vp],
     "ldk_w4a16_config": [_i64, _i64, _i64, _i32, _ip, _ip, _ip],
+    "ldk_w4a16_kernel_name": [_i64, _i64, _i64, _i32, ctypes.c_char_p, _i64],
     "ldk_w4a16_rmsnorm_matmul": [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i32, _vp, _i64, _vp],
     "ldk_w4a16_swiglu_matmul": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _vp],
@@ -110,8 +111,21 @@ def check(status: int, what: str) -> None:
     raise RuntimeError(f"{what}: {msg}")
 
 
+class _TensorPtr(ctypes.c_void_p):
+    """A device pointer argument that keeps its tensor alive. ctypes holds the argument objects
+    until the foreign call returns, so a temporary such as `ptr(t.contiguous())` cannot go back
+    to torch's caching allocator (and be handed to the next temporary of the same call) before
+    the launch is enqueued; after that, the allocator's stream ordering protects it."""
+
+    __slots__ = ("tensor",)
+
+
 def ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    if t is None:
+        return None
+    p = _TensorPtr(t.data_ptr())
+    p.tensor = t
+    return p
 
 
 def stream(device: torch.device):
@@ -141,6 +155,27 @@ def require_gpu(*tensors: torch.Tensor | None, what: str) -> torch.device:
     if dev is None:
         raise RuntimeError(f"{what}: no tensor given")
     return dev
+
+
+def on_gpu(*tensors: torch.Tensor | None, what: str):
+    """For the weight-format routines, which the reference writes as device-agnostic torch code
+    (kernels/quant.py:20-49, kernels/fp8.py:25-35) and its tests call on CPU tensors: returns
+    (run_device, home_device, tensors on run_device). Tensors on a GPU stay there; CPU tensors are
+    copied to the current ROCm GPU, where the HIP kernel runs, and the caller moves its results
+    back to `home_device`. Without a visible GPU this raises: there is no CPU implementation."""
+    given = [t for t in tensors if t is not None]
+    if not given:
+        raise RuntimeError(f"{what}: no tensor given")
+    home = given[0].device
+    if any(t.device != home for t in given):
+        raise RuntimeError(f"{what}: tensors on different devices")
+    if home.type == "cuda":
+        return home, home, list(tensors)
+    if home.type != "cpu" or not torch.cuda.is_available():
+        raise RuntimeError(f"{what}: needs a ROCm GPU to run its HIP kernel (got {home} tensors "
+                           "and no visible GPU); this library has no CPU path")
+    run = torch.device("cuda", torch.cuda.current_device())
+    return run, home, [None if t is None else t.to(run) for t in tensors]
 
 
 _workspaces: dict[int, torch.Tensor] = {}

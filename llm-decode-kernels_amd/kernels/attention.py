@@ -109,9 +109,10 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
         q = q.contiguous()
     dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, what="decode_attention")
     out = torch.empty((1, 1, n_heads * hd), dtype=torch.float16, device=dev)
+    freq = inv_freq.contiguous()
     with _lib.device_guard(dev):
         st = _lib.load().ldk_decode_attention(
-            _lib.ptr(q), _lib.ptr(pos), _lib.ptr(inv_freq.contiguous()), _lib.ptr(k_cache),
+            _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache),
             _lib.ptr(vt_cache), _lib.ptr(out), n_heads, n_kv, hd, L, float(scale), _lib.stream(dev))
     _lib.check(st, "decode_attention")
     return out

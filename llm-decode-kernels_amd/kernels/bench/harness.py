@@ -11,6 +11,7 @@
 
 from __future__ import annotations
 
+import contextlib
 import gc
 import math
 import statistics
@@ -26,13 +27,10 @@ MEMORY_BUDGET = 8 * 2**30  # bytes of rotating copies per case (of 288 GB HBM)
 
 
 def tensor_bytes(obj) -> int:
-    if isinstance(obj, torch.Tensor):
-        return obj.numel() * obj.element_size()
-    if isinstance(obj, (list, tuple)):
-        return sum(tensor_bytes(o) for o in obj)
-    if isinstance(obj, dict):
-        return sum(tensor_bytes(o) for o in obj.values())
-    return 0
+    """Bytes of every tensor in a (nested) list/tuple/dict."""
+    from torch.utils._pytree import tree_leaves
+
+    return sum(t.nbytes for t in tree_leaves(obj) if isinstance(t, torch.Tensor))
 
 
 def n_copies(bytes_per_set: int, cache_bytes: int = MALL_BYTES, cap: int = 1024) -> int:
@@ -42,23 +40,39 @@ def n_copies(bytes_per_set: int, cache_bytes: int = MALL_BYTES, cap: int = 1024)
     return int(min(max(want, 2), budget, cap))
 
 
-def capture(body: Callable, retries: int = 1):
-    """Capture body() into a graph (GC off during capture, one retry), return (graph, result)."""
-    last = None
-    for _ in range(retries + 1):
-        graph = torch.cuda.CUDAGraph()
-        gc.collect()
-        gc.disable()
-        try:
-            with torch.cuda.graph(graph, capture_error_mode="thread_local"):
-                out = body()
-            return graph, out
-        except Exception as e:  # noqa: BLE001 - capture failures are retried once
-            last = e
-            torch.cuda.synchronize()
-        finally:
+@contextlib.contextmanager
+def _gc_paused():
+    """Python's collector may free a tensor whose memory a capture is recording into."""
+    was = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
             gc.enable()
-    raise last
+
+
+def capture(body: Callable):
+    """(graph, body's result) for one capture of body() on a side stream."""
+    graph = torch.cuda.CUDAGraph()
+    with _gc_paused(), torch.cuda.graph(graph, capture_error_mode="thread_local"):
+        result = body()
+    return graph, result
+
+
+def replay_ms(graph, replays: int, stream=None) -> float:
+    """ms of `replays` back-to-back replays of `graph`, HIP events on `stream` (default: the
+    current stream), which is where the replays run."""
+    stream = stream or torch.cuda.current_stream()
+    start, end = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end)
 
 
 class GraphTimer:
@@ -83,15 +97,7 @@ class GraphTimer:
 
     def time_replays(self, replays: int) -> float:
         """Total ms of `replays` back-to-back replays, HIP events on the replay stream."""
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(self.stream):
-            start.record(self.stream)
-            for _ in range(replays):
-                self.graph.replay()
-            end.record(self.stream)
-        end.synchronize()
-        return start.elapsed_time(end)
+        return replay_ms(self.graph, replays, self.stream)
 
     def median_ms_per_call(self) -> float:
         first = self.time_replays(1)

@@ -1,14 +1,17 @@
 """End-to-end decode on one MI355X: the Qwen2.5-1.5B architecture, random-init (seed 4), fp16
 library GEMMs vs this build's swapped kernels (config 4).
 
-Measures per backend, same runner, hipGraphs on both sides (the reference's kernels/e2e/run.py):
+Measures per backend, same runner, hipGraphs on both sides (what the reference's
+kernels/e2e/run.py measures on its GPUs):
 - decode tokens/s at batch 1: a 128-token prompt of uniform random ids, then `decode_steps`
   greedy steps, each step one graph replay (forward + argmax + bookkeeping), median of 3 runs;
 - the swapped layers alone: all 28 layers' projections, fused add+norms and the activation for
-  one decode step, as one graph (`layers_only_ms`, run.py:166-201);
+  one decode step, as one graph (`layers_only_ms`, the reference's run.py:166-201);
 - the layer weight bytes each backend reads per token.
+Every backend runs the same lm_head (`--head gemv|torch`, kernels/e2e/model.py's QwenRunner).
 
-    python -m kernels.e2e.run [--backends fp16,ours] [--steps 256] [--prompt 128] [--json out]
+    python -m kernels.e2e.run [--backends fp16,ours] [--steps 256] [--prompt 128] [--head gemv]
+                              [--json out]
 """
 
 from __future__ import annotations
@@ -22,122 +25,108 @@ import time
 
 import torch
 
-from kernels.bench.harness import capture
+from kernels.bench.harness import capture, replay_ms
 from kernels.e2e.model import QwenRunner, make_backend, random_qwen2
 
 
-def _events():
-    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-
 class GraphDecoder:
-    """One greedy decode step captured in a hipGraph (run.py:58-111)."""
+    """Greedy batch-1 decoding, one hipGraph replay per token (the reference's run.py:58-122).
+
+    The decode state lives on the device in one int64 buffer: [token, position, log of emitted
+    tokens by position]. A step is the runner's forward on (token, position) followed by
+    `kernels.sample.greedy_step` (argmax, log, advance) in one launch; the prompt's last logits go
+    through the same launch, so the first new token is logged at position P - 1 like every
+    later one at its own position."""
 
     def __init__(self, runner: QwenRunner):
         self.r = runner
-        dev = runner.embed.device
-        self.tok = torch.zeros(1, 1, dtype=torch.long, device=dev)
-        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
-        self.out = torch.zeros(runner.max_len, dtype=torch.long, device=dev)
+        self.state = torch.zeros(2 + runner.max_len, dtype=torch.long, device=runner.embed.device)
+        self.tok = self.state[:1].view(1, 1)
+        self.pos = self.state[1:2]
+        self.out = self.state[2:]
         self.graph = None
 
-    def _step(self):
-        """forward + greedy bookkeeping. The argmax and the out/tok/pos updates run as one HIP
-        launch (kernels.sample.greedy_step) on every backend: torch's vocabulary-sized argmax
-        clears a semaphore with a memset node, which is not reliable under graph replay here."""
+    def step(self):
         from kernels.sample import greedy_step
 
-        logits = self.r.forward(self.tok, self.pos)
-        greedy_step(logits[:, -1], self.tok, self.pos, self.out)
+        greedy_step(self.r.forward(self.tok, self.pos), self.tok, self.pos, self.out)
 
     def prefill(self, ids: torch.Tensor) -> int:
+        """Runs the prompt; leaves the first new token in `tok` and `out[P-1]`, position P."""
+        from kernels.sample import greedy_step
+
         P = ids.shape[1]
         logits = self.r.forward(ids, torch.arange(P, device=ids.device))
-        self.tok.copy_(logits[:, -1].argmax(-1).view(1, 1))
-        self.pos.fill_(P)
-        self.out.zero_()
-        self.out[P - 1] = self.tok.view(-1)[0]  # position P-1 holds the first new token
+        self.state.zero_()
+        self.pos.fill_(P - 1)
+        greedy_step(logits, self.tok, self.pos, self.out)
         return P
 
-    def capture(self, ids):
-        """Eager warm-up first (the first library call per device allocates the split-K
-        workspace), then capture on a side stream."""
+    def capture(self, ids: torch.Tensor, warmup: int = 3):
+        """Eager steps on a side stream first (each library entry allocates its per-device
+        workspace on its first call, which must not happen under capture), then the capture of
+        one step from the state a fresh prefill leaves."""
         self.prefill(ids)
-        self._step()
-        torch.cuda.synchronize()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for _ in range(3):
-                self._step()
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self.step()
+        torch.cuda.current_stream().wait_stream(side)
         self.prefill(ids)
-        self.graph, _ = capture(self._step)
+        self.graph, _ = capture(self.step)
         torch.cuda.synchronize()
 
-    def generate(self, ids, steps: int) -> tuple[list[int], float]:
+    def generate(self, ids: torch.Tensor, steps: int) -> tuple[list[int], float]:
+        """Prefill, then `steps` replays. Returns the steps + 1 new tokens and the seconds the
+        replays took (HIP events on the current stream)."""
         P = self.prefill(ids)
         torch.cuda.synchronize()
-        start, end = _events()
-        start.record()
-        for _ in range(steps):
-            self.graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        tokens = self.out[P - 1: P - 1 + steps + 1].tolist()
-        return tokens, start.elapsed_time(end) / 1e3
+        ms = replay_ms(self.graph, steps)
+        return self.out[P - 1: P + steps].tolist(), ms / 1e3
 
 
 def decode_speed(runner, ids, steps: int, repeats: int = 3) -> dict:
+    """Median decode rate over `repeats` generations of `steps` tokens after one prompt."""
     dec = GraphDecoder(runner)
     dec.capture(ids)
-    rates, tokens = [], None
-    for _ in range(repeats):
-        tokens, sec = dec.generate(ids, steps)
-        rates.append(steps / sec)
+    runs = [dec.generate(ids, steps) for _ in range(repeats)]
     del dec
-    return {"tok_s": statistics.median(rates), "tok_s_min": min(rates), "tok_s_max": max(rates),
-            "ms_per_token": 1e3 / statistics.median(rates), "steps": steps, "tokens": tokens}
+    rates = sorted(steps / sec for _, sec in runs)
+    med = statistics.median(rates)
+    return {"tok_s": med, "tok_s_min": rates[0], "tok_s_max": rates[-1],
+            "ms_per_token": 1e3 / med, "steps": steps, "tokens": runs[-1][0]}
 
 
-def layers_only_ms(runner, M: int = 1) -> float:
-    """Graph time of the swapped ops alone for one decode step (run.py:166-201): per layer the
-    qkv, o, gate_up and down projections, two add+norms and the activation, through the
-    backend's norm_linear/linear_norm_linear/act_linear (fused launches on the fused backends)."""
+def layers_only_ms(runner, M: int = 1, samples: int = 7, replays: int = 10) -> float:
+    """Graph time of the swapped ops alone for one decode step (the reference's run.py:166-201):
+    per layer the qkv, o, gate_up and down projections, two add+norms and the activation,
+    through the backend's norm_linear/linear_norm_linear/act_linear (fused launches on the fused
+    backends). Median over `samples` of `replays` back-to-back replays."""
     be, eps = runner.backend, runner.eps
     dev = runner.embed.device
     H = runner.embed.shape[1]
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(1, M, H, device=dev, dtype=torch.float16, generator=g)
     res = torch.randn(1, M, H, device=dev, dtype=torch.float16, generator=g)
-    nq, hd = runner.n_heads, runner.head_dim
+    q_width = runner.n_heads * runner.head_dim
 
-    def step():
+    def body():
         h, r = x, res
         for L in runner.layers:
             qkv, r = be.norm_linear(h, L.ln1, eps, r, L.qkv)
-            gate_up, r = be.linear_norm_linear(qkv[..., : nq * hd].contiguous(), L.o, r, L.ln2,
+            gate_up, r = be.linear_norm_linear(qkv[..., :q_width].contiguous(), L.o, r, L.ln2,
                                                eps, L.gate_up)
             h = be.act_linear(gate_up, L.down)
 
     for _ in range(3):
-        step()
+        body()
     torch.cuda.synchronize()
-    graph, _ = capture(step)
+    graph, _ = capture(body)
     graph.replay()
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(7):
-        start, end = _events()
-        start.record()
-        for _ in range(10):
-            graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        times.append(start.elapsed_time(end) / 10)
+    ms = statistics.median(replay_ms(graph, replays) / replays for _ in range(samples))
     del graph
-    return statistics.median(times)
+    return ms
 
 
 def run(params: dict) -> dict:
@@ -145,6 +134,7 @@ def run(params: dict) -> dict:
     steps = int(params.get("decode_steps", 256))
     prompt_len = int(params.get("prompt_len", 128))
     seed = int(params.get("seed", 4))
+    head = params.get("head", "gemv")
     t0 = time.time()
     hf = random_qwen2(seed=seed)
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -152,10 +142,10 @@ def run(params: dict) -> dict:
     max_len = -(-(prompt_len + steps + 8) // 32) * 32  # the cache tiles hold 32 positions
     result = {"model": "Qwen2.5-1.5B architecture, random init (HF init, seed %d)" % seed,
               "prompt_len": prompt_len, "decode_steps": steps, "max_len": max_len,
-              "backends": {}}
+              "head": head, "backends": {}}
     for name in backends:
-        print(f"[e2e] backend {name} ({time.time() - t0:.0f}s)", flush=True)
-        runner = QwenRunner(hf, make_backend(name), max_len=max_len)
+        print(f"[e2e] backend {name}, head {head} ({time.time() - t0:.0f}s)", flush=True)
+        runner = QwenRunner(hf, make_backend(name), max_len=max_len, head=head)
         r = {"weights": runner.weight_bytes()}
         r["decode"] = decode_speed(runner, ids, steps)
         r["layers_only_ms"] = layers_only_ms(runner)
@@ -183,10 +173,11 @@ def main(argv=None) -> int:
     ap.add_argument("--backends", default="fp16,ours")
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--head", default="gemv", choices=QwenRunner.HEADS)
     ap.add_argument("--json", default=None)
     args = ap.parse_args(argv)
     res = run({"backends": args.backends.split(","), "decode_steps": args.steps,
-               "prompt_len": args.prompt})
+               "prompt_len": args.prompt, "head": args.head})
     text = json.dumps(res, indent=1)
     if args.json:
         with open(args.json, "w") as f:

@@ -4,7 +4,8 @@ Drop-in for the reference's `kernels/fp8.py`: weights are float8 e4m3fn with one
 channel, stored [K, N] (N contiguous). gfx950 decodes OCP e4m3 natively (v_cvt_pk_f32_fp8), so
 the weight bytes go straight from a 128-bit load to fp32 FMAs; the scale is applied once after
 the K reduction (fp8.py:120). Quantize/dequantize run HIP kernels that reproduce the reference
-bit for bit. Decode shapes run the wave64 VALU GEMV with an in-workgroup split-K at M <= 2 and
+bit for bit; like the reference's torch code they take CPU tensors too (run on the current ROCm
+GPU, results returned on the CPU). Decode shapes run the wave64 VALU GEMV with an in-workgroup split-K at M <= 2 and
 the MFMA kernel (in-register byte transpose, exact e4m3 -> fp16) from 3 rows.
 Prefill rows (M > 16) run the MFMA kernel in 16-row blocks up to PREFILL_NATIVE_MAX_M rows
 (`config={"prefill": "native" | "dequant"}` forces a path); more rows dequantize once and run a
@@ -25,7 +26,7 @@ def quantize_fp8(weight: torch.Tensor):
     """[N, K] -> (wq float8_e4m3fn [K, N], scale [N] in weight's dtype) with per-output-channel
     absmax scaling (fp8.py:25-30)."""
     N, K = weight.shape
-    dev = _lib.require_gpu(weight, what="quantize_fp8")
+    dev, home, (weight,) = _lib.on_gpu(weight, what="quantize_fp8")
     w = weight.contiguous()
     code = _lib.dtype_code(w.dtype)
     wq = torch.empty((K, N), dtype=FP8, device=dev)
@@ -33,13 +34,13 @@ def quantize_fp8(weight: torch.Tensor):
     with _lib.device_guard(dev):
         _lib.check(_lib.load().ldk_fp8_quantize(_lib.ptr(w), code, _lib.ptr(wq), _lib.ptr(scale),
                                                 N, K, _lib.stream(dev)), "quantize_fp8")
-    return wq, scale
+    return wq.to(home), scale.to(home)
 
 
 def dequantize_fp8(wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """-> [N, K] in scale's dtype (fp8.py:33-35)."""
     K, N = wq.shape
-    dev = _lib.require_gpu(wq, scale, what="dequantize_fp8")
+    dev, home, (wq, scale) = _lib.on_gpu(wq, scale, what="dequantize_fp8")
     code = _lib.dtype_code(scale.dtype)
     out = torch.empty((N, K), dtype=scale.dtype, device=dev)
     q = wq.contiguous()
@@ -47,7 +48,7 @@ def dequantize_fp8(wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     with _lib.device_guard(dev):
         _lib.check(_lib.load().ldk_fp8_dequant(_lib.ptr(q), _lib.ptr(s), code, _lib.ptr(out), N, K,
                                                _lib.stream(dev)), "dequantize_fp8")
-    return out
+    return out.to(home)
 
 
 # Rows up to which the MFMA kernel (16-row blocks over the e4m3 weights) runs; more rows

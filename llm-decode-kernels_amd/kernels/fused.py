@@ -125,6 +125,7 @@ def linear_rmsnorm_w4a16_matmul(x, qweight1, scales1, zeros1, bias1, residual, w
             raise ValueError("linear_rmsnorm_w4a16_matmul: scales and zeros must be float16")
     b1 = None if bias1 is None else bias1.to(torch.float16).contiguous()
     b2 = None if bias2 is None else bias2.to(torch.float16).contiguous()
+    s1, z1, s2, z2 = (t.contiguous() for t in (scales1, zeros1, scales2, zeros2))
     h = torch.empty((*x.shape[:-1], N1), dtype=torch.float16, device=dev)
     stats = torch.empty(nstats, dtype=torch.float32, device=dev)
     y2 = torch.empty((*x.shape[:-1], N2), dtype=torch.float16, device=dev)
@@ -133,12 +134,12 @@ def linear_rmsnorm_w4a16_matmul(x, qweight1, scales1, zeros1, bias1, residual, w
         ws, ws_bytes = _lib.workspace(dev)
         st = lib.ldk_w4a16_matmul_residual_stats(
             _lib.ptr(x), _lib.ptr(residual), _lib.ptr(h), _lib.ptr(stats), _lib.ptr(qweight1),
-            _lib.ptr(scales1.contiguous()), _lib.ptr(zeros1.contiguous()), _lib.ptr(b1), N1, K1,
+            _lib.ptr(s1), _lib.ptr(z1), _lib.ptr(b1), N1, K1,
             group_size, ws, ws_bytes, _lib.stream(dev))
         _lib.check(st, "linear_rmsnorm_w4a16_matmul")
         st = lib.ldk_w4a16_rmsnorm_stats_matmul(
             _lib.ptr(h), _lib.ptr(stats), nstats, _lib.ptr(weight), float(eps), _lib.ptr(qweight2),
-            _lib.ptr(scales2.contiguous()), _lib.ptr(zeros2.contiguous()), _lib.ptr(b2),
+            _lib.ptr(s2), _lib.ptr(z2), _lib.ptr(b2),
             _lib.ptr(y2), N2, K2, group_size, ws, ws_bytes, _lib.stream(dev))
         _lib.check(st, "linear_rmsnorm_w4a16_matmul")
     return y2, h

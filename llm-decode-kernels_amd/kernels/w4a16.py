@@ -126,6 +126,14 @@ def config_for(M: int, N: int, K: int, group_size: int = 128) -> str:
     return f"{path},block_n={bn.value},split_k={sk.value},{mode}{extra}"
 
 
+def kernel_name(M: int, N: int, K: int, group_size: int = 128) -> str:
+    """The kernel instantiation the library runs for a shape, as the profiler names it."""
+    buf = ctypes.create_string_buffer(256)
+    _lib.check(_lib.load().ldk_w4a16_kernel_name(M, N, K, group_size, buf, len(buf)),
+               "w4a16_kernel_name")
+    return buf.value.decode()
+
+
 def export_choices() -> dict:
     """Configurations used so far (w4a16.py:333-335)."""
     return {",".join(map(str, k)): v for k, v in _decode_choice.items()}
@@ -145,4 +153,4 @@ def best_configs() -> dict:
 
 
 __all__ = ["w4a16_matmul", "export_choices", "import_choices", "best_configs", "config_for",
-           "PACK"]
+           "kernel_name", "PACK"]

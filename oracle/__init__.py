@@ -12,6 +12,9 @@ Modules and the reference code each one restates (paths relative to the referenc
                      `kernels/rmsnorm.py:71-74` and `kernels/swiglu.py:64-65`.
 - `oracle.fp8`       OCP e4m3 encode/decode, per-channel FP8 quantizer and W8A16 reference,
                      `kernels/fp8.py:21-39` and `tests/test_fp8.py:20`.
+- `oracle.torch_cpu` the same references as torch ops on CPU tensors (the reference's own CPU
+                     path, timed on all host cores by `bench.py`'s `cpu_baseline`), pinned
+                     against the numpy modules above.
 
 Every function is pinned by checks in `tests/test_oracle_*.py` that do not retype its formula:
 the reference tests' known-answer values (`tests/test_quant.py:15-18,34-35`), hand-derived

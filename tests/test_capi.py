@@ -218,8 +218,6 @@ def test_python_ops_refuse_cpu_tensors():
 
     w = torch.randn(64, 128).half()
     with pytest.raises(RuntimeError, match="ROCm GPU"):
-        quantize_rtn(w)
-    with pytest.raises(RuntimeError, match="ROCm GPU"):
         rmsnorm(torch.randn(2, 64).half(), torch.ones(64).half())
     qw = torch.zeros(16, 64, dtype=torch.int32)
     s = torch.ones(1, 64).half()
@@ -237,3 +235,20 @@ def test_reference_assertions_kept():
     with pytest.raises(AssertionError):
         w4a16_matmul(torch.randn(1, 128).half(), torch.zeros(8, 4, dtype=torch.int32),
                      torch.ones(1, 4).half(), torch.ones(1, 4).half())
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="with a GPU, CPU tensors run there (GPU tier)")
+def test_format_routines_need_a_gpu_for_cpu_tensors():
+    """The weight-format routines take CPU tensors like the reference's torch code, but run them
+    through the HIP kernels on a GPU: without one they raise rather than compute on the host."""
+    from kernels.fp8 import dequantize_fp8, quantize_fp8
+    from kernels.quant import dequantize, pack_int4, quantize_rtn, unpack_int4
+
+    w = torch.randn(64, 128).half()
+    q = torch.zeros(16, 8, dtype=torch.int32)
+    for call in (lambda: quantize_rtn(w), lambda: pack_int4(q), lambda: unpack_int4(q[:2]),
+                 lambda: dequantize(q[:2], torch.ones(1, 8).half(), torch.ones(1, 8).half(), 16),
+                 lambda: quantize_fp8(w),
+                 lambda: dequantize_fp8(torch.zeros(8, 4).to(torch.float8_e4m3fn), torch.ones(4).half())):
+        with pytest.raises(RuntimeError, match="needs a ROCm GPU"):
+            call()

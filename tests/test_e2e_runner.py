@@ -57,7 +57,7 @@ def test_lm_suffix_needs_quantized_backend():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("ours", ["ours", "ours_hip"])
+@pytest.mark.parametrize("ours", ["ours", "ours_cuda"])
 def test_ours_matches_w4_reference(ours):
     model = _tiny_model(torch.float16, "cuda")
     ids = torch.randint(0, 512, (1, 5), device="cuda")
@@ -108,7 +108,7 @@ def test_graph_decoder_matches_eager_steps(vocab):
     P = dec.prefill(ids)
     eager = [int(dec.tok.item())]
     for _ in range(12):
-        dec._step()
+        dec.step()
         eager.append(int(dec.tok.item()))
     assert P == 9 and toks == eager
 
@@ -177,6 +177,31 @@ def test_fused_attention_graph_decoder_matches_eager_steps():
     P = dec.prefill(ids)
     eager = [int(dec.tok.item())]
     for _ in range(24):
-        dec._step()
+        dec.step()
         eager.append(int(dec.tok.item()))
     assert P == 17 and toks == eager
+
+
+def test_make_backend_names():
+    for name in ("fp16", "w4_ref", "ours", "ours_cuda", "ours_fp8"):
+        assert make_backend(name).name == name and not make_backend(name).quant_lm_head
+    for name in ("w4_ref_lm", "ours_lm", "ours_cuda_lm", "ours_fp8_lm"):
+        be = make_backend(name)
+        assert be.name == name and be.quant_lm_head and be.quantized
+    with pytest.raises(KeyError):
+        make_backend("ours_triton")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", ["fp16", "ours", "ours_fp8"])
+def test_gemv_head_matches_torch_head(backend):
+    """The runner's two lm_head paths (this build's one-row GEMV with the final norm in its
+    launch, and the reference's norm then F.linear) give the same logits on every backend."""
+    model = _qwen_heads_model("cuda", vocab=4096)
+    ids = torch.randint(0, 4096, (1, 12), device="cuda")
+    outs = {}
+    for head in ("gemv", "torch"):
+        r = QwenRunner(model, make_backend(backend), max_len=64, head=head)
+        r.forward(ids[:, :11], torch.arange(11, device="cuda"))
+        outs[head] = r.forward(ids[:, 11:], torch.tensor([11], device="cuda")).float()
+    torch.testing.assert_close(outs["gemv"], outs["torch"], atol=1e-2, rtol=1e-2)

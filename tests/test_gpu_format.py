@@ -107,3 +107,53 @@ def test_weight_bytes_matches_buffers():
     qw, s, z = quantize_rtn(torch.zeros(17920, 1536, dtype=torch.float16, device="cuda"))
     nbytes = sum(t.numel() * t.element_size() for t in (qw, s, z))
     assert nbytes == weight_bytes(17920, 1536) == 14_622_720
+
+
+# ------------------------------------------------ CPU tensors in, CPU tensors out (reference
+# quant.py:20-49 and fp8.py:25-35 are device-agnostic torch code; its tests call them on the CPU)
+def test_cpu_inputs_bit_exact_and_returned_on_cpu():
+    from kernels.fp8 import dequantize_fp8, quantize_fp8
+    from oracle import fp8 as of
+
+    w, _ = cases.w4a16_case(1, 256, 1536, seed=0)  # fp16 [N, K] on the CPU
+    qw, s, z = quantize_rtn(w, 128)
+    oqw, os_, oz = oq.quantize_rtn(w.numpy(), 128)
+    assert qw.device.type == s.device.type == z.device.type == "cpu"
+    assert np.array_equal(qw.numpy(), oqw)
+    assert np.array_equal(bits16(s), bits16(os_)) and np.array_equal(bits16(z), bits16(oz))
+    deq = dequantize(qw, s, z, 128)
+    assert deq.device.type == "cpu"
+    assert np.array_equal(bits16(deq), bits16(dequantize_ref(oqw, os_, oz, 128)))
+    q = torch.from_numpy(np.random.default_rng(3).integers(0, 16, (64, 40)).astype(np.int32))
+    packed = pack_int4(q)
+    assert packed.device.type == "cpu" and np.array_equal(packed.numpy(), oq.pack_int4(q.numpy()))
+    assert torch.equal(unpack_int4(packed), q)
+    wq, sc = quantize_fp8(w)
+    owq, osc = of.quantize_fp8(w.numpy())
+    assert wq.device.type == sc.device.type == "cpu"
+    assert np.array_equal(wq.view(torch.uint8).numpy(), owq) and np.array_equal(bits16(sc), bits16(osc))
+    back = dequantize_fp8(wq, sc)
+    assert back.device.type == "cpu"
+    assert np.array_equal(bits16(back), bits16(of.dequantize_fp8(owq, osc)))
+
+
+def test_mixed_devices_rejected():
+    q = torch.zeros((8, 4), dtype=torch.int32)  # K = 64: one group of 64
+    with pytest.raises(RuntimeError, match="different devices"):
+        dequantize(q.cuda(), torch.zeros((1, 4), dtype=torch.float16),
+                   torch.zeros((1, 4), dtype=torch.float16, device="cuda"), 64)
+
+
+def test_dequantize_column_sliced_scales_and_zeros():
+    """Non-contiguous scales/zeros (column slices of a wider tensor) are copied to temporaries
+    that must both stay alive until the launch is enqueued."""
+    N, K = 96, 512
+    w, _ = cases.w4a16_case(1, 2 * N, K, seed=8)
+    oqw, os_, oz = oq.quantize_rtn(w.numpy(), 128)
+    qw_t, s_t, z_t = dev(oqw), dev(os_), dev(oz)
+    qs, ss, zs = qw_t[:, N:], s_t[:, N:], z_t[:, N:]
+    assert not ss.is_contiguous() and not zs.is_contiguous()
+    out = dequantize(qs, ss, zs, 128)
+    ref = dequantize_ref(np.ascontiguousarray(oqw[:, N:]), np.ascontiguousarray(os_[:, N:]),
+                         np.ascontiguousarray(oz[:, N:]), 128)
+    assert np.array_equal(bits16(out), bits16(ref))

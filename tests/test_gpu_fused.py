@@ -206,3 +206,25 @@ def test_rejects_aliased_residual_output():
         _lib.ptr(x), _lib.ptr(x), _lib.ptr(x), _lib.ptr(w), 1e-6, _lib.ptr(qw), _lib.ptr(s),
         _lib.ptr(z), None, _lib.ptr(out), 1536, 1536, 128, ws, nb, _lib.stream(x.device))
     assert st == _lib.ERR_INVALID
+
+
+def test_linear_rmsnorm_pair_column_sliced_scales_and_zeros():
+    """Scales/zeros passed as column slices of wider tensors (non-contiguous): each copy must
+    stay alive until its launch is enqueued, else two copies can share one freed block."""
+    N1, K1, N2 = 1536, 1536, 2048
+    qw1, s1, z1, b1 = _weights(2 * N1, K1, 71, bias=True)
+    qw2, s2, z2, _ = _weights(2 * N2, N1, 72)
+    qw1c, qw2c = qw1[:, N1:].contiguous(), qw2[:, N2:].contiguous()
+    s1v, z1v, s2v, z2v = s1[:, N1:], z1[:, N1:], s2[:, N2:], z2[:, N2:]
+    assert not any(t.is_contiguous() for t in (s1v, z1v, s2v, z2v))
+    b1 = b1[N1:].cuda()
+    x = cases.activations(1, K1, cases.gen(73)).cuda()
+    _, r, wn = cases.rmsnorm_case(1, N1, 74)
+    y2, h = linear_rmsnorm_w4a16_matmul(x, qw1c, s1v, z1v, b1, r.cuda(), wn.cuda(), 1e-6,
+                                        qw2c, s2v, z2v, None)
+    y2c, hc = linear_rmsnorm_w4a16_matmul(x, qw1c, s1v.contiguous(), z1v.contiguous(), b1,
+                                          r.cuda(), wn.cuda(), 1e-6, qw2c, s2v.contiguous(),
+                                          z2v.contiguous(), None)
+    assert torch.equal(h, hc) and torch.equal(y2, y2c)
+    xn = rmsnorm_ref(to_np(hc), wn.numpy(), 1e-6)
+    assert_north_star(to_np(y2), _oracle_linear(xn, qw2c, s2v.contiguous(), z2v.contiguous(), None))

@@ -9,7 +9,7 @@ import torch
 
 from _util import assert_north_star, bits16, dev, to_np
 from kernels.bench import cases
-from kernels.hip.w4a16_hip import w4a16_decode_hip
+from kernels.cuda.w4a16_cuda import w4a16_decode_cuda
 from kernels.w4a16 import w4a16_matmul
 from oracle import quant as oq
 from oracle.reference import dequantize_ref, w4a16_ref
@@ -284,7 +284,7 @@ def test_qkv_fused_with_bias():
 # ---------------------------------------------------------------- the native decode entry
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 16])
 def test_decode_entry(M):
-    _run(M, 1536, 1536, entry=w4a16_decode_hip)
+    _run(M, 1536, 1536, entry=w4a16_decode_cuda)
 
 
 # ------------------------------------------------------------- prefill rows (M > 16)
@@ -325,7 +325,7 @@ def test_prefill_one_hot_rows_reproduce_dequantized_weight():
 def test_decode_entry_rejects_17_rows():
     """As the reference's CUDA entry (tests/test_w4a16_cuda.py:43-45)."""
     with pytest.raises(RuntimeError):
-        _run(17, 128, 128, entry=w4a16_decode_hip)
+        _run(17, 128, 128, entry=w4a16_decode_cuda)
 
 
 def test_deterministic():
