@@ -127,6 +127,22 @@ int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block
 int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_size, char* buf,
                           int64_t buf_len);
 
+/* ldk_w4a16_matmul without a workspace argument, for callers that cannot allocate: code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc. No counterpart in the
+ * reference. The split-K partial sums go to a library-owned device array of
+ * LDK_NOALLOC_SCRATCH_BYTES per GPU (a file-scope __device__ array, held until the process ends);
+ * the call allocates nothing. Its first call on a device looks up the array's device address and
+ * clears it with one fill kernel on `stream`; the kernels leave it zero again after every call.
+ * The plan is ldk_w4a16_matmul's with a workspace of that size (every default decode plan fits);
+ * an explicit split_k whose partials do not fit returns LDK_ERR_INVALID with the bytes it needs.
+ * All calls on one GPU share the array: calls that overlap on one GPU (unordered streams) race,
+ * so order them (one stream, or events). Other arguments and results as ldk_w4a16_matmul. */
+#define LDK_NOALLOC_SCRATCH_BYTES (4u << 20)
+int ldk_w4a16_matmul_noalloc(const void* x, int64_t ldx, const int32_t* qweight,
+                             const void* scales, const void* zeros, const void* bias, void* out,
+                             int64_t ldo, int64_t M, int64_t N, int64_t K, int group_size,
+                             int block_n, int split_k, int flags, void* stream);
+
 /* Fused decode entries (M = 1, group_size 128). Each forms the activation row inside the W4A16
  * kernel's x staging instead of in a kernel of its own, one launch fewer per use. Same
  * qweight/scales/zeros/bias/out/workspace rules as ldk_w4a16_matmul.

@@ -46,6 +46,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 
 #include "ldk_common.h"
 
@@ -1437,39 +1438,111 @@ extern "C" int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_
   return plan_kernel_name(p, gsh - 3, buf, (size_t)buf_len);
 }
 
+static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                             const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                             int group_size, int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  int gsh_rows = 0;
+  int st = validate(fn, x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
+  if (st) return st;
+  if (M > 65535LL * 32) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld too large", fn, (long long)M);
+  if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_CPW_MASK))
+    return ldk::fail(LDK_ERR_INVALID, "%s: unknown flags 0x%x", fn, flags);
+  if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "%s: FACTORED and EXACT are exclusive", fn);
+  if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "%s: VALU and MFMA paths are exclusive", fn);
+  if ((flags & LDK_FACTORED) && (flags & LDK_PATH_VALU) && M > 2)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: FACTORED on the VALU kernel takes M <= 2; more rows run it on the MFMA kernel", fn);
+  if ((flags & LDK_EXACT) && (flags & LDK_PATH_MFMA))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel computes the factored form; EXACT runs on the VALU kernels (M <= 8)", fn);
+  if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the VALU kernel takes M <= 8", fn);
+  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 16, 32, 64 or 128 (MFMA)", fn, block_n);
+  if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && (M <= 2 || (flags & (LDK_EXACT | LDK_PATH_VALU))))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=128 is the MFMA kernel's tile (M > 2 or the MFMA flag)", fn);
+  if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d must be >= 0", fn, split_k);
+  if (split_k > kMaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: split_k=%d above %d", fn, split_k, kMaxSplits);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
+  const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
+  if (p.kern == kMfma && block_n && block_n != 32 && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel uses block_n 32, 64 or 128", fn);
+  if (split_k > 1 && p.splits == 1 && (K / group_size) > 1 && M <= 16) {
+    const Plan want = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, SIZE_MAX);
+    return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d needs %zu bytes of workspace for its partial sums, %lld available",
+                     fn, split_k, workspace_need(want, M, N), (long long)(workspace ? workspace_bytes : 0));
+  }
+  const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                 (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, gsh_rows};
+  return launch_plan(a, p, workspace, (hipStream_t)stream);
+}
+
 extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweight, const void* scales, const void* zeros,
                                 const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, int group_size,
                                 int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
                                 void* stream) {
-  int gsh_rows = 0;
-  int st = validate("w4a16_matmul", x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
+  return w4a16_matmul_impl("w4a16_matmul", x, ldx, qweight, scales, zeros, bias, out, ldo, M, N, K, group_size, block_n,
+                           split_k, flags, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------- allocation-free entry point
+//
+// ldk_w4a16_matmul_noalloc is ldk_w4a16_matmul with the split-K workspace taken from `scratch`, a
+// file-scope device array of LDK_NOALLOC_SCRATCH_BYTES per GPU, instead of a caller-provided
+// buffer: for callers that cannot allocate (code under graph capture that has no workspace yet,
+// tight serving loops, harnesses that forbid hipMalloc). Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in for the symbol): the first call on each device
+// looks up the device address with hipGetSymbolAddress, with that device current, clears the
+// array once with a fill kernel, and keeps the address per device. The kernels leave every
+// accumulator word and side slot they use zero again, so later calls need no clearing. Calls on
+// one GPU share its array: calls that overlap on one GPU (different streams, no ordering) race.
+namespace {
+constexpr size_t kScratchBytes = LDK_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];  // device address of `scratch` per device, set on first use
+
+__global__ void zero_fill_kernel(u32x4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// The current device's scratch address, looked up (and the array cleared on `stream`) on the
+// first call on that device.
+int current_scratch(const char* fn, hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return ldk::fail(LDK_ERR_LAUNCH, "%s: no current HIP device (or device %d >= %d)", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return ldk::fail(LDK_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                       hipGetErrorString(e));
+    if (!ldk::aligned(ptr, 256)) return ldk::fail(LDK_ERR_ALIGN, "%s: scratch is not 256-byte aligned", fn);
+    (void)hipGetLastError();
+    zero_fill_kernel<<<256, 256, 0, stream>>>(static_cast<u32x4*>(ptr), kScratchBytes / 16);
+    const int st = ldk::check_launch("w4a16_matmul_noalloc scratch clear");
+    if (st) return st;
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return LDK_OK;
+}
+}  // namespace
+
+extern "C" int ldk_w4a16_matmul_noalloc(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                                        const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M,
+                                        int64_t N, int64_t K, int group_size, int block_n, int split_k, int flags,
+                                        void* stream) {
+  static const char* fn = "w4a16_matmul_noalloc";
+  void* ws = nullptr;
+  const int st = current_scratch(fn, (hipStream_t)stream, &ws);
   if (st) return st;
-  if (M > 65535LL * 32) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: M=%lld too large", (long long)M);
-  if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_CPW_MASK))
-    return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: unknown flags 0x%x", flags);
-  if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: FACTORED and EXACT are exclusive");
-  if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: VALU and MFMA paths are exclusive");
-  if ((flags & LDK_FACTORED) && (flags & LDK_PATH_VALU) && M > 2)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: FACTORED on the VALU kernel takes M <= 2; more rows run it on the MFMA kernel");
-  if ((flags & LDK_EXACT) && (flags & LDK_PATH_MFMA))
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel computes the factored form; EXACT runs on the VALU kernels (M <= 8)");
-  if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the VALU kernel takes M <= 8");
-  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=%d must be 16, 32, 64 or 128 (MFMA)", block_n);
-  if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && (M <= 2 || (flags & (LDK_EXACT | LDK_PATH_VALU))))
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: block_n=128 is the MFMA kernel's tile (M > 2 or the MFMA flag)");
-  if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d must be >= 0", split_k);
-  if (split_k > kMaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: split_k=%d above %d", split_k, kMaxSplits);
-  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
-    return ldk::fail(LDK_ERR_ALIGN, "w4a16_matmul: workspace must be a 256-byte aligned pointer");
-  const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
-  if (p.kern == kMfma && block_n && block_n != 32 && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16_matmul: the MFMA kernel uses block_n 32, 64 or 128");
-  if (split_k > 1 && p.splits == 1 && (K / group_size) > 1 && M <= 16)
-    return ldk::fail(LDK_ERR_INVALID, "w4a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
-  const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
-                 (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, gsh_rows};
-  return launch_plan(a, p, workspace, (hipStream_t)stream);
+  return w4a16_matmul_impl(fn, x, ldx, qweight, scales, zeros, bias, out, ldo, M, N, K, group_size, block_n, split_k,
+                           flags, ws, (int64_t)kScratchBytes, stream);
 }
 
 extern "C" int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const void* scales, const void* zeros,

@@ -48,6 +48,8 @@ SIGNATURES = {
                          _vp, _i64, _vp],
     "ldk_w4a16_config": [_i64, _i64, _i64, _i32, _ip, _ip, _ip],
     "ldk_w4a16_kernel_name": [_i64, _i64, _i64, _i32, ctypes.c_char_p, _i64],
+    "ldk_w4a16_matmul_noalloc": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32,
+                                 _i32, _i32, _i32, _vp],
     "ldk_w4a16_rmsnorm_matmul": [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i32, _vp, _i64, _vp],
     "ldk_w4a16_swiglu_matmul": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _vp],
