@@ -158,8 +158,39 @@ def case_copy(reps):
         torch.neg(a, out=b)
 
 
+def case_probes(kind: str, reps: int):
+    """The roofline's calibration kernels (kernels/bench/probe.hip) at config 0's size: the packed
+    gate_up weight, 192 x 17920 int32 = 13.76 MB, in rotating copies that defeat the MALL."""
+    from kernels.bench import probes
+
+    if kind == "empty1":
+        for _ in range(reps):
+            probes.empty(1, 64)
+        return
+    if kind == "empty_grid":  # the headline kernel's grid: 800 workgroups of 384 lanes
+        for _ in range(reps):
+            probes.empty(800, 384)
+        return
+    R, N = 192, 17920
+    copies = n_copies(R * N * 4)
+    buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(N // 32 * 384, dtype=torch.int32, device="cuda")
+    for i in range(reps):
+        if kind == "stream":
+            probes.stream(buf[i % copies], sink, loads=1)
+        elif kind == "stream16":
+            probes.stream(buf[i % copies], sink, loads=16)
+        else:
+            probes.tile(buf[i % copies], sink)
+
+
 CASES = {
     "calib_neg64MiB": lambda r: case_copy(r),
+    "probe_empty_1wg": lambda r: case_probes("empty1", r),
+    "probe_empty_800wg": lambda r: case_probes("empty_grid", r),
+    "probe_stream_13.76MB": lambda r: case_probes("stream", r),
+    "probe_stream16_13.76MB": lambda r: case_probes("stream16", r),
+    "probe_tile_gate_up": lambda r: case_probes("tile", r),
     "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
     "w4a16_down_m1": lambda r: case_w4a16(1, 1536, 8960, r),
     "w4a16_gate_up_m2": lambda r: case_w4a16(2, 17920, 1536, r),
