@@ -44,7 +44,9 @@ enum ldk_flags {
   LDK_EXACT = 2,     /* W4A16: dequantize each weight to fp16 exactly as dequantize_ref first (the
                         VALU kernels, M <= 8; not with LDK_PATH_MFMA) */
   LDK_PATH_VALU = 4, /* force the wave64 VALU (dot2) skinny kernel */
-  LDK_PATH_MFMA = 8, /* force the MFMA kernel */
+  LDK_PATH_MFMA = 8, /* force the MFMA kernel (decode rows; prefill rows in 32-row blocks) */
+  LDK_PATH_GEMM = 64, /* W4A16: force the prefill GEMM (128-row tiles over all of K, exact
+                         dequantization on the matrix cores); the library's choice for many rows */
   /* W4A16 tuning: chunks of loads a wave keeps in flight per round (bits 4-5; 0 = table) */
   LDK_CPW_1 = 16,
   LDK_CPW_2 = 32,
@@ -85,16 +87,18 @@ int ldk_w4a16_dequant(const int32_t* qweight, const void* scales, const void* ze
  * it once per device, zero-filled, 256-byte aligned, and passes it to every call. It holds one
  * 64-bit fixed-point accumulator per output of a split launch and, after them, one fp32 side
  * slot per output and split for partials outside the fixed-point range (|p| >= 2^21, inf, NaN);
- * the kernels leave every word and slot zero again by the end of each launch, so it never needs
- * re-clearing (also under graph replay). Calls that share one workspace must be ordered (same
- * stream or synchronized). */
+ * the prefill GEMM's K split keeps fp32 partial tiles there. Every call leaves all of it zero
+ * again, so it never needs re-clearing (also under graph replay). Calls that share one workspace
+ * must be ordered (same stream or synchronized). */
 int64_t ldk_workspace_bytes(void);
 
 /* out [M, N] = x [M, K] @ dequant(qweight, scales, zeros)^T (+ bias [N]), fp32 accumulation,
  * fp16 output. Replaces kernels/w4a16.py:301-330 (w4a16_matmul) and its launch paths
  * w4a16.py:214-279. group_size a power of two in 32..256 dividing K; N % 4 == 0; x, qweight
- * 16-byte aligned with ldx % 8 == 0; scales, zeros 8-byte aligned. M > 16 (prefill) runs the
- * MFMA kernel in 32-row blocks without a cross-workgroup split (split_k is ignored there).
+ * 16-byte aligned with ldx % 8 == 0; scales, zeros 8-byte aligned. Prefill rows (M > 16) run
+ * the prefill GEMM (group_size >= 64; 128-row tiles over all of K, every weight dequantized as
+ * dequantize_ref does it, fp32 accumulation) or, for fewer rows, the MFMA kernel in 32-row blocks
+ * without a cross-workgroup split (split_k is ignored there).
  *   block_n: output columns per workgroup, 16/32/64 (0 = table),
  *   split_k: workgroups splitting K per column tile (0 = table; > 1 needs the workspace),
  *   flags:   LDK_FACTORED / LDK_EXACT / LDK_PATH_VALU / LDK_PATH_MFMA, LDK_CPW_* (0 = table),

@@ -49,6 +49,7 @@
 #include <mutex>
 
 #include "ldk_common.h"
+#include "prefill.h"
 
 namespace {
 
@@ -1400,7 +1401,7 @@ int plan_flags(const Plan& p) {
 
 }  // namespace
 
-extern "C" int64_t ldk_workspace_bytes(void) { return (int64_t)32 << 20; }
+extern "C" int64_t ldk_workspace_bytes(void) { return (int64_t)64 << 20; }
 
 extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n, int* split_k, int* flags) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_config: sizes must be positive");
@@ -1412,6 +1413,30 @@ extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size,
   if (split_k) *split_k = p.splits;
   if (flags) *flags = plan_flags(p);
   return LDK_OK;
+}
+
+// Rows from which the prefill GEMM (prefill.hip) may replace the MFMA kernel's 32-row blocks.
+static constexpr int64_t kGemmRows = 64;
+
+static bool gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, bool forced) {
+  return (forced || M > 16) && ldk::w4a16_gemm_supported(M, N, K, group_size, ldx) && (!out || ldk::aligned(out, 8)) &&
+         ldo % 4 == 0;
+}
+
+// The library's choice for prefill rows, from graph-timed sweeps on MI355X over the Qwen2.5-1.5B
+// shapes (M = 128 .. 2048): the 32-row blocks re-read the packed weights per block but split K over
+// the waves of a workgroup, which wins while the weights dominate and the tiles are few (qkv/o at
+// M <= 512: 8.4-15 us against 12.5-22 us); the GEMM reads them once per 128-row tile and wins on
+// wide shapes (gate_up M = 128: 26 against 34 us; M = 2048: 119 against 372 us), on long K with a
+// K split (down M = 512: 38 against 47 us) and from 1024 rows everywhere. A tuning argument that
+// names another kernel keeps it.
+static bool uses_gemm(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, int block_n,
+               int split_k, int flags) {
+  if (flags & LDK_PATH_GEMM) return true;
+  if (M <= kGemmRows || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA | LDK_EXACT | LDK_FACTORED)))
+    return false;
+  if (!(N >= 8192 || (K >= 4096 && M >= 128) || M >= 1024)) return false;
+  return gemm_applies(M, N, K, group_size, ldx, out, ldo, false);
 }
 
 // Name of the kernel instantiation launch_plan runs for a plan, as the profiler lists it.
@@ -1434,6 +1459,10 @@ extern "C" int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_
   if (M <= 0 || N <= 0 || K <= 0 || !buf || buf_len <= 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: bad arguments");
   const int gsh = log2_exact(group_size);
   if (gsh < 5 || gsh > 8 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: bad group_size %d", group_size);
+  if (uses_gemm(M, N, K, group_size, K, nullptr, N % 4 == 0 ? N : 1, 0, 0, 0)) {
+    const int n = snprintf(buf, (size_t)buf_len, "%s", ldk::w4a16_gemm_kernel_name(M, N, K, 0));
+    return n < 0 || n >= buf_len ? ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: buffer too small") : LDK_OK;
+  }
   const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
   return plan_kernel_name(p, gsh - 3, buf, (size_t)buf_len);
 }
@@ -1446,8 +1475,22 @@ static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const i
   int st = validate(fn, x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
   if (st) return st;
   if (M > 65535LL * 32) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld too large", fn, (long long)M);
-  if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_CPW_MASK))
+  if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_PATH_GEMM | LDK_CPW_MASK))
     return ldk::fail(LDK_ERR_INVALID, "%s: unknown flags 0x%x", fn, flags);
+  if (flags & LDK_PATH_GEMM) {
+    if (flags & (LDK_PATH_VALU | LDK_PATH_MFMA | LDK_FACTORED))
+      return ldk::fail(LDK_ERR_INVALID, "%s: the GEMM path excludes the VALU/MFMA paths and FACTORED", fn);
+    if (!gemm_applies(M, N, K, group_size, ldx, out, ldo, true))
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the prefill GEMM takes group_size >= 64, N %% 4 == 0 and an 8-byte "
+                       "aligned output with ldo %% 4 == 0 (M=%lld N=%lld K=%lld group_size=%d)", fn, (long long)M,
+                       (long long)N, (long long)K, group_size);
+  }
+  if (uses_gemm(M, N, K, group_size, ldx, out, ldo, block_n, split_k, flags)) {
+    const ldk::W4GemmArgs g{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                            (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, group_size,
+                            workspace, workspace ? workspace_bytes : 0, block_n, split_k};
+    return ldk::w4a16_gemm_launch(g, (hipStream_t)stream);
+  }
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "%s: FACTORED and EXACT are exclusive", fn);
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "%s: VALU and MFMA paths are exclusive", fn);
   if ((flags & LDK_FACTORED) && (flags & LDK_PATH_VALU) && M > 2)
@@ -1455,8 +1498,9 @@ static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const i
   if ((flags & LDK_EXACT) && (flags & LDK_PATH_MFMA))
     return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel computes the factored form; EXACT runs on the VALU kernels (M <= 8)", fn);
   if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the VALU kernel takes M <= 8", fn);
-  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 16, 32, 64 or 128 (MFMA)", fn, block_n);
+  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128 && !(block_n == 256 && (flags & LDK_PATH_GEMM)))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 16, 32, 64 or 128 (MFMA; 128 or 256 on the GEMM path)", fn,
+                     block_n);
   if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && (M <= 2 || (flags & (LDK_EXACT | LDK_PATH_VALU))))
     return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=128 is the MFMA kernel's tile (M > 2 or the MFMA flag)", fn);
   if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d must be >= 0", fn, split_k);

@@ -24,7 +24,7 @@ OK, ERR_INVALID, ERR_ALIGN, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3, 4
 # dtype codes (enum ldk_dtype).
 F16, BF16, F32 = 0, 1, 2
 # flags (enum ldk_flags).
-FACTORED, EXACT, PATH_VALU, PATH_MFMA = 1, 2, 4, 8
+FACTORED, EXACT, PATH_VALU, PATH_MFMA, PATH_GEMM = 1, 2, 4, 8, 64
 CPW_FLAGS = {1: 16, 2: 32, 4: 48}  # chunks of loads per wave and round (LDK_CPW_*)
 CPW_MASK = 48
 

@@ -14,13 +14,11 @@ libldk_amd.so whose tile and K-split come from the library's per-shape table:
   same factored form on the matrix cores. `config={"FACTORED": False}` (EXACT, M <= 8) instead
   dequantizes each weight exactly as dequantize_ref and accumulates with v_dot2_f32_f16.
 
-Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268): up to
-PREFILL_NATIVE_MAX_M rows run the MFMA kernel in 32-row blocks over the packed weights (each
-block decodes the weights once for its two 16-row tiles; the other blocks re-read them from the
-MALL). Measured on MI355X against dequantize-once + hipBLASLt, it is faster at every Qwen2.5-1.5B
-shape up to 256 rows and slower beyond, so more rows dequantize the weight once with the
-bit-exact HIP dequantizer and run one hipBLASLt fp16 GEMM through torch. `config={"prefill":
-"native" | "dequant"}` forces either.
+Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268): more than 64 rows
+run the prefill GEMM (csrc/prefill.hip: 128-row tiles over all of K on the matrix cores, every
+weight dequantized exactly as dequantize_ref does it, fp32 accumulation); 17-64 rows run the MFMA
+kernel in 32-row blocks. `config={"prefill": "gemm" | "blocks" | "dequant"}` forces the GEMM, the
+32-row blocks, or a one-time bit-exact dequantization followed by the library fp16 GEMM (torch).
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
 `GEMV` (force the VALU decode kernels, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
@@ -43,9 +41,7 @@ from kernels.quant import PACK, dequantize
 
 _decode_choice: dict[tuple, str] = {}  # (m_key, N, K, bias) -> chosen configuration, for export
 
-# Rows up to which the hand-written MFMA kernel (32-row blocks over the packed weights) runs;
-# more rows dequantize once and run the library fp16 GEMM.
-PREFILL_NATIVE_MAX_M = 256
+PREFILL_PATHS = ("gemm", "blocks", "native", "dequant")  # "native": the library's choice
 
 
 def _next_pow2(n: int) -> int:
@@ -101,8 +97,14 @@ def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=No
     z = zeros if zeros.is_contiguous() else zeros.contiguous()
     b = None if bias is None else bias.to(torch.float16).contiguous()
     prefill = (config or {}).get("prefill")
-    if M <= 16 or (prefill != "dequant" and (prefill == "native" or M <= PREFILL_NATIVE_MAX_M)):
+    if prefill is not None and prefill not in PREFILL_PATHS:
+        raise ValueError(f"w4a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
+    if M <= 16 or prefill != "dequant":
         block_n, split_k, flags = _flags_from_config(config, M)
+        if M > 16 and prefill == "gemm":
+            flags |= _lib.PATH_GEMM
+        elif M > 16 and prefill == "blocks":
+            flags |= _lib.PATH_MFMA
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
         key = (min(_next_pow2(M), 16), N, K, bias is not None)

@@ -288,25 +288,69 @@ def test_decode_entry(M):
 
 
 # ------------------------------------------------------------- prefill rows (M > 16)
-@pytest.mark.parametrize("M", [17, 32, 33, 100, 128, 256])
+@pytest.mark.parametrize("M", [17, 32, 33, 65, 100, 128, 256])
 @pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (17920, 1536, False),
                                       (1536, 8960, False), (96, 384, True)])
-def test_prefill_native_rows(M, N, K, bias):
-    """The MFMA kernel in 32-row blocks (the reference's prefill path, w4a16.py:264-268 and
-    tests/test_w4a16.py:93-97): row tails inside a block, bias, every Qwen width class."""
-    _run(M, N, K, bias=bias, config={"prefill": "native"})
+@pytest.mark.parametrize("path", ["blocks", "gemm"])
+def test_prefill_native_rows(M, N, K, bias, path):
+    """Prefill rows (the reference's prefill path, w4a16.py:264-268 and tests/test_w4a16.py:93-97)
+    through the MFMA kernel in 32-row blocks and through the prefill GEMM: row tails inside a
+    tile, bias, every Qwen width class."""
+    _run(M, N, K, bias=bias, config={"prefill": path})
+
+
+@pytest.mark.parametrize("M", [300, 512, 2048])
+@pytest.mark.parametrize("N,K", [(2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)])
+def test_prefill_gemm_reference_sizes(M, N, K):
+    """The library's choice for many rows (the prefill GEMM) at the reference's slow-test size
+    (M = 2048, tests/test_w4a16.py:93-97) on every Qwen2.5-1.5B linear shape, and row tails."""
+    _run(M, N, K, bias=(N == 2048))
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+def test_prefill_gemm_group_sizes(gs):
+    _run(200, 4096, 2048, gs=gs, config={"prefill": "gemm"})
+    _run(130, 17920, 1024, gs=gs, config={"prefill": "gemm"})
+
+
+def test_prefill_group_32_takes_the_blocks():
+    """The GEMM steps K by 64; group 32 keeps the 32-row blocks, still correct."""
+    _run(200, 1024, 512, gs=32)
+
+
+def test_prefill_gemm_strided_rows_and_narrow_n():
+    x, qw, s, z, _ = _make(150, 96, 768, 21)
+    wide = np.zeros((150, 1024), dtype=np.float16)
+    wide[:, 100:868] = x
+    xs = dev(wide)[:, 100:868]
+    assert xs.stride(0) == 1024
+    out = w4a16_matmul(xs, dev(qw), dev(s), dev(z), config={"prefill": "gemm"})
+    assert_north_star(out, w4a16_ref(x, qw, s, z))
+
+
+def test_prefill_gemm_one_hot_rows_reproduce_dequantized_weight():
+    """x = e_k rows through the GEMM: row m of the output is column k of dequant(W) bit for bit,
+    so each weight is dequantized exactly as dequantize_ref does it."""
+    N, K = 17920, 1536
+    _, qw, s, z, _ = _make(1, N, K, 6)
+    ks = [0, 7, 64, 130, 511, 1024, 1535, 1000, 5] * 15  # 135 rows: two row tiles, a tail
+    x = np.zeros((len(ks), K), dtype=np.float16)
+    x[np.arange(len(ks)), ks] = 1.0
+    out = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z), config={"prefill": "gemm"})
+    deq = dequantize_ref(qw, s, z)
+    assert np.array_equal(bits16(out), bits16(deq[:, ks].T))
 
 
 @pytest.mark.parametrize("gs", [32, 64, 256])
 def test_prefill_native_group_sizes(gs):
-    _run(48, 4096, 2048, gs=gs, config={"prefill": "native"})
-    _run(40, 17920, 1024, gs=gs, config={"prefill": "native"})
+    _run(48, 4096, 2048, gs=gs, config={"prefill": "blocks"})
+    _run(40, 17920, 1024, gs=gs, config={"prefill": "blocks"})
 
 
 def test_prefill_paths_agree():
-    """Above the native threshold the wrapper dequantizes once and runs the library GEMM; both
-    paths meet the bar on the same inputs."""
-    for path in ("native", "dequant"):
+    """The three prefill paths (GEMM, 32-row blocks, dequantize + library GEMM) meet the bar on
+    the same inputs."""
+    for path in ("gemm", "blocks", "native", "dequant"):
         _run(300, 2048, 1536, config={"prefill": path})
 
 
@@ -317,7 +361,7 @@ def test_prefill_one_hot_rows_reproduce_dequantized_weight():
     ks = [0, 7, 130, 511, 1024, 1535] * 6  # 36 rows, two row blocks
     x = np.zeros((len(ks), K), dtype=np.float16)
     x[np.arange(len(ks)), ks] = 1.0
-    out = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z), config={"prefill": "native"})
+    out = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z), config={"prefill": "blocks"})
     deq = dequantize_ref(qw, s, z)
     assert np.array_equal(bits16(out), bits16(deq[:, ks].T))
 
@@ -333,3 +377,17 @@ def test_deterministic():
     a = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z))
     b = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z))
     assert torch.equal(a, b)
+
+
+def test_prefill_gemm_k_split_deterministic_and_leaves_workspace_clean():
+    """Long K and few tiles (down at 512 rows) split K over workgroups; the partials are summed
+    in split order by a second launch (same bits every call), and zeroed, so a decode split-K
+    call right after sees a clean workspace."""
+    x, qw, s, z, _ = _make(512, 1536, 8960, 22)
+    args = (dev(x), dev(qw), dev(s), dev(z))
+    outs = [w4a16_matmul(*args, config={"prefill": "gemm"}) for _ in range(3)]
+    assert all(torch.equal(o, outs[0]) for o in outs[1:])
+    assert_north_star(outs[0], w4a16_ref(x, qw, s, z))
+    x1 = x[:1].copy()
+    y1 = w4a16_matmul(dev(x1), *args[1:], config={"split_k": 5})
+    assert_north_star(y1, w4a16_ref(x1, qw, s, z))
