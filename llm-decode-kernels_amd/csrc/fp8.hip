@@ -16,6 +16,7 @@
 #include <algorithm>
 
 #include "ldk_common.h"
+#include "prefill.h"
 
 namespace {
 
@@ -627,26 +628,54 @@ extern "C" int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, 
   return ldk::check_launch("fp8_dequant");
 }
 
+// Rows from which the prefill GEMM (prefill.hip) replaces the MFMA kernel's 16-row blocks. The
+// blocks re-read the e4m3 weights (twice the bytes of int4) once per 16 rows; the GEMM reads them
+// once per 64- or 128-row tile.
+static constexpr int64_t kW8GemmRows = 64;
+
+static bool w8_gemm_applies(int64_t M, int64_t N, int64_t K, int64_t ldx, const void* out, int64_t ldo) {
+  return ldk::gemm_supported(ldk::WFmt::kE4M3, M, N, K, 0, ldx) && ldk::aligned(out, 8) && ldo % 4 == 0;
+}
+
+// The library's choice: the GEMM for more than kW8GemmRows rows unless a tuning argument names
+// another kernel.
+static bool w8_uses_gemm(int64_t M, int64_t N, int64_t K, int64_t ldx, const void* out, int64_t ldo, int block_n,
+                         int split_k, int flags) {
+  if (flags & LDK_PATH_GEMM) return true;
+  if (M <= kW8GemmRows || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA))) return false;
+  return w8_gemm_applies(M, N, K, ldx, out, ldo);
+}
+
 extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias, void* out,
                                 int64_t ldo, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int flags,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
   if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: null pointer");
   if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: M, N, K must be positive");
-  if (M > 65535LL * 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld too large", (long long)M);
-  if (M > 16 && (flags & LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the VALU kernel takes M <= 16");
   if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N=%lld must be a multiple of 16", (long long)N);
   if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: K=%lld must be a multiple of 8", (long long)K);
   if (ldx < K || ldo < N) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: row stride smaller than K/N");
   if (!ldk::aligned(x, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
     return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: wq must be 16-byte aligned");
   if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N or K too large");
-  if (flags & ~(LDK_PATH_VALU | LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: flags 0x%x not supported", flags);
-  if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: VALU and MFMA paths are exclusive");
-  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: block_n=%d must be 16, 32, 64 or 128", block_n);
+  if (flags & ~(LDK_PATH_VALU | LDK_PATH_MFMA | LDK_PATH_GEMM))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: flags 0x%x not supported", flags);
+  if (!!(flags & LDK_PATH_VALU) + !!(flags & LDK_PATH_MFMA) + !!(flags & LDK_PATH_GEMM) > 1)
+    return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: the VALU, MFMA and GEMM paths are exclusive");
   if (split_k < 0 || split_k > kW8MaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: split_k=%d outside 0..%d", split_k, kW8MaxSplits);
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: workspace must be a 256-byte aligned pointer");
+  if ((flags & LDK_PATH_GEMM) && !w8_gemm_applies(M, N, K, ldx, out, ldo))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the prefill GEMM takes K %% 64 == 0 and an 8-byte aligned "
+                     "output with ldo %% 4 == 0 (M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+  if (w8_uses_gemm(M, N, K, ldx, out, ldo, block_n, split_k, flags)) {
+    const ldk::GemmArgs g{(const half_t*)x, ldx, wq, (const half_t*)scale, nullptr, (const half_t*)bias, (half_t*)out, ldo,
+                          (int)M, (int)N, (int)K, 0, workspace, workspace ? workspace_bytes : 0, block_n, split_k};
+    return ldk::gemm_launch(ldk::WFmt::kE4M3, g, (hipStream_t)stream);
+  }
+  if (M > 65535LL * 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld too large", (long long)M);
+  if (M > 16 && (flags & LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the VALU kernel takes M <= 16");
+  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: block_n=%d must be 16, 32, 64 or 128", block_n);
   // MFMA from 3 rows (the VALU kernel's fp32 FMAs grow with M; measured at M = 4: 17.4 us VALU,
   // 9.5 us MFMA at M = 8 on gate_up); block_n other than 128 keeps the
   // VALU kernel, which has the narrower tiles.

@@ -1,5 +1,6 @@
-// Internal interface of the prefill (many-row) W4A16 GEMM in prefill.hip, called by the
-// ldk_w4a16_matmul dispatch in w4a16.hip. Not part of the C ABI.
+// Internal interface of the prefill (many-row) weight-only GEMMs in prefill.hip, called by the
+// ldk_w4a16_matmul dispatch in w4a16.hip and the ldk_w8a16_matmul dispatch in fp8.hip. Not part
+// of the C ABI.
 #pragma once
 
 #include <stdint.h>
@@ -8,31 +9,38 @@
 
 namespace ldk {
 
-struct W4GemmArgs {
+// Weight formats of the prefill GEMM.
+enum class WFmt {
+  kInt4,  // packed int4 [K/8, N] int32 words, asymmetric: fp16 scales and zeros [K/group, N]
+  kE4M3,  // OCP float8 e4m3fn [K, N] bytes, one fp16 scale per output column [N]
+};
+
+struct GemmArgs {
   const half_t* x;  // [M, K] fp16, row stride ldx
   int64_t ldx;
-  const uint32_t* qw;  // packed int4 [K/8, N]
-  const half_t* s;     // scales [K/group, N]
-  const half_t* z;     // zeros [K/group, N]
+  const void* w;       // weights in the format's layout
+  const half_t* s;     // kInt4: scales [K/group, N]; kE4M3: column scales [N]
+  const half_t* z;     // kInt4: zeros [K/group, N]; kE4M3: unused
   const half_t* bias;  // [N] or null
   half_t* out;         // [M, N] fp16, row stride ldo
   int64_t ldo;
   int M, N, K;
-  int group_size;    // a power of two >= 64 dividing K
+  int group_size;    // kInt4: a power of two >= 64 dividing K
   void* workspace;   // fp32 partial tiles of a K split (may be null: no split)
   int64_t workspace_bytes;
   int block_n;       // output-tile width 128 or 256 (0: the library's choice)
   int split_k;       // workgroups splitting K per tile (0: the library's choice)
 };
 
-// Whether the prefill GEMM takes this shape (group_size >= 64, K a multiple of 64, N a multiple
-// of 8, sizes within its indexing), and launches it (with a K split over workgroups when the
-// shape gives too few tiles and the workspace holds the partials; a second launch then sums them
-// in split order). Both leave the last-error message on failure.
-bool w4a16_gemm_supported(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx);
-int w4a16_gemm_launch(const W4GemmArgs& a, hipStream_t stream);
+// Whether the prefill GEMM takes this shape (K a multiple of 64; kInt4: group_size >= 64, N a
+// multiple of 8; kE4M3: N a multiple of 16; sizes within its 32-bit buffer offsets), and launches
+// it (with a K split over workgroups when the shape's K is long and the workspace holds the
+// partials; a second launch then sums them in split order). Both leave the last-error message on
+// failure.
+bool gemm_supported(WFmt f, int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx);
+int gemm_launch(WFmt f, const GemmArgs& a, hipStream_t stream);
 
-// Name of the kernel instantiation w4a16_gemm_launch runs for a shape (for reports).
-const char* w4a16_gemm_kernel_name(int64_t M, int64_t N, int64_t K, int block_n);
+// Name of the kernel instantiation gemm_launch runs for a shape (for reports).
+const char* gemm_kernel_name(WFmt f, int64_t M, int64_t N, int64_t K, int block_n);
 
 }  // namespace ldk

@@ -1419,23 +1419,24 @@ extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size,
 static constexpr int64_t kGemmRows = 64;
 
 static bool gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, bool forced) {
-  return (forced || M > 16) && ldk::w4a16_gemm_supported(M, N, K, group_size, ldx) && (!out || ldk::aligned(out, 8)) &&
+  return (forced || M > 16) && ldk::gemm_supported(ldk::WFmt::kInt4, M, N, K, group_size, ldx) && (!out || ldk::aligned(out, 8)) &&
          ldo % 4 == 0;
 }
 
 // The library's choice for prefill rows, from graph-timed sweeps on MI355X over the Qwen2.5-1.5B
-// shapes (M = 128 .. 2048): the 32-row blocks re-read the packed weights per block but split K over
+// shapes (M = 65 .. 2048): the 32-row blocks re-read the packed weights per block but split K over
 // the waves of a workgroup, which wins while the weights dominate and the tiles are few (qkv/o at
-// M <= 512: 8.4-15 us against 12.5-22 us); the GEMM reads them once per 128-row tile and wins on
-// wide shapes (gate_up M = 128: 26 against 34 us; M = 2048: 119 against 372 us), on long K with a
-// K split (down M = 512: 38 against 47 us) and from 1024 rows everywhere. A tuning argument that
-// names another kernel keeps it.
+// M <= 256: 8.0-8.5 us against 12.4 us; down at M = 256: 25.7 against 31.1 us); the GEMM reads
+// them once per 64/128-row tile and wins on wide shapes at every row count (gate_up M = 65: 18.4
+// against 22.2 us; M = 2048: 116 against 364 us) and on every shape from 512 rows (qkv M = 512:
+// 12.6 against 15.1 us; down M = 512: 34.8 against 47.5 us). A tuning argument that names another
+// kernel keeps it.
 static bool uses_gemm(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, int block_n,
                int split_k, int flags) {
   if (flags & LDK_PATH_GEMM) return true;
   if (M <= kGemmRows || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA | LDK_EXACT | LDK_FACTORED)))
     return false;
-  if (!(N >= 8192 || (K >= 4096 && M >= 128) || M >= 1024)) return false;
+  if (!(N >= 8192 || M >= 512)) return false;
   return gemm_applies(M, N, K, group_size, ldx, out, ldo, false);
 }
 
@@ -1460,7 +1461,7 @@ extern "C" int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_
   const int gsh = log2_exact(group_size);
   if (gsh < 5 || gsh > 8 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: bad group_size %d", group_size);
   if (uses_gemm(M, N, K, group_size, K, nullptr, N % 4 == 0 ? N : 1, 0, 0, 0)) {
-    const int n = snprintf(buf, (size_t)buf_len, "%s", ldk::w4a16_gemm_kernel_name(M, N, K, 0));
+    const int n = snprintf(buf, (size_t)buf_len, "%s", ldk::gemm_kernel_name(ldk::WFmt::kInt4, M, N, K, 0));
     return n < 0 || n >= buf_len ? ldk::fail(LDK_ERR_INVALID, "w4a16_kernel_name: buffer too small") : LDK_OK;
   }
   const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
@@ -1486,10 +1487,10 @@ static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const i
                        (long long)N, (long long)K, group_size);
   }
   if (uses_gemm(M, N, K, group_size, ldx, out, ldo, block_n, split_k, flags)) {
-    const ldk::W4GemmArgs g{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
-                            (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, group_size,
-                            workspace, workspace ? workspace_bytes : 0, block_n, split_k};
-    return ldk::w4a16_gemm_launch(g, (hipStream_t)stream);
+    const ldk::GemmArgs g{(const half_t*)x, ldx, qweight, (const half_t*)scales, (const half_t*)zeros,
+                          (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, group_size,
+                          workspace, workspace ? workspace_bytes : 0, block_n, split_k};
+    return ldk::gemm_launch(ldk::WFmt::kInt4, g, (hipStream_t)stream);
   }
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "%s: FACTORED and EXACT are exclusive", fn);
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "%s: VALU and MFMA paths are exclusive", fn);

@@ -7,9 +7,11 @@ the K reduction (fp8.py:120). Quantize/dequantize run HIP kernels that reproduce
 bit for bit; like the reference's torch code they take CPU tensors too (run on the current ROCm
 GPU, results returned on the CPU). Decode shapes run the wave64 VALU GEMV with an in-workgroup split-K at M <= 2 and
 the MFMA kernel (in-register byte transpose, exact e4m3 -> fp16) from 3 rows.
-Prefill rows (M > 16) run the MFMA kernel in 16-row blocks up to PREFILL_NATIVE_MAX_M rows
-(`config={"prefill": "native" | "dequant"}` forces a path); more rows dequantize once and run a
-torch fp16 GEMM.
+Prefill rows (the reference's tensor-core GEMM, fp8.py:42-91 run at fp8.py:221-222) run
+hand-written kernels at every row count: 17-64 rows the MFMA kernel in 16-row blocks, more rows
+the prefill GEMM (csrc/prefill.hip: 64/128-row tiles, e4m3 tiles transposed and converted to fp16
+in registers, column scale after the K loop, K split over workgroups for long K).
+`config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
 """
 
 from __future__ import annotations
@@ -51,9 +53,7 @@ def dequantize_fp8(wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return out.to(home)
 
 
-# Rows up to which the MFMA kernel (16-row blocks over the e4m3 weights) runs; more rows
-# dequantize once and run the library fp16 GEMM.
-PREFILL_NATIVE_MAX_M = 256
+PREFILL_PATHS = ("gemm", "blocks", "native")  # "native": the library's choice
 
 
 def fp8_bytes(N: int, K: int) -> int:
@@ -64,7 +64,8 @@ def fp8_bytes(N: int, K: int) -> int:
 def w8a16_matmul(x, wq, scale, bias=None, config=None):
     """y = x @ (wq * scale).T (+ bias). x: [..., K] fp16, wq: float8 [K, N], scale: fp16 [N]
     (fp8.py:200-223). `config` honours `GEMV` (force the VALU kernel), `MFMA` (force the MFMA
-    kernel), `block_n` and `split_k`; Triton tile keys are ignored."""
+    kernel), `prefill` (see PREFILL_PATHS), `block_n` and `split_k`; Triton tile keys are
+    ignored."""
     K = x.shape[-1]
     N = wq.shape[1]
     assert wq.shape[0] == K
@@ -80,18 +81,19 @@ def w8a16_matmul(x, wq, scale, bias=None, config=None):
     b = None if bias is None else bias.to(torch.float16).contiguous()
     cfg = config or {}
     prefill = cfg.get("prefill")
-    if M <= 16 or (prefill != "dequant" and (prefill == "native" or M <= PREFILL_NATIVE_MAX_M)):
-        flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
-        if cfg.get("MFMA"):
-            flags |= _lib.PATH_MFMA
-        out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        with _lib.device_guard(dev):
-            ws, ws_bytes = _lib.workspace(dev)
-            st = _lib.load().ldk_w8a16_matmul(
-                _lib.ptr(x2), x2.stride(0), _lib.ptr(q), _lib.ptr(s), _lib.ptr(b), _lib.ptr(out),
-                out.stride(0), M, N, K, int(cfg.get("block_n", 0)), int(cfg.get("split_k", 0)),
-                flags, ws, ws_bytes, _lib.stream(dev))
-        _lib.check(st, "w8a16_matmul")
-    else:
-        out = torch.nn.functional.linear(x2, dequantize_fp8(q, s), b)
+    if prefill is not None and prefill not in PREFILL_PATHS:
+        raise ValueError(f"w8a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
+    flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
+    if cfg.get("MFMA") or (M > 16 and prefill == "blocks"):
+        flags |= _lib.PATH_MFMA
+    elif M > 16 and prefill == "gemm":
+        flags |= _lib.PATH_GEMM
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w8a16_matmul(
+            _lib.ptr(x2), x2.stride(0), _lib.ptr(q), _lib.ptr(s), _lib.ptr(b), _lib.ptr(out),
+            out.stride(0), M, N, K, int(cfg.get("block_n", 0)), int(cfg.get("split_k", 0)),
+            flags, ws, ws_bytes, _lib.stream(dev))
+    _lib.check(st, "w8a16_matmul")
     return out.view(*x.shape[:-1], N)

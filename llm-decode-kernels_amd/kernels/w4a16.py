@@ -14,11 +14,12 @@ libldk_amd.so whose tile and K-split come from the library's per-shape table:
   same factored form on the matrix cores. `config={"FACTORED": False}` (EXACT, M <= 8) instead
   dequantizes each weight exactly as dequantize_ref and accumulates with v_dot2_f32_f16.
 
-Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268): more than 64 rows
-run the prefill GEMM (csrc/prefill.hip: 128-row tiles over all of K on the matrix cores, every
-weight dequantized exactly as dequantize_ref does it, fp32 accumulation); 17-64 rows run the MFMA
-kernel in 32-row blocks. `config={"prefill": "gemm" | "blocks" | "dequant"}` forces the GEMM, the
-32-row blocks, or a one-time bit-exact dequantization followed by the library fp16 GEMM (torch).
+Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268) run hand-written
+kernels at every row count: the library picks, per shape, the prefill GEMM (csrc/prefill.hip:
+64/128-row tiles on the matrix cores, every weight dequantized exactly as dequantize_ref does it,
+fp32 accumulation, K split over workgroups for long K) or the MFMA kernel in 32-row blocks (the
+choice for 17-64 rows and for narrow shapes up to 512 rows, where the blocks' K split over waves
+wins). `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
 `GEMV` (force the VALU decode kernels, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
@@ -37,11 +38,11 @@ import ctypes
 import torch
 
 from kernels import _lib
-from kernels.quant import PACK, dequantize
+from kernels.quant import PACK
 
 _decode_choice: dict[tuple, str] = {}  # (m_key, N, K, bias) -> chosen configuration, for export
 
-PREFILL_PATHS = ("gemm", "blocks", "native", "dequant")  # "native": the library's choice
+PREFILL_PATHS = ("gemm", "blocks", "native")  # "native": the library's choice
 
 
 def _next_pow2(n: int) -> int:
@@ -99,20 +100,16 @@ def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=No
     prefill = (config or {}).get("prefill")
     if prefill is not None and prefill not in PREFILL_PATHS:
         raise ValueError(f"w4a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
-    if M <= 16 or prefill != "dequant":
-        block_n, split_k, flags = _flags_from_config(config, M)
-        if M > 16 and prefill == "gemm":
-            flags |= _lib.PATH_GEMM
-        elif M > 16 and prefill == "blocks":
-            flags |= _lib.PATH_MFMA
-        out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
-        key = (min(_next_pow2(M), 16), N, K, bias is not None)
-        if M <= 16 and key not in _decode_choice:
-            _decode_choice[key] = config_for(M, N, K, group_size)
-    else:
-        w = dequantize(qw, s, z, group_size)
-        out = torch.nn.functional.linear(x2, w, b)
+    block_n, split_k, flags = _flags_from_config(config, M)
+    if M > 16 and prefill == "gemm":
+        flags |= _lib.PATH_GEMM
+    elif M > 16 and prefill == "blocks":
+        flags |= _lib.PATH_MFMA
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
+    key = (min(_next_pow2(M), 16), N, K, bias is not None)
+    if M <= 16 and key not in _decode_choice:
+        _decode_choice[key] = config_for(M, N, K, group_size)
     return out.view(*x.shape[:-1], N)
 
 

@@ -119,8 +119,99 @@ def test_reference_rows(M):
 
 
 def test_prefill_paths_agree():
-    for path in ("native", "dequant"):
+    """The prefill paths (GEMM, 16-row blocks, the library's choice) meet the bar on the same
+    inputs, and an unknown path name is rejected."""
+    for path in ("gemm", "blocks", "native"):
         _run(300, 2048, 1536, config={"prefill": path})
+    with pytest.raises(ValueError, match="prefill"):
+        _run(300, 2048, 1536, config={"prefill": "dequant"})
+
+
+# ---------------------------------------------------- prefill GEMM (csrc/prefill.hip, e4m3)
+@pytest.mark.parametrize("M", [17, 65, 100, 128, 256])
+@pytest.mark.parametrize("N,K,bias", [(2048, 1536, True), (17920, 1536, False),
+                                      (1536, 8960, False), (96, 384, True)])
+def test_prefill_gemm_rows(M, N, K, bias):
+    """The GEMM forced at prefill row counts: row tails inside a 64/128-row tile, bias, a column
+    tile past N (N = 96), long K with a K split (down)."""
+    _run(M, N, K, bias=bias, config={"prefill": "gemm"})
+
+
+@pytest.mark.parametrize("M", [300, 512, 2048])
+@pytest.mark.parametrize("N,K", [(2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)])
+def test_prefill_reference_sizes(M, N, K):
+    """The library's choice for many rows at the reference's slow-test sizes (M = 512 and 2048,
+    tests/test_fp8.py) on every Qwen2.5-1.5B linear shape."""
+    _run(M, N, K, bias=(N == 2048))
+
+
+@pytest.mark.parametrize("block_n,split_k", [(128, 0), (256, 0), (0, 3), (256, 5)])
+def test_prefill_gemm_tile_and_split_arguments(block_n, split_k):
+    _run(300, 1536, 8960, config={"prefill": "gemm", "block_n": block_n, "split_k": split_k})
+    _run(130, 2048, 1536, bias=True, config={"prefill": "gemm", "block_n": block_n, "split_k": split_k})
+
+
+def test_prefill_gemm_one_hot_rows_exact():
+    """x row m = e_k with unit scales through the GEMM: y[m, n] = e4m3(wq[k, n]) exactly, so the
+    LDS row permutation, the byte transpose and the fp8 -> fp16 conversion are checked bit for
+    bit on every finite code, for K rows in every position of a 64-row step."""
+    K, N = 1536, 2048
+    g = torch.Generator().manual_seed(8)
+    codes = torch.randint(0, 256, (K, N), generator=g, dtype=torch.int64).to(torch.uint8).numpy()
+    codes[(codes & 0x7F) == 0x7F] = 0
+    ks = list(range(0, 64)) + [64 * 7 + 3, 1000, 1535, 777, 1024]  # 69 rows: a row tail
+    x = np.zeros((len(ks), K), dtype=np.float16)
+    x[np.arange(len(ks)), ks] = 1.0
+    out = w8a16_matmul(dev(x), dev(codes).view(FP8), torch.ones(N, dtype=torch.float16, device="cuda"),
+                       config={"prefill": "gemm"})
+    ref = of.e4m3_decode(codes[ks]).astype(np.float16)
+    got = to_np(out)
+    nz = ref != 0
+    assert np.array_equal(bits16(got)[nz], bits16(ref)[nz])
+    assert np.all(got[~nz] == 0)
+
+
+def test_prefill_gemm_two_k_groups_odd_steps():
+    """Two K groups in a workgroup over 33 K-steps of 64 (17 and 16: the second group takes one
+    barrier-only step), a partial last column tile (N = 1008), row tails."""
+    _run(300, 1008, 2112, config={"prefill": "gemm"})
+    _run(2048, 1008, 2112, bias=True, config={"prefill": "gemm"})
+
+
+def test_prefill_gemm_strided_rows():
+    w, x = cases.w4a16_case(150, 1536, 768, 21)
+    owq, os_ = of.quantize_fp8(w.numpy())
+    wide = torch.zeros(150, 1024, dtype=torch.float16)
+    wide[:, 100:868] = x
+    xs = wide.cuda()[:, 100:868]
+    assert xs.stride(0) == 1024
+    out = w8a16_matmul(xs, dev(owq).view(FP8), dev(os_), config={"prefill": "gemm"})
+    assert_north_star(out, of.w8a16_ref(x.numpy(), owq, os_, None))
+
+
+def test_prefill_gemm_k_split_deterministic_and_leaves_workspace_clean():
+    """Long K (down at 512 rows) splits K over workgroups; the partials are summed in split order
+    (same bits every call) and zeroed, so a decode split-K call right after sees a clean
+    workspace."""
+    w, x = cases.w4a16_case(512, 1536, 8960, 22)
+    owq, os_ = of.quantize_fp8(w.numpy())
+    args = (x.cuda(), dev(owq).view(FP8), dev(os_))
+    outs = [w8a16_matmul(*args, config={"prefill": "gemm"}) for _ in range(3)]
+    assert all(torch.equal(o, outs[0]) for o in outs[1:])
+    assert_north_star(outs[0], of.w8a16_ref(x.numpy(), owq, os_, None))
+    x1 = x[:1].contiguous()
+    y1 = w8a16_matmul(x1.cuda(), *args[1:], config={"split_k": 5})
+    assert_north_star(y1, of.w8a16_ref(x1.numpy(), owq, os_, None))
+
+
+def test_prefill_gemm_rejects_k_not_multiple_of_64():
+    """K = 96 has no whole 64-deep step: forcing the GEMM is an error, the library's choice
+    keeps the 16-row blocks."""
+    w, x = cases.w4a16_case(100, 48, 96, 4)
+    owq, os_ = of.quantize_fp8(w.numpy())
+    with pytest.raises(RuntimeError, match="prefill GEMM"):
+        w8a16_matmul(x.cuda(), dev(owq).view(FP8), dev(os_), config={"prefill": "gemm"})
+    _run(100, 48, 96)
 
 
 def test_mfma_one_hot_rows_exact():

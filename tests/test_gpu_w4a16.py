@@ -328,6 +328,14 @@ def test_prefill_gemm_strided_rows_and_narrow_n():
     assert_north_star(out, w4a16_ref(x, qw, s, z))
 
 
+def test_prefill_gemm_two_k_groups_odd_steps():
+    """Two K groups in a workgroup over 33 K-steps of 64 (17 and 16: the second group takes one
+    barrier-only step), a partial last column tile (N = 1000), row tails, on one and two column
+    groups (M = 300 and 2048)."""
+    _run(300, 1000, 2112, gs=64, config={"prefill": "gemm"})
+    _run(2048, 1000, 2112, gs=64, bias=True, config={"prefill": "gemm"})
+
+
 def test_prefill_gemm_one_hot_rows_reproduce_dequantized_weight():
     """x = e_k rows through the GEMM: row m of the output is column k of dequant(W) bit for bit,
     so each weight is dequantized exactly as dequantize_ref does it."""
@@ -348,10 +356,19 @@ def test_prefill_native_group_sizes(gs):
 
 
 def test_prefill_paths_agree():
-    """The three prefill paths (GEMM, 32-row blocks, dequantize + library GEMM) meet the bar on
-    the same inputs."""
-    for path in ("gemm", "blocks", "native", "dequant"):
+    """The prefill paths (GEMM, 32-row blocks, the library's choice) meet the bar on the same
+    inputs, and an unknown path name is rejected."""
+    for path in ("gemm", "blocks", "native"):
         _run(300, 2048, 1536, config={"prefill": path})
+    with pytest.raises(ValueError, match="prefill"):
+        _run(300, 2048, 1536, config={"prefill": "dequant"})
+
+
+@pytest.mark.parametrize("block_n,split_k", [(128, 0), (256, 0), (0, 3), (256, 5)])
+def test_prefill_gemm_tile_and_split_arguments(block_n, split_k):
+    """block_n and split_k pick the GEMM's tile and K split when the GEMM is forced."""
+    _run(300, 1536, 8960, config={"prefill": "gemm", "block_n": block_n, "split_k": split_k})
+    _run(130, 2048, 1536, bias=True, config={"prefill": "gemm", "block_n": block_n, "split_k": split_k})
 
 
 def test_prefill_one_hot_rows_reproduce_dequantized_weight():
