@@ -7,9 +7,29 @@
 //   swiglu:  out = fp16(g * rcp(1 + exp(-g))) * u     (silu in fp32 with the hardware reciprocal,
 //            1 ulp, as the reference's Triton kernel divides approximately; fp16 multiply)
 // Both are pure streaming kernels: every element is read once and written once, 16 bytes per lane.
+// Many-row calls read and write with the non-temporal cache policy (STREAM): measured on MI355X in
+// graph replays over rotating buffers, RMSNorm+residual at M = 2048, N = 1536 takes 5.70 us with it
+// against 7.27 us without (55% against 43% of 8 TB/s), SwiGLU at M = 2048, I = 8960 19.9 against
+// 21.7 us and at M = 16 2.34 against 2.71 us. At a few rows the plain policy is as fast or faster
+// (RMSNorm M = 16: 2.31 against 2.41 us), and a decode step's next kernel reads the output at once.
 #include "ldk_common.h"
 
 namespace {
+
+template <bool STREAM, typename T>
+__device__ __forceinline__ T load_v(const T* p) {
+  if constexpr (STREAM) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool STREAM, typename T>
+__device__ __forceinline__ void store_v(T v, T* p) {
+  if constexpr (STREAM) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// Rows from which RMSNorm streams with the non-temporal policy; SwiGLU from kSwigluNtRows rows.
+constexpr int64_t kRmsNtRows = 256;
+constexpr int64_t kSwigluNtRows = 16;
 
 struct RmsArgs {
   const half_t* x;
@@ -27,7 +47,7 @@ struct RmsArgs {
 
 // One workgroup per row; each thread keeps CPT chunks of VEC halves in registers between the
 // sum-of-squares pass and the normalize pass, so the row is read from memory once.
-template <int VEC, int CPT, bool RES>
+template <int VEC, int CPT, bool RES, bool STREAM>
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
   typedef _Float16 hv_t __attribute__((ext_vector_type(VEC)));
   __shared__ float wsum[16];
@@ -46,10 +66,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + i * NT;
     if (c < nchunk) {
-      hv_t v = *reinterpret_cast<const hv_t*>(x + c * VEC);
+      hv_t v = load_v<STREAM>(reinterpret_cast<const hv_t*>(x + c * VEC));
       if constexpr (RES) {
-        v = v + *reinterpret_cast<const hv_t*>(a.r + (int64_t)row * a.ldr + c * VEC);  // fp16 add
-        *reinterpret_cast<hv_t*>(a.res_out + (int64_t)row * a.ldro + c * VEC) = v;
+        v = v + load_v<STREAM>(reinterpret_cast<const hv_t*>(a.r + (int64_t)row * a.ldr + c * VEC));  // fp16 add
+        store_v<STREAM>(v, reinterpret_cast<hv_t*>(a.res_out + (int64_t)row * a.ldro + c * VEC));
       }
       h[i] = v;
 #pragma unroll
@@ -77,7 +97,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(RmsArgs a) {
         asm volatile("" : "+v"(v));  // a -0 * rs must stay -0 (no v_fma_mix with a +0 addend)
         o[j] = (half_t)v;
       }
-      *reinterpret_cast<hv_t*>(a.out + (int64_t)row * a.ldo + c * VEC) = wv[i] * o;  // fp16 multiply
+      store_v<STREAM>(wv[i] * o, reinterpret_cast<hv_t*>(a.out + (int64_t)row * a.ldo + c * VEC));  // fp16 multiply
     }
   }
 }
@@ -93,37 +113,42 @@ struct SwigluArgs {
 };
 
 // One thread per VEC consecutive outputs of one row.
-template <int VEC>
+template <int VEC, bool STREAM>
 __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
   typedef _Float16 hv_t __attribute__((ext_vector_type(VEC)));
   const int64_t per_row = a.I / VEC;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= a.M * per_row) return;
   const int64_t row = i / per_row, c = (i - row * per_row) * VEC;
-  const hv_t g = *reinterpret_cast<const hv_t*>(a.g + row * a.ldg + c);
-  const hv_t u = *reinterpret_cast<const hv_t*>(a.u + row * a.ldu + c);
+  const hv_t g = load_v<STREAM>(reinterpret_cast<const hv_t*>(a.g + row * a.ldg + c));
+  const hv_t u = load_v<STREAM>(reinterpret_cast<const hv_t*>(a.u + row * a.ldu + c));
   hv_t s;
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
     const float f = (float)g[j];
     s[j] = (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
   }
-  *reinterpret_cast<hv_t*>(a.out + row * a.ldo + c) = s * u;  // fp16 multiply
+  store_v<STREAM>(s * u, reinterpret_cast<hv_t*>(a.out + row * a.ldo + c));  // fp16 multiply
 }
 
-template <int VEC, bool RES>
-int launch_rms(const RmsArgs& a, hipStream_t s) {
+template <int VEC, bool RES, bool STREAM>
+int launch_rms_nt(const RmsArgs& a, hipStream_t s) {
   const int nchunk = a.N / VEC;
   int nt = ((nchunk + 63) / 64) * 64;
   if (nt > 1024) nt = 1024;
   const int cpt = (nchunk + nt - 1) / nt;
   (void)hipGetLastError();
-  if (cpt <= 1) rmsnorm_kernel<VEC, 1, RES><<<a.M, nt, 0, s>>>(a);
-  else if (cpt <= 2) rmsnorm_kernel<VEC, 2, RES><<<a.M, nt, 0, s>>>(a);
-  else if (cpt <= 4) rmsnorm_kernel<VEC, 4, RES><<<a.M, nt, 0, s>>>(a);
-  else if (cpt <= 8) rmsnorm_kernel<VEC, 8, RES><<<a.M, nt, 0, s>>>(a);
+  if (cpt <= 1) rmsnorm_kernel<VEC, 1, RES, STREAM><<<a.M, nt, 0, s>>>(a);
+  else if (cpt <= 2) rmsnorm_kernel<VEC, 2, RES, STREAM><<<a.M, nt, 0, s>>>(a);
+  else if (cpt <= 4) rmsnorm_kernel<VEC, 4, RES, STREAM><<<a.M, nt, 0, s>>>(a);
+  else if (cpt <= 8) rmsnorm_kernel<VEC, 8, RES, STREAM><<<a.M, nt, 0, s>>>(a);
   else return ldk::fail(LDK_ERR_UNSUPPORTED, "rmsnorm: N=%d too large", a.N);
   return ldk::check_launch("rmsnorm");
+}
+
+template <int VEC, bool RES>
+int launch_rms(const RmsArgs& a, hipStream_t s) {
+  return a.M >= kRmsNtRows ? launch_rms_nt<VEC, RES, true>(a, s) : launch_rms_nt<VEC, RES, false>(a, s);
 }
 
 }  // namespace
@@ -155,7 +180,12 @@ extern "C" int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t
   const int64_t n = M * (vec ? I / 8 : I);
   if ((n + 255) / 256 > INT32_MAX) return ldk::fail(LDK_ERR_UNSUPPORTED, "swiglu: too large");
   (void)hipGetLastError();
-  if (vec) swiglu_kernel<8><<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(a);
-  else swiglu_kernel<1><<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(a);
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  hipStream_t s = (hipStream_t)stream;
+  const bool nt = M >= kSwigluNtRows;
+  if (vec && nt) swiglu_kernel<8, true><<<grid, 256, 0, s>>>(a);
+  else if (vec) swiglu_kernel<8, false><<<grid, 256, 0, s>>>(a);
+  else if (nt) swiglu_kernel<1, true><<<grid, 256, 0, s>>>(a);
+  else swiglu_kernel<1, false><<<grid, 256, 0, s>>>(a);
   return ldk::check_launch("swiglu");
 }

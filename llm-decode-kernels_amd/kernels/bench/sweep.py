@@ -6,25 +6,34 @@ kernels/bench/sweep.py case generators, lines 139-207, re-done for this build):
 - config 2: W4A16 over the six Qwen2.5-1.5B linear shapes at M in {1, 4, 16}, seed 2;
 - config 3: W8A16 (OCP e4m3) over the same shapes at M in {1, 4, 8, 16}, seed 3.
 
+- prefill: the W4A16 and W8A16 prefill GEMMs over the Qwen2.5-1.5B projections (qkv fused,
+  o, gate_up, down) at M in {512, 2048} (the reference's slow-test rows), as TFLOP/s against the
+  2.5 PFLOP/s dense fp16 MFMA peak.
+
 Every case is timed with `harness.GraphTimer` (rotating input sets sized to 4x the 256 MB MALL,
 one launch per set in one hipGraph, median of 7 samples) and reported as us, GB/s and % of the
 8 TB/s HBM peak with the reference's algorithmic byte formulas. Each row also records the
-kernel configuration the library chose.
+kernel configuration the library chose. The whole sweep runs `--sweeps` times (3 by default)
+and each row reports the median over the sweeps, their min and max, and a flag when the spread
+(max - min) / median exceeds 10% (the reference's aggregation, kernels/bench/sweep.py:229-254).
 
-    python -m kernels.bench.sweep [--only w4a16,fp8,norm,act,fused] [--json out.json]
+    python -m kernels.bench.sweep [--only w4a16,fp8,norm,act,fused,prefill] [--sweeps 3] [--json out.json]
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import statistics
 import sys
 
 import torch
 
 from kernels.bench import cases
 from kernels.bench.harness import GraphTimer, n_copies, tensor_bytes
-from kernels.config import PEAK_GBPS
+from kernels.config import GPU_SPECS, PEAK_GBPS
+
+PEAK_FP16_TFLOPS = GPU_SPECS["MI355X"]["peak_fp16_tflops"]
 
 GS = 128
 
@@ -165,25 +174,98 @@ def fused_rows():
     return rows
 
 
+PREFILL_SHAPES = [("qkv", 2048, 1536), ("o", 1536, 1536), ("gate_up", 17920, 1536), ("down", 1536, 8960)]
+
+
+def _flops_extra(M, N, K, ms) -> dict:
+    tflops = 2 * M * N * K / (ms * 1e-3) / 1e12
+    return {"flops": 2 * M * N * K, "tflops": round(tflops, 1),
+            "pct_mfma": round(100 * tflops / PEAK_FP16_TFLOPS, 2)}
+
+
+def prefill_rows(Ms=(512, 2048)):
+    """The prefill GEMMs (the library's choice for these rows) at the reference's slow-test row
+    counts; bytes are the weights, x and y once each."""
+    from kernels.fp8 import fp8_bytes, quantize_fp8, w8a16_matmul
+    from kernels.quant import quantize_rtn, weight_bytes
+    from kernels.w4a16 import kernel_name, w4a16_matmul
+
+    rows = []
+    for name, N, K in PREFILL_SHAPES:
+        w, _ = cases.w4a16_case(1, N, K, seed=2)
+        qw, s, z = quantize_rtn(w.cuda(), GS)
+        wq, sc = quantize_fp8(w.cuda())
+        for M in Ms:
+            x = cases.activations(M, K, cases.gen(2)).cuda()
+            sets = [(x.clone(), qw.clone(), s.clone(), z.clone())
+                    for _ in range(n_copies(tensor_bytes((x, qw, s, z)) + 2 * M * N))]
+            ms = _time(lambda xx, q, ss, zz: w4a16_matmul(xx, q, ss, zz, GS), sets)
+            extra = {"config": kernel_name(M, N, K, GS), **_flops_extra(M, N, K, ms)}
+            rows.append(_row("w4a16 gemm", f"{name} {N}x{K}", M, ms,
+                             weight_bytes(N, K, GS) + 2 * M * K + 2 * M * N, extra))
+            sets = [(x.clone(), wq.clone(), sc.clone())
+                    for _ in range(n_copies(tensor_bytes((x, wq, sc)) + 2 * M * N))]
+            ms = _time(lambda xx, q, ss: w8a16_matmul(xx, q, ss), sets)
+            rows.append(_row("w8a16 gemm", f"{name} {N}x{K}", M, ms,
+                             fp8_bytes(N, K) + 2 * M * K + 2 * M * N, _flops_extra(M, N, K, ms)))
+            del sets
+    return rows
+
+
 SECTIONS = {"w4a16": w4a16_rows, "fp8": fp8_rows, "norm": norm_rows, "act": act_rows,
-            "fused": fused_rows}
+            "fused": fused_rows, "prefill": prefill_rows}
+
+
+def aggregate(sweeps: list[list[dict]]) -> list[dict]:
+    """Median over sweeps per row (every sweep lists the same cases in the same order), with the
+    min, max and a >10% spread flag (kernels/bench/sweep.py:229-254 of the reference)."""
+    out = []
+    for rs in zip(*sweeps):
+        us = [r["us"] for r in rs]
+        med = statistics.median(us)
+        row = _row(rs[0]["kernel"], rs[0]["shape"], rs[0]["M"], med * 1e-3, rs[0]["bytes"])
+        for k in ("config", "flops"):
+            if k in rs[0]:
+                row[k] = rs[0][k]
+        if "flops" in row:
+            row.update(_flops_extra(1, row["flops"] // 2, 1, med * 1e-3))
+        spread = 100 * (max(us) - min(us)) / med
+        row.update({"sweeps": len(us), "us_min": min(us), "us_max": max(us),
+                    "spread_pct": round(spread, 2), "flag_spread": spread > 10})
+        out.append(row)
+    return out
+
+
+def _line(r) -> str:
+    t = f"  {r['tflops']:7.1f} TFLOP/s {r['pct_mfma']:5.2f}%" if "tflops" in r else ""
+    agg = f"  [{r['us_min']:.3f}-{r['us_max']:.3f}{' SPREAD' if r['flag_spread'] else ''}]" if "sweeps" in r else ""
+    return (f"{r['kernel']:12s} {r['shape']:22s} M={r['M']:<5d} {r['us']:9.3f} us "
+            f"{r['gbps']:8.1f} GB/s {r['pct_peak']:6.2f}%{t}{agg}  {r.get('config', '')}")
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", default="w4a16,fp8,norm,act")
+    ap.add_argument("--sweeps", type=int, default=3)
     ap.add_argument("--json", default=None)
     args = ap.parse_args(argv)
     torch.cuda.init()
-    rows = []
-    for sec in args.only.split(","):
-        for r in SECTIONS[sec]():
-            print(f"{r['kernel']:12s} {r['shape']:22s} M={r['M']:<5d} {r['us']:9.3f} us "
-                  f"{r['gbps']:8.1f} GB/s {r['pct_peak']:6.2f}%  {r.get('config', '')}", flush=True)
-            rows.append(r)
+    sweeps = []
+    for i in range(args.sweeps):
+        rows = []
+        for sec in args.only.split(","):
+            for r in SECTIONS[sec]():
+                print(f"[sweep {i + 1}/{args.sweeps}] " + _line(r), flush=True)
+                rows.append(r)
+        sweeps.append(rows)
+    agg = aggregate(sweeps)
+    print(f"median of {args.sweeps} sweeps:")
+    for r in agg:
+        print(_line(r), flush=True)
     if args.json:
         with open(args.json, "w") as f:
-            json.dump({"peak_gbps": PEAK_GBPS, "rows": rows}, f, indent=1)
+            json.dump({"peak_gbps": PEAK_GBPS, "peak_fp16_tflops": PEAK_FP16_TFLOPS,
+                       "sweeps": args.sweeps, "rows": agg, "per_sweep": sweeps}, f, indent=1)
     return 0
 
 
