@@ -165,8 +165,9 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
   static_assert(S >= 2 && S <= 4, "ring of 2 to 4 stages");
   static_assert(KG == 1 || KG == 2, "one or two K groups");
   static_assert(KG * S * C::STAGE <= 160 * 1024, "LDS");
-  // the K groups' accumulators meet in st0 (tiles t < MT / 2) and st1 (the rest)
-  static_assert(KG == 1 || WAVES * (MT / 2) * NT * 64 * 16 <= KG * C::STAGE, "reduction fits two stage slots");
+  // the K groups' accumulators meet in st0 (tiles t < MH) and st1 (the rest)
+  constexpr int MH = MT > 1 ? MT / 2 : 1;
+  static_assert(KG == 1 || WAVES * MH * NT * 64 * 16 <= KG * C::STAGE, "reduction fits two stage slots");
   constexpr int SLOT = KG * C::STAGE;
   __shared__ __align__(16) unsigned char st0[SLOT], st1[SLOT], st2[S >= 3 ? SLOT : 16], st3[S == 4 ? SLOT : 16];
 
@@ -344,14 +345,14 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
       for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
-          (t < MT / 2 ? red0 : red1)[((wave * (MT / 2) + t % (MT / 2)) * NT + j) * 64 + lane] = acc[t][j];
+          (t < MH ? red0 : red1)[((wave * MH + t % MH) * NT + j) * 64 + lane] = acc[t][j];
     }
     ring_barrier();
     if (kg == 1) return;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[t][j] += (t < MT / 2 ? red0 : red1)[((wave * (MT / 2) + t % (MT / 2)) * NT + j) * 64 + lane];
+      for (int j = 0; j < NT; ++j) acc[t][j] += (t < MH ? red0 : red1)[((wave * MH + t % MH) * NT + j) * 64 + lane];
   }
 
   // acc[t][j][i] is row 16t + 4kb + i of the tile, column n0 + 4 * c16 + j

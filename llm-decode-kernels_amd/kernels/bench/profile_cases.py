@@ -31,7 +31,7 @@ def _rotate(fn, sets, reps):
         fn(*sets[i % len(sets)])
 
 
-def case_w4a16(M, N, K, reps):
+def case_w4a16(M, N, K, reps, config=None):
     from kernels.quant import quantize_rtn
     from kernels.w4a16 import w4a16_matmul
 
@@ -40,7 +40,7 @@ def case_w4a16(M, N, K, reps):
     x = cases.activations(M, K, cases.gen(2)).cuda()
     sets = [(x.clone(), qw.clone(), s.clone(), z.clone())
             for _ in range(n_copies(tensor_bytes((x, qw, s, z))))]
-    _rotate(lambda xx, q, sc, zz: w4a16_matmul(xx, q, sc, zz, GS), sets, reps)
+    _rotate(lambda xx, q, sc, zz: w4a16_matmul(xx, q, sc, zz, GS, config=config), sets, reps)
 
 
 def case_fp8(M, N, K, reps):
@@ -209,6 +209,22 @@ CASES = {
     "attention_l4096": lambda r: case_attention(r, L=4096, pos=4000),
     "rmsnorm_res_m2048": lambda r: case_rmsnorm(2048, 1536, r),
     "swiglu_m2048": lambda r: case_swiglu(2048, 8960, r),
+    # decode rows 4 and 8 on the VALU kernel (forced) against the library's MFMA kernel
+    "w4a16_gate_up_m4_valu": lambda r: case_w4a16(4, 17920, 1536, r, {"GEMV": True}),
+    "w4a16_gate_up_m8": lambda r: case_w4a16(8, 17920, 1536, r),
+    "w4a16_gate_up_m8_valu": lambda r: case_w4a16(8, 17920, 1536, r, {"GEMV": True}),
+    "w4a16_down_m4": lambda r: case_w4a16(4, 1536, 8960, r),
+    "w4a16_down_m4_valu": lambda r: case_w4a16(4, 1536, 8960, r, {"GEMV": True}),
+    # prefill GEMMs (the library's choice at these rows)
+    "w4a16_qkv_m2048": lambda r: case_w4a16(2048, 2048, 1536, r),
+    "w4a16_o_m2048": lambda r: case_w4a16(2048, 1536, 1536, r),
+    "w4a16_gate_up_m2048": lambda r: case_w4a16(2048, 17920, 1536, r),
+    "w4a16_down_m2048": lambda r: case_w4a16(2048, 1536, 8960, r),
+    "w4a16_gate_up_m512": lambda r: case_w4a16(512, 17920, 1536, r),
+    "fp8_qkv_m2048": lambda r: case_fp8(2048, 2048, 1536, r),
+    "fp8_o_m2048": lambda r: case_fp8(2048, 1536, 1536, r),
+    "fp8_gate_up_m2048": lambda r: case_fp8(2048, 17920, 1536, r),
+    "fp8_down_m2048": lambda r: case_fp8(2048, 1536, 8960, r),
 }
 
 

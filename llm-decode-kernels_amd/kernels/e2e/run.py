@@ -144,14 +144,14 @@ def run(params: dict) -> dict:
               "prompt_len": prompt_len, "decode_steps": steps, "max_len": max_len,
               "head": head, "backends": {}}
     for name in backends:
-        print(f"[e2e] backend {name}, head {head} ({time.time() - t0:.0f}s)", flush=True)
+        print(f"[e2e] backend {name}, head {head} ({time.time() - t0:.0f}s)", file=sys.stderr, flush=True)
         runner = QwenRunner(hf, make_backend(name), max_len=max_len, head=head)
         r = {"weights": runner.weight_bytes()}
         r["decode"] = decode_speed(runner, ids, steps)
         r["layers_only_ms"] = layers_only_ms(runner)
         result["backends"][name] = r
         print(f"[e2e] {name}: {r['decode']['tok_s']:.1f} tok/s, layers only "
-              f"{r['layers_only_ms']:.3f} ms ({time.time() - t0:.0f}s)", flush=True)
+              f"{r['layers_only_ms']:.3f} ms ({time.time() - t0:.0f}s)", file=sys.stderr, flush=True)
         del runner
         gc.collect()
         torch.cuda.empty_cache()
