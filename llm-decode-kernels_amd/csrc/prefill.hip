@@ -157,7 +157,7 @@ struct GemmCfg {
 // groups' accumulators meet in LDS at the end. That doubles the waves on a tile without the fp32
 // partials in memory that a split over workgroups costs.
 template <WFmt F, int WAVES, int MT, int S, int KG>
-__device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float* partial) {
+__device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float* partial, int mfast) {
   using C = GemmCfg<F, WAVES, MT, S>;
   using T = Fmt<F>;
   constexpr bool kInt4 = F == WFmt::kInt4;
@@ -177,8 +177,13 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
   const int kg = KG == 1 ? 0 : wid / WAVES;                   // K group
   const int gofs = kg * C::STAGE;                             // the K group's part of a stage slot
   const int c16 = lane & 15, kb = lane >> 4;
-  const int n0 = blockIdx.x * (64 * WAVES) + 64 * wave;
-  const int m0 = blockIdx.y * BM;
+  // mfast: the grid's x dimension walks the row tiles, so consecutive workgroups (which the
+  // dispatcher deals round-robin to the 8 XCDs) share a column tile, and each XCD keeps a fixed
+  // subset of the row tiles: its slice of x stays in its L2 and each weight tile it reads serves
+  // all of its row tiles. Otherwise x walks the column tiles.
+  const int bn = mfast ? blockIdx.y : blockIdx.x, bm = mfast ? blockIdx.x : blockIdx.y;
+  const int n0 = bn * (64 * WAVES) + 64 * wave;
+  const int m0 = bm * BM;
   const int mrows = min(a.M - m0, BM);
   // K-steps [kbeg, kbeg + nks) of split blockIdx.z; K group g takes [kbeg + g h, + gn) of them
   const int kbeg0 = blockIdx.z * kps;
@@ -396,14 +401,14 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
 
 template <int WAVES, int MT, int S, int KG>
 __global__ __launch_bounds__(WAVES * KG * 64) __attribute__((amdgpu_waves_per_eu(2))) void w4a16_gemm_kernel(
-    ldk::GemmArgs a, int kps, float* partial) {
-  gemm_body<WFmt::kInt4, WAVES, MT, S, KG>(a, kps, partial);
+    ldk::GemmArgs a, int kps, float* partial, int mfast) {
+  gemm_body<WFmt::kInt4, WAVES, MT, S, KG>(a, kps, partial, mfast);
 }
 
 template <int WAVES, int MT, int S, int KG>
 __global__ __launch_bounds__(WAVES * KG * 64) __attribute__((amdgpu_waves_per_eu(2))) void w8a16_gemm_kernel(
-    ldk::GemmArgs a, int kps, float* partial) {
-  gemm_body<WFmt::kE4M3, WAVES, MT, S, KG>(a, kps, partial);
+    ldk::GemmArgs a, int kps, float* partial, int mfast) {
+  gemm_body<WFmt::kE4M3, WAVES, MT, S, KG>(a, kps, partial, mfast);
 }
 
 // y[m, n] = fp16(sum over splits of partial[split][m][n] (x colscale[n]) (+ bias[n])), the splits
@@ -443,6 +448,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(float* partial, int sp
 //    workgroups instead (the partials of few rows are cheap).
 struct GemmShape {
   int waves, mt, kg, splits;
+  int mfast;  // grid x walks the row tiles (see gemm_body)
 };
 
 constexpr int kLongK = 48;  // K-steps of 64 from which a shape counts as long
@@ -474,31 +480,38 @@ GemmShape pick_shape(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int s
     sp = std::min<int64_t>(sp, ws_bytes / (M * N * 4));
     return (int)std::max<int64_t>(1, std::min<int64_t>(sp, 64));
   };
-  if (block_n == 256) return {4, 8, 1, splits(tiles(4, 8))};
+  if (block_n == 256) return {4, 8, 1, splits(tiles(4, 8)), 0};
   if (block_n == 128) {
     const int mt = tiles(2, 8) >= 512 ? 8 : 4;
-    return {2, mt, 1, splits(tiles(2, mt))};
+    return {2, mt, 1, splits(tiles(2, mt)), 0};
   }
-  if (tiles(4, 8) * splits(tiles(4, 8)) >= 384) return {4, 8, 1, splits(tiles(4, 8))};
+  // long K with at least 16 row tiles: row tiles on the grid's fast axis (down M = 1024 / 2048:
+  // int4 53.6 -> 51.6 / 80.0 -> 76.7 us, e4m3 50.7 -> 49.8 / 78.2 -> 75.2 us; on the short-K
+  // shapes it helped or hurt by a few percent either way, and at 8 row tiles it lost 13%)
+  auto mfast = [&](int mt) { return long_k && (M + 16 * mt - 1) / (16 * mt) >= 16 ? 1 : 0; };
+  if (tiles(4, 8) * splits(tiles(4, 8)) >= 384) return {4, 8, 1, splits(tiles(4, 8)), mfast(8)};
   for (int w : {4, 2, 1}) {
     const int64_t t = tiles(w, 4);
     const int sp = splits(t);
     const int kg = !long_k && split_k <= 0 && t * sp * w < 2048 && steps / sp >= 16 ? 2 : 1;
-    if (w == 1 || (t * sp >= 192 && lds_of(f, w, 4, kg) <= 80 * 1024)) return {w, 4, kg, sp};
+    if (w == 1 || (t * sp >= 192 && lds_of(f, w, 4, kg) <= 80 * 1024)) return {w, 4, kg, sp, mfast(4)};
   }
-  return {1, 4, 1, 1};  // not reached
+  return {1, 4, 1, 1, 0};  // not reached
 }
 
 template <WFmt F, int WAVES, int MT, int KG, int S = stages_of(F, WAVES, MT, KG)>
-int launch(const ldk::GemmArgs& a, int splits, hipStream_t s) {
+int launch(const ldk::GemmArgs& a, int splits, int mfast, hipStream_t s) {
   const int64_t tn = (a.N + 64 * WAVES - 1) / (64 * WAVES), tm = (a.M + 16 * MT - 1) / (16 * MT);
   const int steps = a.K / kStep, kps = (steps + splits - 1) / splits;
   const int nz = (steps + kps - 1) / kps;  // splits actually used (none empty)
   float* partial = nz > 1 ? static_cast<float*>(a.workspace) : nullptr;
-  const dim3 grid((unsigned)tn, (unsigned)tm, (unsigned)nz);
+  if (tn > 65535) mfast = 0;  // the column tiles then stay in the grid's x dimension
+  const dim3 grid = mfast ? dim3((unsigned)tm, (unsigned)tn, (unsigned)nz) : dim3((unsigned)tn, (unsigned)tm, (unsigned)nz);
   (void)hipGetLastError();
-  if constexpr (F == WFmt::kInt4) w4a16_gemm_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, partial);
-  else w8a16_gemm_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, partial);
+  if constexpr (F == WFmt::kInt4)
+    w4a16_gemm_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, partial, mfast);
+  else
+    w8a16_gemm_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, partial, mfast);
   int st = ldk::check_launch(F == WFmt::kInt4 ? "w4a16_gemm" : "w8a16_gemm");
   if (st || nz == 1) return st;
   const int64_t quads = (int64_t)a.M * (a.N / 4);
@@ -515,14 +528,14 @@ template <WFmt F>
 int launch_fmt(const ldk::GemmArgs& a, hipStream_t s) {
   const GemmShape sh = shape_for(F, a);
   switch (sh.waves * 100 + sh.mt * 10 + sh.kg) {
-    case 481: return launch<F, 4, 8, 1>(a, sh.splits, s);
-    case 281: return launch<F, 2, 8, 1>(a, sh.splits, s);
-    case 441: return launch<F, 4, 4, 1>(a, sh.splits, s);
-    case 442: return launch<F, 4, 4, 2>(a, sh.splits, s);
-    case 241: return launch<F, 2, 4, 1>(a, sh.splits, s);
-    case 242: return launch<F, 2, 4, 2>(a, sh.splits, s);
-    case 141: return launch<F, 1, 4, 1>(a, sh.splits, s);
-    case 142: return launch<F, 1, 4, 2>(a, sh.splits, s);
+    case 481: return launch<F, 4, 8, 1>(a, sh.splits, sh.mfast, s);
+    case 281: return launch<F, 2, 8, 1>(a, sh.splits, sh.mfast, s);
+    case 441: return launch<F, 4, 4, 1>(a, sh.splits, sh.mfast, s);
+    case 442: return launch<F, 4, 4, 2>(a, sh.splits, sh.mfast, s);
+    case 241: return launch<F, 2, 4, 1>(a, sh.splits, sh.mfast, s);
+    case 242: return launch<F, 2, 4, 2>(a, sh.splits, sh.mfast, s);
+    case 141: return launch<F, 1, 4, 1>(a, sh.splits, sh.mfast, s);
+    case 142: return launch<F, 1, 4, 2>(a, sh.splits, sh.mfast, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "gemm: shape %d x %d with %d K groups not instantiated", sh.waves, sh.mt, sh.kg);
 }

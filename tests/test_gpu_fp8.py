@@ -171,6 +171,11 @@ def test_prefill_gemm_one_hot_rows_exact():
     assert np.all(got[~nz] == 0)
 
 
+def test_prefill_gemm_long_k_row_tiles_fast_with_tail():
+    """Long K with 16 row tiles (row tiles on the grid's fast axis), a partial last row tile."""
+    _run(2000, 1536, 8960, bias=True, config={"prefill": "gemm"})
+
+
 def test_prefill_gemm_two_k_groups_odd_steps():
     """Two K groups in a workgroup over 33 K-steps of 64 (17 and 16: the second group takes one
     barrier-only step), a partial last column tile (N = 1008), row tails."""

@@ -328,6 +328,12 @@ def test_prefill_gemm_strided_rows_and_narrow_n():
     assert_north_star(out, w4a16_ref(x, qw, s, z))
 
 
+def test_prefill_gemm_long_k_row_tiles_fast_with_tail():
+    """Long K with 16 row tiles puts the row tiles on the grid's fast axis; 2000 rows leave a
+    partial last row tile, with the K split and its reduce launch."""
+    _run(2000, 1536, 8960, bias=True, config={"prefill": "gemm"})
+
+
 def test_prefill_gemm_two_k_groups_odd_steps():
     """Two K groups in a workgroup over 33 K-steps of 64 (17 and 16: the second group takes one
     barrier-only step), a partial last column tile (N = 1000), row tails, on one and two column
