@@ -107,8 +107,10 @@ def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=No
         flags |= _lib.PATH_MFMA
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
+    # the library's choice is recorded for the decode shapes it chose (w4a16.py:322-326): a call
+    # whose config forced a variant records nothing, as the reference's forced path picks nothing
     key = (min(_next_pow2(M), 16), N, K, bias is not None)
-    if M <= 16 and key not in _decode_choice:
+    if M <= 16 and not config and key not in _decode_choice:
         _decode_choice[key] = config_for(M, N, K, group_size)
     return out.view(*x.shape[:-1], N)
 

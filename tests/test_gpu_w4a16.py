@@ -414,3 +414,21 @@ def test_prefill_gemm_k_split_deterministic_and_leaves_workspace_clean():
     x1 = x[:1].copy()
     y1 = w4a16_matmul(dev(x1), *args[1:], config={"split_k": 5})
     assert_north_star(y1, w4a16_ref(x1, qw, s, z))
+
+
+def test_choice_export_records_only_the_library_choice():
+    """A call whose config forces a variant records nothing; a call left to the library records
+    the table's choice for its decode key, which export/import round-trip (w4a16.py:322-342)."""
+    from kernels import w4a16 as mod
+
+    mod._decode_choice.clear()
+    x, qw, s, z, _ = _make(1, 1536, 1536, 3)
+    args = (dev(x), dev(qw), dev(s), dev(z))
+    w4a16_matmul(*args, config={"GEMV": True, "block_n": 32})
+    assert mod.export_choices() == {}
+    w4a16_matmul(*args)
+    exported = mod.export_choices()
+    assert exported == {"1,1536,1536,False": mod.config_for(1, 1536, 1536)}
+    mod._decode_choice.clear()
+    mod.import_choices(exported)
+    assert mod.export_choices() == exported
