@@ -436,14 +436,15 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(float* partial, int sp
 }
 
 // Tile shape, K groups and K split per problem. From graph-timed sweeps on MI355X over the
-// Qwen2.5-1.5B shapes (M = 512 / 2048, int4 and e4m3):
-//  * 128 x 256 tiles (4 waves of 128 rows) when they give at least 384 workgroups, with the K split
-//    for long K: gate_up M = 2048 (int4 117 us, e4m3 114 us), down M = 2048 (80 / 77 us, 5 splits,
-//    against 90 / 81 us on 64-row tiles).
-//  * Otherwise 64-row tiles, on the widest workgroup (4, 2 or 1 column groups) that still gives
-//    most CUs one and, with two K groups, leaves LDS for two per CU: qkv M = 2048 on 4 x 64 columns
-//    and two K groups (int4 20 us, against 29 us on one K group and 28 us for dequantize +
-//    hipBLASLt); qkv M = 512 on 1 x 64 columns and two K groups (int4 12.7 us, e4m3 11.9 us).
+// Qwen2.5-1.5B shapes (M = 512 / 1024 / 2048, int4 and e4m3):
+//  * Long K: the largest tile whose split grid still gives most CUs a workgroup, with the split
+//    count that balances the CUs (below): down M = 2048 on 128 x 256 tiles split 5 ways (int4
+//    75 us, e4m3 74 us, against 90 / 81 us on 64-row tiles).
+//  * Short K: 128 x 256 tiles when they give at least 384 workgroups (gate_up M = 2048: int4
+//    117 us, e4m3 114 us); otherwise 64-row tiles on the widest workgroup (4, 2 or 1 column groups)
+//    that still gives most CUs one and, with two K groups, leaves LDS for two per CU (qkv M = 2048
+//    on 4 x 64 columns and two K groups: int4 20 us, against 29 us on one K group and 28 us for
+//    dequantize + hipBLASLt); where that leaves one column group, 32-row tiles on two.
 //  * Two K groups when a short-K shape leaves fewer than two waves per SIMD; long K splits over
 //    workgroups instead (the partials of few rows are cheap).
 struct GemmShape {
@@ -457,7 +458,7 @@ constexpr int kLongK = 48;  // K-steps of 64 from which a shape counts as long
 // registers of a second workgroup per CU (occupancy 1) and loses; one column group with two K
 // groups gains from a third stage, which its small LDS footprint leaves room for.
 constexpr int stages_of(WFmt f, int waves, int mt, int kg) {
-  return waves == 4 && mt == 8 ? (f == WFmt::kInt4 ? 3 : 2) : waves == 1 && kg == 2 ? 3 : 2;
+  return waves == 4 && mt == 8 ? (f == WFmt::kInt4 ? 3 : 2) : (waves == 1 && kg == 2) || mt <= 2 ? 3 : 2;
 }
 
 // LDS of a workgroup: KG rings of S stages (x tile, weights, int4 scales and zeros).
@@ -471,30 +472,48 @@ GemmShape pick_shape(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int s
   const int64_t steps = K / kStep;
   const bool long_k = steps >= kLongK;
   auto tiles = [&](int waves, int mt) { return ((N + 64 * waves - 1) / (64 * waves)) * ((M + 16 * mt - 1) / (16 * mt)); };
-  // K split (long K, or split_k): toward 512 workgroups, at most 6 ways and at least 8 K-steps per
-  // split, as far as the workspace holds the fp32 partials
+  // K split (long K, or split_k), as far as the workspace holds the fp32 partials: the count that
+  // minimises the busiest CU's share of the work, ceil(t s / 256) / s for t tiles (one or two
+  // workgroups per CU run at once), at most 6 ways and 8 K-steps per split. down M = 1024 on
+  // 48 tiles: 5 splits (240 workgroups, one per CU) 47.6 us, 6 splits (288: 32 CUs with two)
+  // 51.0 us (int4).
   auto splits = [&](int64_t t) {
-    int64_t sp = split_k > 0 ? std::min<int64_t>(split_k, steps)
-                 : long_k    ? std::min<int64_t>(std::min<int64_t>((512 + t - 1) / t, 6), steps / 8)
-                             : 1;
-    sp = std::min<int64_t>(sp, ws_bytes / (M * N * 4));
-    return (int)std::max<int64_t>(1, std::min<int64_t>(sp, 64));
+    const int64_t room = std::max<int64_t>(1, std::min<int64_t>(64, ws_bytes / (M * N * 4)));
+    if (split_k > 0) return (int)std::min<int64_t>(std::min<int64_t>(split_k, steps), room);
+    if (!long_k) return 1;
+    const int64_t most = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(6, steps / 8), room));
+    int64_t best = 1;
+    for (int64_t sp = 2; sp <= most; ++sp)  // ceil(t sp / 256) / sp < ceil(t best / 256) / best
+      if (((t * sp + 255) / 256) * best < ((t * best + 255) / 256) * sp) best = sp;
+    return (int)best;
   };
+  // long K with at least 16 row tiles: row tiles on the grid's fast axis (down M = 1024 / 2048:
+  // int4 53.6 -> 51.6 / 80.0 -> 76.7 us, e4m3 50.7 -> 49.8 / 78.2 -> 75.2 us; on the short-K
+  // shapes it helped or hurt by a few percent either way, and at 8 row tiles it lost 13%)
+  auto mfast = [&](int mt) { return long_k && (M + 16 * mt - 1) / (16 * mt) >= 16 ? 1 : 0; };
   if (block_n == 256) return {4, 8, 1, splits(tiles(4, 8)), 0};
   if (block_n == 128) {
     const int mt = tiles(2, 8) >= 512 ? 8 : 4;
     return {2, mt, 1, splits(tiles(2, mt)), 0};
   }
-  // long K with at least 16 row tiles: row tiles on the grid's fast axis (down M = 1024 / 2048:
-  // int4 53.6 -> 51.6 / 80.0 -> 76.7 us, e4m3 50.7 -> 49.8 / 78.2 -> 75.2 us; on the short-K
-  // shapes it helped or hurt by a few percent either way, and at 8 row tiles it lost 13%)
-  auto mfast = [&](int mt) { return long_k && (M + 16 * mt - 1) / (16 * mt) >= 16 ? 1 : 0; };
-  if (tiles(4, 8) * splits(tiles(4, 8)) >= 384) return {4, 8, 1, splits(tiles(4, 8)), mfast(8)};
+  if (long_k) {  // the largest tile whose split grid still gives most CUs a workgroup
+    for (int w : {4, 2, 1})
+      for (int mt : {8, 4}) {
+        if (w != 4 && mt == 8) continue;
+        const int64_t t = tiles(w, mt);
+        const int sp = splits(t);
+        if (t * sp >= 192 || (w == 1 && mt == 4)) return {w, mt, 1, sp, mfast(mt)};
+      }
+  }
+  if (tiles(4, 8) >= 384) return {4, 8, 1, 1, 0};
   for (int w : {4, 2, 1}) {
     const int64_t t = tiles(w, 4);
-    const int sp = splits(t);
-    const int kg = !long_k && split_k <= 0 && t * sp * w < 2048 && steps / sp >= 16 ? 2 : 1;
-    if (w == 1 || (t * sp >= 192 && lds_of(f, w, 4, kg) <= 80 * 1024)) return {w, 4, kg, sp, mfast(4)};
+    const int kg = split_k <= 0 && t * w < 2048 && steps >= 16 ? 2 : 1;
+    if (w > 1 && !(t >= 192 && lds_of(f, w, 4, kg) <= 80 * 1024)) continue;
+    // one column group of 64-row tiles: 32-row tiles on two column groups when they still give
+    // most CUs a workgroup (qkv M = 512: 10.5 against 12.7 us int4, 10.4 against 12.1 us e4m3)
+    if (w == 1 && kg == 2 && tiles(2, 2) >= 192) return {2, 2, 2, 1, 0};
+    return {w, 4, kg, splits(t), 0};
   }
   return {1, 4, 1, 1, 0};  // not reached
 }
@@ -536,6 +555,7 @@ int launch_fmt(const ldk::GemmArgs& a, hipStream_t s) {
     case 242: return launch<F, 2, 4, 2>(a, sh.splits, sh.mfast, s);
     case 141: return launch<F, 1, 4, 1>(a, sh.splits, sh.mfast, s);
     case 142: return launch<F, 1, 4, 2>(a, sh.splits, sh.mfast, s);
+    case 222: return launch<F, 2, 2, 2>(a, sh.splits, sh.mfast, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "gemm: shape %d x %d with %d K groups not instantiated", sh.waves, sh.mt, sh.kg);
 }

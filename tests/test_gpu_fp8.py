@@ -171,6 +171,13 @@ def test_prefill_gemm_one_hot_rows_exact():
     assert np.all(got[~nz] == 0)
 
 
+def test_prefill_gemm_32_row_tiles_with_tail():
+    """qkv-like short K at about 500 rows runs 32-row tiles on two column groups and two K
+    groups; 500 rows leave a partial last row tile."""
+    _run(500, 2048, 1536, bias=True, config={"prefill": "gemm"})
+    _run(512, 1536, 1536, config={"prefill": "gemm"})
+
+
 def test_prefill_gemm_long_k_row_tiles_fast_with_tail():
     """Long K with 16 row tiles (row tiles on the grid's fast axis), a partial last row tile."""
     _run(2000, 1536, 8960, bias=True, config={"prefill": "gemm"})

@@ -328,6 +328,13 @@ def test_prefill_gemm_strided_rows_and_narrow_n():
     assert_north_star(out, w4a16_ref(x, qw, s, z))
 
 
+def test_prefill_gemm_32_row_tiles_with_tail():
+    """qkv-like short K at about 500 rows runs 32-row tiles on two column groups and two K
+    groups; 500 rows leave a partial last row tile."""
+    _run(500, 2048, 1536, bias=True, config={"prefill": "gemm"})
+    _run(512, 1536, 1536, config={"prefill": "gemm"})
+
+
 def test_prefill_gemm_long_k_row_tiles_fast_with_tail():
     """Long K with 16 row tiles puts the row tiles on the grid's fast axis; 2000 rows leave a
     partial last row tile, with the K split and its reduce launch."""
