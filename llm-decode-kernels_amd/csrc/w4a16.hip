@@ -993,9 +993,148 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
   });
 }
 
+// ----------------------------------------------- MFMA kernel with x staged in LDS (decode rows)
+//
+// Decode rows (3 .. 16) on wide and medium shapes with group size 128 and K <= 12 groups: one
+// workgroup per 32-column tile over all of K (gate_up: 560 workgroups, the M = 1 kernel's grid),
+// NW waves of GPW groups each, so no split-K and no atomics.
+//
+// The x operand is what limits the wide-tile MFMA kernel at these rows: its A fragments (16 rows x
+// 64 bytes per load) are re-read by every workgroup straight from L2. Here each wave first loads
+// the x rows of its own groups with coalesced 16-byte loads (16 lanes = 256 contiguous bytes of one
+// row), issued before its weight loads, turns them into A records in LDS and reads its A fragments
+// back with ds_read_b128 (no workgroup barrier: a wave only reads the records it wrote):
+//  - record of (packed row r, row m) = the A fragment of lane (c16 = m, kb = r % 4): pairs
+//    (x0,x4) (x1/16,x5/16) (x2,x6) (x3/16,x7/16), stored at [r][m ^ (r % MP)] so that the 16
+//    lanes writing one row's 16 packed rows and the 16 lanes reading one packed row's 16 rows hit
+//    distinct LDS banks;
+//  - per (group, row) the offset c = 1024 * sum(A) (the magic 1024 of every decoded weight times
+//    the staged x) and sum(x), reduced over the 16 lanes of a group with DPP row rotations, for
+//    the epilogue s * (sum x*(1024+q) - c - z * sum x) = s * sum x*(q - z).
+// B is one v_and_or_b32 per pair (odd nibbles in place as 16q, met by x/16): 5 VALU ops per 8
+// weights and no all-ones MFMA for sum(x). A lane loads 8 bytes (two columns) per packed row, the
+// M = 1 kernel's 128-byte tile; the waves' partial tiles meet in LDS at the end.
+// Measured on MI355X (graph replays, rotating sets): gate_up M = 4 / 8 / 16 7.5 / 8.0 / 9.3 us on
+// the wide-tile kernel against 6.3 / 6.9 / 7.8 us here, q/o 4.3 / 4.4 / 5.1 against 3.7 / 3.9 / 4.1.
+template <int MP, int NW, int GPW>
+__global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
+  static_assert(MP == 4 || MP == 8 || MP == 16, "row tile");
+  constexpr int NG = NW * GPW, WUNITS = GPW * MP * 16, WUPT = WUNITS / 64;
+  static_assert(WUNITS % 64 == 0, "whole staging units per lane");
+  typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+  __shared__ __align__(16) u32x4 xs[NG * 16 * MP];  // A records; the waves' partial tiles at the end
+  __shared__ float2_t st[NG][MP];                   // (c, sum x) per group and row
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, kb = lane >> 4;
+  ldk::pin_sgpr(a.x);
+  ldk::pin_sgpr(a.qw);
+  const int ng = (a.K >> 3) >> 4;  // groups of 16 packed rows; ng <= NG
+  const int n0 = blockIdx.x * 32;
+  const int M = a.M;
+  // ---- this wave's x rows first (unit u = lane + 64 i: packed row rr of group wave*GPW + u/(16 MP), row m)
+  u32x4 xr[WUPT];
+#pragma unroll
+  for (int i = 0; i < WUPT; ++i) {
+    const int u = lane + 64 * i, rr = u & 15, m = (u >> 4) % MP, g = min(wave * GPW + u / (16 * MP), ng - 1);
+    xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)min(m, M - 1) * a.ldx + 8 * (16 * g + rr));
+  }
+  // ---- then its weights: K step ks of group g is packed row 16 g + 4 ks + kb, columns n0 + 2 c16 (+1)
+  u32x2 w[GPW][4];
+  uint32_t sv[GPW], zv[GPW];
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int g = min(wave * GPW + gi, ng - 1);  // clamped: surplus waves load valid memory, use nothing
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      w[gi][ks] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x2*>(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + n0 + 2 * c16));
+    sv[gi] = *reinterpret_cast<const uint32_t*>(a.s + (int64_t)g * a.N + n0 + 2 * c16);
+    zv[gi] = *reinterpret_cast<const uint32_t*>(a.z + (int64_t)g * a.N + n0 + 2 * c16);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
+  // ---- A records and the per-(group, row) offsets
+  const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
+#pragma unroll
+  for (int i = 0; i < WUPT; ++i) {
+    const int u = lane + 64 * i, rr = u & 15, m = (u >> 4) % MP, g = wave * GPW + u / (16 * MP);
+    const u32x4 d = m < M ? xr[i] : u32x4{0u, 0u, 0u, 0u};  // rows past M stage zeros
+    const half2_t a0 = ldk::u2h2(perm_lo(d[0], d[2])), a1 = ldk::u2h2(perm_hi(d[0], d[2]));
+    const half2_t a2 = ldk::u2h2(perm_lo(d[1], d[3])), a3 = ldk::u2h2(perm_hi(d[1], d[3]));
+    const half2_t b1 = a1 * sixteenth, b3 = a3 * sixteenth;
+    const float se = ((float)a0[0] + (float)a0[1]) + ((float)a2[0] + (float)a2[1]);
+    float c = 1024.0f * (se + (((float)b1[0] + (float)b1[1]) + ((float)b3[0] + (float)b3[1])));
+    float sx = se + (((float)a1[0] + (float)a1[1]) + ((float)a3[0] + (float)a3[1]));
+    // sums over the 16 packed rows of the group: the 16 lanes of a DPP row, in a fixed order
+    c += ldk::row_ror<1>(c);
+    sx += ldk::row_ror<1>(sx);
+    c += ldk::row_ror<2>(c);
+    sx += ldk::row_ror<2>(sx);
+    c += ldk::row_ror<4>(c);
+    sx += ldk::row_ror<4>(sx);
+    c += ldk::row_ror<8>(c);
+    sx += ldk::row_ror<8>(sx);
+    if (g < ng) {
+      xs[(16 * g + rr) * MP + (m ^ (rr & (MP - 1)))] =
+          u32x4{ldk::h22u(a0), ldk::h22u(b1), ldk::h22u(a2), ldk::h22u(b3)};
+      if (rr == 0) st[g][m] = float2_t{c, sx};
+    }
+  }
+  ldk::wave_lds_sync();
+  // ---- MFMA over the wave's groups: tile t holds columns n0 + 2 c16 + t
+  const uint32_t magic = ldk::vgpr_const<kMagic>();
+  const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
+  float4_t acc[2] = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, float4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int g = wave * GPW + gi;
+    if (g >= ng) break;  // uniform
+    float4_t tmp[2] = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, float4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int r = 16 * g + 4 * ks + kb;
+      u32x4 ar = u32x4{0u, 0u, 0u, 0u};
+      if (c16 < MP) ar = xs[r * MP + (c16 ^ (r & (MP - 1)))];
+      const half8v A = __builtin_bit_cast(half8v, ar);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t wc = w[gi][ks][t], v = wc >> 8;
+        const u32x4 b{(wc & mlo) | magic, (wc & mhi) | magic, (v & mlo) | magic, (v & mhi) | magic};
+        tmp[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), tmp[t], 0, 0, 0);
+      }
+    }
+    const half2_t s2 = ldk::u2h2(sv[gi]), z2 = ldk::u2h2(zv[gi]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // element i of lane (c16, kb): row 4 kb + i
+      if (4 * kb + i < MP) {
+        const float2_t k = st[g][4 * kb + i];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          acc[t][i] = __builtin_fmaf((float)s2[t], tmp[t][i] - __builtin_fmaf((float)z2[t], k[1], k[0]), acc[t][i]);
+      }
+    }
+  }
+  // ---- the NW partial tiles meet in LDS (over the records, once every wave is done with them)
+  ldk::lds_barrier();
+  float* red = reinterpret_cast<float*>(xs);  // [NW][MP][32]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (4 * kb + i < MP)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) red[(wave * MP + 4 * kb + i) * 32 + 2 * c16 + t] = acc[t][i];
+  }
+  ldk::lds_barrier();
+  for (int o = threadIdx.x; o < MP * 32; o += NW * 64) {
+    const int row = o >> 5, col = o & 31;
+    if (row >= M) break;  // o grows with row
+    float v = ldk::sum_waves(red + row * 32 + col, MP * 32, NW);
+    if (a.bias) v += (float)a.bias[n0 + col];
+    a.out[(int64_t)row * a.ldo + n0 + col] = (half_t)v;
+  }
+}
+
 // ------------------------------------------------------------------------------------ dispatch
 
-enum Kern { kM1 = 0, kValu = 1, kMfma = 2 };
+enum Kern { kM1 = 0, kValu = 1, kMfma = 2, kMfmaX = 3 };
 
 struct Plan {
   Kern kern;
@@ -1039,7 +1178,7 @@ int m1_max_waves(int ln, int mr) {
 int gemv_pxw(const Plan& p) { return (p.cpw * p.rpl * p.mt + p.ln - 1) / p.ln; }
 
 size_t plan_lds_bytes(const Plan& p, int64_t M) {
-  if (p.kern == kM1) return 0;  // static LDS
+  if (p.kern == kM1 || p.kern == kMfmaX) return 0;  // static LDS
   if (p.kern == kMfma) return (size_t)p.nw * std::min<int64_t>(M, 16 * p.mtile) * (4 * p.ln) * 4;
   return (size_t)p.nw * 64 * gemv_pxw(p) * 16 + (size_t)p.nw * p.mt * 4 * p.ln * 4;
 }
@@ -1061,6 +1200,42 @@ size_t workspace_need(const Plan& p, int64_t M, int64_t N) {
 int cpw_from_flags(int flags) {
   const int v = (flags & LDK_CPW_MASK) >> 4;
   return v ? 1 << (v - 1) : 0;
+}
+
+// The MFMA kernel with x staged in LDS takes decode rows 3-16 with group size 128 when its
+// whole-K 32-column tiles fill the GPU (at least 32 of them) and K holds at most 12 groups (its
+// LDS); a tuning argument that names another variant (block_n, split_k, EXACT, VALU, chunks per
+// wave) keeps the wide-tile kernel or the VALU kernel.
+bool mfma_x_applies(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int split_k, int flags) {
+  return M >= 3 && M <= 16 && gsh_rows == 4 && N % 32 == 0 && N / 32 >= 32 && (K >> 7) <= 12 && block_n == 0 &&
+         split_k <= 1 && !(flags & (LDK_EXACT | LDK_PATH_VALU | LDK_CPW_MASK));
+}
+
+template <int MP, int NW, int GPW>
+int launch_mfma_x_t(const W4Args& a, hipStream_t s) {
+  (void)hipGetLastError();
+  w4a16_mfma_x_kernel<MP, NW, GPW><<<(unsigned)(a.N / 32), NW * 64, 0, s>>>(a);
+  return ldk::check_launch("w4a16_mfma_x");
+}
+
+template <int MP>
+int launch_mfma_x_mp(const W4Args& a, int nw, int gpw, hipStream_t s) {
+  if (nw == 12 && gpw == 1) return launch_mfma_x_t<MP, 12, 1>(a, s);
+  if (nw == 6 && gpw == 2) return launch_mfma_x_t<MP, 6, 2>(a, s);
+  if (nw == 6 && gpw == 1) return launch_mfma_x_t<MP, 6, 1>(a, s);
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: x-staged MFMA kernel with %d waves of %d groups not instantiated", nw, gpw);
+}
+
+int launch_mfma_x(const W4Args& a, const Plan& p, hipStream_t s) {
+  // the kernel's grid and LDS assume these; the plan only picks it when they hold
+  if (a.gsh_rows != 4 || a.N % 32 || a.M > p.mt || (int64_t)p.nw * p.cpw < ((a.K >> 3) >> 4))
+    return ldk::fail(LDK_ERR_INVALID, "w4a16: x-staged MFMA plan does not fit M=%d N=%d K=%d", a.M, a.N, a.K);
+  switch (p.mt) {
+    case 4: return launch_mfma_x_mp<4>(a, p.nw, p.cpw, s);
+    case 8: return launch_mfma_x_mp<8>(a, p.nw, p.cpw, s);
+    case 16: return launch_mfma_x_mp<16>(a, p.nw, p.cpw, s);
+  }
+  return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: x-staged MFMA row tile %d", p.mt);
 }
 
 // Chooses the kernel, column tile, rows per lane, chunks per wave, workgroup size and split
@@ -1087,6 +1262,23 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const bool mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
   const bool m1 = !mfma && !(flags & LDK_EXACT) && M <= 2;  // the factored VALU kernel
   p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
+  if (mfma && mfma_x_applies(M, N, K, gsh_rows, block_n, split_k, flags)) {
+    // x staged in LDS, whole 32-column tiles: twelve waves of one group, or six of two for up to
+    // four rows on grids of at least one tile per CU (gate_up M = 4: 6.3 against 6.4 us; q/o M = 4
+    // on 48 tiles: 3.9 against 3.7 us with twelve)
+    p.kern = kMfmaX;
+    p.mt = M <= 4 ? 4 : M <= 8 ? 8 : 16;
+    p.ln = 8;
+    p.rpl = 4;
+    const int64_t ngx = (K / 8) >> gsh_rows;
+    p.nw = ngx <= 6 ? 6 : (M <= 4 && N / 32 >= 256) ? 6 : 12;
+    p.cpw = (int)((ngx + p.nw - 1) / p.nw);
+    p.splits = 1;
+    p.gps = (int)ngx;
+    p.full = 0;
+    p.mtile = 1;
+    return p;
+  }
   p.mt = mfma ? 16 : round_mt(M);
   p.mtile = mfma && M > 16 ? 2 : 1;
   if (mfma) {  // 128 columns on shapes wide enough to fill the CUs with them, else 64 (and 64 for
@@ -1357,6 +1549,7 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: block_n=%d not supported (16, 32 or 64)", 4 * p.ln);
   }
   if (pro != kProNone) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: fused prologues run on the M = 1 kernel");
+  if (p.kern == kMfmaX) return launch_mfma_x(a, p, s);
   if (p.kern == kMfma) {
     if (p.ln == 8) return launch_mfma_nh<1, 2>(a, sp, p, lds, s);  // 32-column tiles
     return p.ln == 16 ? launch_mfma_nh<1, 4>(a, sp, p, lds, s) : launch_mfma_nh<2, 4>(a, sp, p, lds, s);
@@ -1395,7 +1588,7 @@ int validate(const char* fn, const void* x, int64_t ldx, const int32_t* qw, cons
 
 int plan_flags(const Plan& p) {
   const int cpw_code = p.kern == kValu ? (p.cpw == 1 ? 1 : p.cpw == 2 ? 2 : 3) : 0;
-  return (p.kern == kMfma ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.kern == kValu ? LDK_EXACT : LDK_FACTORED) |
+  return (p.kern == kMfma || p.kern == kMfmaX ? LDK_PATH_MFMA : LDK_PATH_VALU) | (p.kern == kValu ? LDK_EXACT : LDK_FACTORED) |
          (cpw_code << 4);
 }
 
@@ -1446,6 +1639,8 @@ static int plan_kernel_name(const Plan& p, int gsh_rows, char* buf, size_t len) 
   int n = 0;
   if (p.kern == kM1) {
     n = snprintf(buf, len, "w4a16_m1_kernel<%d, %d, %d, 0, %d>", p.ln, p.nw, gsh_rows == 4 ? 4 : 0, p.mt);
+  } else if (p.kern == kMfmaX) {
+    n = snprintf(buf, len, "w4a16_mfma_x_kernel<%d, %d, %d>", p.mt, p.nw, p.cpw);
   } else if (p.kern == kValu) {
     n = snprintf(buf, len, "w4a16_gemv_kernel<%d, %d, %d, %d>", p.mt, p.ln, p.rpl, p.cpw);
   } else {

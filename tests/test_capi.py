@@ -196,7 +196,7 @@ def test_config_query():
     assert fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU
     st = _lib.load().ldk_w4a16_config(16, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
-    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 128
+    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 32  # x staged in LDS, 32-column tiles
     # two rows: the factored VALU kernel; from three rows the MFMA kernel, also on small shapes
     st = _lib.load().ldk_w4a16_config(2, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
@@ -204,6 +204,22 @@ def test_config_query():
     st = _lib.load().ldk_w4a16_config(3, 1536, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
     assert st == 0 and fl.value & _lib.PATH_MFMA
+
+
+def test_decode_rows_plan_kernels():
+    """Decode rows 3-16 on shapes of >= 32 whole 32-column tiles and K <= 12 groups of 128 run the
+    MFMA kernel with x staged in LDS; narrow shapes (k/v), long K (down) and forced tile widths
+    keep the wide-tile MFMA kernel; one and two rows the factored VALU kernel."""
+    from kernels.w4a16 import kernel_name
+    assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
+    assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2>"
+    assert kernel_name(8, 1536, 1536) == "w4a16_mfma_x_kernel<8, 12, 1>"
+    assert kernel_name(3, 4096, 512) == "w4a16_mfma_x_kernel<4, 6, 1>"
+    assert kernel_name(16, 256, 1536).startswith("w4a16_mfma_kernel<")
+    assert kernel_name(16, 1536, 8960).startswith("w4a16_mfma_kernel<")
+    assert kernel_name(16, 17920, 1536, 64).startswith("w4a16_mfma_kernel<")
+    assert kernel_name(2, 17920, 1536).startswith("w4a16_m1_kernel<")
+    assert kernel_name(17, 17920, 1536).startswith("w4a16_mfma_kernel<")
 
 
 def test_workspace_size():

@@ -263,6 +263,52 @@ def test_one_hot_multi_row():
     assert np.array_equal(bits16(out), bits16(np.ascontiguousarray(deq[:, ::3][:, :16].T)))
 
 
+# ---------------------------------------------------------------- MFMA kernel with x staged in LDS
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("N,K", [(17920, 1536), (2048, 1536), (1536, 1536), (1024, 512)])
+def test_mfma_x_rows(M, N, K):
+    """Decode rows on the x-staged MFMA kernel: row tiles of 4/8/16 with rows past M staged as
+    zeros, twelve waves of one group, six of two (gate_up at <= 4 rows) and six of one (K = 512:
+    four groups, two waves idle)."""
+    from kernels.w4a16 import kernel_name
+    assert kernel_name(M, N, K).startswith("w4a16_mfma_x_kernel<")
+    _run(M, N, K)
+
+
+def test_mfma_x_bias_strided_rows_and_repeat():
+    from kernels.w4a16 import kernel_name
+    assert kernel_name(7, 2048, 1536).startswith("w4a16_mfma_x_kernel<")
+    _run(7, 2048, 1536, bias=True)
+    x, qw, s, z, _ = _make(7, 2048, 1536, 5)
+    big = torch.zeros(7, 2048, dtype=torch.float16, device="cuda")
+    big[:, :1536] = dev(x)
+    qwd, sd, zd = dev(qw), dev(s), dev(z)
+    a = w4a16_matmul(big[:, :1536], qwd, sd, zd)
+    assert_north_star(a, w4a16_ref(x, qw, s, z))
+    b = w4a16_matmul(big[:, :1536], qwd, sd, zd)
+    assert torch.equal(a, b)  # deterministic
+
+
+@pytest.mark.parametrize("M", [16, 5])
+def test_mfma_x_one_hot_rows_reproduce_dequantized_weight(M):
+    """Row m = e_k(m): every output row is a column of dequant(W) exactly, for every k of K = 1536
+    (even and odd nibbles, all twelve groups, every packed row of the LDS records)."""
+    from kernels.w4a16 import kernel_name
+    N, K = 1024, 1536
+    assert kernel_name(M, N, K).startswith("w4a16_mfma_x_kernel<")
+    _, qw, s, z, _ = _make(1, N, K, 11)
+    deq = dequantize_ref(qw, s, z, 128)
+    qwd, sd, zd = dev(qw), dev(s), dev(z)
+    rng = np.random.default_rng(3)
+    order = rng.permutation(K)
+    for c in range(0, K, M):
+        ks = order[c:c + M]
+        x = torch.zeros(len(ks), K, dtype=torch.float16, device="cuda")
+        x[torch.arange(len(ks)), torch.as_tensor(ks)] = 1.0
+        got = w4a16_matmul(x, qwd, sd, zd).cpu().numpy()
+        assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, ks].T))), c
+
+
 # ---------------------------------------------------------------- config 0 and config 2
 def test_config0_headline():
     """Config 0: M=1, gate_up 17920 x 1536, seed 0 (weights quantized by the oracle)."""
