@@ -995,9 +995,11 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 
 // ----------------------------------------------- MFMA kernel with x staged in LDS (decode rows)
 //
-// Decode rows (3 .. 16) on wide and medium shapes with group size 128 and K <= 12 groups: one
-// workgroup per 32-column tile over all of K (gate_up: 560 workgroups, the M = 1 kernel's grid),
-// NW waves of GPW groups each, so no split-K and no atomics.
+// Decode rows (3 .. 16) with group size 128 and K <= 1536 (12 groups): one workgroup per 32-column
+// tile over all of K (gate_up: 560 workgroups, the M = 1 kernel's grid; k/v: 8), NW waves of GPW
+// groups each, no split-K and no atomics. Longer K (down: 70 groups) stays on the wide-tile kernel:
+// split over workgroups into ranges of 12 groups this kernel measured slower there (M = 4 / 8 / 16:
+// 5.5 / 6.1 / 7.1 against 5.2 / 5.5 / 6.9 us).
 //
 // The x operand is what limits the wide-tile MFMA kernel at these rows: its A fragments (16 rows x
 // 64 bytes per load) are re-read by every workgroup straight from L2. Here each wave first loads
@@ -1014,8 +1016,9 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 // B is one v_and_or_b32 per pair (odd nibbles in place as 16q, met by x/16): 5 VALU ops per 8
 // weights and no all-ones MFMA for sum(x). A lane loads 8 bytes (two columns) per packed row, the
 // M = 1 kernel's 128-byte tile; the waves' partial tiles meet in LDS at the end.
-// Measured on MI355X (graph replays, rotating sets): gate_up M = 4 / 8 / 16 7.5 / 8.0 / 9.3 us on
-// the wide-tile kernel against 6.3 / 6.9 / 7.8 us here, q/o 4.3 / 4.4 / 5.1 against 3.7 / 3.9 / 4.1.
+// Measured on MI355X (graph replays, rotating sets), wide-tile kernel against this one: gate_up
+// M = 4 / 8 / 16 7.50 / 8.07 / 9.37 -> 6.13 / 6.82 / 7.73 us, q/o 4.26 / 4.40 / 5.12 -> 3.61 /
+// 3.86 / 4.12, k/v (8 tiles) 4.12 / 4.29 / 5.00 -> 3.60 / 3.80 / 4.17.
 template <int MP, int NW, int GPW>
 __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "row tile");
@@ -1028,17 +1031,20 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   const int c16 = lane & 15, kb = lane >> 4;
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.qw);
-  const int ng = (a.K >> 3) >> 4;  // groups of 16 packed rows; ng <= NG
+  const int ng = (a.K >> 3) >> 4;  // groups of 16 packed rows, <= NG
   const int n0 = blockIdx.x * 32;
+  const int col = min(n0 + 2 * c16, a.N - 2);  // clamped: tail lanes load valid memory, store nothing
   const int M = a.M;
-  // ---- this wave's x rows first (unit u = lane + 64 i: packed row rr of group wave*GPW + u/(16 MP), row m)
+  // ---- this wave's x rows first (unit u = lane + 64 i: packed row rr of group wave * GPW + u / (16 MP),
+  //      row m)
   u32x4 xr[WUPT];
 #pragma unroll
   for (int i = 0; i < WUPT; ++i) {
-    const int u = lane + 64 * i, rr = u & 15, m = (u >> 4) % MP, g = min(wave * GPW + u / (16 * MP), ng - 1);
+    const int u = lane + 64 * i, rr = u & 15, m = (u >> 4) % MP;
+    const int g = min(wave * GPW + u / (16 * MP), ng - 1);
     xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)min(m, M - 1) * a.ldx + 8 * (16 * g + rr));
   }
-  // ---- then its weights: K step ks of group g is packed row 16 g + 4 ks + kb, columns n0 + 2 c16 (+1)
+  // ---- then its weights: K step ks of group g is packed row 16 g + 4 ks + kb, columns col, col + 1
   u32x2 w[GPW][4];
   uint32_t sv[GPW], zv[GPW];
 #pragma unroll
@@ -1047,9 +1053,9 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       w[gi][ks] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x2*>(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + n0 + 2 * c16));
-    sv[gi] = *reinterpret_cast<const uint32_t*>(a.s + (int64_t)g * a.N + n0 + 2 * c16);
-    zv[gi] = *reinterpret_cast<const uint32_t*>(a.z + (int64_t)g * a.N + n0 + 2 * c16);
+          reinterpret_cast<const u32x2*>(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + col));
+    sv[gi] = *reinterpret_cast<const uint32_t*>(a.s + (int64_t)g * a.N + col);
+    zv[gi] = *reinterpret_cast<const uint32_t*>(a.z + (int64_t)g * a.N + col);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
   // ---- A records and the per-(group, row) offsets
@@ -1091,7 +1097,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
     float4_t tmp[2] = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, float4_t{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int r = 16 * g + 4 * ks + kb;
+      const int r = 16 * g + 4 * ks + kb;  // packed row (r % MP = (4 ks + kb) % MP)
       u32x4 ar = u32x4{0u, 0u, 0u, 0u};
       if (c16 < MP) ar = xs[r * MP + (c16 ^ (r & (MP - 1)))];
       const half8v A = __builtin_bit_cast(half8v, ar);
@@ -1118,18 +1124,20 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   float* red = reinterpret_cast<float*>(xs);  // [NW][MP][32]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (4 * kb + i < MP)
+    if (4 * kb + i < M)
 #pragma unroll
       for (int t = 0; t < 2; ++t) red[(wave * MP + 4 * kb + i) * 32 + 2 * c16 + t] = acc[t][i];
   }
   ldk::lds_barrier();
-  for (int o = threadIdx.x; o < MP * 32; o += NW * 64) {
-    const int row = o >> 5, col = o & 31;
-    if (row >= M) break;  // o grows with row
-    float v = ldk::sum_waves(red + row * 32 + col, MP * 32, NW);
-    if (a.bias) v += (float)a.bias[n0 + col];
-    a.out[(int64_t)row * a.ldo + n0 + col] = (half_t)v;
-  }
+  const int n = M * 32;  // outputs o = row * 32 + column of the tile
+  auto store = [&](int o, float v) {
+    const int nn = n0 + (o & 31);
+    if (nn < a.N) {
+      if (a.bias) v += (float)a.bias[nn];
+      a.out[(int64_t)(o >> 5) * a.ldo + nn] = (half_t)v;
+    }
+  };
+  for (int o = threadIdx.x; o < n; o += NW * 64) store(o, ldk::sum_waves(red + o, MP * 32, NW));
 }
 
 // ------------------------------------------------------------------------------------ dispatch
@@ -1202,19 +1210,18 @@ int cpw_from_flags(int flags) {
   return v ? 1 << (v - 1) : 0;
 }
 
-// The MFMA kernel with x staged in LDS takes decode rows 3-16 with group size 128 when its
-// whole-K 32-column tiles fill the GPU (at least 32 of them) and K holds at most 12 groups (its
-// LDS); a tuning argument that names another variant (block_n, split_k, EXACT, VALU, chunks per
-// wave) keeps the wide-tile kernel or the VALU kernel.
-bool mfma_x_applies(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int split_k, int flags) {
-  return M >= 3 && M <= 16 && gsh_rows == 4 && N % 32 == 0 && N / 32 >= 32 && (K >> 7) <= 12 && block_n == 0 &&
-         split_k <= 1 && !(flags & (LDK_EXACT | LDK_PATH_VALU | LDK_CPW_MASK));
+// The MFMA kernel with x staged in LDS takes decode rows 3-16 with group size 128 and K of at
+// most 12 groups; a tuning argument that names another variant (block_n, split_k, EXACT, VALU,
+// chunks per wave) keeps the wide-tile kernel or the VALU kernel.
+bool mfma_x_applies(int64_t M, int64_t K, int gsh_rows, int block_n, int split_k, int flags) {
+  return M >= 3 && M <= 16 && gsh_rows == 4 && (K >> 7) <= 12 && block_n == 0 && split_k <= 1 &&
+         !(flags & (LDK_EXACT | LDK_PATH_VALU | LDK_CPW_MASK));
 }
 
 template <int MP, int NW, int GPW>
 int launch_mfma_x_t(const W4Args& a, hipStream_t s) {
   (void)hipGetLastError();
-  w4a16_mfma_x_kernel<MP, NW, GPW><<<(unsigned)(a.N / 32), NW * 64, 0, s>>>(a);
+  w4a16_mfma_x_kernel<MP, NW, GPW><<<(unsigned)((a.N + 31) / 32), NW * 64, 0, s>>>(a);
   return ldk::check_launch("w4a16_mfma_x");
 }
 
@@ -1227,8 +1234,8 @@ int launch_mfma_x_mp(const W4Args& a, int nw, int gpw, hipStream_t s) {
 }
 
 int launch_mfma_x(const W4Args& a, const Plan& p, hipStream_t s) {
-  // the kernel's grid and LDS assume these; the plan only picks it when they hold
-  if (a.gsh_rows != 4 || a.N % 32 || a.M > p.mt || (int64_t)p.nw * p.cpw < ((a.K >> 3) >> 4))
+  // the kernel's LDS holds nw * cpw groups (all of K) and MP = mt rows
+  if (a.gsh_rows != 4 || a.M > p.mt || ((a.K >> 3) >> 4) > p.nw * p.cpw || (a.N + 31) / 32 > INT32_MAX)
     return ldk::fail(LDK_ERR_INVALID, "w4a16: x-staged MFMA plan does not fit M=%d N=%d K=%d", a.M, a.N, a.K);
   switch (p.mt) {
     case 4: return launch_mfma_x_mp<4>(a, p.nw, p.cpw, s);
@@ -1262,19 +1269,19 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   const bool mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
   const bool m1 = !mfma && !(flags & LDK_EXACT) && M <= 2;  // the factored VALU kernel
   p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
-  if (mfma && mfma_x_applies(M, N, K, gsh_rows, block_n, split_k, flags)) {
+  if (mfma && mfma_x_applies(M, K, gsh_rows, block_n, split_k, flags)) {
     // x staged in LDS, whole 32-column tiles: twelve waves of one group, or six of two for up to
     // four rows on grids of at least one tile per CU (gate_up M = 4: 6.3 against 6.4 us; q/o M = 4
-    // on 48 tiles: 3.9 against 3.7 us with twelve)
+    // on 48 tiles: 3.9 against 3.7 us with twelve), six of one for K <= 768
+    const int ngx = (int)((K / 8) >> gsh_rows);
     p.kern = kMfmaX;
     p.mt = M <= 4 ? 4 : M <= 8 ? 8 : 16;
     p.ln = 8;
     p.rpl = 4;
-    const int64_t ngx = (K / 8) >> gsh_rows;
     p.nw = ngx <= 6 ? 6 : (M <= 4 && N / 32 >= 256) ? 6 : 12;
-    p.cpw = (int)((ngx + p.nw - 1) / p.nw);
+    p.cpw = (ngx + p.nw - 1) / p.nw;
     p.splits = 1;
-    p.gps = (int)ngx;
+    p.gps = ngx;
     p.full = 0;
     p.mtile = 1;
     return p;

@@ -207,16 +207,18 @@ def test_config_query():
 
 
 def test_decode_rows_plan_kernels():
-    """Decode rows 3-16 on shapes of >= 32 whole 32-column tiles and K <= 12 groups of 128 run the
-    MFMA kernel with x staged in LDS; narrow shapes (k/v), long K (down) and forced tile widths
-    keep the wide-tile MFMA kernel; one and two rows the factored VALU kernel."""
+    """Decode rows 3-16 with group size 128 and K <= 1536 run the MFMA kernel with x staged in LDS;
+    longer K (down), other group sizes and forced variants keep the wide-tile MFMA kernel; one and
+    two rows the factored VALU kernel; more than 16 the MFMA blocks."""
     from kernels.w4a16 import kernel_name
     assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
     assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2>"
     assert kernel_name(8, 1536, 1536) == "w4a16_mfma_x_kernel<8, 12, 1>"
     assert kernel_name(3, 4096, 512) == "w4a16_mfma_x_kernel<4, 6, 1>"
-    assert kernel_name(16, 256, 1536).startswith("w4a16_mfma_kernel<")
+    assert kernel_name(16, 256, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
+    assert kernel_name(16, 200, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
     assert kernel_name(16, 1536, 8960).startswith("w4a16_mfma_kernel<")
+    assert kernel_name(8, 1536, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(16, 17920, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(2, 17920, 1536).startswith("w4a16_m1_kernel<")
     assert kernel_name(17, 17920, 1536).startswith("w4a16_mfma_kernel<")

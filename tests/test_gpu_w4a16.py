@@ -265,11 +265,13 @@ def test_one_hot_multi_row():
 
 # ---------------------------------------------------------------- MFMA kernel with x staged in LDS
 @pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 12, 16])
-@pytest.mark.parametrize("N,K", [(17920, 1536), (2048, 1536), (1536, 1536), (1024, 512)])
+@pytest.mark.parametrize("N,K", [(17920, 1536), (2048, 1536), (1536, 1536), (1024, 512), (256, 1536),
+                                 (200, 1536), (4100, 1280)])
 def test_mfma_x_rows(M, N, K):
     """Decode rows on the x-staged MFMA kernel: row tiles of 4/8/16 with rows past M staged as
     zeros, twelve waves of one group, six of two (gate_up at <= 4 rows) and six of one (K = 512:
-    four groups, two waves idle)."""
+    four groups, two waves idle; K = 1280: ten groups, two waves idle); column tails inside a
+    32-column tile (N = 200, 4100)."""
     from kernels.w4a16 import kernel_name
     assert kernel_name(M, N, K).startswith("w4a16_mfma_x_kernel<")
     _run(M, N, K)
