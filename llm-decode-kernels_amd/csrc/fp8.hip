@@ -533,7 +533,11 @@ W8Plan make_w8_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, i
   if (split_k > 0) {
     kps = (K + split_k - 1) / split_k;
   } else {
-    const int64_t per = (passes(p.rpl) + kW8MaxSplits - 1) / kW8MaxSplits;  // passes per split
+    int64_t per = (passes(p.rpl) + kW8MaxSplits - 1) / kW8MaxSplits;  // passes per split
+    // two passes per split where that still gives every CU 1.5 workgroups: half the split-K
+    // partials (gate_up M = 1: 420 workgroups of two passes 7.60 us, 840 of one 7.92 us; two
+    // passes are not overlapped, so the grids below keep one)
+    if (per == 1 && tiles * p.mblocks * ((passes(p.rpl) + 1) / 2) >= 384) per = 2;
     kps = per * rpp;
   }
   kps = (kps + 7) / 8 * 8;
