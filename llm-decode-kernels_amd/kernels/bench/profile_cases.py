@@ -215,6 +215,13 @@ CASES = {
     "w4a16_gate_up_m8_valu": lambda r: case_w4a16(8, 17920, 1536, r, {"GEMV": True}),
     "w4a16_down_m4": lambda r: case_w4a16(4, 1536, 8960, r),
     "w4a16_down_m4_valu": lambda r: case_w4a16(4, 1536, 8960, r, {"GEMV": True}),
+    # decode rows 4-16: the library's x-staged MFMA kernel against the wide-tile MFMA kernel (forced)
+    "w4a16_gate_up_m4_wide": lambda r: case_w4a16(4, 17920, 1536, r, {"MFMA": True, "block_n": 128}),
+    "w4a16_gate_up_m16_wide": lambda r: case_w4a16(16, 17920, 1536, r, {"MFMA": True, "block_n": 128}),
+    "w4a16_o_m16": lambda r: case_w4a16(16, 1536, 1536, r),
+    "w4a16_o_m16_wide": lambda r: case_w4a16(16, 1536, 1536, r, {"MFMA": True, "block_n": 32}),
+    "w4a16_k_m16": lambda r: case_w4a16(16, 256, 1536, r),
+    "w4a16_k_m16_wide": lambda r: case_w4a16(16, 256, 1536, r, {"MFMA": True, "block_n": 32}),
     # prefill GEMMs (the library's choice at these rows)
     "w4a16_qkv_m2048": lambda r: case_w4a16(2048, 2048, 1536, r),
     "w4a16_o_m2048": lambda r: case_w4a16(2048, 1536, 1536, r),
