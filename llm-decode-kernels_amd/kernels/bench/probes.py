@@ -1,6 +1,7 @@
 """ctypes binding of kernels/bench/libldk_probe.so, the calibration kernels of the roofline
 measurements (kernels/bench/probe.hip): an empty kernel, a contiguous read and the W4A16 M = 1
-kernel's tile pattern as loads only. Used by kernels.bench.profile_cases."""
+kernel's tile pattern as loads only, and K pieces with their cross-workgroup reductions. Used by
+kernels.bench.profile_cases."""
 
 from __future__ import annotations
 
@@ -25,6 +26,7 @@ def _load():
         lib.ldk_probe_empty.argtypes = [_i32, _i32, _vp]
         lib.ldk_probe_stream.argtypes = [_vp, _i64, _i32, _vp, _vp]
         lib.ldk_probe_tile.argtypes = [_vp, _i32, _i32, _vp, _vp]
+        lib.ldk_probe_piece.argtypes = [_i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp]
         _lib_probe = lib
     return _lib_probe
 
@@ -56,3 +58,16 @@ def tile(qweight: torch.Tensor, sink: torch.Tensor):
     assert sink.dtype == torch.int32 and sink.numel() >= N // 32 * 384
     _ok(_load().ldk_probe_tile(_vp(qweight.data_ptr()), R, N, _vp(sink.data_ptr()), _stream()),
         "probe_tile")
+
+
+PIECE_SHAPES = {"whole32x192": 0, "piece64x64": 1, "piece256x16": 2, "piece256x4": 3}
+PIECE_REDUCTIONS = {"none": 0, "store": 1, "fixed_atomic": 2, "f32_atomic": 3}
+
+
+def piece(shape: str, red: str, qweight: torch.Tensor, ws: torch.Tensor, out: torch.Tensor):
+    """qweight [R, N] int32 read as `shape` pieces, partials met by `red` (probe.hip)."""
+    R, N = qweight.shape
+    assert qweight.dtype == torch.int32 and qweight.is_contiguous()
+    assert ws.nbytes >= N * 8 + 64 * N * 4 and out.dtype == torch.float16 and out.numel() >= N
+    _ok(_load().ldk_probe_piece(PIECE_SHAPES[shape], PIECE_REDUCTIONS[red], _vp(qweight.data_ptr()), R, N,
+                                _vp(ws.data_ptr()), _vp(out.data_ptr()), _stream()), "probe_piece")

@@ -11,7 +11,8 @@ launch reads its weights from HBM. Cases run one after another, `--reps` launche
     rocprofv3 --pmc VALUBusy MfmaUtil -d OUT -o prof -- python3 -m kernels.bench.profile_cases
     python3 -m kernels.bench.counters OUT        # one table per kernel and grid
 
-`--cases` picks a subset by name (comma-separated).
+`--cases` picks a subset by name (comma-separated). `--graph` times each case instead, in hipGraph
+replays over the same rotating sets (the sweep's method), and prints microseconds per launch.
 """
 
 from __future__ import annotations
@@ -26,7 +27,19 @@ from kernels.bench.harness import n_copies, tensor_bytes
 GS = 128
 
 
+GRAPH = False  # --graph: time each case in hipGraph replays instead of launching it eagerly
+
+
 def _rotate(fn, sets, reps):
+    if GRAPH:
+        from kernels.bench.harness import GraphTimer
+
+        timer = GraphTimer(fn, sets)
+        try:
+            print(f"  graph-timed: {timer.median_ms_per_call() * 1e3:.3f} us per launch", flush=True)
+        finally:
+            timer.close()
+        return
     for i in range(reps):
         fn(*sets[i % len(sets)])
 
@@ -163,25 +176,38 @@ def case_probes(kind: str, reps: int):
     gate_up weight, 192 x 17920 int32 = 13.76 MB, in rotating copies that defeat the MALL."""
     from kernels.bench import probes
 
+    # 74 launches per set list, as many as a rotating case has: a graph of one empty node would
+    # time the graph launch itself
     if kind == "empty1":
-        for _ in range(reps):
-            probes.empty(1, 64)
+        _rotate(lambda: probes.empty(1, 64), [()] * 74, reps)
         return
     if kind == "empty_grid":  # the headline kernel's grid: 800 workgroups of 384 lanes
-        for _ in range(reps):
-            probes.empty(800, 384)
+        _rotate(lambda: probes.empty(800, 384), [()] * 74, reps)
         return
     R, N = 192, 17920
     copies = n_copies(R * N * 4)
     buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
     sink = torch.zeros(N // 32 * 384, dtype=torch.int32, device="cuda")
-    for i in range(reps):
-        if kind == "stream":
-            probes.stream(buf[i % copies], sink, loads=1)
-        elif kind == "stream16":
-            probes.stream(buf[i % copies], sink, loads=16)
-        else:
-            probes.tile(buf[i % copies], sink)
+    sets = [(buf[i],) for i in range(copies)]
+    if kind == "stream":
+        _rotate(lambda b: probes.stream(b, sink, loads=1), sets, reps)
+    elif kind == "stream16":
+        _rotate(lambda b: probes.stream(b, sink, loads=16), sets, reps)
+    else:
+        _rotate(lambda b: probes.tile(b, sink), sets, reps)
+
+
+def case_piece(shape: str, red: str, reps: int):
+    """The packed gate_up weight (13.76 MB, rotating copies) read as K pieces per workgroup, their
+    partials met by one of the reductions of kernels/bench/probe.hip."""
+    from kernels.bench import probes
+
+    R, N = 192, 17920
+    copies = n_copies(R * N * 4)
+    buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
+    ws = torch.zeros(N * 8 + 64 * N * 4, dtype=torch.uint8, device="cuda")
+    out = torch.zeros(N, dtype=torch.float16, device="cuda")
+    _rotate(lambda b: probes.piece(shape, red, b, ws, out), [(buf[i],) for i in range(copies)], reps)
 
 
 CASES = {
@@ -191,6 +217,13 @@ CASES = {
     "probe_stream_13.76MB": lambda r: case_probes("stream", r),
     "probe_stream16_13.76MB": lambda r: case_probes("stream16", r),
     "probe_tile_gate_up": lambda r: case_probes("tile", r),
+    # K pieces of the same bytes and the cost of meeting their partials (probe.hip)
+    **{f"probe_{shape}_{red}": (lambda r, shape=shape, red=red: case_piece(shape, red, r))
+       for shape, reds in (("whole32x192", ("none", "store", "fixed_atomic")),
+                           ("piece64x64", ("none", "store", "fixed_atomic", "f32_atomic")),
+                           ("piece256x16", ("none", "store", "fixed_atomic")),
+                           ("piece256x4", ("none",)))
+       for red in reds},
     "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
     "w4a16_down_m1": lambda r: case_w4a16(1, 1536, 8960, r),
     "w4a16_gate_up_m2": lambda r: case_w4a16(2, 17920, 1536, r),
@@ -239,12 +272,18 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=40)
     ap.add_argument("--cases", default=",".join(CASES))
+    ap.add_argument("--graph", action="store_true",
+                    help="time each case in hipGraph replays (kernels.bench.harness.GraphTimer)")
     args = ap.parse_args(argv)
+    global GRAPH
+    GRAPH = args.graph
     torch.cuda.init()
     for name in args.cases.split(","):
+        print(f"case {name}:", flush=True)
         CASES[name](args.reps)
         torch.cuda.synchronize()
-        print(f"case {name}: {args.reps} launches", flush=True)
+        if not GRAPH:
+            print(f"  {args.reps} launches", flush=True)
     return 0
 
 
