@@ -338,8 +338,9 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 //  * B operand: for each 32-row K step it loads rows k0 + 8 kb + i (i < 8) at columns
 //    n0 + 8 c16 .. +7, one 8-byte load per row (16 lanes cover a 128-byte line of a row);
 //    an in-register 8x8 byte transpose (v_perm_b32, 4x4 blocks) gives each of its 8 columns its
-//    8 consecutive K bytes, decoded exactly to fp16 (v_cvt_pk_f32_fp8, then v_cvt_pkrtz: every
-//    e4m3 value is an fp16 value). Column j of the lane feeds MFMA tile j (column c16 of tile j
+//    8 consecutive K bytes, decoded exactly to fp16 by gfx950's v_cvt_scalef32_pk_f16_fp8 at
+//    scale 1 (two bytes per op; every e4m3 value is an fp16 value: against v_cvt_pk_f32_fp8 then
+//    v_cvt_pkrtz, half the decode ops). Column j of the lane feeds MFMA tile j (column c16 of tile j
 //    is the real column n0 + 8 c16 + j).
 //  * A operand: x row m = c16, K block 8 kb, one 16-byte load (zeros past M or past K).
 // A workgroup owns 128 columns and a K range; its waves take K steps round-robin, KSW per pass
@@ -408,11 +409,9 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
       for (int j = 0; j < 8; ++j) {
         u32x4 b;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(t[j][h], false);
-          const float2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(t[j][h], true);
-          b[2 * h + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo[0], lo[1]));
-          b[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(hi[0], hi[1]));
+        for (int h = 0; h < 2; ++h) {  // two e4m3 bytes to two fp16 per op (scale 1: exact)
+          b[2 * h + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(t[j][h], 1.0f, false));
+          b[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(t[j][h], 1.0f, true));
         }
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), acc[j], 0, 0, 0);
       }

@@ -240,3 +240,46 @@ def test_mfma_one_hot_rows_exact():
     ref = of.e4m3_decode(codes[::3][:16]).astype(np.float16)
     assert np.array_equal(bits16(to_np(out)) & 0x7FFF | (bits16(ref) & 0x8000) * (ref != 0),
                           bits16(ref) & 0x7FFF | (bits16(ref) & 0x8000) * (ref != 0))
+
+
+# ---------------------------------------------------------------- decode rows through the library's plan
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 16])
+@pytest.mark.parametrize("N,K", [(17920, 1536), (2048, 1536), (1536, 1536), (256, 1536), (1040, 512),
+                                 (48, 96)])
+def test_decode_rows_default_plan(M, N, K):
+    """Decode rows 3-16 on the library's choice (the MFMA kernel), on the Qwen shapes, a column
+    tail (N = 1040) and short K, against the oracle."""
+    _run(M, N, K)
+
+
+def test_decode_rows_bias_strided_and_unaligned_rows():
+    """Bias; x as a row-strided view (ldx > K); x not 16-byte aligned."""
+    _run(7, 2048, 1536, bias=True)
+    w, x = cases.w4a16_case(6, 1024, 768, 7)
+    owq, os_ = of.quantize_fp8(w.numpy())
+    ref = of.w8a16_ref(x.numpy(), owq, os_, None)
+    big = torch.zeros(6, 1024, dtype=torch.float16, device="cuda")
+    big[:, :768] = x.cuda()
+    assert_north_star(w8a16_matmul(big[:, :768], dev(owq).view(FP8), dev(os_)), ref)
+    off = torch.zeros(6 * 768 + 1, dtype=torch.float16, device="cuda")
+    xv = off[1:].view(6, 768)
+    xv.copy_(x.cuda())
+    assert_north_star(w8a16_matmul(xv, dev(owq).view(FP8), dev(os_)), ref)
+
+
+def test_mfma_every_code_exact():
+    """x row m = e_k and scale 1 through the MFMA kernel at K = 32: y[m, n] = e4m3(wq[k, n])
+    exactly for every finite code (32 rows x 256 columns hold them all)."""
+    K, N = 32, 256
+    codes = ((np.arange(K)[:, None] * 16 + np.arange(N)[None, :] * 7) % 256).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    wq = dev(codes).view(FP8)
+    ones = torch.ones(N, dtype=torch.float16, device="cuda")
+    for k0 in (0, 16):
+        x = torch.zeros(16, K, dtype=torch.float16, device="cuda")
+        x[torch.arange(16), k0 + torch.arange(16)] = 1.0
+        got = to_np(w8a16_matmul(x, wq, ones))
+        ref = of.e4m3_decode(codes[k0:k0 + 16]).astype(np.float16)
+        nz = ref != 0
+        assert np.array_equal(bits16(got)[nz], bits16(ref)[nz]), k0
+        assert np.all(got[~nz] == 0)
