@@ -82,7 +82,9 @@ __device__ __forceinline__ void ring_barrier() {
 // compiler's wait insertion then does not track them, so it adds no conservative vmcnt wait before
 // the LDS reads of other stages (it would after the loop's back edge, where it no longer knows
 // which LDS array each pending load writes); the ring's own vmcnt waits order them. M0 holds the
-// LDS base. The address is base + voffset + soffset; only voffset is checked against the
+// LDS base for the load; the asm restores M0's previous value itself (M0 is reserved to the
+// compiler, which does not save a clobbered M0). The address is base + voffset + soffset; only
+// voffset is checked against the
 // resource's size, so every load that relies on the check (x rows past M, scales past N) keeps
 // its whole offset in voffset, and soffset carries only the uniform K-step offset of loads that
 // stay inside their arrays.
@@ -90,10 +92,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 __device__ __forceinline__ void dma_buffer16(u32x4 rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
-               :
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %1, %2, %4 offen lds\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
                : "v"(voffset), "s"(rsrc), "s"(lds_base), "s"(soffset)
-               : "memory", "m0");
+               : "memory");
 }
 // Raw buffer descriptor over [p, p + bytes): a load at an offset past it returns zeros (and, to
 // LDS, writes zeros).
