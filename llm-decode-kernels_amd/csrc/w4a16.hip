@@ -1011,14 +1011,18 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 //    lanes writing one row's 16 packed rows and the 16 lanes reading one packed row's 16 rows hit
 //    distinct LDS banks;
 //  - per (group, row) the offset c = 1024 * sum(A) (the magic 1024 of every decoded weight times
-//    the staged x) and sum(x), reduced over the 16 lanes of a group with DPP row rotations, for
-//    the epilogue s * (sum x*(1024+q) - c - z * sum x) = s * sum x*(q - z).
+//    the staged x) and sum(x), for the epilogue s * (sum x*(1024+q) - c - z * sum x) =
+//    s * sum x*(q - z), come from one more MFMA per K step against a constant B whose columns
+//    0-7 pick the even pairs and 8-15 the odd (x/16) pairs: E = sum of the even x, O = sum of the
+//    odd x / 16, c = 1024 (E + O), sum x = E + 16 O (a DPP rotation by 8 lanes brings the two
+//    halves together). Summing them in the staging lanes instead (DPP row reductions of two
+//    values per record) cost 0.35 us at 16 rows on gate_up.
 // B is one v_and_or_b32 per pair (odd nibbles in place as 16q, met by x/16): 5 VALU ops per 8
 // weights and no all-ones MFMA for sum(x). A lane loads 8 bytes (two columns) per packed row, the
 // M = 1 kernel's 128-byte tile; the waves' partial tiles meet in LDS at the end.
 // Measured on MI355X (graph replays, rotating sets), wide-tile kernel against this one: gate_up
-// M = 4 / 8 / 16 7.50 / 8.07 / 9.37 -> 6.13 / 6.82 / 7.73 us, q/o 4.26 / 4.40 / 5.12 -> 3.61 /
-// 3.86 / 4.12, k/v (8 tiles) 4.12 / 4.29 / 5.00 -> 3.60 / 3.80 / 4.17.
+// M = 4 / 8 / 16 7.50 / 8.07 / 9.37 -> 5.91 / 6.68 / 7.48 us, q/o 4.26 / 4.40 / 5.12 -> 3.48 /
+// 3.69 / 3.99, k/v (8 tiles) 4.12 / 4.29 / 5.00 -> 3.33 / 3.49 / 3.85.
 template <int MP, int NW, int GPW>
 __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "row tile");
@@ -1026,7 +1030,6 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   static_assert(WUNITS % 64 == 0, "whole staging units per lane");
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
   __shared__ __align__(16) u32x4 xs[NG * 16 * MP];  // A records; the waves' partial tiles at the end
-  __shared__ float2_t st[NG][MP];                   // (c, sum x) per group and row
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
   ldk::pin_sgpr(a.x);
@@ -1058,34 +1061,22 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
     zv[gi] = *reinterpret_cast<const uint32_t*>(a.z + (int64_t)g * a.N + col);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
-  // ---- A records and the per-(group, row) offsets
+  // ---- A records
   const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
 #pragma unroll
   for (int i = 0; i < WUPT; ++i) {
     const int u = lane + 64 * i, rr = u & 15, m = (u >> 4) % MP, g = wave * GPW + u / (16 * MP);
     const u32x4 d = m < M ? xr[i] : u32x4{0u, 0u, 0u, 0u};  // rows past M stage zeros
-    const half2_t a0 = ldk::u2h2(perm_lo(d[0], d[2])), a1 = ldk::u2h2(perm_hi(d[0], d[2]));
-    const half2_t a2 = ldk::u2h2(perm_lo(d[1], d[3])), a3 = ldk::u2h2(perm_hi(d[1], d[3]));
-    const half2_t b1 = a1 * sixteenth, b3 = a3 * sixteenth;
-    const float se = ((float)a0[0] + (float)a0[1]) + ((float)a2[0] + (float)a2[1]);
-    float c = 1024.0f * (se + (((float)b1[0] + (float)b1[1]) + ((float)b3[0] + (float)b3[1])));
-    float sx = se + (((float)a1[0] + (float)a1[1]) + ((float)a3[0] + (float)a3[1]));
-    // sums over the 16 packed rows of the group: the 16 lanes of a DPP row, in a fixed order
-    c += ldk::row_ror<1>(c);
-    sx += ldk::row_ror<1>(sx);
-    c += ldk::row_ror<2>(c);
-    sx += ldk::row_ror<2>(sx);
-    c += ldk::row_ror<4>(c);
-    sx += ldk::row_ror<4>(sx);
-    c += ldk::row_ror<8>(c);
-    sx += ldk::row_ror<8>(sx);
-    if (g < ng) {
+    const half2_t b1 = ldk::u2h2(perm_hi(d[0], d[2])) * sixteenth, b3 = ldk::u2h2(perm_hi(d[1], d[3])) * sixteenth;
+    if (g < ng)
       xs[(16 * g + rr) * MP + (m ^ (rr & (MP - 1)))] =
-          u32x4{ldk::h22u(a0), ldk::h22u(b1), ldk::h22u(a2), ldk::h22u(b3)};
-      if (rr == 0) st[g][m] = float2_t{c, sx};
-    }
+          u32x4{perm_lo(d[0], d[2]), ldk::h22u(b1), perm_lo(d[1], d[3]), ldk::h22u(b3)};
   }
   ldk::wave_lds_sync();
+  // the stats MFMA's B: column c16 < 8 ones at the even pairs (1, 1, 0, 0, 1, 1, 0, 0), c16 >= 8
+  // at the odd ones
+  const uint32_t one2 = 0x3C003C00u, ev = c16 < 8 ? one2 : 0u, od = c16 < 8 ? 0u : one2;
+  const half8v bstat = __builtin_bit_cast(half8v, u32x4{ev, od, ev, od});
   // ---- MFMA over the wave's groups: tile t holds columns n0 + 2 c16 + t
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
@@ -1095,12 +1086,14 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
     const int g = wave * GPW + gi;
     if (g >= ng) break;  // uniform
     float4_t tmp[2] = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, float4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    float4_t sacc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};  // E (c16 < 8) or O (c16 >= 8) per row
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int r = 16 * g + 4 * ks + kb;  // packed row (r % MP = (4 ks + kb) % MP)
       u32x4 ar = u32x4{0u, 0u, 0u, 0u};
       if (c16 < MP) ar = xs[r * MP + (c16 ^ (r & (MP - 1)))];
       const half8v A = __builtin_bit_cast(half8v, ar);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bstat, sacc, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t wc = w[gi][ks][t], v = wc >> 8;
@@ -1111,12 +1104,12 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
     const half2_t s2 = ldk::u2h2(sv[gi]), z2 = ldk::u2h2(zv[gi]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // element i of lane (c16, kb): row 4 kb + i
-      if (4 * kb + i < MP) {
-        const float2_t k = st[g][4 * kb + i];
+      const float mine = sacc[i], other = ldk::row_ror<8>(mine);  // lane c16 ^ 8 of the same row
+      const float e = c16 < 8 ? mine : other, o = c16 < 8 ? other : mine;
+      const float c = 1024.0f * (e + o), sx = __builtin_fmaf(16.0f, o, e);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          acc[t][i] = __builtin_fmaf((float)s2[t], tmp[t][i] - __builtin_fmaf((float)z2[t], k[1], k[0]), acc[t][i]);
-      }
+      for (int t = 0; t < 2; ++t)
+        acc[t][i] = __builtin_fmaf((float)s2[t], tmp[t][i] - __builtin_fmaf((float)z2[t], sx, c), acc[t][i]);
     }
   }
   // ---- the NW partial tiles meet in LDS (over the records, once every wave is done with them)
