@@ -459,9 +459,14 @@ struct W8Plan {
 
 constexpr int kW8MfmaWaves = 8;
 
-// MFMA plan (M >= 8): 128-column tiles; K splits so that a workgroup's K steps fit one pass of
-// at most 6 per wave, and small tile counts split further (>= 8 steps per piece) to give the
-// grid some 64 workgroups.
+// MFMA plan: 128-column tiles. Shapes of at least 128 tiles split K only as far as one pass of
+// at most 6 K steps per wave needs (gate_up: 140 workgroups over all of K; a split there adds
+// 2-3 us of fixed-point atomics at 8-16 rows). Narrower decode shapes take pieces of 16 K steps
+// (2 per wave, 64 KB of weights), halved while the grid has fewer than 64 workgroups. On MI355X
+// (graph-timed, M = 4 / 8 / 16): down 1536x8960 in 18 pieces 7.46 / 8.95 / 10.88 us against 6
+// pieces of 47 steps 9.41 / 10.61 / 12.55 (72 workgroups streaming 196 KB each); k/v 256x1536 in
+// 24 pieces of 2 steps 3.90 / 5.09 / 6.77 against 6 of 8 steps 4.44 / 5.44 / 7.11; q/o stays at
+// 6 pieces of 8 steps (72 workgroups: 5.02 / 6.03 / 7.80, 12 pieces 5.43 / 6.67 / 8.47).
 W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t ws_bytes) {
   W8Plan p{};
   p.mfma = true;
@@ -471,9 +476,17 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t w
   p.nw = kW8MfmaWaves;
   const int64_t tiles = (N + 127) / 128;
   const int64_t steps = (K + 31) / 32;
-  int64_t splits = split_k > 0 ? split_k
-                               : std::max<int64_t>((steps + 6 * p.nw - 1) / (6 * p.nw),
-                                                   std::min<int64_t>(steps / 8, (64 + tiles - 1) / tiles));
+  const int64_t one_pass = (steps + 6 * p.nw - 1) / (6 * p.nw);  // fewest splits of one pass each
+  int64_t splits;
+  if (split_k > 0) {
+    splits = split_k;
+  } else if (tiles >= 128 || M > 16) {
+    splits = std::max<int64_t>(one_pass, std::min<int64_t>(steps / 8, (64 + tiles - 1) / tiles));
+  } else {
+    int64_t piece = 16;
+    while (piece > 2 && tiles * ((steps + piece - 1) / piece) < 64) piece /= 2;
+    splits = std::max<int64_t>(one_pass, (steps + piece - 1) / piece);
+  }
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, kW8MaxSplits));
   const int64_t sps = (steps + splits - 1) / splits;  // K steps per split
   p.kps = (int)(sps * 32);

@@ -1258,7 +1258,11 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // kernel (4 VALU ops per 8 weights for all 16 rows of its B operand). A block_n only the VALU
   // kernels take (16 or 32) keeps M <= 8 on the VALU path. EXACT keeps M <= 8 on the VALU
   // kernels, which dequantize every weight as dequantize_ref does.
-  const bool mfma_auto = M > 8 || (!(flags & LDK_EXACT) && M > 2 && (block_n == 0 || block_n >= 64));
+  // Two rows on a narrow shape of more than 2 MB (down) also take the MFMA kernel, split K ten
+  // ways: 4.9 against 5.4 us for the two-row VALU kernel (wide shapes keep it: gate_up 5.7 us).
+  const bool narrow_long = N < 128 * 128 && wbytes > (2 << 20);
+  const bool mfma_auto = M > 8 || (!(flags & LDK_EXACT) && (M > 2 || (M == 2 && narrow_long && block_n == 0)) &&
+                                   (block_n == 0 || block_n >= 64));
   const bool mfma = (flags & LDK_PATH_MFMA) || (mfma_auto && !(flags & LDK_PATH_VALU));
   const bool m1 = !mfma && !(flags & LDK_EXACT) && M <= 2;  // the factored VALU kernel
   p.kern = mfma ? kMfma : m1 ? kM1 : kValu;
@@ -1313,8 +1317,11 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // workgroup per CU). Multi-row splits carry M outputs per column through returning atomics,
   // so small shapes keep whole tiles and split K over the waves of a workgroup instead (q/o at
   // M = 16: 5.9 us whole, 25 us split twelve ways).
+  // (MFMA: about 240 workgroups for up to 4 rows, 192 beyond, where each split's atomics carry
+  // more rows: down M = 2 / 4 / 8 / 16 in 10 splits 4.9 / 5.0 / 5.9 / 7.6 us, in 8 splits
+  // 5.3 / 5.2 / 5.5 / 6.9)
   if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20) && M <= 16)
-    splits = m1 ? std::max<int64_t>(2, 256 / tiles) : (192 + tiles - 1) / tiles;
+    splits = m1 ? std::max<int64_t>(2, 256 / tiles) : ((M <= 4 ? 240 : 192) + tiles - 1) / tiles;
   if (M > 16) splits = 1;  // row blocks fill the grid; a K split would carry every row through atomics
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);

@@ -208,8 +208,9 @@ def test_config_query():
 
 def test_decode_rows_plan_kernels():
     """Decode rows 3-16 with group size 128 and K <= 1536 run the MFMA kernel with x staged in LDS;
-    longer K (down), other group sizes and forced variants keep the wide-tile MFMA kernel; one and
-    two rows the factored VALU kernel; more than 16 the MFMA blocks."""
+    longer K (down), other group sizes and forced variants keep the wide-tile MFMA kernel, which
+    also takes two rows of down; one and two rows otherwise the factored VALU kernel; more than 16
+    the MFMA blocks."""
     from kernels.w4a16 import kernel_name
     assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
     assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2>"
@@ -221,6 +222,8 @@ def test_decode_rows_plan_kernels():
     assert kernel_name(8, 1536, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(16, 17920, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(2, 17920, 1536).startswith("w4a16_m1_kernel<")
+    assert kernel_name(2, 1536, 8960).startswith("w4a16_mfma_kernel<")  # two rows, narrow > 2 MB
+    assert kernel_name(2, 1536, 1536).startswith("w4a16_m1_kernel<")
     assert kernel_name(17, 17920, 1536).startswith("w4a16_mfma_kernel<")
 
 
