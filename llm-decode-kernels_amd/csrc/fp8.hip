@@ -345,30 +345,43 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 //  * A operand: x row m = c16, K block 8 kb, one 16-byte load (zeros past M or past K).
 // A workgroup owns 128 columns and a K range; its waves take K steps round-robin, KSW per pass
 // with every load of the pass in flight; partial tiles meet in LDS, then the per-channel scale.
-template <int NW, int KSW>
+// 64-column tiles share each 128-byte line of a K row with their neighbour: tiles 2p and 2p + 1
+// run as workgroups b and b + 8, which the dispatcher places on the same XCD (workgroup b goes to
+// XCD b % 8) at about the same time, so the line comes into that XCD's L2 once. The tiles past the
+// last whole group of 16 keep their own index.
+__device__ __forceinline__ int w8_pair_tile(int b, int tiles) {
+  if (b >= (tiles & ~15)) return b;
+  const int r = b >> 3;
+  return 2 * (8 * (r >> 1) + (b & 7)) + (r & 1);
+}
+
+template <int NW, int KSW, int CW>
 __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split sp) {
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
-  constexpr int CW = 128;
+  static_assert(CW == 128 || CW == 64, "128 or 64 columns");
+  constexpr int CPL = CW / 16;  // columns per lane: one MFMA tile each
+  typedef uint32_t wrow_t __attribute__((ext_vector_type(CPL / 4)));
   extern __shared__ __align__(16) float wred[];  // [NW][16][CW]
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.wq);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
-  const int tile = blockIdx.x, split = blockIdx.y;
+  const int tile = CW == 64 ? w8_pair_tile((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+  const int split = blockIdx.y;
   const int m0 = blockIdx.z * 16;  // row block (rows past 16 re-read the weights from the MALL)
   const int n0 = tile * CW;
-  const int col = min(n0 + 8 * c16, a.N - 8);  // clamped: tail lanes load valid memory, store nothing
+  const int col = min(n0 + CPL * c16, a.N - CPL);  // clamped: tail lanes load valid memory, store nothing
   const int rb = split * sp.kps, re = min(a.K, rb + sp.kps);
   const int nks = (re - rb + 31) / 32;  // K steps of this workgroup
   const bool xrow_ok = m0 + c16 < a.M;
   const half_t* xrow = a.x + (int64_t)min(m0 + c16, a.M - 1) * a.ldx;
 
-  float4_t acc[8];
+  float4_t acc[CPL];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < CPL; ++j) acc[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int s0 = wave; s0 < nks; s0 += NW * KSW) {
-    u32x2 w[KSW][8];
+    wrow_t w[KSW][8];
     u32x4 xa[KSW];
 #pragma unroll
     for (int u = 0; u < KSW; ++u) {
@@ -379,7 +392,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int r = min(kblk + i, re - 1);
-        w[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.wq + (int64_t)r * a.N + col));
+        w[u][i] = __builtin_nontemporal_load(reinterpret_cast<const wrow_t*>(a.wq + (int64_t)r * a.N + col));
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight before the first wait
@@ -387,12 +400,12 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
     for (int u = 0; u < KSW; ++u) {
       if (s0 + u * NW >= nks) break;  // uniform
       const half8v A = __builtin_bit_cast(half8v, xa[u]);
-      // 8x8 byte transpose: t[c][h] = rows 4h..4h+3 of column c
-      uint32_t t[8][2];
+      // 8 x CPL byte transpose: t[c][h] = rows 4h..4h+3 of column c
+      uint32_t t[CPL][2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {  // columns 4q .. 4q+3
+        for (int q = 0; q < CPL / 4; ++q) {  // columns 4q .. 4q+3
           const uint32_t ra = w[u][4 * h + 0][q], rbb = w[u][4 * h + 1][q];
           const uint32_t rc = w[u][4 * h + 2][q], rd = w[u][4 * h + 3][q];
           const uint32_t ab_lo = __builtin_amdgcn_perm(rbb, ra, 0x05010400u);  // a0 b0 a1 b1
@@ -406,7 +419,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
         }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < CPL; ++j) {
         u32x4 b;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {  // two e4m3 bytes to two fp16 per op (scale 1: exact)
@@ -418,13 +431,14 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
     }
   }
 
-  // tile j, element i of lane l: row 4 kb + i, column 8 c16 + j of the workgroup's 128
+  // tile j, element i of lane l: row 4 kb + i, column CPL c16 + j of the workgroup's CW
   float* red = wred + (size_t)wave * 16 * CW;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float* rrow = red + (4 * kb + i) * CW + 8 * c16;
-    *reinterpret_cast<float4_t*>(rrow) = float4_t{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
-    *reinterpret_cast<float4_t*>(rrow + 4) = float4_t{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+    float* rrow = red + (4 * kb + i) * CW + CPL * c16;
+#pragma unroll
+    for (int q = 0; q < CPL / 4; ++q)
+      *reinterpret_cast<float4_t*>(rrow + 4 * q) = float4_t{acc[4 * q][i], acc[4 * q + 1][i], acc[4 * q + 2][i], acc[4 * q + 3][i]};
   }
   ldk::lds_barrier();
   const int mrows = min(a.M - m0, 16);
@@ -459,22 +473,26 @@ struct W8Plan {
 
 constexpr int kW8MfmaWaves = 8;
 
-// MFMA plan: 128-column tiles. Shapes of at least 128 tiles split K only as far as one pass of
-// at most 6 K steps per wave needs (gate_up: 140 workgroups over all of K; a split there adds
-// 2-3 us of fixed-point atomics at 8-16 rows). Narrower decode shapes take pieces of 16 K steps
-// (2 per wave, 64 KB of weights), halved while the grid has fewer than 64 workgroups. On MI355X
-// (graph-timed, M = 4 / 8 / 16): down 1536x8960 in 18 pieces 7.46 / 8.95 / 10.88 us against 6
-// pieces of 47 steps 9.41 / 10.61 / 12.55 (72 workgroups streaming 196 KB each); k/v 256x1536 in
-// 24 pieces of 2 steps 3.90 / 5.09 / 6.77 against 6 of 8 steps 4.44 / 5.44 / 7.11; q/o stays at
-// 6 pieces of 8 steps (72 workgroups: 5.02 / 6.03 / 7.80, 12 pieces 5.43 / 6.67 / 8.47).
-W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t ws_bytes) {
+// MFMA plan. Shapes of at least 128 tiles of 128 columns (gate_up: 140) keep 128-column tiles
+// and split K only as far as one pass of at most 6 K steps per wave needs, so gate_up runs
+// whole K (a three-way split helps only at 4 rows, 8.9 -> 8.3 us, and costs 1-3 us of fixed-point
+// atomics at 8-16 rows; 64-column tiles there measured 12.1 / 12.7 / 15.0 against 8.9 / 9.5 /
+// 10.6 us at M = 4 / 8 / 16). Narrower decode shapes take 64-column tiles and pieces of 16 K
+// steps (2 per wave), halved while the grid has fewer than 64 workgroups. On MI355X (graph-timed,
+// M = 4 / 8 / 16), against 128-column tiles in six pieces: down 1536x8960 (18 pieces) 9.41 /
+// 10.61 / 12.55 -> 7.37 / 7.55 / 9.07 us, q/o 1536x1536 (3 pieces) 5.02 / 6.03 / 7.80 -> 5.01 /
+// 5.12 / 6.17, k/v 256x1536 (24 pieces of 2 steps) 4.44 / 5.44 / 7.11 -> 3.96 / 4.03 / 5.09. Half
+// the columns halve each workgroup's 16-row LDS reduction and its share of the epilogue's
+// outputs, which is where the 8- and 16-row cases spent their extra time.
+W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes) {
   W8Plan p{};
   p.mfma = true;
   p.mt = 16;
   p.mblocks = 1;
-  p.ln = 8;
+  const bool narrow = (N + 127) / 128 < 128 && M <= 16;
+  p.ln = block_n == 64 || (block_n == 0 && narrow) ? 4 : 8;
   p.nw = kW8MfmaWaves;
-  const int64_t tiles = (N + 127) / 128;
+  const int64_t tiles = (N + 16 * p.ln - 1) / (16 * p.ln);
   const int64_t steps = (K + 31) / 32;
   const int64_t one_pass = (steps + 6 * p.nw - 1) / (6 * p.nw);  // fewest splits of one pass each
   int64_t splits;
@@ -491,7 +509,7 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t w
   const int64_t sps = (steps + splits - 1) / splits;  // K steps per split
   p.kps = (int)(sps * 32);
   p.splits = (int)((steps + sps - 1) / sps);
-  p.words = ((M + 15) / 16) * tiles * 16 * 128;
+  p.words = ((M + 15) / 16) * tiles * 16 * (16 * p.ln);
   if (p.splits > 1 && (int64_t)ldk::splitk_bytes(p.words, p.splits) > ws_bytes) {
     p.splits = 1;
     p.kps = (int)(steps * 32);
@@ -501,24 +519,29 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int split_k, int64_t w
   return p;
 }
 
-template <int KSW>
+template <int KSW, int CW>
 int launch_w8_mfma_t(const W8Args& a, const W8Split& sp, hipStream_t s) {
   constexpr int NW = kW8MfmaWaves;
-  const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)sp.splits, (unsigned)((a.M + 15) / 16));
-  const size_t lds = (size_t)NW * 16 * 128 * 4;
+  const dim3 grid((unsigned)((a.N + CW - 1) / CW), (unsigned)sp.splits, (unsigned)((a.M + 15) / 16));
+  const size_t lds = (size_t)NW * 16 * CW * 4;
   (void)hipGetLastError();
-  w8a16_mfma_kernel<NW, KSW><<<grid, NW * 64, lds, s>>>(a, sp);
+  w8a16_mfma_kernel<NW, KSW, CW><<<grid, NW * 64, lds, s>>>(a, sp);
   return ldk::check_launch("w8a16_mfma");
 }
 
-int launch_w8_mfma(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+template <int CW>
+int launch_w8_mfma_cw(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
   switch (p.ksw) {
-    case 1: return launch_w8_mfma_t<1>(a, sp, s);
-    case 2: return launch_w8_mfma_t<2>(a, sp, s);
-    case 4: return launch_w8_mfma_t<4>(a, sp, s);
-    case 6: return launch_w8_mfma_t<6>(a, sp, s);
+    case 1: return launch_w8_mfma_t<1, CW>(a, sp, s);
+    case 2: return launch_w8_mfma_t<2, CW>(a, sp, s);
+    case 4: return launch_w8_mfma_t<4, CW>(a, sp, s);
+    case 6: return launch_w8_mfma_t<6, CW>(a, sp, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d K steps per wave not instantiated", p.ksw);
+}
+
+int launch_w8_mfma(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  return p.ln == 4 ? launch_w8_mfma_cw<64>(a, sp, p, s) : launch_w8_mfma_cw<128>(a, sp, p, s);
 }
 
 int w8_round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
@@ -696,9 +719,10 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   // 9.5 us MFMA at M = 8 on gate_up); block_n other than 128 keeps the
   // VALU kernel, which has the narrower tiles.
   const bool mfma = M > 16 || (flags & LDK_PATH_MFMA) || (M >= 3 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
-  if (mfma && block_n && block_n != 128) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the MFMA kernel uses block_n=128");
+  if (mfma && block_n && block_n != 128 && block_n != 64)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the MFMA kernel takes block_n 64 or 128");
   const int64_t wsb = workspace ? workspace_bytes : 0;
-  const W8Plan p = mfma ? make_w8_mfma_plan(M, N, K, split_k, wsb) : make_w8_plan(M, N, K, block_n, split_k, wsb);
+  const W8Plan p = mfma ? make_w8_mfma_plan(M, N, K, block_n, split_k, wsb) : make_w8_plan(M, N, K, block_n, split_k, wsb);
   if (split_k > 1 && p.splits == 1)
     return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
   const W8Args a{(const half_t*)x, ldx, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K};

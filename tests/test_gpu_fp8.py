@@ -283,3 +283,29 @@ def test_mfma_every_code_exact():
         nz = ref != 0
         assert np.array_equal(bits16(got)[nz], bits16(ref)[nz]), k0
         assert np.all(got[~nz] == 0)
+
+
+@pytest.mark.parametrize("M", [3, 4, 16, 17, 40])
+@pytest.mark.parametrize("N,K", [(17920, 1536), (1536, 8960), (208, 1536), (2064, 512)])
+def test_mfma_64_column_tiles(M, N, K):
+    """The MFMA kernel on 64-column tiles (block_n 64): tile pairs sharing a line are placed on
+    one XCD through the workgroup order, the tiles past the last group of 16 keep their index
+    (2064 columns: 33 tiles, the last one ragged)."""
+    _run(M, N, K, config={"MFMA": True, "block_n": 64})
+
+
+def test_mfma_64_column_tiles_every_code_exact():
+    """One-hot rows through the 64-column MFMA kernel reproduce every finite code exactly."""
+    K, N = 32, 256
+    codes = ((np.arange(K)[:, None] * 16 + np.arange(N)[None, :] * 7) % 256).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    wq = dev(codes).view(FP8)
+    ones = torch.ones(N, dtype=torch.float16, device="cuda")
+    for k0 in (0, 16):
+        x = torch.zeros(16, K, dtype=torch.float16, device="cuda")
+        x[torch.arange(16), k0 + torch.arange(16)] = 1.0
+        got = to_np(w8a16_matmul(x, wq, ones, config={"MFMA": True, "block_n": 64}))
+        ref = of.e4m3_decode(codes[k0:k0 + 16]).astype(np.float16)
+        nz = ref != 0
+        assert np.array_equal(bits16(got)[nz], bits16(ref)[nz]), k0
+        assert np.all(got[~nz] == 0)
