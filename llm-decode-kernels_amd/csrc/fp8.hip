@@ -333,7 +333,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 // ------------------------------------------------------------------------ W8A16 MFMA kernel
 //
 // Rows in blocks of 16 (padded; grid z walks the blocks, which re-read the weights from the
-// MALL) on v_mfma_f32_16x16x32_f16, for M >= 3 where the VALU kernel's
+// MALL) on v_mfma_f32_16x16x32_f16, for M >= 2 where the VALU kernel's
 // fp32 FMAs (16 x M per 16 weights) bound it. Lane l = (c16 = l % 16, kb = l / 16) of a wave:
 //  * B operand: for each 32-row K step it loads rows k0 + 8 kb + i (i < 8) at columns
 //    n0 + 8 c16 .. +7, one 8-byte load per row (16 lanes cover a 128-byte line of a row);
@@ -478,11 +478,12 @@ constexpr int kW8MfmaWaves = 8;
 // whole K (a three-way split helps only at 4 rows, 8.9 -> 8.3 us, and costs 1-3 us of fixed-point
 // atomics at 8-16 rows; 64-column tiles there measured 12.1 / 12.7 / 15.0 against 8.9 / 9.5 /
 // 10.6 us at M = 4 / 8 / 16). Narrower decode shapes take 64-column tiles and pieces of 16 K
-// steps (2 per wave), halved while the grid has fewer than 64 workgroups. On MI355X (graph-timed,
-// M = 4 / 8 / 16), against 128-column tiles in six pieces: down 1536x8960 (18 pieces) 9.41 /
-// 10.61 / 12.55 -> 7.37 / 7.55 / 9.07 us, q/o 1536x1536 (3 pieces) 5.02 / 6.03 / 7.80 -> 5.01 /
-// 5.12 / 6.17, k/v 256x1536 (24 pieces of 2 steps) 4.44 / 5.44 / 7.11 -> 3.96 / 4.03 / 5.09. Half
-// the columns halve each workgroup's 16-row LDS reduction and its share of the epilogue's
+// steps (2 per wave), halved down to 4 while the grid has fewer than 128 workgroups. On MI355X
+// (graph-timed, M = 4 / 8 / 16), against 128-column tiles in six pieces: down 1536x8960 (18
+// pieces of 16 steps, 432 workgroups) 9.41 / 10.61 / 12.55 -> 7.37 / 7.55 / 9.07 us; q/o
+// 1536x1536 (6 pieces of 8, 144 workgroups) 5.02 / 6.03 / 7.80 -> 4.62 / 4.71 / 5.74 (3 pieces:
+// 5.04 / 5.17 / 6.26); k/v 256x1536 (12 pieces of 4) 4.44 / 5.44 / 7.11 -> 3.87 / 3.92 / 4.89.
+// Half the columns halve each workgroup's 16-row LDS reduction and its share of the epilogue's
 // outputs, which is where the 8- and 16-row cases spent their extra time.
 W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes) {
   W8Plan p{};
@@ -502,7 +503,7 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
     splits = std::max<int64_t>(one_pass, std::min<int64_t>(steps / 8, (64 + tiles - 1) / tiles));
   } else {
     int64_t piece = 16;
-    while (piece > 2 && tiles * ((steps + piece - 1) / piece) < 64) piece /= 2;
+    while (piece > 4 && tiles * ((steps + piece - 1) / piece) < 128) piece /= 2;
     splits = std::max<int64_t>(one_pass, (steps + piece - 1) / piece);
   }
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, kW8MaxSplits));
@@ -715,10 +716,11 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   if (M > 16 && (flags & LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the VALU kernel takes M <= 16");
   if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: block_n=%d must be 16, 32, 64 or 128", block_n);
-  // MFMA from 3 rows (the VALU kernel's fp32 FMAs grow with M; measured at M = 4: 17.4 us VALU,
-  // 9.5 us MFMA at M = 8 on gate_up); block_n other than 128 keeps the
+  // MFMA from 2 rows (the VALU kernel's fp32 FMAs grow with M; measured at M = 4: 17.4 us VALU,
+  // 9.5 us MFMA at M = 8 on gate_up; at M = 2 gate_up / down / q/o / k/v 8.91 / 6.71 / 4.79 /
+  // 4.05 us VALU against 8.62 / 6.66 / 4.19 / 3.51 MFMA); block_n other than 128 keeps the
   // VALU kernel, which has the narrower tiles.
-  const bool mfma = M > 16 || (flags & LDK_PATH_MFMA) || (M >= 3 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
+  const bool mfma = M > 16 || (flags & LDK_PATH_MFMA) || (M >= 2 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
   if (mfma && block_n && block_n != 128 && block_n != 64)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the MFMA kernel takes block_n 64 or 128");
   const int64_t wsb = workspace ? workspace_bytes : 0;

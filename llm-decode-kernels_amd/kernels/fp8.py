@@ -5,8 +5,8 @@ channel, stored [K, N] (N contiguous). gfx950 decodes OCP e4m3 natively (v_cvt_p
 the weight bytes go straight from a 128-bit load to fp32 FMAs; the scale is applied once after
 the K reduction (fp8.py:120). Quantize/dequantize run HIP kernels that reproduce the reference
 bit for bit; like the reference's torch code they take CPU tensors too (run on the current ROCm
-GPU, results returned on the CPU). Decode shapes run the wave64 VALU GEMV with an in-workgroup split-K at M <= 2 and
-the MFMA kernel (in-register byte transpose, exact e4m3 -> fp16) from 3 rows.
+GPU, results returned on the CPU). Decode shapes run the wave64 VALU GEMV with an in-workgroup
+split-K at M = 1 and the MFMA kernel (in-register byte transpose, exact e4m3 -> fp16) from 2 rows.
 Prefill rows (the reference's tensor-core GEMM, fp8.py:42-91 run at fp8.py:221-222) run
 hand-written kernels at every row count: 17-64 rows the MFMA kernel in 16-row blocks, more rows
 the prefill GEMM (csrc/prefill.hip: 64/128-row tiles, e4m3 tiles transposed and converted to fp16

@@ -243,12 +243,13 @@ def test_mfma_one_hot_rows_exact():
 
 
 # ---------------------------------------------------------------- decode rows through the library's plan
-@pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 16])
-@pytest.mark.parametrize("N,K", [(17920, 1536), (2048, 1536), (1536, 1536), (256, 1536), (1040, 512),
-                                 (48, 96)])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 9, 16])
+@pytest.mark.parametrize("N,K", [(17920, 1536), (2048, 1536), (1536, 1536), (256, 1536), (1536, 8960),
+                                 (1040, 512), (48, 96)])
 def test_decode_rows_default_plan(M, N, K):
-    """Decode rows 3-16 on the library's choice (the MFMA kernel), on the Qwen shapes, a column
-    tail (N = 1040) and short K, against the oracle."""
+    """Decode rows 2-16 on the library's choice (the MFMA kernel: 128-column tiles over all of K
+    on gate_up, 64-column tiles split into K pieces on the narrower shapes), on the Qwen shapes,
+    a column tail (N = 1040) and short K, against the oracle."""
     _run(M, N, K)
 
 
