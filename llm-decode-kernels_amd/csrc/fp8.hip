@@ -474,9 +474,9 @@ struct W8Plan {
 constexpr int kW8MfmaWaves = 8;
 
 // MFMA plan. Shapes of at least 128 tiles of 128 columns (gate_up: 140) keep 128-column tiles
-// and split K only as far as one pass of at most 6 K steps per wave needs, so gate_up runs
-// whole K (a three-way split helps only at 4 rows, 8.9 -> 8.3 us, and costs 1-3 us of fixed-point
-// atomics at 8-16 rows; 64-column tiles there measured 12.1 / 12.7 / 15.0 against 8.9 / 9.5 /
+// and, from 5 rows, split K only as far as one pass of at most 6 K steps per wave needs, so
+// gate_up runs whole K (a three-way split costs 1-3 us of fixed-point atomics at 8-16 rows;
+// up to 4 rows it pays, below; 64-column tiles there measured 12.1 / 12.7 / 15.0 against 8.9 / 9.5 /
 // 10.6 us at M = 4 / 8 / 16). Narrower decode shapes take 64-column tiles and pieces of 16 K
 // steps (2 per wave), halved down to 4 while the grid has fewer than 128 workgroups. On MI355X
 // (graph-timed, M = 4 / 8 / 16), against 128-column tiles in six pieces: down 1536x8960 (18
@@ -499,6 +499,10 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
   int64_t splits;
   if (split_k > 0) {
     splits = split_k;
+  } else if (tiles >= 128 && M <= 4) {  // pieces of 16 steps: gate_up M = 2 / 3 / 4 in three,
+                                        // 8.76 / 8.83 / 8.73 -> 7.91 / 8.11 / 8.39 us (at 5 rows
+                                        // and more the pieces' atomics cost more than they save)
+    splits = std::max<int64_t>(one_pass, (steps + 15) / 16);
   } else if (tiles >= 128 || M > 16) {
     splits = std::max<int64_t>(one_pass, std::min<int64_t>(steps / 8, (64 + tiles - 1) / tiles));
   } else {
