@@ -158,8 +158,8 @@ struct W8Split {
 constexpr int kW8MaxSplits = 40;
 static_assert(kW8MaxSplits <= ldk::kFixMaxSplits, "split count field");
 
-__device__ __forceinline__ ldk::SplitK w8_split_ctx(const W8Split& sp) {
-  return ldk::SplitK{sp.acc, sp.side, sp.splits, (int)blockIdx.y};
+__device__ __forceinline__ ldk::SplitK w8_split_ctx(const W8Split& sp, int split = (int)blockIdx.y) {
+  return ldk::SplitK{sp.acc, sp.side, sp.splits, split};
 }
 
 // Prologues (one row) that form the activation while it is staged, with the steps of the
@@ -345,14 +345,25 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 //  * A operand: x row m = c16, K block 8 kb, one 16-byte load (zeros past M or past K).
 // A workgroup owns 128 columns and a K range; its waves take K steps round-robin, KSW per pass
 // with every load of the pass in flight; partial tiles meet in LDS, then the per-channel scale.
-// 64-column tiles share each 128-byte line of a K row with their neighbour: tiles 2p and 2p + 1
-// run as workgroups b and b + 8, which the dispatcher places on the same XCD (workgroup b goes to
-// XCD b % 8) at about the same time, so the line comes into that XCD's L2 once. The tiles past the
-// last whole group of 16 keep their own index.
-__device__ __forceinline__ int w8_pair_tile(int b, int tiles) {
-  if (b >= (tiles & ~15)) return b;
-  const int r = b >> 3;
-  return 2 * (8 * (r >> 1) + (b & 7)) + (r & 1);
+// 64-column tiles share each 128-byte line of a K row with their neighbour. Their launch is one
+// dimension over (tile, K split) pieces: the two pieces of each line pair (tiles 2q and 2q + 1,
+// one split) run as workgroups L and L + 8 of a group of 16, which the dispatcher places on the
+// same XCD (workgroup L goes to XCD L % 8) at about the same time, so the line comes into that
+// XCD's L2 once. The pairs past the last whole group of 16, then an odd last tile per split, follow
+// in plain order.
+__device__ __forceinline__ void w8_pair_piece(int b, int tiles, int& tile, int& split) {
+  const int q = tiles >> 1;  // line pairs per split
+  const int paired = 2 * q * (int)(gridDim.x / tiles);
+  const int full = paired & ~15;
+  if (b < paired) {
+    const int p = b < full ? 8 * (b >> 4) + (b & 7) : (b >> 1);  // pair index
+    const int member = b < full ? (b >> 3) & 1 : b & 1;
+    split = p / q;
+    tile = 2 * (p - split * q) + member;
+  } else {
+    split = b - paired;
+    tile = tiles - 1;
+  }
 }
 
 template <int NW, int KSW, int CW>
@@ -366,8 +377,9 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
   ldk::pin_sgpr(a.wq);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
-  const int tile = CW == 64 ? w8_pair_tile((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
-  const int split = blockIdx.y;
+  const int ntiles = (a.N + CW - 1) / CW;
+  int tile = (int)blockIdx.x, split = (int)blockIdx.y;
+  if constexpr (CW == 64) w8_pair_piece((int)blockIdx.x, ntiles, tile, split);
   const int m0 = blockIdx.z * 16;  // row block (rows past 16 re-read the weights from the MALL)
   const int n0 = tile * CW;
   const int col = min(n0 + CPL * c16, a.N - CPL);  // clamped: tail lanes load valid memory, store nothing
@@ -455,7 +467,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_mfma_kernel(W8Args a, W8Split s
       a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)v;
     } else {
       float tot;
-      if (ldk::splitk_add(w8_split_ctx(sp), sp.acc + ((size_t)blockIdx.z * gridDim.x + tile) * 16 * CW + o, v, &tot)) {
+      if (ldk::splitk_add(w8_split_ctx(sp, split), sp.acc + ((size_t)blockIdx.z * ntiles + tile) * 16 * CW + o, v, &tot)) {
         if (a.bias) tot += (float)a.bias[n];
         a.out[(int64_t)(m0 + m) * a.ldo + n] = (half_t)tot;
       }
@@ -527,7 +539,9 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
 template <int KSW, int CW>
 int launch_w8_mfma_t(const W8Args& a, const W8Split& sp, hipStream_t s) {
   constexpr int NW = kW8MfmaWaves;
-  const dim3 grid((unsigned)((a.N + CW - 1) / CW), (unsigned)sp.splits, (unsigned)((a.M + 15) / 16));
+  const unsigned tiles = (unsigned)((a.N + CW - 1) / CW), blocks = (unsigned)((a.M + 15) / 16);
+  // 64-column tiles: one dimension over (tile, split) pieces (w8_pair_piece)
+  const dim3 grid = CW == 64 ? dim3(tiles * (unsigned)sp.splits, 1, blocks) : dim3(tiles, (unsigned)sp.splits, blocks);
   const size_t lds = (size_t)NW * 16 * CW * 4;
   (void)hipGetLastError();
   w8a16_mfma_kernel<NW, KSW, CW><<<grid, NW * 64, lds, s>>>(a, sp);

@@ -232,6 +232,13 @@ CASES = {
     "w4a16_down_m16": lambda r: case_w4a16(16, 1536, 8960, r),
     "fp8_gate_up_m1": lambda r: case_fp8(1, 17920, 1536, r),
     "fp8_gate_up_m16": lambda r: case_fp8(16, 17920, 1536, r),
+    # decode rows of the other shapes: W4A16 down at two rows (MFMA), FP8 at 4 and 16 rows
+    "w4a16_down_m2": lambda r: case_w4a16(2, 1536, 8960, r),
+    "fp8_gate_up_m4": lambda r: case_fp8(4, 17920, 1536, r),
+    "fp8_down_m4": lambda r: case_fp8(4, 1536, 8960, r),
+    "fp8_down_m16": lambda r: case_fp8(16, 1536, 8960, r),
+    "fp8_o_m16": lambda r: case_fp8(16, 1536, 1536, r),
+    "fp8_k_m16": lambda r: case_fp8(16, 256, 1536, r),
     "rms_qkv_m1": lambda r: case_rms_w4a16(2048, 1536, r, True),
     "rms_gate_up_m1": lambda r: case_rms_w4a16(17920, 1536, r, False),
     "swiglu_down_m1": lambda r: case_swiglu_w4a16(1536, 8960, r),
