@@ -171,9 +171,10 @@ def case_copy(reps):
         torch.neg(a, out=b)
 
 
-def case_probes(kind: str, reps: int):
+def case_probes(kind: str, reps: int, N: int = 17920):
     """The roofline's calibration kernels (kernels/bench/probe.hip) at config 0's size: the packed
-    gate_up weight, 192 x 17920 int32 = 13.76 MB, in rotating copies that defeat the MALL."""
+    gate_up weight, 192 x 17920 int32 = 13.76 MB (or 192 x N), in rotating copies that defeat the
+    MALL."""
     from kernels.bench import probes
 
     # 74 launches per set list, as many as a rotating case has: a graph of one empty node would
@@ -184,7 +185,7 @@ def case_probes(kind: str, reps: int):
     if kind == "empty_grid":  # the headline kernel's grid: 800 workgroups of 384 lanes
         _rotate(lambda: probes.empty(800, 384), [()] * 74, reps)
         return
-    R, N = 192, 17920
+    R = 192
     copies = n_copies(R * N * 4)
     buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
     sink = torch.zeros(N // 32 * 384, dtype=torch.int32, device="cuda")
@@ -202,7 +203,7 @@ def case_piece(shape: str, red: str, reps: int):
     partials met by one of the reductions of kernels/bench/probe.hip."""
     from kernels.bench import probes
 
-    R, N = 192, 17920
+    R = 192
     copies = n_copies(R * N * 4)
     buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
     ws = torch.zeros(N * 8 + 64 * N * 4, dtype=torch.uint8, device="cuda")
@@ -225,6 +226,11 @@ CASES = {
                            ("piece256x4", ("none",)))
        for red in reds},
     "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
+    # the M = 1 kernel and the read floors at K = 1536 and wider N (2x, 4x gate_up, and the
+    # 151936-row vocabulary of the quantized lm_head): where launch and ramp stop dominating
+    **{f"w4a16_m1_n{n}": (lambda r, n=n: case_w4a16(1, n, 1536, r)) for n in (35840, 71680, 151936)},
+    **{f"probe_{kind}_n{n}": (lambda r, kind=kind, n=n: case_probes(kind, r, N=n))
+       for kind in ("stream", "tile") for n in (35840, 71680, 151936)},
     "w4a16_down_m1": lambda r: case_w4a16(1, 1536, 8960, r),
     "w4a16_gate_up_m2": lambda r: case_w4a16(2, 17920, 1536, r),
     "w4a16_gate_up_m4": lambda r: case_w4a16(4, 17920, 1536, r),
