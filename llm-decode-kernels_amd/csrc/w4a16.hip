@@ -1018,25 +1018,32 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 //    halves together). Summing them in the staging lanes instead (DPP row reductions of two
 //    values per record) cost 0.35 us at 16 rows on gate_up.
 // B is one v_and_or_b32 per pair (odd nibbles in place as 16q, met by x/16): 5 VALU ops per 8
-// weights and no all-ones MFMA for sum(x). A lane loads 8 bytes (two columns) per packed row, the
-// M = 1 kernel's 128-byte tile; the waves' partial tiles meet in LDS at the end.
+// weights and no all-ones MFMA for sum(x). A lane loads CPL = 2 words (two columns) per packed
+// row, the M = 1 kernel's 128-byte tile, or 4 (64-column tiles, two lines per packed row, for the
+// wide shapes at 5-16 rows, where the x rows every workgroup stages cost more than the weights);
+// the waves' partial tiles meet in LDS at the end.
 // Measured on MI355X (graph replays, rotating sets), wide-tile kernel against this one: gate_up
 // M = 4 / 8 / 16 7.50 / 8.07 / 9.37 -> 5.91 / 6.68 / 7.48 us, q/o 4.26 / 4.40 / 5.12 -> 3.48 /
 // 3.69 / 3.99, k/v (8 tiles) 4.12 / 4.29 / 5.00 -> 3.33 / 3.49 / 3.85.
-template <int MP, int NW, int GPW>
+template <int MP, int NW, int GPW, int CPL>
 __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "row tile");
+  static_assert(CPL == 2 || CPL == 4, "two or four columns per lane");
   constexpr int NG = NW * GPW, WUNITS = GPW * MP * 16, WUPT = WUNITS / 64;
+  constexpr int CWT = 16 * CPL;  // columns of the tile
   static_assert(WUNITS % 64 == 0, "whole staging units per lane");
+  static_assert(NW * MP * CWT * 4 <= NG * 16 * MP * 16, "the partial tiles fit over the records");
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+  typedef uint32_t wrow_t __attribute__((ext_vector_type(CPL)));      // CPL packed words of a row
+  typedef uint32_t sz_t __attribute__((ext_vector_type(CPL / 2)));    // CPL fp16 scales or zeros
   __shared__ __align__(16) u32x4 xs[NG * 16 * MP];  // A records; the waves' partial tiles at the end
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.qw);
   const int ng = (a.K >> 3) >> 4;  // groups of 16 packed rows, <= NG
-  const int n0 = blockIdx.x * 32;
-  const int col = min(n0 + 2 * c16, a.N - 2);  // clamped: tail lanes load valid memory, store nothing
+  const int n0 = blockIdx.x * CWT;
+  const int col = min(n0 + CPL * c16, a.N - CPL);  // clamped: tail lanes load valid memory, store nothing
   const int M = a.M;
   // ---- this wave's x rows first (unit u = lane + 64 i: packed row rr of group wave * GPW + u / (16 MP),
   //      row m)
@@ -1047,18 +1054,19 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
     const int g = min(wave * GPW + u / (16 * MP), ng - 1);
     xr[i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)min(m, M - 1) * a.ldx + 8 * (16 * g + rr));
   }
-  // ---- then its weights: K step ks of group g is packed row 16 g + 4 ks + kb, columns col, col + 1
-  u32x2 w[GPW][4];
-  uint32_t sv[GPW], zv[GPW];
+  // ---- then its weights: K step ks of group g is packed row 16 g + 4 ks + kb, columns col ..
+  //      col + CPL - 1
+  wrow_t w[GPW][4];
+  sz_t sv[GPW], zv[GPW];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
     const int g = min(wave * GPW + gi, ng - 1);  // clamped: surplus waves load valid memory, use nothing
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       w[gi][ks] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x2*>(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + col));
-    sv[gi] = *reinterpret_cast<const uint32_t*>(a.s + (int64_t)g * a.N + col);
-    zv[gi] = *reinterpret_cast<const uint32_t*>(a.z + (int64_t)g * a.N + col);
+          reinterpret_cast<const wrow_t*>(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + col));
+    sv[gi] = *reinterpret_cast<const sz_t*>(a.s + (int64_t)g * a.N + col);
+    zv[gi] = *reinterpret_cast<const sz_t*>(a.z + (int64_t)g * a.N + col);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
   // ---- A records
@@ -1077,15 +1085,19 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   // at the odd ones
   const uint32_t one2 = 0x3C003C00u, ev = c16 < 8 ? one2 : 0u, od = c16 < 8 ? 0u : one2;
   const half8v bstat = __builtin_bit_cast(half8v, u32x4{ev, od, ev, od});
-  // ---- MFMA over the wave's groups: tile t holds columns n0 + 2 c16 + t
+  // ---- MFMA over the wave's groups: tile t holds columns n0 + CPL c16 + t
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
-  float4_t acc[2] = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, float4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+  float4_t acc[CPL];
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
     const int g = wave * GPW + gi;
     if (g >= ng) break;  // uniform
-    float4_t tmp[2] = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, float4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    float4_t tmp[CPL];
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) tmp[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float4_t sacc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};  // E (c16 < 8) or O (c16 >= 8) per row
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -1095,42 +1107,43 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
       const half8v A = __builtin_bit_cast(half8v, ar);
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, bstat, sacc, 0, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < CPL; ++t) {
         const uint32_t wc = w[gi][ks][t], v = wc >> 8;
         const u32x4 b{(wc & mlo) | magic, (wc & mhi) | magic, (v & mlo) | magic, (v & mhi) | magic};
         tmp[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), tmp[t], 0, 0, 0);
       }
     }
-    const half2_t s2 = ldk::u2h2(sv[gi]), z2 = ldk::u2h2(zv[gi]);
+    typedef _Float16 halfc_t __attribute__((ext_vector_type(CPL)));
+    const halfc_t s2 = __builtin_bit_cast(halfc_t, sv[gi]), z2 = __builtin_bit_cast(halfc_t, zv[gi]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // element i of lane (c16, kb): row 4 kb + i
       const float mine = sacc[i], other = ldk::row_ror<8>(mine);  // lane c16 ^ 8 of the same row
       const float e = c16 < 8 ? mine : other, o = c16 < 8 ? other : mine;
       const float c = 1024.0f * (e + o), sx = __builtin_fmaf(16.0f, o, e);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < CPL; ++t)
         acc[t][i] = __builtin_fmaf((float)s2[t], tmp[t][i] - __builtin_fmaf((float)z2[t], sx, c), acc[t][i]);
     }
   }
   // ---- the NW partial tiles meet in LDS (over the records, once every wave is done with them)
   ldk::lds_barrier();
-  float* red = reinterpret_cast<float*>(xs);  // [NW][MP][32]
+  float* red = reinterpret_cast<float*>(xs);  // [NW][MP][CWT]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (4 * kb + i < M)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) red[(wave * MP + 4 * kb + i) * 32 + 2 * c16 + t] = acc[t][i];
+      for (int t = 0; t < CPL; ++t) red[(wave * MP + 4 * kb + i) * CWT + CPL * c16 + t] = acc[t][i];
   }
   ldk::lds_barrier();
-  const int n = M * 32;  // outputs o = row * 32 + column of the tile
+  const int n = M * CWT;  // outputs o = row * CWT + column of the tile
   auto store = [&](int o, float v) {
-    const int nn = n0 + (o & 31);
+    const int nn = n0 + (o & (CWT - 1));
     if (nn < a.N) {
       if (a.bias) v += (float)a.bias[nn];
-      a.out[(int64_t)(o >> 5) * a.ldo + nn] = (half_t)v;
+      a.out[(int64_t)(o / CWT) * a.ldo + nn] = (half_t)v;
     }
   };
-  for (int o = threadIdx.x; o < n; o += NW * 64) store(o, ldk::sum_waves(red + o, MP * 32, NW));
+  for (int o = threadIdx.x; o < n; o += NW * 64) store(o, ldk::sum_waves(red + o, MP * CWT, NW));
 }
 
 // ------------------------------------------------------------------------------------ dispatch
@@ -1211,29 +1224,39 @@ bool mfma_x_applies(int64_t M, int64_t K, int gsh_rows, int block_n, int split_k
          !(flags & (LDK_EXACT | LDK_PATH_VALU | LDK_CPW_MASK));
 }
 
-template <int MP, int NW, int GPW>
+template <int MP, int NW, int GPW, int CPL>
 int launch_mfma_x_t(const W4Args& a, hipStream_t s) {
   (void)hipGetLastError();
-  w4a16_mfma_x_kernel<MP, NW, GPW><<<(unsigned)((a.N + 31) / 32), NW * 64, 0, s>>>(a);
+  w4a16_mfma_x_kernel<MP, NW, GPW, CPL><<<(unsigned)((a.N + 16 * CPL - 1) / (16 * CPL)), NW * 64, 0, s>>>(a);
   return ldk::check_launch("w4a16_mfma_x");
 }
 
-template <int MP>
+template <int MP, int CPL>
 int launch_mfma_x_mp(const W4Args& a, int nw, int gpw, hipStream_t s) {
-  if (nw == 12 && gpw == 1) return launch_mfma_x_t<MP, 12, 1>(a, s);
-  if (nw == 6 && gpw == 2) return launch_mfma_x_t<MP, 6, 2>(a, s);
-  if (nw == 6 && gpw == 1) return launch_mfma_x_t<MP, 6, 1>(a, s);
+  if (nw == 12 && gpw == 1) return launch_mfma_x_t<MP, 12, 1, CPL>(a, s);
+  if (nw == 6 && gpw == 2) return launch_mfma_x_t<MP, 6, 2, CPL>(a, s);
+  if (nw == 6 && gpw == 1) return launch_mfma_x_t<MP, 6, 1, CPL>(a, s);
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: x-staged MFMA kernel with %d waves of %d groups not instantiated", nw, gpw);
 }
 
 int launch_mfma_x(const W4Args& a, const Plan& p, hipStream_t s) {
-  // the kernel's LDS holds nw * cpw groups (all of K) and MP = mt rows
-  if (a.gsh_rows != 4 || a.M > p.mt || ((a.K >> 3) >> 4) > p.nw * p.cpw || (a.N + 31) / 32 > INT32_MAX)
+  // the kernel's LDS holds nw * cpw groups (all of K) and MP = mt rows; 64-column tiles (ln 16)
+  // take N a multiple of 4 (whole 16-byte loads of the clamped last lane)
+  if (a.gsh_rows != 4 || a.M > p.mt || ((a.K >> 3) >> 4) > p.nw * p.cpw || (a.N + 31) / 32 > INT32_MAX ||
+      (p.ln != 8 && p.ln != 16) || (p.ln == 16 && a.N % 4))
     return ldk::fail(LDK_ERR_INVALID, "w4a16: x-staged MFMA plan does not fit M=%d N=%d K=%d", a.M, a.N, a.K);
-  switch (p.mt) {
-    case 4: return launch_mfma_x_mp<4>(a, p.nw, p.cpw, s);
-    case 8: return launch_mfma_x_mp<8>(a, p.nw, p.cpw, s);
-    case 16: return launch_mfma_x_mp<16>(a, p.nw, p.cpw, s);
+  if (p.ln == 16) {
+    switch (p.mt) {
+      case 4: return launch_mfma_x_mp<4, 4>(a, p.nw, p.cpw, s);
+      case 8: return launch_mfma_x_mp<8, 4>(a, p.nw, p.cpw, s);
+      case 16: return launch_mfma_x_mp<16, 4>(a, p.nw, p.cpw, s);
+    }
+  } else {
+    switch (p.mt) {
+      case 4: return launch_mfma_x_mp<4, 2>(a, p.nw, p.cpw, s);
+      case 8: return launch_mfma_x_mp<8, 2>(a, p.nw, p.cpw, s);
+      case 16: return launch_mfma_x_mp<16, 2>(a, p.nw, p.cpw, s);
+    }
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: x-staged MFMA row tile %d", p.mt);
 }
@@ -1273,7 +1296,12 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     const int ngx = (int)((K / 8) >> gsh_rows);
     p.kern = kMfmaX;
     p.mt = M <= 4 ? 4 : M <= 8 ? 8 : 16;
-    p.ln = 8;
+    // 64-column tiles from 5 rows on shapes of at least 256 of them: every workgroup stages its
+    // x rows once for twice the columns, halving the x traffic through L2, which at 16 rows is
+    // twice the weight bytes (gate_up M = 8 / 16: 6.48 / 7.36 -> 6.23 / 6.96 us; at 4 rows, and
+    // on the narrow shapes with their half as many workgroups, 32 columns stay faster: gate_up
+    // M = 4 5.88 against 6.67 us, q/o M = 16 3.98 against 4.54)
+    p.ln = (M > 4 && N % 64 == 0 && N / 64 >= 256) ? 16 : 8;
     p.rpl = 4;
     p.nw = ngx <= 6 ? 6 : (M <= 4 && N / 32 >= 256) ? 6 : 12;
     p.cpw = (ngx + p.nw - 1) / p.nw;
@@ -1647,7 +1675,7 @@ static int plan_kernel_name(const Plan& p, int gsh_rows, char* buf, size_t len) 
   if (p.kern == kM1) {
     n = snprintf(buf, len, "w4a16_m1_kernel<%d, %d, %d, 0, %d>", p.ln, p.nw, gsh_rows == 4 ? 4 : 0, p.mt);
   } else if (p.kern == kMfmaX) {
-    n = snprintf(buf, len, "w4a16_mfma_x_kernel<%d, %d, %d>", p.mt, p.nw, p.cpw);
+    n = snprintf(buf, len, "w4a16_mfma_x_kernel<%d, %d, %d, %d>", p.mt, p.nw, p.cpw, p.ln / 4);
   } else if (p.kern == kValu) {
     n = snprintf(buf, len, "w4a16_gemv_kernel<%d, %d, %d, %d>", p.mt, p.ln, p.rpl, p.cpw);
   } else {

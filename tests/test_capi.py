@@ -196,7 +196,7 @@ def test_config_query():
     assert fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU
     st = _lib.load().ldk_w4a16_config(16, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
-    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 32  # x staged in LDS, 32-column tiles
+    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 64  # x staged in LDS, 64-column tiles
     # two rows: the factored VALU kernel; from three rows the MFMA kernel, also on small shapes
     st = _lib.load().ldk_w4a16_config(2, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
                                       ctypes.byref(fl))
@@ -212,12 +212,15 @@ def test_decode_rows_plan_kernels():
     also takes two rows of down; one and two rows otherwise the factored VALU kernel; more than 16
     the MFMA blocks."""
     from kernels.w4a16 import kernel_name
-    assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
-    assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2>"
-    assert kernel_name(8, 1536, 1536) == "w4a16_mfma_x_kernel<8, 12, 1>"
-    assert kernel_name(3, 4096, 512) == "w4a16_mfma_x_kernel<4, 6, 1>"
-    assert kernel_name(16, 256, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
-    assert kernel_name(16, 200, 1536) == "w4a16_mfma_x_kernel<16, 12, 1>"
+    assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 4>"  # 64-column tiles
+    assert kernel_name(8, 17920, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 4>"
+    assert kernel_name(5, 17920, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 4>"
+    assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2, 2>"
+    assert kernel_name(8, 1536, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 2>"
+    assert kernel_name(3, 4096, 512) == "w4a16_mfma_x_kernel<4, 6, 1, 2>"
+    assert kernel_name(16, 256, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2>"
+    assert kernel_name(16, 200, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2>"
+    assert kernel_name(16, 16400, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2>"  # N % 64 != 0
     assert kernel_name(16, 1536, 8960).startswith("w4a16_mfma_kernel<")
     assert kernel_name(8, 1536, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(16, 17920, 1536, 64).startswith("w4a16_mfma_kernel<")

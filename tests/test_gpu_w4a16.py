@@ -311,6 +311,25 @@ def test_mfma_x_one_hot_rows_reproduce_dequantized_weight(M):
         assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, ks].T))), c
 
 
+@pytest.mark.parametrize("M", [16, 6])
+def test_mfma_x_64_column_tiles_one_hot(M):
+    """64-column tiles (wide shapes from 5 rows: each lane's four words per packed row feed four
+    MFMA tiles): one-hot rows return columns of dequant(W) exactly over K = 1536, N = 16384."""
+    from kernels.w4a16 import kernel_name
+    N, K = 16384, 1536
+    assert kernel_name(M, N, K).endswith(", 4>")
+    _, qw, s, z, _ = _make(1, N, K, 12)
+    deq = dequantize_ref(qw, s, z, 128)
+    qwd, sd, zd = dev(qw), dev(s), dev(z)
+    order = np.random.default_rng(4).permutation(K)
+    for c in range(0, K, 4 * M):  # a quarter of K's positions, all twelve groups
+        ks = order[c:c + M]
+        x = torch.zeros(len(ks), K, dtype=torch.float16, device="cuda")
+        x[torch.arange(len(ks)), torch.as_tensor(ks)] = 1.0
+        got = w4a16_matmul(x, qwd, sd, zd).cpu().numpy()
+        assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, ks].T))), c
+
+
 # ---------------------------------------------------------------- config 0 and config 2
 def test_config0_headline():
     """Config 0: M=1, gate_up 17920 x 1536, seed 0 (weights quantized by the oracle)."""
