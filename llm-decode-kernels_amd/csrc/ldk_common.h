@@ -41,11 +41,15 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
 }
 
-// SwiGLU's activation of one gate value with the steps of the standalone SwiGLU kernel: silu in
-// fp32 with the hardware reciprocal, rounded to fp16 (the caller multiplies by u in fp16).
+// SwiGLU's activation of one gate value, shared by the standalone SwiGLU kernel and the fused
+// prologues (so their staged values are the same bits): silu in fp32, exp(-f) as 2^(-f log2 e) on
+// the hardware exp2 and the division as the hardware reciprocal, rounded to fp16 (the caller
+// multiplies by u in fp16). Large |f| saturate as in fp32 arithmetic: 2^(+big) = inf gives -0 for
+// very negative gates, 2^(-big) = 0 gives f.
 __device__ __forceinline__ half_t silu_f16(half_t g) {
   const float f = (float)g;
-  return (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
+  const float e = __builtin_amdgcn_exp2f(f * -1.44269504088896341f);
+  return (half_t)(f * __builtin_amdgcn_rcpf(1.0f + e));
 }
 
 // RMSNorm's staged value of one element with the steps of the standalone RMSNorm kernel:

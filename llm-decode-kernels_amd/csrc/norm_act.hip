@@ -124,10 +124,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
   const hv_t u = load_v<STREAM>(reinterpret_cast<const hv_t*>(a.u + row * a.ldu + c));
   hv_t s;
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) {
-    const float f = (float)g[j];
-    s[j] = (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
-  }
+  for (int j = 0; j < VEC; ++j) s[j] = ldk::silu_f16(g[j]);
   store_v<STREAM>(s * u, reinterpret_cast<hv_t*>(a.out + row * a.ldo + c));  // fp16 multiply
 }
 

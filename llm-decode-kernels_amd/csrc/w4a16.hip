@@ -228,10 +228,7 @@ __device__ __forceinline__ u32x4 pro_stage(u32x4 xr, u32x4 x2, u32x4 x3, float r
     const half8_t g = __builtin_bit_cast(half8_t, xr), u = __builtin_bit_cast(half8_t, x2);
     half8_t sv;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float f = (float)g[j];
-      sv[j] = (half_t)(f * __builtin_amdgcn_rcpf(1.0f + expf(-f)));
-    }
+    for (int j = 0; j < 8; ++j) sv[j] = ldk::silu_f16(g[j]);
     return __builtin_bit_cast(u32x4, sv * u);  // fp16 multiply
   } else {
     half8_t h = __builtin_bit_cast(half8_t, xr);
