@@ -358,21 +358,29 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
       for (int b = 0; b < 8; ++b) ow[wave][4 * kb + r][16 * b + c16] = o[b][r];
     }
   ldk::lds_barrier();
-  // thread item (head j, dim d): weights exp(m_w - M) of the waves that saw a live position
+  // thread item (head j, dim d): weights exp(m_w - M) of the waves that saw a live position. All
+  // 3 x kWaves LDS reads are issued before the first use and the dead waves get weight 0 (their l
+  // and O are 0, so the FMA adds nothing) instead of a branch, which made each wave's reads wait
+  // for the previous wave's exp (0.65 us of a 6.4 us launch at 130 live positions)
   const bool single = nlive == 1;
   for (int e = tid; e < nh * kHD; e += kWaves * 64) {
     const int j = e >> 7, d = e & (kHD - 1);
+    float mv[kWaves], lv[kWaves], ov[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      mv[w] = mw[w][j];
+      lv[w] = lw[w][j];
+      ov[w] = ow[w][j][d];
+    }
     float M = -__builtin_inff();
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mw[w][j]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mv[w]);
     float l = 0.0f, acc = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      if (mw[w][j] != -__builtin_inff()) {
-        const float f = __expf(mw[w][j] - M);
-        l = __builtin_fmaf(lw[w][j], f, l);
-        acc = __builtin_fmaf(ow[w][j][d], f, acc);
-      }
+      const float f = mv[w] != -__builtin_inff() ? __expf(mv[w] - M) : 0.0f;
+      l = __builtin_fmaf(lv[w], f, l);
+      acc = __builtin_fmaf(ov[w], f, acc);
     }
     if (single) {
       a.out[(int64_t)(hbase + j) * kHD + d] = (half_t)(l > 0.0f ? acc / l : 0.0f);
