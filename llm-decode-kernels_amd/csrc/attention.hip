@@ -131,6 +131,7 @@ struct IntC {
 
 __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs a) {
   __shared__ __align__(16) half_t vnew[kWaves][kHD];     // v_new by dim, one copy per wave
+  __shared__ __align__(16) half_t knew[kHD];              // the roped k_new, for wave 0's cache write
   __shared__ __align__(16) half_t cs[kWaves][2][64];      // RoPE cos, sin by dim, per wave
   __shared__ float mw[kWaves][kTile], lw[kWaves][kTile];  // per-wave max and sum per head
   __shared__ __align__(16) float ow[kWaves][kTile][kHD];  // per-wave unnormalised outputs
@@ -231,25 +232,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
       for (int e = 0; e < 4; ++e) s_new = __builtin_amdgcn_fdot2(ldk::u2h2(qb[s][e]), ldk::u2h2(kn[e]), s_new, false);
     }
     s_new = ldk::add_xor32(ldk::add_xor16(s_new)) * a.scale;
-    // v_new by dim for this wave's V patch (wave-local LDS exchange), and the cache write at pos
-    // by wave 0 of the range holding pos (head tile 0): lanes c16 = 0 store k_new's 8-dim runs
-    // (adjacent in a K tile row), lanes kb = 0 store v_new down the V^T tiles' rows
+    // v_new by dim for this wave's V patch (wave-local LDS exchange)
     if (c16 == 0) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) *reinterpret_cast<u32x4*>(&vnew[wave][8 * kb + 32 * s]) = vx[s];
     }
     ldk::wave_lds_sync();
-    if (wave == 0 && tile == 0 && npos >= s0 && npos < s0 + S) {
-      if (c16 == 0) {
-        half_t* kw = a.k + (int64_t)kvh * L * kHD;
+    // the writing wave keeps the roped k_new in LDS too; the cache stores themselves go out after
+    // its last chunk (below): issued here, ahead of the remaining chunk loads, the 8 scattered V^T
+    // stores held those loads' in-order vmcnt waits (0.2-0.5 us per launch)
+    if (wave == 0 && c16 == 0) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) *reinterpret_cast<half8_t*>(&kw[k_offset(npos, 8 * kb + 32 * s)]) = kh[s];
-      }
-      if (kb == 0) {
-        half_t* vw = a.vt + (int64_t)kvh * kHD * L;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) vw[vt_offset(16 * b + c16, npos)] = vnew[wave][16 * b + c16];
-      }
+      for (int s = 0; s < 4; ++s) *reinterpret_cast<half8_t*>(&knew[8 * kb + 32 * s]) = kh[s];
     }
   };
 
@@ -343,6 +337,23 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
       chunks(IntC<2>(), IntC<0>(), k);
     else
       chunks(IntC<1>(), IntC<0>(), k);
+  }
+  // the cache write at pos by wave 0 of the range holding pos (head tile 0): lanes c16 = 0 store
+  // k_new's 8-dim runs (adjacent in a K tile row), lanes kb = 0 store v_new down the V^T tiles'
+  // rows. This launch's scores and P.V took both from registers; later launches read them.
+  if (wave == 0 && tile == 0 && npos >= s0 && npos < s0 + S) {
+    if (c16 == 0) {
+      half_t* kw = a.k + (int64_t)kvh * L * kHD;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        *reinterpret_cast<half8_t*>(&kw[k_offset(npos, 8 * kb + 32 * s)]) =
+            *reinterpret_cast<const half8_t*>(&knew[8 * kb + 32 * s]);
+    }
+    if (kb == 0) {
+      half_t* vw = a.vt + (int64_t)kvh * kHD * L;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) vw[vt_offset(16 * b + c16, npos)] = vnew[0][16 * b + c16];
+    }
   }
 
   // ---- the waves meet: per-wave (m, l) per head and O rows of the tile's live heads
