@@ -259,6 +259,18 @@ int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_f
                          void* vt_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
                          float scale, void* stream);
 
+/* ldk_decode_attention's range kernel alone, for a consumer that merges the ranges itself
+ * (ldk_w4a16_attn_matmul_residual_stats): the cache is split into ranges of rlen positions (a
+ * multiple of 32, at most 32 ranges), every range live at *pos (a lone one too) leaves its
+ * {max, sum} and unnormalised output in library-owned device memory, and there is no merge
+ * launch and no output. Cache write, numerics and argument rules as ldk_decode_attention;
+ * nq <= 128. The partials stay valid until the next attention call on the device; calls must be
+ * stream-ordered. No counterpart entry exists in the reference: it is one half of this build's
+ * fusion of the attention's merge into the o projection (kernels/e2e/model.py:212-233 there). */
+int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
+                                void* vt_cache, int nq, int nkv, int head_dim, int64_t max_len, int64_t rlen,
+                                float scale, void* stream);
+
 /* Residual + RMSNorm carried across the two projections around it (decode, one row), as a pair
  * of launches that replaces linear + rmsnorm(x, residual) + linear of the reference's layer
  * (kernels/e2e/model.py:79-97, 226-233: o_proj, post_attention_layernorm, gate_up). Group size
@@ -277,6 +289,19 @@ int ldk_w4a16_matmul_residual_stats(const void* x, const void* residual, void* h
                                     const int32_t* qweight, const void* scales, const void* zeros,
                                     const void* bias, int64_t N, int64_t K, int group_size,
                                     void* workspace, int64_t workspace_bytes, void* stream);
+/* ldk_w4a16_matmul_residual_stats with x the attention output that ldk_decode_attention_ranges
+ * left as partials (nq heads, max_len positions in ranges of rlen, at *pos): each x value is the
+ * ranges' merge exp(m_r - max m)-weighted, o / l rounded once to fp16, formed in the projection's
+ * x staging (the merge launch's arithmetic; the sum of the weighted l is a chain in range order
+ * there, a lane reduction in the merge launch, so x can differ from it in the last fp16 bit).
+ * K = nq * 128, at most 4 ranges (ceil(max_len / rlen) <= 4), group size 128, pos 8-byte aligned.
+ * One launch in place of the attention's merge launch and the projection. No counterpart entry
+ * exists in the reference. */
+int ldk_w4a16_attn_matmul_residual_stats(const int64_t* pos, int64_t max_len, int64_t rlen, int nq,
+                                         const void* residual, void* h_out, float* row_stats,
+                                         const int32_t* qweight, const void* scales, const void* zeros,
+                                         const void* bias, int64_t N, int64_t K, int group_size,
+                                         void* workspace, int64_t workspace_bytes, void* stream);
 int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int nstats,
                                    const void* norm_weight, float eps, const int32_t* qweight,
                                    const void* scales, const void* zeros, const void* bias,

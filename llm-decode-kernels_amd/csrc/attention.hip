@@ -45,7 +45,9 @@
 // fp16 q and K with fp32 accumulation; softmax in fp32 with its numerators rounded to fp16 before
 // they weight V, the V sum and the normalisation in fp32, the output rounded once to fp16.
 #include <algorithm>
+#include <mutex>
 
+#include "attention.h"
 #include "ldk_common.h"
 
 namespace {
@@ -56,8 +58,9 @@ constexpr int kTile = 16;    // query heads per workgroup: the MFMA tile's 16 co
 constexpr int kChunk = 32;   // positions per score chunk and per P.V step
 constexpr int kBlock = 512;  // positions per softmax block: 16 chunks, two per wave
 constexpr int64_t kMaxLen = 1 << 20;
-constexpr int kMaxSplits = 32;  // position ranges per head tile
-constexpr int kMaxHeads = 128;  // query heads that can split (more run one range per tile)
+constexpr int kMaxSplits = ldk::kAttnMaxSplits;  // position ranges per head tile
+constexpr int kMaxHeads = ldk::kAttnMaxHeads;    // query heads that can split (more run one range per tile)
+static_assert(kHD == ldk::kAttnHeadDim, "head_dim of the partials");
 constexpr uint32_t kDead = 0x80000000u;  // buffer offset past every resource: the load returns 0
 constexpr int kTileHalves = 512;         // halves per 1 KB cache tile
 
@@ -88,6 +91,7 @@ struct AttnArgs {
   int ntile;              // workgroups per kv head along x: ceil((nq / nkv) / 16) head tiles
   int rlen;               // positions per range (gridDim.y ranges), a multiple of 32
   float scale;
+  int partials;           // 1: every range writes its partials, also a lone live range (no output)
 };
 
 // fp16 RoPE of the pair (x0, x1) = (x[d], x[d + 64]) of a 128-vector (rotate_half pairs d with
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   // 3 x kWaves LDS reads are issued before the first use and the dead waves get weight 0 (their l
   // and O are 0, so the FMA adds nothing) instead of a branch, which made each wave's reads wait
   // for the previous wave's exp (0.65 us of a 6.4 us launch at 130 live positions)
-  const bool single = nlive == 1;
+  const bool single = nlive == 1 && !a.partials;
   for (int e = tid; e < nh * kHD; e += kWaves * 64) {
     const int j = e >> 7, d = e & (kHD - 1);
     float mv[kWaves], lv[kWaves], ov[kWaves];
@@ -472,10 +476,70 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
   const int nsplit = (int)((max_len + rlen - 1) / rlen);
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, (half_t*)out,
-                   nq, nkv, (int)max_len, ntile, (int)rlen, scale};
+                   nq, nkv, (int)max_len, ntile, (int)rlen, scale, 0};
   (void)hipGetLastError();
   decode_attention_kernel<<<dim3(nkv * ntile, nsplit), kWaves * 64, 0, (hipStream_t)stream>>>(a);
   if (nsplit > 1)
     attention_merge_kernel<<<nq, 64, 0, (hipStream_t)stream>>>(pos, (half_t*)out, (int)max_len, (int)rlen);
   return ldk::check_launch("decode_attention");
 }
+
+// Decode attention that leaves its result as per-range partials for a consumer that merges them
+// (the W4A16 o projection's x staging, ldk_w4a16_attn_matmul_residual_stats): the range kernel of
+// ldk_decode_attention with `rlen` positions per range, every range (a lone live one too) writing
+// {m, l} and its unnormalised output to the library's partials, and no merge launch. Cache write
+// and numerics as ldk_decode_attention.
+extern "C" int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
+                                           void* vt_cache, int nq, int nkv, int head_dim, int64_t max_len,
+                                           int64_t rlen, float scale, void* stream) {
+  if (!qkv || !pos || !inv_freq || !k_cache || !vt_cache) return ldk::fail(LDK_ERR_INVALID, "decode_attention_ranges: null pointer");
+  if (head_dim != kHD) return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention_ranges: head_dim=%d (only 128)", head_dim);
+  if (nq <= 0 || nkv <= 0 || nq % nkv) return ldk::fail(LDK_ERR_INVALID, "decode_attention_ranges: nq=%d must be a positive multiple of nkv=%d", nq, nkv);
+  if (nq > kMaxHeads) return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention_ranges: nq=%d above %d heads", nq, kMaxHeads);
+  if (max_len < kChunk || max_len > kMaxLen || max_len % kChunk)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention_ranges: max_len=%lld must be a multiple of 32 in 32..%lld",
+                     (long long)max_len, (long long)kMaxLen);
+  if (rlen < kChunk || rlen % kChunk || rlen > max_len || (max_len + rlen - 1) / rlen > kMaxSplits)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention_ranges: rlen=%lld must be a multiple of 32 giving 1..%d ranges of %lld",
+                     (long long)rlen, kMaxSplits, (long long)max_len);
+  if (!ldk::aligned(k_cache, 16) || !ldk::aligned(vt_cache, 16) || !ldk::aligned(pos, 8))
+    return ldk::fail(LDK_ERR_ALIGN, "decode_attention_ranges: k_cache and vt_cache 16-byte, pos 8-byte aligned");
+  const int nsplit = (int)((max_len + rlen - 1) / rlen);
+  const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
+  const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, nullptr,
+                   nq, nkv, (int)max_len, ntile, (int)rlen, scale, 1};
+  (void)hipGetLastError();
+  decode_attention_kernel<<<dim3(nkv * ntile, nsplit), kWaves * 64, 0, (hipStream_t)stream>>>(a);
+  return ldk::check_launch("decode_attention_ranges");
+}
+
+namespace ldk {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_part_mu;
+const float* g_part_o[kMaxDevices];  // device addresses of g_o / g_ml per device, set on first use
+const float* g_part_ml[kMaxDevices];
+}  // namespace
+
+int attention_partials(const float** o, const float** ml) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(LDK_ERR_LAUNCH, "attention partials: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_part_mu);
+  if (!g_part_o[dev]) {
+    void* po = nullptr;
+    void* pm = nullptr;
+    const hipError_t e1 = hipGetSymbolAddress(&po, HIP_SYMBOL(g_o));
+    const hipError_t e2 = hipGetSymbolAddress(&pm, HIP_SYMBOL(g_ml));
+    if (e1 != hipSuccess || e2 != hipSuccess || !po || !pm)
+      return fail(LDK_ERR_LAUNCH, "attention partials: hipGetSymbolAddress failed on device %d", dev);
+    g_part_o[dev] = static_cast<const float*>(po);
+    g_part_ml[dev] = static_cast<const float*>(pm);
+  }
+  *o = g_part_o[dev];
+  *ml = g_part_ml[dev];
+  return LDK_OK;
+}
+
+}  // namespace ldk

@@ -49,6 +49,7 @@
 #include <mutex>
 
 #include "ldk_common.h"
+#include "attention.h"
 #include "prefill.h"
 
 namespace {
@@ -203,12 +204,19 @@ __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, con
 // and one epilogue, for the projection that feeds a residual + RMSNorm:
 //  - kEpiResStat (whole tiles, x as given): h = fp16(y + residual) with y the fp16 output (the
 //    reference's linear, then the norm's residual add), stored as the output, and the tile's
-//    sum of h^2 stored to stats[tile].
+//    sum of h^2 stored to stats[tile];
+//  - kProAttnStat: the kEpiResStat epilogue, with x merged in the staging from the decode
+//    attention's per-range partials (ldk_decode_attention_ranges): for the 8 dims of head h a
+//    lane stages, x = sum_r f_r o_r / sum_r f_r l_r with f_r = exp(m_r - max m) over the ranges
+//    live at pos, rounded once to fp16 (the merge launch's arithmetic, except that its sum of the
+//    f_r l_r is a lane reduction, here a chain in range order, and its division per value is one
+//    reciprocal per 8 values here: the two can differ in the last fp32 bit).
 enum Prologue {
   kProNone = 0, kProRms = 1, kProRmsRes = 2, kProSwiglu = 3, kProRmsX = 4, kProRmsResX = 5,
-  kProRmsPre = 6, kEpiResStat = 7
+  kProRmsPre = 6, kEpiResStat = 7, kProAttnStat = 8
 };
 constexpr int kMaxRowStats = 256;  // per-tile partials a kProRmsPre launch reads
+constexpr int kAttnRanges = 4;     // attention ranges a kProAttnStat launch merges (registers)
 
 struct ProArgs {
   const half_t* res;  // kProRmsRes, kEpiResStat: residual added before the norm
@@ -217,6 +225,11 @@ struct ProArgs {
   float eps;
   float* stats;       // kEpiResStat: per-tile sums of h^2 (written); kProRmsPre: read
   int nstats;
+  // kProAttnStat: the attention's partials (attention.h), its position and range geometry
+  const float* att_o;
+  const float* att_ml;
+  const int64_t* att_pos;
+  int att_len, att_rlen;
 };
 
 // The staged 8 activations of one packed row from the raw loads (x, second operand, norm weight).
@@ -264,7 +277,8 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
   constexpr bool kExact = PRO == kProRmsX || PRO == kProRmsResX;
   constexpr bool kRes = PRO == kProRmsRes || PRO == kProRmsResX;
   constexpr bool kRms = kExact || PRO == kProRms || PRO == kProRmsRes;
-  constexpr bool kPre = PRO == kProRmsPre, kEpi = PRO == kEpiResStat;
+  constexpr bool kAttn = PRO == kProAttnStat;
+  constexpr bool kPre = PRO == kProRmsPre, kEpi = PRO == kEpiResStat || kAttn;
   constexpr int kStatV = 2;  // row vectors per thread loaded ahead of the pass (general variants)
   __shared__ __align__(16) unsigned char xrec[NW][MR][RPW][32];
   __shared__ __align__(16) float4_t red[NW][MR][LN];
@@ -292,10 +306,31 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
     u32x4 xr[XL], x2, x3;
     u32x2 sv, zv;
     u32x4 w[RPL];
+    u32x4 ao[kAttn ? kAttnRanges : 1][2];  // kProAttnStat: the 8 dims' o of each range
+    u32x2 am[kAttn ? kAttnRanges : 1];     // and its {m, l}
   };
+  // kProAttnStat: the ranges live at the attention's position (its clamping of pos)
+  int att_live = 1;
+  if constexpr (kAttn) {
+    const int64_t pin = *pa.att_pos;
+    const int pos = pin >= 0 && pin < pa.att_len ? (int)pin : pin < 0 ? -1 : pa.att_len - 1;
+    att_live = pos < 0 ? 1 : pos / pa.att_rlen + 1;
+  }
   auto load_pass = [&](int gp, Pass& P) {
     const int xo = 8 * min((gp << rsh) + lane, R - 1);
-    if constexpr (MR == 1) {
+    if constexpr (kAttn) {
+      // packed row xo / 8 is dims 8 (row % 16) .. + 7 of head row / 16. All kAttnRanges ranges
+      // are loaded (in bounds: the partials hold kAttnMaxSplits), so the loads do not wait for
+      // pos; the ranges past the live ones are left out by selects when x is formed
+      const int hrow = xo >> 3, h = hrow >> 4, d0 = (hrow & 15) * 8;
+#pragma unroll
+      for (int r = 0; r < kAttnRanges; ++r) {
+        const float* o = pa.att_o + (h * ldk::kAttnMaxSplits + r) * ldk::kAttnHeadDim + d0;
+        P.ao[r][0] = *reinterpret_cast<const u32x4*>(o);
+        P.ao[r][1] = *reinterpret_cast<const u32x4*>(o + 4);
+        P.am[r] = *reinterpret_cast<const u32x2*>(pa.att_ml + (h * ldk::kAttnMaxSplits + r) * 2);
+      }
+    } else if constexpr (MR == 1) {
       P.xr[0] = *reinterpret_cast<const u32x4*>(a.x + xo);
     } else {
 #pragma unroll
@@ -438,7 +473,38 @@ void w4a16_m1_kernel(W4Args a, SplitArgs sp, int out_vec, ProArgs pa) {
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (MR == 1) {
-      if (lane < RPW) store_fact_record(&xrec[wave][0][lane][0], pro_stage<PRO>(P.xr[0], P.x2, P.x3, rs));
+      if constexpr (kAttn) {
+        if (lane < RPW) {
+          float M = -__builtin_inff();
+#pragma unroll
+          for (int r = 0; r < kAttnRanges; ++r) M = fmaxf(M, r < att_live ? ldk::u2f(P.am[r][0]) : -__builtin_inff());
+          // the ranges past the live ones hold an earlier call's values (any bits): selects, not
+          // products with a zero weight, leave them out
+          float f[kAttnRanges], l = 0.0f;
+#pragma unroll
+          for (int r = 0; r < kAttnRanges; ++r) {
+            f[r] = __expf(ldk::u2f(P.am[r][0]) - M);
+            const float lr = __builtin_fmaf(ldk::u2f(P.am[r][1]), f[r], l);
+            l = r < att_live ? lr : l;
+          }
+          // one division for the 8 dims (o * (1 / l) can differ from o / l in the last fp32 bit)
+          const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+          half8_t xh;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float o = 0.0f;
+#pragma unroll
+            for (int r = 0; r < kAttnRanges; ++r) {
+              const float orr = __builtin_fmaf(ldk::u2f(P.ao[r][j >> 2][j & 3]), f[r], o);
+              o = r < att_live ? orr : o;
+            }
+            xh[j] = (half_t)(l > 0.0f ? o * inv : 0.0f);  // no live position: 0 (o may be NaN)
+          }
+          store_fact_record(&xrec[wave][0][lane][0], __builtin_bit_cast(u32x4, xh));
+        }
+      } else {
+        if (lane < RPW) store_fact_record(&xrec[wave][0][lane][0], pro_stage<PRO>(P.xr[0], P.x2, P.x3, rs));
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < XL; ++i) {
@@ -1443,6 +1509,7 @@ int launch_m1_t(const W4Args& a, const SplitArgs& sp, int mr, int pro, const Pro
         case kProSwiglu: w4a16_m1_kernel<LN, NW, 4, kProSwiglu, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         case kProRmsPre: w4a16_m1_kernel<LN, NW, 4, kProRmsPre, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         case kEpiResStat: w4a16_m1_kernel<LN, NW, 4, kEpiResStat, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
+        case kProAttnStat: w4a16_m1_kernel<LN, NW, 4, kProAttnStat, 1><<<grid, NW * 64, 0, stream>>>(a, sp, out_vec, pa); break;
         default: return ldk::fail(LDK_ERR_INVALID, "w4a16: unknown prologue %d", pro);
       }
       return ldk::check_launch("w4a16_m1");
@@ -1922,6 +1989,46 @@ extern "C" int ldk_w4a16_matmul_residual_stats(const void* x, const void* residu
                  (const half_t*)bias, (half_t*)h_out, N, 1, (int)N, (int)K, gsh_rows};
   const ProArgs pa{(const half_t*)residual, nullptr, nullptr, 0.0f, row_stats, (int)tiles};
   return launch_plan(a, p, workspace, (hipStream_t)stream, kEpiResStat, pa);
+}
+
+// The o projection of a decode layer straight from the decode attention's per-range partials
+// (left by ldk_decode_attention_ranges for nq heads over a cache of max_len positions in ranges of
+// rlen, at the position *pos): x is merged in the x staging (kProAttnStat), then as
+// ldk_w4a16_matmul_residual_stats: h_out = fp16(x W^T (+ bias) + residual) and the per-tile sums
+// of h^2 in row_stats for ldk_w4a16_rmsnorm_stats_matmul. One launch where the attention's merge
+// launch and the projection were two. K = nq * 128, at most 4 ranges, group size 128.
+extern "C" int ldk_w4a16_attn_matmul_residual_stats(const int64_t* pos, int64_t max_len, int64_t rlen, int nq,
+                                                    const void* residual, void* h_out, float* row_stats,
+                                                    const int32_t* qweight, const void* scales, const void* zeros,
+                                                    const void* bias, int64_t N, int64_t K, int group_size,
+                                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* fn = "w4a16_attn_matmul_residual_stats";
+  if (!pos || !residual || !row_stats) return ldk::fail(LDK_ERR_INVALID, "%s: null pos, residual or row_stats", fn);
+  int gsh_rows = 0;
+  int st = validate(fn, residual, K, qweight, scales, zeros, h_out, N, 1, N, K, group_size, &gsh_rows);
+  if (st) return st;
+  if (nq <= 0 || nq > ldk::kAttnMaxHeads || K != (int64_t)nq * ldk::kAttnHeadDim)
+    return ldk::fail(LDK_ERR_INVALID, "%s: K=%lld must be nq * 128 with 1 <= nq <= %d", fn, (long long)K, ldk::kAttnMaxHeads);
+  if (gsh_rows != 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: group_size %d (the fused prologues take 128)", fn, group_size);
+  if (max_len <= 0 || rlen <= 0 || rlen % 32 || (max_len + rlen - 1) / rlen > kAttnRanges || max_len > INT32_MAX)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: max_len=%lld in ranges of rlen=%lld (a multiple of 32) must give 1..%d ranges",
+                     fn, (long long)max_len, (long long)rlen, kAttnRanges);
+  if (!ldk::aligned(pos, 8) || !ldk::aligned(h_out, 8) || !ldk::aligned(row_stats, 4))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: pos and h_out 8-byte, row_stats 4-byte aligned", fn);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
+  const float *po = nullptr, *pm = nullptr;
+  st = ldk::attention_partials(&po, &pm);
+  if (st) return st;
+  const Plan p = residual_stats_plan(N, K, gsh_rows, workspace ? (size_t)workspace_bytes : 0);
+  const int64_t tiles = (N + plan_cw(p) - 1) / plan_cw(p);
+  if (tiles > kMaxRowStats)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: %lld column tiles exceed %d partials", fn, (long long)tiles, kMaxRowStats);
+  const W4Args a{(const half_t*)residual, K, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
+                 (const half_t*)bias, (half_t*)h_out, N, 1, (int)N, (int)K, gsh_rows};
+  const ProArgs pa{(const half_t*)residual, nullptr, nullptr, 0.0f, row_stats, (int)tiles, po, pm, pos, (int)max_len,
+                   (int)rlen};
+  return launch_plan(a, p, workspace, (hipStream_t)stream, kProAttnStat, pa);
 }
 
 extern "C" int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int nstats, const void* norm_weight,

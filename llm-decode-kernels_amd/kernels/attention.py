@@ -8,6 +8,8 @@ It replaces, for decode steps, the attention block of the reference's Qwen2 runn
 
 from __future__ import annotations
 
+from typing import NamedTuple
+
 import torch
 
 from kernels import _lib
@@ -116,3 +118,54 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
             _lib.ptr(vt_cache), _lib.ptr(out), n_heads, n_kv, hd, L, float(scale), _lib.stream(dev))
     _lib.check(st, "decode_attention")
     return out
+
+
+# Most position ranges the o projection's merge takes (csrc/w4a16.hip, kAttnRanges).
+MERGE_MAX_RANGES = 4
+
+
+class AttnRanges(NamedTuple):
+    """The decode attention left as per-range partials in the library's device memory (see
+    decode_attention_ranges): what the consumer that merges them needs to know."""
+
+    pos: torch.Tensor
+    max_len: int
+    rlen: int
+    n_heads: int
+
+
+def ranges_len(max_len: int, max_ranges: int = MERGE_MAX_RANGES) -> int:
+    """Positions per range for a cache of max_len: the shortest multiple of 32 that gives at
+    most max_ranges ranges."""
+    per = -(-max_len // max_ranges)
+    return max(CHUNK, -(-per // CHUNK) * CHUNK)
+
+
+def decode_attention_ranges(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tensor,
+                            k_cache: torch.Tensor, vt_cache: torch.Tensor, n_heads: int, n_kv: int,
+                            scale: float, rlen: int) -> AttnRanges:
+    """decode_attention's range kernel alone (ldk_decode_attention_ranges): the cache is split
+    into ranges of rlen positions and every live range leaves its partials for a consumer that
+    merges them (kernels.fused.attn_linear_rmsnorm_w4a16_matmul); no output tensor. The cache
+    is updated at pos as decode_attention updates it."""
+    hd = HEAD_DIM
+    assert qkv.shape[-1] == (n_heads + 2 * n_kv) * hd and qkv.numel() == qkv.shape[-1]
+    L = k_cache.shape[-5] * CHUNK
+    assert k_cache.shape[-6:] == k_cache_shape(n_kv, L) and k_cache.numel() == n_kv * L * hd
+    assert vt_cache.shape[-5:] == vt_cache_shape(n_kv, L) and vt_cache.numel() == n_kv * L * hd
+    assert k_cache.is_contiguous() and vt_cache.is_contiguous()
+    if qkv.dtype != torch.float16 or k_cache.dtype != torch.float16 or vt_cache.dtype != torch.float16:
+        raise ValueError("decode_attention_ranges: qkv and the cache must be float16")
+    if pos.dtype != torch.int64 or inv_freq.dtype != torch.float32:
+        raise ValueError("decode_attention_ranges: pos int64, inv_freq float32")
+    q = qkv.reshape(-1)
+    if q.stride(0) != 1:
+        q = q.contiguous()
+    dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, what="decode_attention_ranges")
+    freq = inv_freq.contiguous()
+    with _lib.device_guard(dev):
+        st = _lib.load().ldk_decode_attention_ranges(
+            _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache), _lib.ptr(vt_cache),
+            n_heads, n_kv, hd, L, int(rlen), float(scale), _lib.stream(dev))
+    _lib.check(st, "decode_attention_ranges")
+    return AttnRanges(pos, L, int(rlen), n_heads)

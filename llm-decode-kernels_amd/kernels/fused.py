@@ -145,6 +145,55 @@ def linear_rmsnorm_w4a16_matmul(x, qweight1, scales1, zeros1, bias1, residual, w
     return y2, h
 
 
+def attn_linear_rmsnorm_w4a16_matmul(ranges, qweight1, scales1, zeros1, bias1, residual, weight,
+                                     eps, qweight2, scales2, zeros2, bias2=None, group_size=128):
+    """linear_rmsnorm_w4a16_matmul with x the decode attention output that
+    kernels.attention.decode_attention_ranges left as per-range partials (`ranges`): the first
+    projection merges the ranges in its x staging (ldk_w4a16_attn_matmul_residual_stats), so the
+    attention's merge launch and the o projection are one launch. Returns (y2, h) as
+    linear_rmsnorm_w4a16_matmul does. One row, group size 128, K1 = 128 * heads, at most four
+    ranges."""
+    K1 = qweight1.shape[0] * 8
+    N1 = qweight1.shape[1]
+    if group_size != FUSED_GROUP_SIZE:
+        raise ValueError(f"attn_linear_rmsnorm_w4a16_matmul: group_size {group_size} (fused: 128)")
+    if K1 != 128 * ranges.n_heads:
+        raise ValueError("attn_linear_rmsnorm_w4a16_matmul: K must be 128 * the attention's heads")
+    if residual.dtype != torch.float16 or residual.numel() != N1 or weight.dtype != torch.float16:
+        raise ValueError("attn_linear_rmsnorm_w4a16_matmul: fp16 residual of N1 values and weight")
+    K2, N2 = N1, qweight2.shape[1]
+    assert qweight2.shape[0] * 8 == K2 and weight.numel() == K2
+    dev = _lib.require_gpu(ranges.pos, residual, weight, qweight1, scales1, zeros1, bias1, qweight2,
+                           scales2, zeros2, bias2, what="attn_linear_rmsnorm_w4a16_matmul")
+    for t in (scales1, zeros1, scales2, zeros2):
+        if t.dtype != torch.float16:
+            raise ValueError("attn_linear_rmsnorm_w4a16_matmul: scales and zeros must be float16")
+    nstats = int(_lib.load().ldk_w4a16_row_stats_count(N1, K1, group_size))
+    if not 0 < nstats <= 256:
+        raise ValueError(f"attn_linear_rmsnorm_w4a16_matmul: {nstats} row partials (1..256)")
+    b1 = None if bias1 is None else bias1.to(torch.float16).contiguous()
+    b2 = None if bias2 is None else bias2.to(torch.float16).contiguous()
+    s1, z1, s2, z2 = (t.contiguous() for t in (scales1, zeros1, scales2, zeros2))
+    r = residual if residual.is_contiguous() else residual.contiguous()
+    h = torch.empty(residual.shape, dtype=torch.float16, device=dev)
+    stats = torch.empty(nstats, dtype=torch.float32, device=dev)
+    y2 = torch.empty((*residual.shape[:-1], N2), dtype=torch.float16, device=dev)
+    lib = _lib.load()
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = lib.ldk_w4a16_attn_matmul_residual_stats(
+            _lib.ptr(ranges.pos), ranges.max_len, ranges.rlen, ranges.n_heads, _lib.ptr(r),
+            _lib.ptr(h), _lib.ptr(stats), _lib.ptr(qweight1), _lib.ptr(s1), _lib.ptr(z1),
+            _lib.ptr(b1), N1, K1, group_size, ws, ws_bytes, _lib.stream(dev))
+        _lib.check(st, "attn_linear_rmsnorm_w4a16_matmul")
+        st = lib.ldk_w4a16_rmsnorm_stats_matmul(
+            _lib.ptr(h), _lib.ptr(stats), nstats, _lib.ptr(weight), float(eps), _lib.ptr(qweight2),
+            _lib.ptr(s2), _lib.ptr(z2), _lib.ptr(b2),
+            _lib.ptr(y2), N2, K2, group_size, ws, ws_bytes, _lib.stream(dev))
+        _lib.check(st, "attn_linear_rmsnorm_w4a16_matmul")
+    return y2, h
+
+
 def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
     """y = w8a16_matmul(swiglu_fused(gate_up), wq, scale) (+ bias); gate_up: [..., 2K] fp16,
     wq: [K, N] float8_e4m3fn, scale: [N] fp16. One row runs one launch (ldk_w8a16_swiglu_matmul),

@@ -163,6 +163,28 @@ def test_fused_decode_attention_matches_torch_path(backend):
 
 
 @pytest.mark.gpu
+def test_attention_merged_in_o_projection_matches_merge_launch():
+    """The default decode step (the attention's four position ranges merged in the o
+    projection's x staging) against the same runner with the attention's own output (one range,
+    no merge): close logits at every step across the range edges, identical KV caches."""
+    model = _qwen_heads_model("cuda")
+    merged = QwenRunner(model, make_backend("ours"), max_len=416)
+    plain = QwenRunner(model, make_backend("ours"), max_len=416)
+    plain.merge_attention = False
+    ids = torch.randint(0, 512, (1, 140), device="cuda")
+    P = 120
+    merged.forward(ids[:, :P], torch.arange(P, device="cuda"))
+    plain.forward(ids[:, :P], torch.arange(P, device="cuda"))
+    for t in range(P, 140):  # crosses the first range edge (128)
+        pos = torch.tensor([t], device="cuda")
+        a = plain.forward(ids[:, t: t + 1], pos)
+        b = merged.forward(ids[:, t: t + 1], pos)
+        torch.testing.assert_close(b.float(), a.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(merged.k_cache.float(), plain.k_cache.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(merged.vt_cache.float(), plain.vt_cache.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.gpu
 def test_fused_attention_graph_decoder_matches_eager_steps():
     """The captured decode step with the fused attention replays exactly the eager steps."""
     from kernels.e2e.run import GraphDecoder

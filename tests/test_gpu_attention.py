@@ -164,3 +164,69 @@ def test_negative_pos_attends_nothing():
                            kc, vt, nq, nkv, hd ** -0.5)
     assert torch.equal(kc, kc0) and torch.equal(vt, vt0)
     assert torch.count_nonzero(out) == 0
+
+
+def _w4_linear(g, N, K):
+    from kernels.quant import quantize_rtn
+
+    w = (torch.randn(N, K, generator=g) * 0.02).half()
+    qw, s, z = quantize_rtn(w.cuda(), 128)
+    return qw, s, z
+
+
+@pytest.mark.parametrize("L,pos", [(416, 0), (416, 31), (416, 127), (416, 128), (416, 200),
+                                   (416, 383), (416, 384), (416, 415), (416, 700), (416, -3),
+                                   (256, 255), (128, 77), (32, 5)])
+def test_ranges_merged_in_o_projection(L, pos):
+    """decode_attention_ranges + attn_linear_rmsnorm_w4a16_matmul (the attention's ranges merged
+    in the o projection's x staging) against decode_attention + linear_rmsnorm_w4a16_matmul on the
+    same inputs: pos in each of the four ranges of 416 positions (128 each, the last one 32) and
+    at their edges, past the cache (the whole cache, no write) and negative (no position: zeros),
+    and shorter caches (256: ranges of 64; 128: 32; 32: one range). The cache updates are
+    bit-identical; y and the residual stream h agree to the north-star bound (the merged x can
+    differ from the merge launch's in the last fp16 bit)."""
+    from _util import assert_north_star
+    from kernels.attention import decode_attention_ranges, ranges_len
+    from kernels.fused import attn_linear_rmsnorm_w4a16_matmul, linear_rmsnorm_w4a16_matmul
+
+    nq, nkv, hd, H, I2 = 12, 2, 128, 1536, 2 * 1024
+    g = torch.Generator().manual_seed(1000 + L + pos)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    _, _, kt_a, vt_a = _caches(g, nkv, L)
+    kt_b, vt_b = kt_a.clone(), vt_a.clone()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    p = torch.tensor([pos], device="cuda")
+    qo, so, zo = _w4_linear(g, H, nq * hd)
+    qg, sg, zg = _w4_linear(g, I2, H)
+    bo = (torch.randn(H, generator=g) * 0.1).half().cuda()
+    res = torch.randn(1, 1, H, generator=g).half().cuda()
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).half().cuda()
+
+    attn = decode_attention(qkv, p, inv_freq, kt_a, vt_a, nq, nkv, hd ** -0.5)
+    y_ref, h_ref = linear_rmsnorm_w4a16_matmul(attn, qo, so, zo, bo, res, nw, 1e-6, qg, sg, zg)
+    rng = decode_attention_ranges(qkv, p, inv_freq, kt_b, vt_b, nq, nkv, hd ** -0.5, ranges_len(L))
+    y, h = attn_linear_rmsnorm_w4a16_matmul(rng, qo, so, zo, bo, res, nw, 1e-6, qg, sg, zg)
+    assert torch.equal(kt_a, kt_b) and torch.equal(vt_a, vt_b)
+    for got, ref in ((h, h_ref), (y, y_ref)):
+        assert torch.isfinite(got).all()
+        assert_north_star(got.cpu(), ref.float().cpu().numpy())
+        d = (got.float() - ref.float()).abs()
+        assert (d <= 2e-3 * ref.float().abs() + 2e-3).float().mean() >= 0.999
+
+
+def test_ranges_entry_rejects_bad_ranges():
+    """More than the four ranges the o projection merges, or a range length that is not a
+    multiple of 32, is refused before any launch."""
+    from kernels import _lib
+
+    lib = _lib.load()
+    p = torch.zeros(1, dtype=torch.long, device="cuda")
+    dummy = torch.zeros(16, dtype=torch.int32, device="cuda")
+    st = lib.ldk_w4a16_attn_matmul_residual_stats(
+        _lib.ptr(p), 416, 64, 12, _lib.ptr(dummy), _lib.ptr(dummy), _lib.ptr(dummy),
+        _lib.ptr(dummy), _lib.ptr(dummy), _lib.ptr(dummy), None, 1536, 1536, 128, None, 0, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    st = lib.ldk_decode_attention_ranges(_lib.ptr(dummy), _lib.ptr(p), _lib.ptr(dummy),
+                                         _lib.ptr(dummy), _lib.ptr(dummy), 12, 2, 128, 416, 100,
+                                         0.1, None)
+    assert st == _lib.ERR_UNSUPPORTED
