@@ -265,11 +265,17 @@ int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_f
  * {max, sum} and unnormalised output in library-owned device memory, and there is no merge
  * launch and no output. Cache write, numerics and argument rules as ldk_decode_attention;
  * nq <= 128. The partials stay valid until the next attention call on the device; calls must be
- * stream-ordered. No counterpart entry exists in the reference: it is one half of this build's
- * fusion of the attention's merge into the o projection (kernels/e2e/model.py:212-233 there). */
+ * stream-ordered. The same launch can warm the caches for the launches after it: nwarm (0..8)
+ * device ranges warm[k] of warm_bytes[k] bytes (16-byte aligned, multiples of 16, under 32 GiB
+ * in all) are read by extra workgroups dispatched after the attention's, into the MALL and the
+ * reading XCD's L2, while the attention's few workgroups leave the CUs idle; they change no
+ * result and write nothing. No counterpart entry exists in the reference: it is one half of this
+ * build's fusion of the attention's merge into the o projection (kernels/e2e/model.py:212-233
+ * there). */
 int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
                                 void* vt_cache, int nq, int nkv, int head_dim, int64_t max_len, int64_t rlen,
-                                float scale, void* stream);
+                                float scale, const void* const* warm, const int64_t* warm_bytes, int nwarm,
+                                void* stream);
 
 /* Residual + RMSNorm carried across the two projections around it (decode, one row), as a pair
  * of launches that replaces linear + rmsnorm(x, residual) + linear of the reference's layer

@@ -8,6 +8,7 @@ It replaces, for decode steps, the attention block of the reference's Qwen2 runn
 
 from __future__ import annotations
 
+import ctypes
 from typing import NamedTuple
 
 import torch
@@ -122,6 +123,8 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
 
 # Most position ranges the o projection's merge takes (csrc/w4a16.hip, kAttnRanges).
 MERGE_MAX_RANGES = 4
+# Most byte ranges one attention launch warms (csrc/attention.hip, kWarmMax).
+WARM_MAX_RANGES = 8
 
 
 class AttnRanges(NamedTuple):
@@ -143,11 +146,15 @@ def ranges_len(max_len: int, max_ranges: int = MERGE_MAX_RANGES) -> int:
 
 def decode_attention_ranges(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tensor,
                             k_cache: torch.Tensor, vt_cache: torch.Tensor, n_heads: int, n_kv: int,
-                            scale: float, rlen: int) -> AttnRanges:
+                            scale: float, rlen: int, warm=()) -> AttnRanges:
     """decode_attention's range kernel alone (ldk_decode_attention_ranges): the cache is split
     into ranges of rlen positions and every live range leaves its partials for a consumer that
     merges them (kernels.fused.attn_linear_rmsnorm_w4a16_matmul); no output tensor. The cache
-    is updated at pos as decode_attention updates it."""
+    is updated at pos as decode_attention updates it.
+
+    warm: up to WARM_MAX_RANGES contiguous device tensors (16-byte aligned, sizes multiples of
+    16 bytes) that the same launch reads into the caches with its spare workgroups, for the
+    launches after it (the next projections' weights); they change no result."""
     hd = HEAD_DIM
     assert qkv.shape[-1] == (n_heads + 2 * n_kv) * hd and qkv.numel() == qkv.shape[-1]
     L = k_cache.shape[-5] * CHUNK
@@ -161,11 +168,19 @@ def decode_attention_ranges(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torc
     q = qkv.reshape(-1)
     if q.stride(0) != 1:
         q = q.contiguous()
-    dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, what="decode_attention_ranges")
+    warm = [t for t in warm if t.numel()]
+    if len(warm) > WARM_MAX_RANGES:
+        raise ValueError(f"decode_attention_ranges: at most {WARM_MAX_RANGES} warm ranges")
+    for t in warm:
+        if not t.is_contiguous():
+            raise ValueError("decode_attention_ranges: warm tensors must be contiguous")
+    dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, *warm, what="decode_attention_ranges")
     freq = inv_freq.contiguous()
+    wp = (ctypes.c_void_p * max(1, len(warm)))(*[t.data_ptr() for t in warm])
+    wb = (ctypes.c_int64 * max(1, len(warm)))(*[t.numel() * t.element_size() for t in warm])
     with _lib.device_guard(dev):
         st = _lib.load().ldk_decode_attention_ranges(
             _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache), _lib.ptr(vt_cache),
-            n_heads, n_kv, hd, L, int(rlen), float(scale), _lib.stream(dev))
+            n_heads, n_kv, hd, L, int(rlen), float(scale), wp, wb, len(warm), _lib.stream(dev))
     _lib.check(st, "decode_attention_ranges")
     return AttnRanges(pos, L, int(rlen), n_heads)

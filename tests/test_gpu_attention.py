@@ -228,5 +228,67 @@ def test_ranges_entry_rejects_bad_ranges():
     assert st == _lib.ERR_UNSUPPORTED
     st = lib.ldk_decode_attention_ranges(_lib.ptr(dummy), _lib.ptr(p), _lib.ptr(dummy),
                                          _lib.ptr(dummy), _lib.ptr(dummy), 12, 2, 128, 416, 100,
-                                         0.1, None)
+                                         0.1, None, None, 0, None)
     assert st == _lib.ERR_UNSUPPORTED
+
+
+def test_ranges_warm_changes_nothing():
+    """The attention launch that also reads byte ranges into the caches (decode_attention_ranges'
+    warm tensors: the o and gate_up weights, a 40 MB buffer that takes several passes of the
+    warming workgroups, ranges of 16 bytes and of odd 16-byte multiples, an empty tensor) leaves
+    the cache update and the merged o projection bit-identical to the launch without them."""
+    from kernels.attention import decode_attention_ranges, ranges_len
+    from kernels.fused import attn_linear_rmsnorm_w4a16_matmul
+
+    nq, nkv, hd, H, I2, L = 12, 2, 128, 1536, 2 * 1024, 416
+    g = torch.Generator().manual_seed(77)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    _, _, kt_a, vt_a = _caches(g, nkv, L)
+    kt_b, vt_b = kt_a.clone(), vt_a.clone()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    qo, so, zo = _w4_linear(g, H, nq * hd)
+    qg, sg, zg = _w4_linear(g, I2, H)
+    res = torch.randn(1, 1, H, generator=g).half().cuda()
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).half().cuda()
+    big = torch.randint(0, 1 << 30, (10 << 20,), dtype=torch.int32, generator=g).cuda()
+    odd = torch.zeros(16 * 37 + 16 * 4099, dtype=torch.uint8, device="cuda")
+    warm = [qo, qg, sg, zg, big, odd[:16], odd[16 * 37:], torch.empty(0, device="cuda")]
+    for pos in (0, 200, 415):
+        p = torch.tensor([pos], device="cuda")
+        outs = []
+        for kt, vt, w in ((kt_a, vt_a, ()), (kt_b, vt_b, warm)):
+            rng = decode_attention_ranges(qkv, p, inv_freq, kt, vt, nq, nkv, hd ** -0.5,
+                                          ranges_len(L), warm=w)
+            outs.append(attn_linear_rmsnorm_w4a16_matmul(rng, qo, so, zo, None, res, nw, 1e-6,
+                                                         qg, sg, zg))
+        assert torch.equal(kt_a, kt_b) and torch.equal(vt_a, vt_b)
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_ranges_warm_rejects_bad_ranges():
+    """Warm ranges are checked before any launch: more than 8, a null array, a pointer that is
+    not 16-byte aligned and a size that is not a multiple of 16 are refused."""
+    import ctypes
+
+    from kernels import _lib
+
+    lib = _lib.load()
+    p = torch.zeros(1, dtype=torch.long, device="cuda")
+    buf = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    qkv = torch.zeros(16 * 128, dtype=torch.float16, device="cuda")
+    kt = torch.zeros(2 * 32 * 128, dtype=torch.float16, device="cuda")
+    freq = torch.zeros(64, dtype=torch.float32, device="cuda")
+
+    def call(ptrs, sizes, n, arrays=True):
+        wp = (ctypes.c_void_p * 9)(*ptrs) if arrays else None
+        wb = (ctypes.c_int64 * 9)(*sizes) if arrays else None
+        return lib.ldk_decode_attention_ranges(_lib.ptr(qkv), _lib.ptr(p), _lib.ptr(freq),
+                                               _lib.ptr(kt), _lib.ptr(kt), 12, 2, 128, 32, 32,
+                                               0.1, wp, wb, n, None)
+
+    base = buf.data_ptr()
+    assert call([base] * 9, [16] * 9, 9) == _lib.ERR_INVALID
+    assert call([], [], 1, arrays=False) == _lib.ERR_INVALID
+    assert call([base + 8], [16], 1) == _lib.ERR_ALIGN
+    assert call([base], [24], 1) == _lib.ERR_ALIGN
+    assert call([base], [-16], 1) == _lib.ERR_ALIGN
