@@ -250,14 +250,16 @@ int ldk_swiglu(const void* gate, int64_t ldg, const void* up, int64_t ldu, void*
  * writes nothing and returns zeros. Caches of more than 512 positions are split into up to 32
  * position ranges whose partials go through library-owned device memory to a second launch on
  * the same stream that merges them (graph capture is safe); calls on one device must be
- * stream-ordered.
+ * stream-ordered. warm, warm_bytes, nwarm: byte ranges the launch reads into the caches for the
+ * launches after it, as ldk_decode_attention_ranges takes them (nwarm = 0: none).
  * Replaces the per-layer attention of the
  * reference's runner for decode steps (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into
  * the cache, scaled_dot_product_attention with the causal mask; the reference's cache is
  * [batch][kv][max_len][head_dim] for both K and V). */
 int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
                          void* vt_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
-                         float scale, void* stream);
+                         float scale, const void* const* warm, const int64_t* warm_bytes, int nwarm,
+                         void* stream);
 
 /* ldk_decode_attention's range kernel alone, for a consumer that merges the ranges itself
  * (ldk_w4a16_attn_matmul_residual_stats): the cache is split into ranges of rlen positions (a

@@ -498,11 +498,49 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
   out[(int64_t)h * kHD + lane + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
 }
 
+// The warm ranges of an attention launch (see WarmRanges) from the caller's arrays, and the
+// number of warming workgroups to add to its grid.
+int make_warm(const void* const* warm, const int64_t* warm_bytes, int nwarm, const char* what, WarmRanges& w,
+              uint32_t& nwg) {
+  if (nwarm < 0 || nwarm > kWarmMax || (nwarm > 0 && (!warm || !warm_bytes)))
+    return ldk::fail(LDK_ERR_INVALID, "%s: nwarm=%d must be 0..%d with both arrays", what, nwarm, kWarmMax);
+  uint64_t end = 0, need = 0;
+  for (int k = 0; k < nwarm; ++k) {
+    if (!warm[k] || warm_bytes[k] < 0 || warm_bytes[k] % 16 || !ldk::aligned(warm[k], 16))
+      return ldk::fail(LDK_ERR_ALIGN, "%s: warm range %d must be non-null, 16-byte aligned, a multiple of 16 bytes (%lld)",
+                       what, k, (long long)warm_bytes[k]);
+    end += (uint64_t)warm_bytes[k] / 16;
+    if (end >= (1ull << 31)) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: warm ranges above 32 GiB", what);
+    w.p[k] = static_cast<const u32x4*>(warm[k]);
+    w.end[k] = (uint32_t)end;
+    need += ((uint64_t)warm_bytes[k] / 16 + kWaves * 64 * kWarmLoads - 1) / (kWaves * 64 * kWarmLoads);
+  }
+  // Warming workgroups per range: enough for kWarmLoads loads per lane where they all fit in
+  // kWarmWorkgroups, else in proportion to the range's bytes (at least one per non-empty range).
+  uint32_t wge = 0;
+  for (int k = 0; k < nwarm; ++k) {
+    const uint64_t units = w.end[k] - (k ? w.end[k - 1] : 0);
+    uint64_t c = (units + kWaves * 64 * kWarmLoads - 1) / (kWaves * 64 * kWarmLoads);
+    if (need > (uint64_t)kWarmWorkgroups && units)
+      c = std::max<uint64_t>(1, units * (kWarmWorkgroups - kWarmMax) / end);
+    wge += (uint32_t)c;
+    w.wg_end[k] = wge;
+  }
+  for (int k = nwarm; k < kWarmMax; ++k) {  // empty ranges
+    w.p[k] = nwarm ? w.p[nwarm - 1] : nullptr;
+    w.end[k] = (uint32_t)end;
+    w.wg_end[k] = wge;
+  }
+  nwg = wge;
+  return LDK_OK;
+}
+
 }  // namespace
 
 extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
                                     void* vt_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
-                                    float scale, void* stream) {
+                                    float scale, const void* const* warm, const int64_t* warm_bytes, int nwarm,
+                                    void* stream) {
   if (!qkv || !pos || !inv_freq || !k_cache || !vt_cache || !out) return ldk::fail(LDK_ERR_INVALID, "decode_attention: null pointer");
   if (head_dim != kHD) return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention: head_dim=%d (only 128)", head_dim);
   if (nq <= 0 || nkv <= 0 || nq % nkv) return ldk::fail(LDK_ERR_INVALID, "decode_attention: nq=%d must be a positive multiple of nkv=%d", nq, nkv);
@@ -527,11 +565,14 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
     rlen = std::max<int64_t>(128, (nchunk + kMaxSplits - 1) / kMaxSplits * kChunk);
   const int nsplit = (int)((max_len + rlen - 1) / rlen);
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
+  WarmRanges w{};
+  uint32_t nwg = 0;
+  if (const int st = make_warm(warm, warm_bytes, nwarm, "decode_attention", w, nwg)) return st;
   const int nattn = nkv * ntile * nsplit;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, (half_t*)out,
-                   nq, nkv, (int)max_len, ntile, (int)rlen, scale, 0, nattn, WarmRanges{}};
+                   nq, nkv, (int)max_len, ntile, (int)rlen, scale, 0, nattn, w};
   (void)hipGetLastError();
-  decode_attention_kernel<<<nattn, kWaves * 64, 0, (hipStream_t)stream>>>(a);
+  decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
   if (nsplit > 1)
     attention_merge_kernel<<<nq, 64, 0, (hipStream_t)stream>>>(pos, (half_t*)out, (int)max_len, (int)rlen);
   return ldk::check_launch("decode_attention");
@@ -560,38 +601,10 @@ extern "C" int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, 
     return ldk::fail(LDK_ERR_ALIGN, "decode_attention_ranges: k_cache and vt_cache 16-byte, pos 8-byte aligned");
   const int nsplit = (int)((max_len + rlen - 1) / rlen);
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
-  if (nwarm < 0 || nwarm > kWarmMax || (nwarm > 0 && (!warm || !warm_bytes)))
-    return ldk::fail(LDK_ERR_INVALID, "decode_attention_ranges: nwarm=%d must be 0..%d with both arrays", nwarm, kWarmMax);
   WarmRanges w{};
-  uint64_t end = 0, need = 0;
-  for (int k = 0; k < nwarm; ++k) {
-    if (!warm[k] || warm_bytes[k] < 0 || warm_bytes[k] % 16 || !ldk::aligned(warm[k], 16))
-      return ldk::fail(LDK_ERR_ALIGN, "decode_attention_ranges: warm range %d must be non-null, 16-byte aligned, "
-                       "a multiple of 16 bytes (%lld)", k, (long long)warm_bytes[k]);
-    end += (uint64_t)warm_bytes[k] / 16;
-    if (end >= (1ull << 31)) return ldk::fail(LDK_ERR_UNSUPPORTED, "decode_attention_ranges: warm ranges above 32 GiB");
-    w.p[k] = static_cast<const u32x4*>(warm[k]);
-    w.end[k] = (uint32_t)end;
-    need += ((uint64_t)warm_bytes[k] / 16 + kWaves * 64 * kWarmLoads - 1) / (kWaves * 64 * kWarmLoads);
-  }
-  // Warming workgroups per range: enough for kWarmLoads loads per lane where they all fit in
-  // kWarmWorkgroups, else in proportion to the range's bytes (at least one per non-empty range).
-  uint32_t wge = 0;
-  for (int k = 0; k < nwarm; ++k) {
-    const uint64_t units = w.end[k] - (k ? w.end[k - 1] : 0);
-    uint64_t c = (units + kWaves * 64 * kWarmLoads - 1) / (kWaves * 64 * kWarmLoads);
-    if (need > (uint64_t)kWarmWorkgroups && units)
-      c = std::max<uint64_t>(1, units * (kWarmWorkgroups - kWarmMax) / end);
-    wge += (uint32_t)c;
-    w.wg_end[k] = wge;
-  }
-  for (int k = nwarm; k < kWarmMax; ++k) {  // empty ranges
-    w.p[k] = nwarm ? w.p[nwarm - 1] : nullptr;
-    w.end[k] = (uint32_t)end;
-    w.wg_end[k] = wge;
-  }
+  uint32_t nwg = 0;
+  if (const int st = make_warm(warm, warm_bytes, nwarm, "decode_attention_ranges", w, nwg)) return st;
   const int nattn = nkv * ntile * nsplit;
-  const int nwg = (int)wge;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, nullptr,
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 1, nattn, w};
   (void)hipGetLastError();

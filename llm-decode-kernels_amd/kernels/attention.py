@@ -92,11 +92,12 @@ def supported(head_dim: int, max_len: int, batch: int, tokens: int) -> bool:
 
 def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tensor,
                      k_cache: torch.Tensor, vt_cache: torch.Tensor, n_heads: int, n_kv: int,
-                     scale: float) -> torch.Tensor:
+                     scale: float, warm=()) -> torch.Tensor:
     """qkv [..., (n_heads + 2 n_kv) * 128] fp16 (one token); pos int64 [1]; inv_freq fp32 [64];
     k_cache [.., n_kv, L/32, 2, 4, 16, 32] and vt_cache [.., n_kv, L/32, 8, 16, 32] fp16, this
     layer's tiled caches (k_to_tiles / vt_to_tiles), updated at pos. Returns the attention output
-    [1, 1, n_heads * 128] fp16."""
+    [1, 1, n_heads * 128] fp16. warm: tensors the launch reads into the caches for the launches
+    after it, as decode_attention_ranges takes them."""
     hd = HEAD_DIM
     assert qkv.shape[-1] == (n_heads + 2 * n_kv) * hd and qkv.numel() == qkv.shape[-1]
     L = k_cache.shape[-5] * CHUNK
@@ -110,15 +111,36 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
     q = qkv.reshape(-1)
     if q.stride(0) != 1:
         q = q.contiguous()
-    dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, what="decode_attention")
+    warm = _warm_list(warm, "decode_attention")
+    dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, *warm, what="decode_attention")
     out = torch.empty((1, 1, n_heads * hd), dtype=torch.float16, device=dev)
     freq = inv_freq.contiguous()
+    wp, wb = _warm_arrays(warm)
     with _lib.device_guard(dev):
         st = _lib.load().ldk_decode_attention(
             _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache),
-            _lib.ptr(vt_cache), _lib.ptr(out), n_heads, n_kv, hd, L, float(scale), _lib.stream(dev))
+            _lib.ptr(vt_cache), _lib.ptr(out), n_heads, n_kv, hd, L, float(scale), wp, wb,
+            len(warm), _lib.stream(dev))
     _lib.check(st, "decode_attention")
     return out
+
+
+def _warm_list(warm, what: str) -> list:
+    """The non-empty warm tensors, checked: at most WARM_MAX_RANGES, each contiguous."""
+    warm = [t for t in warm if t.numel()]
+    if len(warm) > WARM_MAX_RANGES:
+        raise ValueError(f"{what}: at most {WARM_MAX_RANGES} warm ranges")
+    for t in warm:
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: warm tensors must be contiguous")
+    return warm
+
+
+def _warm_arrays(warm: list):
+    """The C arrays of the warm tensors' device addresses and byte sizes."""
+    wp = (ctypes.c_void_p * max(1, len(warm)))(*[t.data_ptr() for t in warm])
+    wb = (ctypes.c_int64 * max(1, len(warm)))(*[t.numel() * t.element_size() for t in warm])
+    return wp, wb
 
 
 # Most position ranges the o projection's merge takes (csrc/w4a16.hip, kAttnRanges).
@@ -168,16 +190,10 @@ def decode_attention_ranges(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torc
     q = qkv.reshape(-1)
     if q.stride(0) != 1:
         q = q.contiguous()
-    warm = [t for t in warm if t.numel()]
-    if len(warm) > WARM_MAX_RANGES:
-        raise ValueError(f"decode_attention_ranges: at most {WARM_MAX_RANGES} warm ranges")
-    for t in warm:
-        if not t.is_contiguous():
-            raise ValueError("decode_attention_ranges: warm tensors must be contiguous")
+    warm = _warm_list(warm, "decode_attention_ranges")
     dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, *warm, what="decode_attention_ranges")
     freq = inv_freq.contiguous()
-    wp = (ctypes.c_void_p * max(1, len(warm)))(*[t.data_ptr() for t in warm])
-    wb = (ctypes.c_int64 * max(1, len(warm)))(*[t.numel() * t.element_size() for t in warm])
+    wp, wb = _warm_arrays(warm)
     with _lib.device_guard(dev):
         st = _lib.load().ldk_decode_attention_ranges(
             _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache), _lib.ptr(vt_cache),

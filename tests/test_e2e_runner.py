@@ -185,6 +185,27 @@ def test_attention_merged_in_o_projection_matches_merge_launch():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("backend", ["ours", "fp16"])
+def test_warming_changes_no_logit(backend):
+    """The fused attention's launch reading the next weights into the caches (QwenRunner.warm_set;
+    the merged ranges on `ours`, the attention with its own output on `fp16`) leaves every decode
+    step's logits and the KV caches bit-identical to the runner without it."""
+    model = _qwen_heads_model("cuda")
+    warm = QwenRunner(model, make_backend(backend), max_len=416)
+    cold = QwenRunner(model, make_backend(backend), max_len=416)
+    assert warm.backend.warms and warm.warm_weights and warm.warm_set(0)
+    cold.warm_weights = False
+    ids = torch.randint(0, 512, (1, 136), device="cuda")
+    P = 124
+    warm.forward(ids[:, :P], torch.arange(P, device="cuda"))
+    cold.forward(ids[:, :P], torch.arange(P, device="cuda"))
+    for t in range(P, 136):  # crosses the first range edge (128)
+        pos = torch.tensor([t], device="cuda")
+        assert torch.equal(warm.forward(ids[:, t: t + 1], pos), cold.forward(ids[:, t: t + 1], pos))
+    assert torch.equal(warm.k_cache, cold.k_cache) and torch.equal(warm.vt_cache, cold.vt_cache)
+
+
+@pytest.mark.gpu
 def test_fused_attention_graph_decoder_matches_eager_steps():
     """The captured decode step with the fused attention replays exactly the eager steps."""
     from kernels.e2e.run import GraphDecoder

@@ -92,12 +92,14 @@ def test_rejects_unsupported_shapes():
 
         st = _lib.load().ldk_decode_attention(
             _lib.ptr(qkv), _lib.ptr(torch.zeros(1, dtype=torch.int64, device="cuda")), _lib.ptr(inv),
-            _lib.ptr(kc), _lib.ptr(vt), _lib.ptr(qkv), 12, 2, 64, 32, 1.0, _lib.stream(qkv.device))
+            _lib.ptr(kc), _lib.ptr(vt), _lib.ptr(qkv), 12, 2, 64, 32, 1.0, None, None, 0,
+            _lib.stream(qkv.device))
         _lib.check(st, "decode_attention")
     with pytest.raises(RuntimeError):  # max_len 40 is not a multiple of 32
         st = _lib.load().ldk_decode_attention(
             _lib.ptr(qkv), _lib.ptr(torch.zeros(1, dtype=torch.int64, device="cuda")), _lib.ptr(inv),
-            _lib.ptr(kc), _lib.ptr(vt), _lib.ptr(qkv), 12, 2, 128, 40, 1.0, _lib.stream(qkv.device))
+            _lib.ptr(kc), _lib.ptr(vt), _lib.ptr(qkv), 12, 2, 128, 40, 1.0, None, None, 0,
+            _lib.stream(qkv.device))
         _lib.check(st, "decode_attention")
 
 
