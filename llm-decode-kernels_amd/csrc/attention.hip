@@ -52,6 +52,7 @@
 
 #include "attention.h"
 #include "ldk_common.h"
+#include "warm.h"
 
 namespace {
 
@@ -83,17 +84,6 @@ __device__ __forceinline__ int vt_offset(int d, int p) {
 __device__ float g_ml[kMaxHeads][kMaxSplits][2];
 __device__ __align__(16) float g_o[kMaxHeads][kMaxSplits][kHD];
 
-// Byte ranges that a launch's spare workgroups read into the caches (the MALL, and the reading
-// XCD's L2) for the launches after it: range k is p[k] [0, end[k] - end[k - 1]) in 16-byte units
-// and is read by the warming workgroups [wg_end[k - 1], wg_end[k]); both cumulative, entries past
-// the used ones repeat the last values (empty ranges with no workgroups).
-constexpr int kWarmMax = 8;
-struct WarmRanges {
-  const u32x4* p[kWarmMax];
-  uint32_t end[kWarmMax];
-  uint32_t wg_end[kWarmMax];
-};
-
 struct AttnArgs {
   const half_t* qkv;
   const int64_t* pos;
@@ -107,7 +97,7 @@ struct AttnArgs {
   float scale;
   int partials;           // 1: every range writes its partials, also a lone live range (no output)
   int nattn;              // attention workgroups (nkv * ntile * ranges); the ones after them warm
-  WarmRanges warm;
+  ldk::WarmRanges warm;
 };
 
 // fp16 RoPE of the pair (x0, x1) = (x[d], x[d + 64]) of a 128-vector (rotate_half pairs d with
@@ -144,35 +134,10 @@ __device__ __forceinline__ float4_t mfma16(u32x4 a, u32x4 b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
 }
 
-// Warming workgroup wg: its range found from the cumulative workgroup counts (scalar selects, no
-// indexing), then kWarmLoads 16-byte loads per lane in flight over its share of the range, each
-// value consumed by an empty asm so that the loads are kept and completed. Indices past the
-// range's end re-read its last 16 bytes (in bounds). Every range is read at the same time.
+// Warming workgroups (warm.h) of the attention's launch: 16 loads per lane, at most one per CU
+// beside the attention's (208 VGPRs: one 512-lane workgroup per CU).
 constexpr int kWarmLoads = 16;
-constexpr int kWarmWorkgroups = 248;  // at most: one per CU beside the attention's (208 VGPRs: one
-                                      // 512-lane workgroup per CU)
-__device__ __forceinline__ void warm_read(const WarmRanges& w, uint32_t wg) {
-  const u32x4* p = w.p[0];
-  uint32_t beg = 0, n = w.end[0], wbeg = 0, nw = w.wg_end[0];
-#pragma unroll
-  for (int k = 1; k < kWarmMax; ++k) {
-    const bool in = wg >= w.wg_end[k - 1];
-    p = in ? w.p[k] : p;
-    beg = in ? w.end[k - 1] : beg;
-    n = in ? w.end[k] : n;
-    wbeg = in ? w.wg_end[k - 1] : wbeg;
-    nw = in ? w.wg_end[k] : nw;
-  }
-  n -= beg;
-  const uint32_t step = (nw - wbeg) * (kWaves * 64);
-  for (uint32_t i0 = (wg - wbeg) * (kWaves * 64) + threadIdx.x; i0 < n; i0 += kWarmLoads * step) {
-    u32x4 v[kWarmLoads];
-#pragma unroll
-    for (int u = 0; u < kWarmLoads; ++u) v[u] = p[min(i0 + u * step, n - 1)];
-#pragma unroll
-    for (int u = 0; u < kWarmLoads; ++u) asm volatile("" ::"v"(v[u]));
-  }
-}
+constexpr int kWarmWorkgroups = 248;
 
 template <int N>
 struct IntC {
@@ -190,7 +155,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   const int c16 = lane & 15, kb = lane >> 4;
   const int gq = a.nq / a.nkv;
   if ((int)blockIdx.x >= a.nattn) {  // uniform: a warming workgroup (dispatched after the attention's)
-    warm_read(a.warm, blockIdx.x - a.nattn);
+    ldk::warm_read<kWaves * 64, kWarmLoads>(a.warm, blockIdx.x - a.nattn);
     return;
   }
   // workgroup b = split * (nkv * ntile) + kvh * ntile + tile
@@ -498,43 +463,6 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
   out[(int64_t)h * kHD + lane + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
 }
 
-// The warm ranges of an attention launch (see WarmRanges) from the caller's arrays, and the
-// number of warming workgroups to add to its grid.
-int make_warm(const void* const* warm, const int64_t* warm_bytes, int nwarm, const char* what, WarmRanges& w,
-              uint32_t& nwg) {
-  if (nwarm < 0 || nwarm > kWarmMax || (nwarm > 0 && (!warm || !warm_bytes)))
-    return ldk::fail(LDK_ERR_INVALID, "%s: nwarm=%d must be 0..%d with both arrays", what, nwarm, kWarmMax);
-  uint64_t end = 0, need = 0;
-  for (int k = 0; k < nwarm; ++k) {
-    if (!warm[k] || warm_bytes[k] < 0 || warm_bytes[k] % 16 || !ldk::aligned(warm[k], 16))
-      return ldk::fail(LDK_ERR_ALIGN, "%s: warm range %d must be non-null, 16-byte aligned, a multiple of 16 bytes (%lld)",
-                       what, k, (long long)warm_bytes[k]);
-    end += (uint64_t)warm_bytes[k] / 16;
-    if (end >= (1ull << 31)) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: warm ranges above 32 GiB", what);
-    w.p[k] = static_cast<const u32x4*>(warm[k]);
-    w.end[k] = (uint32_t)end;
-    need += ((uint64_t)warm_bytes[k] / 16 + kWaves * 64 * kWarmLoads - 1) / (kWaves * 64 * kWarmLoads);
-  }
-  // Warming workgroups per range: enough for kWarmLoads loads per lane where they all fit in
-  // kWarmWorkgroups, else in proportion to the range's bytes (at least one per non-empty range).
-  uint32_t wge = 0;
-  for (int k = 0; k < nwarm; ++k) {
-    const uint64_t units = w.end[k] - (k ? w.end[k - 1] : 0);
-    uint64_t c = (units + kWaves * 64 * kWarmLoads - 1) / (kWaves * 64 * kWarmLoads);
-    if (need > (uint64_t)kWarmWorkgroups && units)
-      c = std::max<uint64_t>(1, units * (kWarmWorkgroups - kWarmMax) / end);
-    wge += (uint32_t)c;
-    w.wg_end[k] = wge;
-  }
-  for (int k = nwarm; k < kWarmMax; ++k) {  // empty ranges
-    w.p[k] = nwarm ? w.p[nwarm - 1] : nullptr;
-    w.end[k] = (uint32_t)end;
-    w.wg_end[k] = wge;
-  }
-  nwg = wge;
-  return LDK_OK;
-}
-
 }  // namespace
 
 extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
@@ -565,9 +493,10 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
     rlen = std::max<int64_t>(128, (nchunk + kMaxSplits - 1) / kMaxSplits * kChunk);
   const int nsplit = (int)((max_len + rlen - 1) / rlen);
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
-  WarmRanges w{};
+  ldk::WarmRanges w;
   uint32_t nwg = 0;
-  if (const int st = make_warm(warm, warm_bytes, nwarm, "decode_attention", w, nwg)) return st;
+  if (const int st = ldk::make_warm(warm, warm_bytes, nwarm, "decode_attention", kWaves * 64, kWarmLoads, kWarmWorkgroups, w, nwg))
+    return st;
   const int nattn = nkv * ntile * nsplit;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, (half_t*)out,
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 0, nattn, w};
@@ -601,9 +530,11 @@ extern "C" int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, 
     return ldk::fail(LDK_ERR_ALIGN, "decode_attention_ranges: k_cache and vt_cache 16-byte, pos 8-byte aligned");
   const int nsplit = (int)((max_len + rlen - 1) / rlen);
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
-  WarmRanges w{};
+  ldk::WarmRanges w;
   uint32_t nwg = 0;
-  if (const int st = make_warm(warm, warm_bytes, nwarm, "decode_attention_ranges", w, nwg)) return st;
+  if (const int st = ldk::make_warm(warm, warm_bytes, nwarm, "decode_attention_ranges", kWaves * 64, kWarmLoads,
+                                    kWarmWorkgroups, w, nwg))
+    return st;
   const int nattn = nkv * ntile * nsplit;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, nullptr,
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 1, nattn, w};

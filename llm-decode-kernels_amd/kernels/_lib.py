@@ -146,6 +146,29 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise ValueError(f"unsupported dtype {dtype}; expected float16, bfloat16 or float32") from None
 
 
+# Most byte ranges one launch warms (csrc/warm.h, kWarmMax).
+WARM_MAX_RANGES = 8
+
+
+def warm_list(warm, what: str) -> list:
+    """The non-empty tensors of a launch's warm ranges, checked: at most WARM_MAX_RANGES, each
+    contiguous."""
+    warm = [t for t in warm if t.numel()]
+    if len(warm) > WARM_MAX_RANGES:
+        raise ValueError(f"{what}: at most {WARM_MAX_RANGES} warm ranges")
+    for t in warm:
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: warm tensors must be contiguous")
+    return warm
+
+
+def warm_arrays(warm: list):
+    """The C arrays of the warm tensors' device addresses and byte sizes."""
+    wp = (ctypes.c_void_p * max(1, len(warm)))(*[t.data_ptr() for t in warm])
+    wb = (ctypes.c_int64 * max(1, len(warm)))(*[t.numel() * t.element_size() for t in warm])
+    return wp, wb
+
+
 def require_gpu(*tensors: torch.Tensor | None, what: str) -> torch.device:
     """All given tensors must live on one ROCm GPU. There is no CPU implementation."""
     dev = None

@@ -8,7 +8,6 @@ It replaces, for decode steps, the attention block of the reference's Qwen2 runn
 
 from __future__ import annotations
 
-import ctypes
 from typing import NamedTuple
 
 import torch
@@ -111,11 +110,11 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
     q = qkv.reshape(-1)
     if q.stride(0) != 1:
         q = q.contiguous()
-    warm = _warm_list(warm, "decode_attention")
+    warm = _lib.warm_list(warm, "decode_attention")
     dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, *warm, what="decode_attention")
     out = torch.empty((1, 1, n_heads * hd), dtype=torch.float16, device=dev)
     freq = inv_freq.contiguous()
-    wp, wb = _warm_arrays(warm)
+    wp, wb = _lib.warm_arrays(warm)
     with _lib.device_guard(dev):
         st = _lib.load().ldk_decode_attention(
             _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache),
@@ -125,28 +124,10 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
     return out
 
 
-def _warm_list(warm, what: str) -> list:
-    """The non-empty warm tensors, checked: at most WARM_MAX_RANGES, each contiguous."""
-    warm = [t for t in warm if t.numel()]
-    if len(warm) > WARM_MAX_RANGES:
-        raise ValueError(f"{what}: at most {WARM_MAX_RANGES} warm ranges")
-    for t in warm:
-        if not t.is_contiguous():
-            raise ValueError(f"{what}: warm tensors must be contiguous")
-    return warm
-
-
-def _warm_arrays(warm: list):
-    """The C arrays of the warm tensors' device addresses and byte sizes."""
-    wp = (ctypes.c_void_p * max(1, len(warm)))(*[t.data_ptr() for t in warm])
-    wb = (ctypes.c_int64 * max(1, len(warm)))(*[t.numel() * t.element_size() for t in warm])
-    return wp, wb
-
-
 # Most position ranges the o projection's merge takes (csrc/w4a16.hip, kAttnRanges).
 MERGE_MAX_RANGES = 4
-# Most byte ranges one attention launch warms (csrc/attention.hip, kWarmMax).
-WARM_MAX_RANGES = 8
+# Most byte ranges one launch warms (csrc/warm.h, kWarmMax).
+WARM_MAX_RANGES = _lib.WARM_MAX_RANGES
 
 
 class AttnRanges(NamedTuple):
@@ -190,10 +171,10 @@ def decode_attention_ranges(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torc
     q = qkv.reshape(-1)
     if q.stride(0) != 1:
         q = q.contiguous()
-    warm = _warm_list(warm, "decode_attention_ranges")
+    warm = _lib.warm_list(warm, "decode_attention_ranges")
     dev = _lib.require_gpu(q, pos, inv_freq, k_cache, vt_cache, *warm, what="decode_attention_ranges")
     freq = inv_freq.contiguous()
-    wp, wb = _warm_arrays(warm)
+    wp, wb = _lib.warm_arrays(warm)
     with _lib.device_guard(dev):
         st = _lib.load().ldk_decode_attention_ranges(
             _lib.ptr(q), _lib.ptr(pos), _lib.ptr(freq), _lib.ptr(k_cache), _lib.ptr(vt_cache),
