@@ -303,6 +303,9 @@ int ldk_w4a16_matmul_residual_stats(const void* x, const void* residual, void* h
  * x staging (the merge launch's arithmetic; the sum of the weighted l is a chain in range order
  * there, a lane reduction in the merge launch, so x can differ from it in the last fp16 bit).
  * K = nq * 128, at most 4 ranges (ceil(max_len / rlen) <= 4), group size 128, pos 8-byte aligned.
+ * The last ldk_decode_attention_ranges call on the device must have left its partials on this
+ * stream with this max_len, rlen and nq, and no ldk_decode_attention range launch (a cache of
+ * more than 512 positions) may have overwritten them since: else LDK_ERR_INVALID, no launch.
  * One launch in place of the attention's merge launch and the projection. No counterpart entry
  * exists in the reference. */
 int ldk_w4a16_attn_matmul_residual_stats(const int64_t* pos, int64_t max_len, int64_t rlen, int nq,

@@ -465,6 +465,10 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
 
 }  // namespace
 
+namespace ldk {
+void note_partials(bool pending, void* stream, int64_t max_len, int64_t rlen, int nq);
+}  // namespace ldk
+
 extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
                                     void* vt_cache, void* out, int nq, int nkv, int head_dim, int64_t max_len,
                                     float scale, const void* const* warm, const int64_t* warm_bytes, int nwarm,
@@ -502,8 +506,10 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 0, nattn, w};
   (void)hipGetLastError();
   decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
-  if (nsplit > 1)
+  if (nsplit > 1) {
     attention_merge_kernel<<<nq, 64, 0, (hipStream_t)stream>>>(pos, (half_t*)out, (int)max_len, (int)rlen);
+    ldk::note_partials(false, stream, 0, 0, 0);  // the partials of a pending range call are overwritten
+  }
   return ldk::check_launch("decode_attention");
 }
 
@@ -540,7 +546,9 @@ extern "C" int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, 
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 1, nattn, w};
   (void)hipGetLastError();
   decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
-  return ldk::check_launch("decode_attention_ranges");
+  const int st = ldk::check_launch("decode_attention_ranges");
+  ldk::note_partials(st == LDK_OK, stream, max_len, rlen, nq);
+  return st;
 }
 
 namespace ldk {
@@ -550,20 +558,44 @@ constexpr int kMaxDevices = 64;
 std::mutex g_part_mu;
 const float* g_part_o[kMaxDevices];  // device addresses of g_o / g_ml per device, set on first use
 const float* g_part_ml[kMaxDevices];
+struct PartialsNote {  // the last ldk_decode_attention_ranges call per device
+  bool pending;
+  void* stream;
+  int64_t max_len, rlen;
+  int nq;
+};
+PartialsNote g_part_note[kMaxDevices];
 }  // namespace
 
-int attention_partials(const float** o, const float** ml) {
+// Records (pending) or forgets the partials' producer on the current device.
+void note_partials(bool pending, void* stream, int64_t max_len, int64_t rlen, int nq) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_part_mu);
+  g_part_note[dev] = PartialsNote{pending, stream, max_len, rlen, nq};
+}
+
+int attention_partials(const char* what, void* stream, int64_t max_len, int64_t rlen, int nq, const float** o,
+                       const float** ml) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(LDK_ERR_LAUNCH, "attention partials: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
+    return fail(LDK_ERR_LAUNCH, "%s: no current HIP device (or device %d >= %d)", what, dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_part_mu);
+  const PartialsNote& n = g_part_note[dev];
+  if (!n.pending)
+    return fail(LDK_ERR_INVALID, "%s: no ldk_decode_attention_ranges partials pending on device %d", what, dev);
+  if (n.stream != stream)
+    return fail(LDK_ERR_INVALID, "%s: the attention ranges were left on another stream; call it on the same stream", what);
+  if (n.max_len != max_len || n.rlen != rlen || n.nq != nq)
+    return fail(LDK_ERR_INVALID, "%s: max_len=%lld rlen=%lld nq=%d, the attention ranges were max_len=%lld rlen=%lld nq=%d",
+                what, (long long)max_len, (long long)rlen, nq, (long long)n.max_len, (long long)n.rlen, n.nq);
   if (!g_part_o[dev]) {
     void* po = nullptr;
     void* pm = nullptr;
     const hipError_t e1 = hipGetSymbolAddress(&po, HIP_SYMBOL(g_o));
     const hipError_t e2 = hipGetSymbolAddress(&pm, HIP_SYMBOL(g_ml));
     if (e1 != hipSuccess || e2 != hipSuccess || !po || !pm)
-      return fail(LDK_ERR_LAUNCH, "attention partials: hipGetSymbolAddress failed on device %d", dev);
+      return fail(LDK_ERR_LAUNCH, "%s: hipGetSymbolAddress of the attention partials failed on device %d", what, dev);
     g_part_o[dev] = static_cast<const float*>(po);
     g_part_ml[dev] = static_cast<const float*>(pm);
   }

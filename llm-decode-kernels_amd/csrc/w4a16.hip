@@ -2018,7 +2018,7 @@ extern "C" int ldk_w4a16_attn_matmul_residual_stats(const int64_t* pos, int64_t 
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
   const float *po = nullptr, *pm = nullptr;
-  st = ldk::attention_partials(&po, &pm);
+  st = ldk::attention_partials(fn, stream, max_len, rlen, nq, &po, &pm);
   if (st) return st;
   const Plan p = residual_stats_plan(N, K, gsh_rows, workspace ? (size_t)workspace_bytes : 0);
   const int64_t tiles = (N + plan_cw(p) - 1) / plan_cw(p);

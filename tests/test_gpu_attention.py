@@ -294,3 +294,45 @@ def test_ranges_warm_rejects_bad_ranges():
     assert call([base + 8], [16], 1) == _lib.ERR_ALIGN
     assert call([base], [24], 1) == _lib.ERR_ALIGN
     assert call([base], [-16], 1) == _lib.ERR_ALIGN
+
+
+def test_ranges_consumer_checks_stream_and_geometry():
+    """The o projection that merges the attention's ranges reads library-owned partials, so it is
+    refused unless the last decode_attention_ranges call on the device left them on its stream
+    with its geometry: another stream, another range length, and partials overwritten by
+    decode_attention's own range launch (a cache of more than 512 positions) are errors; the same
+    stream works."""
+    from kernels.attention import decode_attention_ranges, ranges_len
+    from kernels.fused import attn_linear_rmsnorm_w4a16_matmul
+
+    nq, nkv, hd, H, I2, L = 12, 2, 128, 1536, 2 * 1024, 416
+    g = torch.Generator().manual_seed(78)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    _, _, kt, vt = _caches(g, nkv, L)
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    qo, so, zo = _w4_linear(g, H, nq * hd)
+    qg, sg, zg = _w4_linear(g, I2, H)
+    res = torch.randn(1, 1, H, generator=g).half().cuda()
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).half().cuda()
+    p = torch.tensor([300], device="cuda")
+
+    def merge(rng):
+        return attn_linear_rmsnorm_w4a16_matmul(rng, qo, so, zo, None, res, nw, 1e-6, qg, sg, zg)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        rng = decode_attention_ranges(qkv, p, inv_freq, kt, vt, nq, nkv, hd ** -0.5, ranges_len(L))
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="another stream"):
+        merge(rng)
+    with torch.cuda.stream(side):
+        y, _ = merge(rng)
+        with pytest.raises(ValueError, match="rlen"):
+            merge(rng._replace(rlen=L))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    _, _, kt2, vt2 = _caches(g, nkv, 1024)
+    decode_attention(qkv, torch.tensor([900], device="cuda"), inv_freq, kt2, vt2, nq, nkv, hd ** -0.5)
+    with pytest.raises(ValueError, match="pending"):
+        merge(rng)
