@@ -22,6 +22,12 @@ from kernels.swiglu import swiglu_fused
 from kernels.w4a16 import w4a16_matmul
 
 FUSED_GROUP_SIZE = 128
+# Widest projection that rmsnorm_w4a16_matmul fuses. Every workgroup of the fused launch forms
+# the row statistic itself (its own loads and a barrier) and the launch takes whole column tiles,
+# which costs little on one round of tiles and grows with the rounds: graph-timed at K = 1536,
+# N = 2048 3.46 against 3.37 us plain, N = 17920 7.52 against 5.25, and the 151936-row quantized
+# lm_head 33.4 against 24.0 us, where the norm as a launch of its own (about 2.5 us) wins.
+FUSED_NORM_MAX_N = 65536
 
 
 def _aligned(*ts) -> bool:
@@ -38,7 +44,7 @@ def rmsnorm_w4a16_matmul(x, weight, eps, residual, qweight, scales, zeros, group
     N = qweight.shape[1]
     rows = x.numel() // K
     fuse = (rows == 1 and group_size == FUSED_GROUP_SIZE and x.dtype == torch.float16
-            and weight.dtype == torch.float16 and x.is_cuda
+            and weight.dtype == torch.float16 and x.is_cuda and N <= FUSED_NORM_MAX_N
             and _aligned(x, weight, residual, qweight))
     if not fuse:
         if residual is None:

@@ -45,7 +45,10 @@ def _oracle_linear(xn, qw, s, z, b):
                                       (17920, 1536, False), (512, 8960, False),
                                       (151936, 1536, False)])
 @pytest.mark.parametrize("with_res", [True, False])
-def test_rmsnorm_matmul(N, K, bias, with_res):
+def test_rmsnorm_matmul(N, K, bias, with_res, monkeypatch):
+    import kernels.fused as fused_mod
+
+    monkeypatch.setattr(fused_mod, "FUSED_NORM_MAX_N", 1 << 30)  # the fused launch at every N
     qw, s, z, b = _weights(N, K, 11, bias)
     x, r, w = cases.rmsnorm_case(1, K, 12)
     res = r.cuda() if with_res else None
@@ -68,6 +71,21 @@ def test_rmsnorm_matmul(N, K, bias, with_res):
     y2 = w4a16_matmul(h2, qw, s, z, 128, None if b is None else b.cuda())
     d = (y.view(1, N).float() - y2.float()).abs()
     assert float(d.max()) <= 4e-3 * max(1.0, float(y2.float().abs().max())), float(d.max())
+
+
+def test_rmsnorm_matmul_wide_runs_two_launches():
+    """Above FUSED_NORM_MAX_N columns (the 151936-row quantized lm_head) the wrapper runs the
+    norm as a launch of its own and the plain GEMV: bit-identical to those two calls."""
+    import kernels.fused as fused_mod
+
+    N, K = 151936, 1536
+    assert N > fused_mod.FUSED_NORM_MAX_N
+    qw, s, z, _ = _weights(N, K, 13, False)
+    x, r, w = cases.rmsnorm_case(1, K, 14)
+    x, r, w = x.cuda().view(1, 1, K), r.cuda().view(1, 1, K), w.cuda()
+    y, h = rmsnorm_w4a16_matmul(x, w, 1e-6, r, qw, s, z, 128)
+    h2, res2 = rmsnorm(x, w, 1e-6, residual=r)
+    assert torch.equal(h, res2) and torch.equal(y, w4a16_matmul(h2, qw, s, z, 128))
 
 
 @pytest.mark.parametrize("N,K", [(1536, 8960), (1536, 1536), (256, 8960), (4096, 2048)])
