@@ -191,7 +191,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the W4A16 path would shard by output columns with no exchange; see DESIGN.md)",
+              "(the W4A16 path would shard by output columns, each GPU its own tiles, with no "
+              "exchange)",
               file=sys.stderr)
         return 2
 

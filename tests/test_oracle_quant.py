@@ -37,7 +37,8 @@ def test_pack_bit_positions():
 
 
 def test_weight_bytes_kat():
-    """Reference tests/test_quant.py:34-35 and the SURVEY byte table."""
+    """Reference tests/test_quant.py:34-35, and the byte counts of the four Qwen2.5-1.5B
+    projections: N*K/2 packed bytes plus fp16 scales and zeros per group of 128."""
     assert quant.weight_bytes(1536, 1536) == 1536 * 1536 // 2 + 2 * 12 * 1536 * 2 == 1_253_376
     assert quant.weight_bytes(17920, 1536) == 14_622_720
     assert quant.weight_bytes(1536, 8960) == 7_311_360
