@@ -336,3 +336,21 @@ def test_ranges_consumer_checks_stream_and_geometry():
     decode_attention(qkv, torch.tensor([900], device="cuda"), inv_freq, kt2, vt2, nq, nkv, hd ** -0.5)
     with pytest.raises(ValueError, match="pending"):
         merge(rng)
+
+
+@pytest.mark.parametrize("L,pos", [(416, 300), (1024, 900), (4096, 4000)])
+def test_decode_attention_warm_changes_nothing(L, pos):
+    """decode_attention with warm tensors (one range, and several ranges with their merge
+    launch) returns the same output and cache update, bit for bit, as without them."""
+    nq, nkv, hd = 12, 2, 128
+    g = torch.Generator().manual_seed(79 + L)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    _, _, kt_a, vt_a = _caches(g, nkv, L)
+    kt_b, vt_b = kt_a.clone(), vt_a.clone()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    warm = [torch.randint(0, 1 << 30, (3 << 20,), dtype=torch.int32, generator=g).cuda(),
+            torch.zeros(4096, dtype=torch.uint8, device="cuda")]
+    p = torch.tensor([pos], device="cuda")
+    a = decode_attention(qkv, p, inv_freq, kt_a, vt_a, nq, nkv, hd ** -0.5)
+    b = decode_attention(qkv, p, inv_freq, kt_b, vt_b, nq, nkv, hd ** -0.5, warm=warm)
+    assert torch.equal(a, b) and torch.equal(kt_a, kt_b) and torch.equal(vt_a, vt_b)
