@@ -6,7 +6,9 @@ in torch, oracle/torch_cpu.py) timed beside it on the host cores.
 
 A step is one W4A16 launch over one rotating input set (x, qweight, scales, zeros, output); the
 sets are sized to 4x the 256 MB MALL so every step reads its weights from HBM. Steps run as
-hipGraph replays of one launch per set, HIP events on the replay stream. The timed region holds
+hipGraph replays of one launch per set, HIP events on the replay stream. The --warmup W untimed
+launches run as whole replays (W rounded up; the count run is reported as timed.warmup_launches,
+while "warmup" echoes W as requested). The timed region holds
 7 samples, each of at least max(K, 50 ms worth of) launches in whole replays; ms_per_step is the
 median sample's time per launch. The config-4 decode (fp16 vs swapped tok/s) and the CPU
 baseline are reported beside it. Prints one JSON line.
@@ -239,7 +241,7 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": warm_replays * per_replay,
+        "warmup": args.warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -251,6 +253,7 @@ def main() -> int:
                    "M": M, "N": N, "K": K, "group_size": GS, "rotating_sets": ncopy,
                    "kernel_config": kcfg},
         "timed": {"samples": SAMPLES, "launches_per_sample": replays * per_replay,
+                  "warmup_launches": warm_replays * per_replay,
                   "sample_ms_per_launch": [round(v, 6) for v in samples],
                   "wall_s": round(wall, 3)},
         "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),

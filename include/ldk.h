@@ -116,10 +116,15 @@ int ldk_w4a16_decode(const void* x, int64_t ldx, const int32_t* qweight, const v
                      int64_t N, int64_t K, int group_size, int split_k, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
-/* The configuration the library would use for (M, N, K, group_size) with all-zero tuning
- * arguments and a workspace of ldk_workspace_bytes(): block_n, split_k (workgroups per column
- * tile) and the path/mode/LDK_CPW_* flags. Replaces the choice tables of kernels/w4a16.py:282-298 (_pick_decode_path) and
- * kernels/cuda/w4a16_cuda.py:29-42 (_pick_split), which are exported by w4a16.py:333-355. */
+/* Plan query: what ldk_w4a16_matmul runs for (M, N, K, group_size) with contiguous x and out
+ * (ldx = K, ldo = N) and a workspace of ldk_workspace_bytes(). On entry *block_n, *split_k and
+ * *flags are the tuning arguments a call would pass (all zero: the library's table); on return
+ * they hold what runs: the output columns per workgroup, the workgroups splitting K per column
+ * tile (the K splits of the prefill GEMM), and the path/mode/LDK_CPW_* flags (LDK_PATH_GEMM for
+ * the prefill GEMM). Returns the status the call would return for those arguments, without
+ * launching anything (a query needs no GPU). Replaces the choice tables of kernels/w4a16.py:282-298
+ * (_pick_decode_path) and kernels/cuda/w4a16_cuda.py:29-42 (_pick_split), which are exported by
+ * w4a16.py:333-355. */
 int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n,
                      int* split_k, int* flags);
 
@@ -186,12 +191,21 @@ int ldk_fp8_dequant(const uint8_t* wq, const void* scale, int dtype, void* out, 
 
 /* out [M, N] = x [M, K] @ (e4m3(wq) * scale)^T (+ bias), fp32 accumulation, fp16 out.
  * wq [K, N] e4m3fn, scale [N] fp16. Replaces kernels/fp8.py:200-223 (w8a16_matmul) and its
- * kernels fp8.py:42-127. N % 16 == 0 and 16-byte aligned wq; block_n, split_k, flags and the
- * workspace as for ldk_w4a16_matmul. M > 16 (prefill) runs the MFMA kernel in 16-row blocks. */
+ * kernels fp8.py:42-127, whose column masks take any N: here N % 4 == 0 (K % 8 == 0) and a
+ * 16-byte aligned wq. block_n, split_k, flags and the workspace as for ldk_w4a16_matmul. More than
+ * 64 rows run the prefill GEMM when N % 16 == 0 and K % 64 == 0, else the MFMA kernel in 16-row
+ * blocks. */
 int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale,
                      const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
                      int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
                      void* stream);
+
+/* Plan query for ldk_w8a16_matmul, as ldk_w4a16_config: *block_n, *split_k, *flags in = a
+ * call's tuning arguments, out = what runs (columns per workgroup, K splits, LDK_PATH_VALU /
+ * LDK_PATH_MFMA / LDK_PATH_GEMM) for contiguous x and out and a workspace of
+ * ldk_workspace_bytes(); returns the status the call would return. Replaces the choice table of
+ * kernels/fp8.py:175-187 (_pick), which the reference fills by timing. */
+int ldk_w8a16_config(int64_t M, int64_t N, int64_t K, int* block_n, int* split_k, int* flags);
 
 /* out [1, N] = (silu(g) * u) @ dequant_fp8(wq) (+ bias) for one row gate_up = [g | u] of 2K fp16
  * values: the activation is formed inside the W8A16 GEMV's x staging with the steps of

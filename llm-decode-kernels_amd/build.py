@@ -55,25 +55,8 @@ def _compile(src: Path, save_temps: Path | None) -> Path:
     return obj
 
 
-PROBE_SRC = PKG / "kernels" / "bench" / "probe.hip"
-PROBE_LIB = PKG / "kernels" / "bench" / "libldk_probe.so"
-
-
-def build_probe() -> Path:
-    """kernels/bench/libldk_probe.so: the calibration kernels of the roofline measurements (not
-    part of the product library's C ABI)."""
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *CFLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed on probe.hip:\n" + res.stderr[-4000:])
-    os.replace(tmp, PROBE_LIB)
-    return PROBE_LIB
-
-
 def build(jobs: int | None = None, save_temps: str | None = None, verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link kernels/libldk_amd.so (and the calibration
-    library kernels/bench/libldk_probe.so). Returns the product library's path."""
+    """Compile every csrc/*.hip for gfx950 and link kernels/libldk_amd.so. Returns its path."""
     OBJ.mkdir(exist_ok=True)
     st = Path(save_temps).resolve() if save_temps else None
     if st:
@@ -81,9 +64,7 @@ def build(jobs: int | None = None, save_temps: str | None = None, verbose: bool 
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        probe = ex.submit(build_probe)
         objs = list(ex.map(lambda s: _compile(s, st), srcs))
-        probe.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)

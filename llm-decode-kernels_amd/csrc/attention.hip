@@ -466,7 +466,7 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
 }  // namespace
 
 namespace ldk {
-void note_partials(bool pending, void* stream, int64_t max_len, int64_t rlen, int nq);
+void note_partials(bool pending, void* stream, const int64_t* pos, int64_t max_len, int64_t rlen, int nq);
 }  // namespace ldk
 
 extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const float* inv_freq, void* k_cache,
@@ -508,7 +508,7 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
   decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
   if (nsplit > 1) {
     attention_merge_kernel<<<nq, 64, 0, (hipStream_t)stream>>>(pos, (half_t*)out, (int)max_len, (int)rlen);
-    ldk::note_partials(false, stream, 0, 0, 0);  // the partials of a pending range call are overwritten
+    ldk::note_partials(false, stream, nullptr, 0, 0, 0);  // the partials of a pending range call are overwritten
   }
   return ldk::check_launch("decode_attention");
 }
@@ -547,7 +547,7 @@ extern "C" int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, 
   (void)hipGetLastError();
   decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
   const int st = ldk::check_launch("decode_attention_ranges");
-  ldk::note_partials(st == LDK_OK, stream, max_len, rlen, nq);
+  ldk::note_partials(st == LDK_OK, stream, pos, max_len, rlen, nq);
   return st;
 }
 
@@ -561,6 +561,7 @@ const float* g_part_ml[kMaxDevices];
 struct PartialsNote {  // the last ldk_decode_attention_ranges call per device
   bool pending;
   void* stream;
+  const int64_t* pos;  // the position the ranges were written at
   int64_t max_len, rlen;
   int nq;
 };
@@ -568,15 +569,15 @@ PartialsNote g_part_note[kMaxDevices];
 }  // namespace
 
 // Records (pending) or forgets the partials' producer on the current device.
-void note_partials(bool pending, void* stream, int64_t max_len, int64_t rlen, int nq) {
+void note_partials(bool pending, void* stream, const int64_t* pos, int64_t max_len, int64_t rlen, int nq) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return;
   std::lock_guard<std::mutex> lock(g_part_mu);
-  g_part_note[dev] = PartialsNote{pending, stream, max_len, rlen, nq};
+  g_part_note[dev] = PartialsNote{pending, stream, pos, max_len, rlen, nq};
 }
 
-int attention_partials(const char* what, void* stream, int64_t max_len, int64_t rlen, int nq, const float** o,
-                       const float** ml) {
+int attention_partials(const char* what, void* stream, const int64_t* pos, int64_t max_len, int64_t rlen, int nq,
+                       const float** o, const float** ml) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return fail(LDK_ERR_LAUNCH, "%s: no current HIP device (or device %d >= %d)", what, dev, kMaxDevices);
@@ -586,6 +587,10 @@ int attention_partials(const char* what, void* stream, int64_t max_len, int64_t 
     return fail(LDK_ERR_INVALID, "%s: no ldk_decode_attention_ranges partials pending on device %d", what, dev);
   if (n.stream != stream)
     return fail(LDK_ERR_INVALID, "%s: the attention ranges were left on another stream; call it on the same stream", what);
+  // the consumer recomputes the live ranges from its own *pos: another position array could name
+  // ranges the producer did not write this step
+  if (n.pos != pos)
+    return fail(LDK_ERR_INVALID, "%s: pos is not the position array the attention ranges were written with", what);
   if (n.max_len != max_len || n.rlen != rlen || n.nq != nq)
     return fail(LDK_ERR_INVALID, "%s: max_len=%lld rlen=%lld nq=%d, the attention ranges were max_len=%lld rlen=%lld nq=%d",
                 what, (long long)max_len, (long long)rlen, nq, (long long)n.max_len, (long long)n.rlen, n.nq);

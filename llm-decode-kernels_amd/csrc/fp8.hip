@@ -124,6 +124,9 @@ __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* __restr
 //    before the first wait. A workgroup covers `kps` rows (one or a few passes); workgroups of
 //    one tile that split K meet in the fixed-point workspace (ldk::splitk_add, deterministic, one
 //    launch).
+//  * N % 16 != 0 (TAIL, N % 4 == 0): rows are then only 4-byte aligned, so a lane loads its 16
+//    columns of a row as four dwords, each clamped on its own to the row's last dword (a dword
+//    past N reads valid memory; its outputs are not stored) instead of one 128-bit load.
 //  * Row blocks of MT <= 4 activation rows: a lane keeps 16 * MT fp32 accumulators. More rows
 //    run as more row-block workgroups over the same weights (the 256 MB MALL serves the repeats).
 //  * x of a pass is staged in LDS transposed, [row][m], so one ds_read gives the MT values of
@@ -172,7 +175,7 @@ __device__ __forceinline__ ldk::SplitK w8_split_ctx(const W8Split& sp, int split
 //           the pass (one LDS barrier, which waits for those loads only). The statistic's order
 //           differs from the RMSNorm kernel's, so a staged value can differ from its output by
 //           one fp16 ulp.
-template <int MT, int LN, int NW, int RPL, int PRO>
+template <int MT, int LN, int NW, int RPL, int PRO, bool TAIL>
 __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split sp) {
   static_assert(PRO == 0 || MT == 1, "the prologues take one row");
   constexpr bool kRms = PRO == 2 || PRO == 3, kRes = PRO == 3;
@@ -192,7 +195,8 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
   const int ln = lane % LN, lk = lane / LN;
   const int tile = blockIdx.x, split = blockIdx.y, mb = blockIdx.z;
   const int n0 = tile * CW;
-  const int col = min(n0 + 16 * ln, a.N - 16);  // clamped: tail lanes load valid memory, store nothing
+  // clamped: lanes past N load valid memory and store nothing (TAIL: each dword clamped itself)
+  const int col = TAIL ? n0 + 16 * ln : min(n0 + 16 * ln, a.N - 16);
   const int m0 = mb * MT;
   const int rb = split * sp.kps, re = min(a.K, rb + sp.kps);
   const int lrow = wave * LKW + lk;  // this lane's first row inside a pass
@@ -230,7 +234,14 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
       const int r = min(p0 + lrow + j * LKW * NW, re - 1);  // clamped; such rows meet zero x
-      w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.wq + (int64_t)r * a.N + col));
+      if constexpr (TAIL) {
+        const uint8_t* row = a.wq + (int64_t)r * a.N;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          w[j][d] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row + min(col + 4 * d, a.N - 4)));
+      } else {
+        w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.wq + (int64_t)r * a.N + col));
+      }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the pass is in flight first
     if constexpr (kRms) {
@@ -345,7 +356,9 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
 //  * A operand: x row m = c16, K block 8 kb, one 16-byte load (zeros past M or past K).
 // A workgroup owns 128 columns and a K range; its waves take K steps round-robin, KSW per pass
 // with every load of the pass in flight; partial tiles meet in LDS, then the per-channel scale.
-// 64-column tiles share each 128-byte line of a K row with their neighbour. Their launch is one
+// 64-column tiles share each 128-byte line of a K row with their neighbour. A lane's CPL-byte
+// loads need rows aligned to CPL bytes: N % 8 == 0 for 128 columns, N % 4 == 0 for 64 (the plan
+// takes 64 when N % 8 != 0). Their launch is one
 // dimension over (tile, K split) pieces: the two pieces of each line pair (tiles 2q and 2q + 1,
 // one split) run as workgroups L and L + 8 of a group of 16, which the dispatcher places on the
 // same XCD (workgroup L goes to XCD L % 8) at about the same time, so the line comes into that
@@ -503,7 +516,9 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
   p.mt = 16;
   p.mblocks = 1;
   const bool narrow = (N + 127) / 128 < 128 && M <= 16;
-  p.ln = block_n == 64 || (block_n == 0 && narrow) ? 4 : 8;
+  // 128-column tiles load 8 bytes of a row per lane: rows must be 8-byte aligned (N % 8 == 0);
+  // 64-column tiles load 4 (N % 4 == 0)
+  p.ln = block_n == 64 || (block_n == 0 && (narrow || N % 8)) ? 4 : 8;
   p.nw = kW8MfmaWaves;
   const int64_t tiles = (N + 16 * p.ln - 1) / (16 * p.ln);
   const int64_t steps = (K + 31) / 32;
@@ -606,26 +621,30 @@ W8Plan make_w8_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, i
   return p;
 }
 
-template <int MT, int LN, int NW, int RPL, int PRO>
+template <int MT, int LN, int NW, int RPL, int PRO, bool TAIL>
 int launch_w8_t(const W8Args& a, const W8Split& sp, int mblocks, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 16 * LN - 1) / (16 * LN)), (unsigned)sp.splits, (unsigned)mblocks);
   (void)hipGetLastError();
-  w8a16_gemv_kernel<MT, LN, NW, RPL, PRO><<<grid, NW * 64, 0, s>>>(a, sp);
+  w8a16_gemv_kernel<MT, LN, NW, RPL, PRO, TAIL><<<grid, NW * 64, 0, s>>>(a, sp);
   return ldk::check_launch("w8a16_gemv");
 }
 
-template <int MT, int LN, int PRO>
+template <int MT, int LN, int PRO, bool TAIL = false>
 int launch_w8_rpl(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
   switch (p.rpl) {
-    case 2: return launch_w8_t<MT, LN, 4, 2, PRO>(a, sp, p.mblocks, s);
-    case 4: return launch_w8_t<MT, LN, 4, 4, PRO>(a, sp, p.mblocks, s);
-    case 8: return launch_w8_t<MT, LN, 4, 8, PRO>(a, sp, p.mblocks, s);
+    case 2: return launch_w8_t<MT, LN, 4, 2, PRO, TAIL>(a, sp, p.mblocks, s);
+    case 4: return launch_w8_t<MT, LN, 4, 4, PRO, TAIL>(a, sp, p.mblocks, s);
+    case 8: return launch_w8_t<MT, LN, 4, 8, PRO, TAIL>(a, sp, p.mblocks, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d rows per lane not instantiated", p.rpl);
 }
 
 template <int MT, int PRO>
 int launch_w8_ln(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  if (a.N % 16) {  // rows only 4-byte aligned: the dword-load variant, on 128-column tiles
+    if (p.ln != 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: N %% 16 != 0 runs the VALU kernel on block_n 128 only");
+    return launch_w8_rpl<MT, 8, PRO, true>(a, sp, p, s);
+  }
   switch (p.ln) {
     case 1: return launch_w8_rpl<MT, 1, PRO>(a, sp, p, s);
     case 2: return launch_w8_rpl<MT, 2, PRO>(a, sp, p, s);
@@ -704,51 +723,105 @@ static bool w8_uses_gemm(int64_t M, int64_t N, int64_t K, int64_t ldx, const voi
   return w8_gemm_applies(M, N, K, ldx, out, ldo);
 }
 
-extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias, void* out,
-                                int64_t ldo, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int flags,
-                                void* workspace, int64_t workspace_bytes, void* stream) {
-  if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: null pointer");
-  if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: M, N, K must be positive");
-  if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N=%lld must be a multiple of 16", (long long)N);
-  if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: K=%lld must be a multiple of 8", (long long)K);
-  if (ldx < K || ldo < N) return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: row stride smaller than K/N");
-  if (!ldk::aligned(x, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
-    return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: wq must be 16-byte aligned");
-  if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: N or K too large");
+namespace {
+
+// What a W8A16 call runs: the prefill GEMM, or a decode-kernel plan.
+struct W8Call {
+  bool gemm;
+  W8Plan p;
+};
+
+// A call's shape and tuning arguments checked without its pointers: the errors the call returns
+// for them, and what it runs. ldx, ldo and the output's alignment decide whether the prefill GEMM
+// takes the call (out may be null for a query: taken as aligned); ws_bytes is the workspace the
+// call has.
+int w8_plan_call(const char* fn, int64_t M, int64_t N, int64_t K, int64_t ldx, const void* out, int64_t ldo,
+                 int block_n, int split_k, int flags, int64_t ws_bytes, W8Call* c) {
+  c->gemm = false;
+  if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "%s: M, N, K must be positive", fn);
+  if (N % 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N=%lld must be a multiple of 4", fn, (long long)N);
+  if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: K=%lld must be a multiple of 8", fn, (long long)K);
+  if (ldx < K || ldo < N) return ldk::fail(LDK_ERR_INVALID, "%s: row stride smaller than K/N", fn);
+  if (N > INT32_MAX / 16 || K > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N or K too large", fn);
   if (flags & ~(LDK_PATH_VALU | LDK_PATH_MFMA | LDK_PATH_GEMM))
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: flags 0x%x not supported", flags);
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: flags 0x%x not supported", fn, flags);
   if (!!(flags & LDK_PATH_VALU) + !!(flags & LDK_PATH_MFMA) + !!(flags & LDK_PATH_GEMM) > 1)
-    return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: the VALU, MFMA and GEMM paths are exclusive");
-  if (split_k < 0 || split_k > kW8MaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: split_k=%d outside 0..%d", split_k, kW8MaxSplits);
-  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
-    return ldk::fail(LDK_ERR_ALIGN, "w8a16_matmul: workspace must be a 256-byte aligned pointer");
+    return ldk::fail(LDK_ERR_INVALID, "%s: the VALU, MFMA and GEMM paths are exclusive", fn);
+  if (split_k < 0 || split_k > kW8MaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: split_k=%d outside 0..%d", fn, split_k, kW8MaxSplits);
   if ((flags & LDK_PATH_GEMM) && !w8_gemm_applies(M, N, K, ldx, out, ldo))
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the prefill GEMM takes K %% 64 == 0 and an 8-byte aligned "
-                     "output with ldo %% 4 == 0 (M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the prefill GEMM takes N %% 16 == 0, K %% 64 == 0 and an 8-byte aligned "
+                     "output with ldo %% 4 == 0 (M=%lld N=%lld K=%lld)", fn, (long long)M, (long long)N, (long long)K);
   if (w8_uses_gemm(M, N, K, ldx, out, ldo, block_n, split_k, flags)) {
-    const ldk::GemmArgs g{(const half_t*)x, ldx, wq, (const half_t*)scale, nullptr, (const half_t*)bias, (half_t*)out, ldo,
-                          (int)M, (int)N, (int)K, 0, workspace, workspace ? workspace_bytes : 0, block_n, split_k};
-    return ldk::gemm_launch(ldk::WFmt::kE4M3, g, (hipStream_t)stream);
+    if (block_n && block_n != 128 && block_n != 256)
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 128 or 256 on the GEMM path", fn, block_n);
+    c->gemm = true;
+    return LDK_OK;
   }
-  if (M > 65535LL * 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: M=%lld too large", (long long)M);
-  if (M > 16 && (flags & LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the VALU kernel takes M <= 16");
+  if (M > 65535LL * 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld too large", fn, (long long)M);
+  if (M > 16 && (flags & LDK_PATH_VALU)) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the VALU kernel takes M <= 16", fn);
   if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: block_n=%d must be 16, 32, 64 or 128", block_n);
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 16, 32, 64 or 128", fn, block_n);
   // MFMA from 2 rows (the VALU kernel's fp32 FMAs grow with M; measured at M = 4: 17.4 us VALU,
   // 9.5 us MFMA at M = 8 on gate_up; at M = 2 gate_up / down / q/o / k/v 8.91 / 6.71 / 4.79 /
   // 4.05 us VALU against 8.62 / 6.66 / 4.19 / 3.51 MFMA); block_n other than 128 keeps the
   // VALU kernel, which has the narrower tiles.
   const bool mfma = M > 16 || (flags & LDK_PATH_MFMA) || (M >= 2 && !(flags & LDK_PATH_VALU) && (block_n == 0 || block_n == 128));
   if (mfma && block_n && block_n != 128 && block_n != 64)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_matmul: the MFMA kernel takes block_n 64 or 128");
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel takes block_n 64 or 128", fn);
+  if (mfma && block_n == 128 && N % 8)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=128 on the MFMA kernel takes N %% 8 == 0 (N=%lld)", fn, (long long)N);
+  if (!mfma && N % 16 && block_n && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N %% 16 != 0 runs the VALU kernel on block_n 128 only", fn);
+  c->p = mfma ? make_w8_mfma_plan(M, N, K, block_n, split_k, ws_bytes) : make_w8_plan(M, N, K, block_n, split_k, ws_bytes);
+  if (split_k > 1 && c->p.splits == 1)
+    return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d needs a workspace for the partial sums", fn, split_k);
+  return LDK_OK;
+}
+
+int w8_plan_flags(const W8Plan& p) { return p.mfma ? LDK_PATH_MFMA : LDK_PATH_VALU; }
+
+}  // namespace
+
+extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias, void* out,
+                                int64_t ldo, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int flags,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  static const char* fn = "w8a16_matmul";
+  if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "%s: null pointer", fn);
+  if (!ldk::aligned(x, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: wq must be 16-byte aligned", fn);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
   const int64_t wsb = workspace ? workspace_bytes : 0;
-  const W8Plan p = mfma ? make_w8_mfma_plan(M, N, K, block_n, split_k, wsb) : make_w8_plan(M, N, K, block_n, split_k, wsb);
-  if (split_k > 1 && p.splits == 1)
-    return ldk::fail(LDK_ERR_INVALID, "w8a16_matmul: split_k=%d needs a workspace for the partial sums", split_k);
+  W8Call c;
+  const int st = w8_plan_call(fn, M, N, K, ldx, out, ldo, block_n, split_k, flags, wsb, &c);
+  if (st) return st;
+  if (c.gemm) {
+    const ldk::GemmArgs g{(const half_t*)x, ldx, wq, (const half_t*)scale, nullptr, (const half_t*)bias, (half_t*)out, ldo,
+                          (int)M, (int)N, (int)K, 0, workspace, wsb, block_n, split_k};
+    return ldk::gemm_launch(ldk::WFmt::kE4M3, g, (hipStream_t)stream);
+  }
+  const W8Plan& p = c.p;
   const W8Args a{(const half_t*)x, ldx, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K};
   const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr,
                    p.splits > 1 ? ldk::splitk_side(workspace, p.words) : nullptr};
   return p.mfma ? launch_w8_mfma(a, sp, p, (hipStream_t)stream) : launch_w8(a, sp, p, (hipStream_t)stream);
+}
+
+extern "C" int ldk_w8a16_config(int64_t M, int64_t N, int64_t K, int* block_n, int* split_k, int* flags) {
+  static const char* fn = "w8a16_config";
+  if (!block_n || !split_k || !flags) return ldk::fail(LDK_ERR_INVALID, "%s: null block_n, split_k or flags", fn);
+  W8Call c;
+  const int st = w8_plan_call(fn, M, N, K, K, nullptr, N, *block_n, *split_k, *flags, ldk_workspace_bytes(), &c);
+  if (st) return st;
+  if (c.gemm) {
+    ldk::gemm_plan(ldk::WFmt::kE4M3, M, N, K, *block_n, *split_k, ldk_workspace_bytes(), block_n, split_k);
+    *flags = LDK_PATH_GEMM;
+    return LDK_OK;
+  }
+  *block_n = 16 * c.p.ln;
+  *split_k = c.p.splits;
+  *flags = w8_plan_flags(c.p);
+  return LDK_OK;
 }
 
 // Fused decode entry (one row): the down projection's activation silu(g) * u is formed inside
@@ -759,7 +832,7 @@ extern "C" int ldk_w8a16_swiglu_matmul(const void* gate_up, const uint8_t* wq, c
                                        void* stream) {
   if (!gate_up || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "w8a16_swiglu_matmul: null pointer");
   if (N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_swiglu_matmul: N, K must be positive");
-  if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_swiglu_matmul: N=%lld must be a multiple of 16", (long long)N);
+  if (N % 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_swiglu_matmul: N=%lld must be a multiple of 4", (long long)N);
   if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_swiglu_matmul: K=%lld must be a multiple of 8", (long long)K);
   if (!ldk::aligned(gate_up, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
     return ldk::fail(LDK_ERR_ALIGN, "w8a16_swiglu_matmul: wq must be 16-byte aligned");
@@ -785,7 +858,7 @@ extern "C" int ldk_w8a16_rmsnorm_matmul(const void* x, const void* residual, voi
   if (residual && (residual == residual_out || x == residual_out))
     return ldk::fail(LDK_ERR_INVALID, "w8a16_rmsnorm_matmul: residual_out must not alias x or residual");
   if (N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "w8a16_rmsnorm_matmul: N, K must be positive");
-  if (N % 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_rmsnorm_matmul: N=%lld must be a multiple of 16", (long long)N);
+  if (N % 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_rmsnorm_matmul: N=%lld must be a multiple of 4", (long long)N);
   if (K % 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16_rmsnorm_matmul: K=%lld must be a multiple of 8", (long long)K);
   if (!ldk::aligned(x, 16) || !ldk::aligned(norm_weight, 16) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2) ||
       (residual && (!ldk::aligned(residual, 16) || !ldk::aligned(residual_out, 16))))

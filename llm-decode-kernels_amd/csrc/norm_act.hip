@@ -4,8 +4,11 @@
 // kernels/swiglu.py:14-61. Both keep the reference's fp16 rounding steps (kernels/reference.py:9-24):
 //   rmsnorm: h = fp16(x + r) (written as the new residual); var = sum(h^2) / N in fp32;
 //            out = w * fp16(h * (1 / sqrt(var + eps)))  (fp16 multiply, one rounding)
-//   swiglu:  out = fp16(g * rcp(1 + exp(-g))) * u     (silu in fp32 with the hardware reciprocal,
-//            1 ulp, as the reference's Triton kernel divides approximately; fp16 multiply)
+//   swiglu:  out = fp16(g * rcp(1 + 2^(-g log2 e))) * u   (silu in fp32: exp(-g) on the hardware
+//            exp2 and the division as the hardware reciprocal, as the reference's Triton kernel
+//            divides approximately; rounded to fp16, then an fp16 multiply by u). Large |g|
+//            saturate as in fp32 arithmetic: a very negative g gives 2^(+big) = inf and -0, a
+//            very positive g gives 2^(-big) = 0 and g.
 // Both are pure streaming kernels: every element is read once and written once, 16 bytes per lane.
 // Many-row calls read and write with the non-temporal cache policy (STREAM): measured on MI355X in
 // graph replays over rotating buffers, RMSNorm+residual at M = 2048, N = 1536 takes 5.70 us with it

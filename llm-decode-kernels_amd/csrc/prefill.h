@@ -40,6 +40,11 @@ struct GemmArgs {
 bool gemm_supported(WFmt f, int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx);
 int gemm_launch(WFmt f, const GemmArgs& a, hipStream_t stream);
 
+// The output-tile width (columns per workgroup) and the number of K splits gemm_launch uses for a
+// shape with these tuning arguments and a workspace of ws_bytes (for plan queries).
+void gemm_plan(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes, int* tile_n,
+               int* splits);
+
 // Name of the kernel instantiation gemm_launch runs for a shape (for reports).
 const char* gemm_kernel_name(WFmt f, int64_t M, int64_t N, int64_t K, int block_n);
 

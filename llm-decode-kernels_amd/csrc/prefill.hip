@@ -83,7 +83,10 @@ __device__ __forceinline__ void ring_barrier() {
 // the LDS reads of other stages (it would after the loop's back edge, where it no longer knows
 // which LDS array each pending load writes); the ring's own vmcnt waits order them. M0 holds the
 // LDS base for the load; the asm restores M0's previous value itself (M0 is reserved to the
-// compiler, which does not save a clobbered M0). The address is base + voffset + soffset; only
+// compiler, which does not save a clobbered M0). An LDS DMA that reads M0 right after an SALU
+// write of it needs one wait state on gfx9-family chips (gfx950 included); the compiler's hazard
+// recognizer inserts it for its own M0 writes but cannot see inside this asm string, so the string
+// carries its own s_nop 0. The address is base + voffset + soffset; only
 // voffset is checked against the
 // resource's size, so every load that relies on the check (x rows past M, scales past N) keeps
 // its whole offset in voffset, and soffset carries only the uniform K-step offset of loads that
@@ -93,7 +96,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 __device__ __forceinline__ void dma_buffer16(u32x4 rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds_base) {
   uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %1, %2, %4 offen lds\n\ts_mov_b32 m0, %0"
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %4 offen lds\n\ts_mov_b32 m0, %0"
                : "=&s"(saved)
                : "v"(voffset), "s"(rsrc), "s"(lds_base), "s"(soffset)
                : "memory");
@@ -592,6 +595,14 @@ int gemm_launch(WFmt f, const GemmArgs& a, hipStream_t s) {
   if (a.block_n && a.block_n != 128 && a.block_n != 256)
     return fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 128 or 256", fn, a.block_n);
   return f == WFmt::kInt4 ? launch_fmt<WFmt::kInt4>(a, s) : launch_fmt<WFmt::kE4M3>(a, s);
+}
+
+void gemm_plan(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes, int* tile_n,
+               int* splits) {
+  const GemmShape sh = pick_shape(f, M, N, K, block_n, split_k, ws_bytes);
+  const int steps = (int)(K / kStep), kps = (steps + sh.splits - 1) / sh.splits;
+  *tile_n = 64 * sh.waves;
+  *splits = (steps + kps - 1) / kps;  // as launch(): no empty split
 }
 
 const char* gemm_kernel_name(WFmt f, int64_t M, int64_t N, int64_t K, int block_n) {

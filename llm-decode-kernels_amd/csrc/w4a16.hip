@@ -78,6 +78,8 @@ struct SplitArgs {
   int nsplit;       // number of those split workgroups
   uint64_t smagic;  // ceil(2^32 / splits): b / splits == (b * smagic) >> 32 for b, splits < 2^16
   float* side;      // fp32 side slots of the accumulators (ldk::SplitK), zero between launches
+  int grem;         // 0: every split takes gps groups (the last one the rest); > 0: a split count
+                    // the caller asked for, groups dealt evenly: splits s < grem take gps + 1
 };
 
 // ceil(2^32 / d) for 1 <= d < 2^16: floor(n / d) == (n * magic) >> 32 for every n < 2^16.
@@ -127,8 +129,8 @@ __device__ __forceinline__ TileWork map_block(const SplitArgs& sp, int ng) {
     const int l = bid - base, lim = count / (8 * G) * (8 * G);
     if (w.whole && l < lim) w.tile = (in_split ? sp.full : 0) + (l - l % (8 * G)) + (l % 8) * G + (l % (8 * G)) / 8;
   }
-  w.gb = w.whole ? 0 : split * sp.gps;
-  w.ge = w.whole ? ng : min(ng, w.gb + sp.gps);
+  w.gb = w.whole ? 0 : split * sp.gps + min(split, sp.grem);
+  w.ge = w.whole ? ng : min(ng, w.gb + sp.gps + (split < sp.grem ? 1 : 0));
   return w;
 }
 
@@ -1217,7 +1219,8 @@ struct Plan {
   Kern kern;
   int mt, ln, rpl, cpw;  // row tile, lanes along N (MFMA: 16 * 64-column halves), rows per lane,
                          // chunks (MFMA: groups) per wave and pass
-  int nw, splits, gps;
+  int nw, splits, gps;  // gps: groups of the largest split
+  bool even;  // splits asked for by the caller: the groups are dealt evenly over exactly `splits`
   int full;   // M = 1 kernel: leading tiles run whole while the rest split (0: all tiles alike)
   int mtile;  // MFMA kernel: 16-row tiles per workgroup (1, or 2 when M > 16)
 };
@@ -1417,9 +1420,16 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
   p.splits = (int)((ng + p.gps - 1) / p.gps);
+  // a split count the caller names is run as asked (the reference's SPLIT_K programs, each a K
+  // range): its groups are dealt evenly, so e.g. 4 groups in 3 splits run as 2 + 1 + 1
+  if (split_k > 0 && M <= 16) {
+    p.splits = (int)splits;
+    p.even = p.splits > 1 && ng % p.splits != 0;
+  }
   if (p.splits > 1 && workspace_need(p, M, N) > ws_bytes) {  // no room for partials: one split
     p.splits = 1;
     p.gps = (int)ng;
+    p.even = false;
   }
   // M = 1 with more than one round of 256 tiles: whole tiles give every CU the same whole-tile
   // count, and the remainder tiles split into one-wave-pass pieces that spread over all CUs
@@ -1628,9 +1638,10 @@ int launch_plan(const W4Args& a, const Plan& p, void* ws, hipStream_t s, int pro
                 const ProArgs& pa = ProArgs{}) {
   const int64_t tiles = (a.N + plan_cw(p) - 1) / plan_cw(p);
   const bool split = p.splits > 1;
-  const SplitArgs sp{p.splits, p.gps, split ? static_cast<uint64_t*>(ws) : nullptr, p.full,
+  const int ng = (a.K >> 3) >> a.gsh_rows;
+  const SplitArgs sp{p.splits, p.even ? ng / p.splits : p.gps, split ? static_cast<uint64_t*>(ws) : nullptr, p.full,
                      (int)((tiles - p.full) * p.splits), div_magic(p.splits),
-                     split ? ldk::splitk_side(ws, split_words(p, a.M, a.N)) : nullptr};
+                     split ? ldk::splitk_side(ws, split_words(p, a.M, a.N)) : nullptr, p.even ? ng % p.splits : 0};
   if (sp.full + (int64_t)sp.nsplit >= 65536)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: %lld workgroups exceed the grid mapping limit", (long long)(sp.full + (int64_t)sp.nsplit));
   const size_t lds = plan_lds_bytes(p, a.M);
@@ -1695,18 +1706,6 @@ int plan_flags(const Plan& p) {
 
 extern "C" int64_t ldk_workspace_bytes(void) { return (int64_t)64 << 20; }
 
-extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n, int* split_k, int* flags) {
-  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return ldk::fail(LDK_ERR_INVALID, "w4a16_config: sizes must be positive");
-
-  const int gsh = log2_exact(group_size);
-  if (gsh < 5 || gsh > 8 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "w4a16_config: bad group_size %d", group_size);
-  const Plan p = make_plan(M, N, K, gsh - 3, 0, 0, 0, (size_t)ldk_workspace_bytes());
-  if (block_n) *block_n = plan_cw(p);
-  if (split_k) *split_k = p.splits;
-  if (flags) *flags = plan_flags(p);
-  return LDK_OK;
-}
-
 // Rows from which the prefill GEMM (prefill.hip) may replace the MFMA kernel's 32-row blocks.
 static constexpr int64_t kGemmRows = 64;
 
@@ -1762,13 +1761,64 @@ extern "C" int ldk_w4a16_kernel_name(int64_t M, int64_t N, int64_t K, int group_
   return plan_kernel_name(p, gsh - 3, buf, (size_t)buf_len);
 }
 
-static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
-                             const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
-                             int group_size, int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
-                             void* stream) {
-  int gsh_rows = 0;
-  int st = validate(fn, x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
-  if (st) return st;
+// The launch limits of a plan (instantiated shapes, LDS, grid), checked before anything is
+// launched, so that a plan query reports what the call would do (launch_plan and its launchers
+// keep their own checks). ldx: the row stride of x the call passes (K for a query).
+static int plan_check(const char* fn, const Plan& p, int64_t M, int64_t N, int64_t K, int gsh_rows, int64_t ldx) {
+  const int64_t tiles = (N + plan_cw(p) - 1) / plan_cw(p);
+  if (p.full + (tiles - p.full) * p.splits >= 65536)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: %lld workgroups exceed the grid mapping limit", fn,
+                     (long long)(p.full + (tiles - p.full) * p.splits));
+  if (plan_lds_bytes(p, M) > 160 * 1024)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: LDS need %zu B exceeds 160 KiB", fn, plan_lds_bytes(p, M));
+  const int rpg = 1 << gsh_rows;
+  switch (p.kern) {
+    case kM1:
+      if (p.ln != 4 && p.ln != 8 && p.ln != 16)
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d not supported (16, 32 or 64)", fn, 4 * p.ln);
+      if (rpg > 4 * (64 / p.ln))
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d too wide for group_size %d on the M = 1 kernel", fn,
+                         4 * p.ln, 8 * rpg);
+      if (p.mt > 2 || !m1_lds_ok(p.ln, p.nw, p.mt))
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: %d rows on %d waves of block_n %d not instantiated", fn, p.mt, p.nw,
+                         4 * p.ln);
+      return LDK_OK;
+    case kValu:
+      if (!gemv_shape_ok(p.mt, p.ln, p.rpl, p.cpw))
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: VALU shape mt=%d block_n=%d rpl=%d cpw=%d not instantiated", fn,
+                         p.mt, 4 * p.ln, p.rpl, p.cpw);
+      return LDK_OK;
+    case kMfmaX:
+      if (gsh_rows != 4 || M > p.mt || ((K >> 3) >> 4) > p.nw * p.cpw || (p.ln != 8 && p.ln != 16))
+        return ldk::fail(LDK_ERR_INVALID, "%s: x-staged MFMA plan does not fit M=%lld N=%lld K=%lld", fn, (long long)M,
+                         (long long)N, (long long)K);
+      return LDK_OK;
+    case kMfma:
+      if (p.mtile == 2 && rpg == 32 && p.ln == 32)
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: group_size 256 with M > 16 takes block_n=64", fn);
+      if ((M + 16 * p.mtile - 1) / (16 * p.mtile) > 65535)
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld needs more than 65535 row blocks", fn, (long long)M);
+      if (p.mtile > 1 && p.splits > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: row blocks of 32 take no K split", fn);
+      if ((int64_t)(16 * p.mtile - 1) * ldx * 2 + K * 2 >= (int64_t(1) << 31))
+        return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: a row block of x spans 2 GiB or more (ldx=%lld)", fn, (long long)ldx);
+      return LDK_OK;
+  }
+  return ldk::fail(LDK_ERR_INVALID, "%s: unknown kernel %d", fn, (int)p.kern);
+}
+
+// What a call runs: the prefill GEMM, or a decode-kernel plan.
+struct Call {
+  bool gemm;
+  Plan p;
+};
+
+// A call's shape and tuning arguments checked without its pointers: the errors the call returns
+// for them, and what it runs. ldx, ldo and the output's alignment decide whether the prefill GEMM
+// takes the call (out may be null for a query: taken as aligned); ws_bytes is the workspace the
+// call has.
+static int plan_call(const char* fn, int64_t M, int64_t N, int64_t K, int group_size, int gsh_rows, int64_t ldx,
+                     const void* out, int64_t ldo, int block_n, int split_k, int flags, size_t ws_bytes, Call* c) {
+  c->gemm = false;
   if (M > 65535LL * 32) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld too large", fn, (long long)M);
   if (flags & ~(LDK_FACTORED | LDK_EXACT | LDK_PATH_VALU | LDK_PATH_MFMA | LDK_PATH_GEMM | LDK_CPW_MASK))
     return ldk::fail(LDK_ERR_INVALID, "%s: unknown flags 0x%x", fn, flags);
@@ -1776,15 +1826,16 @@ static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const i
     if (flags & (LDK_PATH_VALU | LDK_PATH_MFMA | LDK_FACTORED))
       return ldk::fail(LDK_ERR_INVALID, "%s: the GEMM path excludes the VALU/MFMA paths and FACTORED", fn);
     if (!gemm_applies(M, N, K, group_size, ldx, out, ldo, true))
-      return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the prefill GEMM takes group_size >= 64, N %% 4 == 0 and an 8-byte "
-                       "aligned output with ldo %% 4 == 0 (M=%lld N=%lld K=%lld group_size=%d)", fn, (long long)M,
-                       (long long)N, (long long)K, group_size);
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the prefill GEMM takes group_size >= 64, N %% 8 == 0, K %% 64 == 0 "
+                       "and an 8-byte aligned output with ldo %% 4 == 0 (M=%lld N=%lld K=%lld group_size=%d)", fn,
+                       (long long)M, (long long)N, (long long)K, group_size);
   }
   if (uses_gemm(M, N, K, group_size, ldx, out, ldo, block_n, split_k, flags)) {
-    const ldk::GemmArgs g{(const half_t*)x, ldx, qweight, (const half_t*)scales, (const half_t*)zeros,
-                          (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, group_size,
-                          workspace, workspace ? workspace_bytes : 0, block_n, split_k};
-    return ldk::gemm_launch(ldk::WFmt::kInt4, g, (hipStream_t)stream);
+    if (block_n && block_n != 128 && block_n != 256)
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 128 or 256 on the GEMM path", fn, block_n);
+    if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d must be >= 0", fn, split_k);
+    c->gemm = true;
+    return LDK_OK;
   }
   if ((flags & LDK_FACTORED) && (flags & LDK_EXACT)) return ldk::fail(LDK_ERR_INVALID, "%s: FACTORED and EXACT are exclusive", fn);
   if ((flags & LDK_PATH_VALU) && (flags & LDK_PATH_MFMA)) return ldk::fail(LDK_ERR_INVALID, "%s: VALU and MFMA paths are exclusive", fn);
@@ -1793,26 +1844,70 @@ static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const i
   if ((flags & LDK_EXACT) && (flags & LDK_PATH_MFMA))
     return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel computes the factored form; EXACT runs on the VALU kernels (M <= 8)", fn);
   if ((flags & LDK_PATH_VALU) && M > 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the VALU kernel takes M <= 8", fn);
-  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128 && !(block_n == 256 && (flags & LDK_PATH_GEMM)))
+  if (block_n && block_n != 16 && block_n != 32 && block_n != 64 && block_n != 128)
     return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 16, 32, 64 or 128 (MFMA; 128 or 256 on the GEMM path)", fn,
                      block_n);
   if (block_n == 128 && !(flags & LDK_PATH_MFMA) && M <= 8 && (M <= 2 || (flags & (LDK_EXACT | LDK_PATH_VALU))))
     return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: block_n=128 is the MFMA kernel's tile (M > 2 or the MFMA flag)", fn);
   if (split_k < 0) return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d must be >= 0", fn, split_k);
   if (split_k > kMaxSplits) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: split_k=%d above %d", fn, split_k, kMaxSplits);
+  c->p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, ws_bytes);
+  if (c->p.kern == kMfma && block_n && block_n != 32 && block_n != 64 && block_n != 128)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel uses block_n 32, 64 or 128", fn);
+  if (split_k > 1 && c->p.splits == 1 && (K / group_size) > 1 && M <= 16) {
+    const Plan want = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, SIZE_MAX);
+    return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d needs %zu bytes of workspace for its partial sums, %zu available",
+                     fn, split_k, workspace_need(want, M, N), ws_bytes);
+  }
+  return plan_check(fn, c->p, M, N, K, gsh_rows, ldx);
+}
+
+static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                             const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                             int group_size, int block_n, int split_k, int flags, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  int gsh_rows = 0;
+  int st = validate(fn, x, ldx, qweight, scales, zeros, out, ldo, M, N, K, group_size, &gsh_rows);
+  if (st) return st;
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
-  const Plan p = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, workspace ? (size_t)workspace_bytes : 0);
-  if (p.kern == kMfma && block_n && block_n != 32 && block_n != 64 && block_n != 128)
-    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: the MFMA kernel uses block_n 32, 64 or 128", fn);
-  if (split_k > 1 && p.splits == 1 && (K / group_size) > 1 && M <= 16) {
-    const Plan want = make_plan(M, N, K, gsh_rows, block_n, split_k, flags, SIZE_MAX);
-    return ldk::fail(LDK_ERR_INVALID, "%s: split_k=%d needs %zu bytes of workspace for its partial sums, %lld available",
-                     fn, split_k, workspace_need(want, M, N), (long long)(workspace ? workspace_bytes : 0));
+  Call c;
+  st = plan_call(fn, M, N, K, group_size, gsh_rows, ldx, out, ldo, block_n, split_k, flags,
+                 workspace ? (size_t)workspace_bytes : 0, &c);
+  if (st) return st;
+  if (c.gemm) {
+    const ldk::GemmArgs g{(const half_t*)x, ldx, qweight, (const half_t*)scales, (const half_t*)zeros,
+                          (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, group_size,
+                          workspace, workspace ? workspace_bytes : 0, block_n, split_k};
+    return ldk::gemm_launch(ldk::WFmt::kInt4, g, (hipStream_t)stream);
   }
   const W4Args a{(const half_t*)x, ldx, (const uint32_t*)qweight, (const half_t*)scales, (const half_t*)zeros,
                  (const half_t*)bias, (half_t*)out, ldo, (int)M, (int)N, (int)K, gsh_rows};
-  return launch_plan(a, p, workspace, (hipStream_t)stream);
+  return launch_plan(a, c.p, workspace, (hipStream_t)stream);
+}
+
+extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n, int* split_k, int* flags) {
+  static const char* fn = "w4a16_config";
+  if (!block_n || !split_k || !flags) return ldk::fail(LDK_ERR_INVALID, "%s: null block_n, split_k or flags", fn);
+  if (M <= 0 || N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "%s: M, N, K must be positive", fn);
+  const int gsh = log2_exact(group_size);
+  if (gsh < 3 || K % group_size) return ldk::fail(LDK_ERR_INVALID, "%s: group_size=%d must be a power of two >= 8 dividing K=%lld", fn, group_size, (long long)K);
+  if (group_size < 32 || group_size > 256) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: group_size=%d outside 32..256", fn, group_size);
+  if (N % 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N=%lld must be a multiple of 4", fn, (long long)N);
+  if (N > INT32_MAX / 8 || K > INT32_MAX / 8) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N or K too large", fn);
+  Call c;
+  const int st = plan_call(fn, M, N, K, group_size, gsh - 3, K, nullptr, N, *block_n, *split_k, *flags,
+                           (size_t)ldk_workspace_bytes(), &c);
+  if (st) return st;
+  if (c.gemm) {
+    ldk::gemm_plan(ldk::WFmt::kInt4, M, N, K, *block_n, *split_k, ldk_workspace_bytes(), block_n, split_k);
+    *flags = LDK_PATH_GEMM;
+    return LDK_OK;
+  }
+  *block_n = plan_cw(c.p);
+  *split_k = c.p.splits;
+  *flags = plan_flags(c.p);
+  return LDK_OK;
 }
 
 extern "C" int ldk_w4a16_matmul(const void* x, int64_t ldx, const int32_t* qweight, const void* scales, const void* zeros,
@@ -2018,7 +2113,7 @@ extern "C" int ldk_w4a16_attn_matmul_residual_stats(const int64_t* pos, int64_t 
   if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
     return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
   const float *po = nullptr, *pm = nullptr;
-  st = ldk::attention_partials(fn, stream, max_len, rlen, nq, &po, &pm);
+  st = ldk::attention_partials(fn, stream, pos, max_len, rlen, nq, &po, &pm);
   if (st) return st;
   const Plan p = residual_stats_plan(N, K, gsh_rows, workspace ? (size_t)workspace_bytes : 0);
   const int64_t tiles = (N + plan_cw(p) - 1) / plan_cw(p);

@@ -65,6 +65,7 @@ SIGNATURES = {
                                  _i64, _vp],
     "ldk_w8a16_matmul": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
                          _vp, _i64, _vp],
+    "ldk_w8a16_config": [_i64, _i64, _i64, _ip, _ip, _ip],
     "ldk_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _f32, _vp],
     "ldk_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
     "ldk_greedy_step": [_vp, _i32, _i64, _vp, _vp, _i64, _vp, _vp],
@@ -219,6 +220,13 @@ def workspace(dev: torch.device):
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _workspaces.get(idx)
     if ws is None:
+        # Allocated under capture, the buffer would come from the graph's private memory pool and
+        # outlive the graph it belongs to (and its zero fill would be a node of that graph).
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"the split-K workspace of cuda:{idx} is allocated by the first library call on that "
+                "device, which must not be under graph capture: run the op once before capturing "
+                "(as a warm-up), or call kernels._lib.workspace(device) first")
         nbytes = int(load().ldk_workspace_bytes())
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
         _workspaces[idx] = ws

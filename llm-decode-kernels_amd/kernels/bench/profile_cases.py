@@ -171,66 +171,12 @@ def case_copy(reps):
         torch.neg(a, out=b)
 
 
-def case_probes(kind: str, reps: int, N: int = 17920):
-    """The roofline's calibration kernels (kernels/bench/probe.hip) at config 0's size: the packed
-    gate_up weight, 192 x 17920 int32 = 13.76 MB (or 192 x N), in rotating copies that defeat the
-    MALL."""
-    from kernels.bench import probes
-
-    # 74 launches per set list, as many as a rotating case has: a graph of one empty node would
-    # time the graph launch itself
-    if kind == "empty1":
-        _rotate(lambda: probes.empty(1, 64), [()] * 74, reps)
-        return
-    if kind == "empty_grid":  # the headline kernel's grid: 800 workgroups of 384 lanes
-        _rotate(lambda: probes.empty(800, 384), [()] * 74, reps)
-        return
-    R = 192
-    copies = n_copies(R * N * 4)
-    buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
-    sink = torch.zeros(N // 32 * 384, dtype=torch.int32, device="cuda")
-    sets = [(buf[i],) for i in range(copies)]
-    if kind == "stream":
-        _rotate(lambda b: probes.stream(b, sink, loads=1), sets, reps)
-    elif kind == "stream16":
-        _rotate(lambda b: probes.stream(b, sink, loads=16), sets, reps)
-    else:
-        _rotate(lambda b: probes.tile(b, sink), sets, reps)
-
-
-def case_piece(shape: str, red: str, reps: int):
-    """The packed gate_up weight (13.76 MB, rotating copies) read as K pieces per workgroup, their
-    partials met by one of the reductions of kernels/bench/probe.hip."""
-    from kernels.bench import probes
-
-    R = 192
-    copies = n_copies(R * N * 4)
-    buf = torch.randint(-2**31, 2**31 - 1, (copies, R, N), dtype=torch.int32, device="cuda")
-    ws = torch.zeros(N * 8 + 64 * N * 4, dtype=torch.uint8, device="cuda")
-    out = torch.zeros(N, dtype=torch.float16, device="cuda")
-    _rotate(lambda b: probes.piece(shape, red, b, ws, out), [(buf[i],) for i in range(copies)], reps)
-
-
 CASES = {
     "calib_neg64MiB": lambda r: case_copy(r),
-    "probe_empty_1wg": lambda r: case_probes("empty1", r),
-    "probe_empty_800wg": lambda r: case_probes("empty_grid", r),
-    "probe_stream_13.76MB": lambda r: case_probes("stream", r),
-    "probe_stream16_13.76MB": lambda r: case_probes("stream16", r),
-    "probe_tile_gate_up": lambda r: case_probes("tile", r),
-    # K pieces of the same bytes and the cost of meeting their partials (probe.hip)
-    **{f"probe_{shape}_{red}": (lambda r, shape=shape, red=red: case_piece(shape, red, r))
-       for shape, reds in (("whole32x192", ("none", "store", "fixed_atomic")),
-                           ("piece64x64", ("none", "store", "fixed_atomic", "f32_atomic")),
-                           ("piece256x16", ("none", "store", "fixed_atomic")),
-                           ("piece256x4", ("none",)))
-       for red in reds},
     "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
     # the M = 1 kernel and the read floors at K = 1536 and wider N (2x, 4x gate_up, and the
     # 151936-row vocabulary of the quantized lm_head): where launch and ramp stop dominating
     **{f"w4a16_m1_n{n}": (lambda r, n=n: case_w4a16(1, n, 1536, r)) for n in (35840, 71680, 151936)},
-    **{f"probe_{kind}_n{n}": (lambda r, kind=kind, n=n: case_probes(kind, r, N=n))
-       for kind in ("stream", "tile") for n in (35840, 71680, 151936)},
     "w4a16_down_m1": lambda r: case_w4a16(1, 1536, 8960, r),
     "w4a16_gate_up_m2": lambda r: case_w4a16(2, 17920, 1536, r),
     "w4a16_gate_up_m4": lambda r: case_w4a16(4, 17920, 1536, r),

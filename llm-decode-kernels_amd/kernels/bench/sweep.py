@@ -17,7 +17,10 @@ kernel configuration the library chose. The whole sweep runs `--sweeps` times (3
 and each row reports the median over the sweeps, their min and max, and a flag when the spread
 (max - min) / median exceeds 10% (the reference's aggregation, kernels/bench/sweep.py:229-254).
 
-    python -m kernels.bench.sweep [--only w4a16,fp8,norm,act,fused,prefill] [--sweeps 3] [--json out.json]
+- copy: the practical ceiling, a device-to-device copy (the reference's case, and copies moving as
+  many bytes as the two largest decode reads).
+
+    python -m kernels.bench.sweep [--only copy,w4a16,fp8,norm,act,fused,prefill] [--sweeps 3] [--json out.json]
 """
 
 from __future__ import annotations
@@ -174,6 +177,24 @@ def fused_rows():
     return rows
 
 
+def copy_rows():
+    """The practical ceiling: a device-to-device copy (dst.copy_(src)), the reference's copy case
+    (kernels/bench/sweep.py:61-70: 64M fp16 elements, 128 MiB read and 128 MiB written), and
+    copies that move as many bytes as the decode kernels' two largest reads (config 0's
+    14,661,632 B and down's 7,332,352 B, half read and half written), on rotating sets like every
+    other row. Bytes are read plus written (2 * 2 * elems)."""
+    rows = []
+    for label, n in (("ref 64M fp16", 64 * 2**20), ("= gate_up M=1 bytes", 14_661_632 // 4),
+                     ("= down M=1 bytes", 7_332_352 // 4)):
+        src = torch.randn(n, dtype=torch.float16, device="cuda")
+        sets = [(src.clone(), torch.empty_like(src)) for _ in range(n_copies(4 * n))]
+        del src
+        ms = _time(lambda a, b: b.copy_(a), sets)
+        rows.append(_row("copy", f"{label} ({n})", 1, ms, 2 * n * 2))
+        del sets
+    return rows
+
+
 PREFILL_SHAPES = [("qkv", 2048, 1536), ("o", 1536, 1536), ("gate_up", 17920, 1536), ("down", 1536, 8960)]
 
 
@@ -212,7 +233,7 @@ def prefill_rows(Ms=(512, 2048)):
     return rows
 
 
-SECTIONS = {"w4a16": w4a16_rows, "fp8": fp8_rows, "norm": norm_rows, "act": act_rows,
+SECTIONS = {"copy": copy_rows, "w4a16": w4a16_rows, "fp8": fp8_rows, "norm": norm_rows, "act": act_rows,
             "fused": fused_rows, "prefill": prefill_rows}
 
 
@@ -245,7 +266,7 @@ def _line(r) -> str:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", default="w4a16,fp8,norm,act")
+    ap.add_argument("--only", default="copy,w4a16,fp8,norm,act")
     ap.add_argument("--sweeps", type=int, default=3)
     ap.add_argument("--json", default=None)
     args = ap.parse_args(argv)

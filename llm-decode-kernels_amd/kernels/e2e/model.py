@@ -234,11 +234,16 @@ class OursFP8Backend(OursBackend):
         super().__init__("matmul")
         self.name = "ours_fp8"
 
-    def pack(self, w, b) -> Linear:
+    def quantize(self, w, b) -> Linear:
+        """e4m3 weights [K, N] with per-channel scales. `quantize` is the hook the reference's
+        runner looks for on formats other than int4 RTN (model.py:109-112,175-176), so this
+        backend also packs its weights correctly under that runner; this runner calls `pack`."""
         from kernels.fp8 import quantize_fp8
 
         wq, per_channel = quantize_fp8(w)
         return Linear(qweight=wq, scales=per_channel, bias=b)
+
+    pack = quantize
 
     def linear(self, x, p: Linear):
         from kernels.fp8 import w8a16_matmul
@@ -516,7 +521,7 @@ class QwenRunner:
             if merge:
                 ranges = decode_attention_ranges(qkv, pos, self.inv_freq, self.k_cache[i],
                                                  self.vt_cache[i], nq, nkv, hd ** -0.5, rlen,
-                                                 self.warm_set(i) if self.warm_weights else ())
+                                                 self.warm_set(i) if self.warm_weights and be.warms else ())
                 gate_up, residual = be.attn_linear_norm_linear(ranges, L.o, residual, L.ln2, eps,
                                                                L.gate_up)
                 h = be.act_linear(gate_up, L.down)

@@ -12,9 +12,14 @@ hand-written kernels at every row count: 17-64 rows the MFMA kernel in 16-row bl
 the prefill GEMM (csrc/prefill.hip: 64/128-row tiles, e4m3 tiles transposed and converted to fp16
 in registers, column scale after the K loop, K split over workgroups for long K).
 `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
+N must be a multiple of 4: rows of any such N run the VALU kernel with 4-byte loads where N % 16
+!= 0, the MFMA kernel on 64-column tiles where N % 8 != 0, and the 16-row MFMA blocks instead of
+the prefill GEMM where N % 16 != 0.
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -61,11 +66,51 @@ def fp8_bytes(N: int, K: int) -> int:
     return N * K + N * 2
 
 
+def _query(M: int, N: int, K: int, block_n: int, split_k: int, flags: int):
+    """(status, (block_n, split_k, flags)) of the library's plan query for ldk_w8a16_matmul."""
+    bn, sk, fl = ctypes.c_int(block_n), ctypes.c_int(split_k), ctypes.c_int(flags)
+    st = _lib.load().ldk_w8a16_config(M, N, K, ctypes.byref(bn), ctypes.byref(sk), ctypes.byref(fl))
+    return st, (bn.value, sk.value, fl.value)
+
+
+def _tuning(config: dict | None, M: int, N: int, K: int) -> tuple[int, int, int]:
+    """(block_n, split_k, flags) of a call's `config`: this build's keys (`GEMV`, `MFMA`,
+    `prefill`, `block_n`, `split_k`) as given; the reference's `SPLIT_K` maps onto `split_k` and
+    its `BLOCK_N` onto `block_n` where the kernel the call runs takes that width (the library's
+    plan query says), as in kernels.w4a16; other Triton keys are ignored."""
+    cfg = config or {}
+    prefill = cfg.get("prefill")
+    if prefill is not None and prefill not in PREFILL_PATHS:
+        raise ValueError(f"w8a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
+    flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
+    if cfg.get("MFMA") or (M > 16 and prefill == "blocks"):
+        flags |= _lib.PATH_MFMA
+    elif M > 16 and prefill == "gemm":
+        flags |= _lib.PATH_GEMM
+    split_k = int(cfg["split_k"] if "split_k" in cfg else cfg.get("SPLIT_K", 0))
+    block_n = int(cfg.get("block_n", 0))
+    if "block_n" not in cfg and cfg.get("BLOCK_N"):
+        want = int(cfg["BLOCK_N"])
+        if _query(M, N, K, want, split_k, flags)[0] == _lib.OK:
+            block_n = want
+    return block_n, split_k, flags
+
+
+def config_for(M: int, N: int, K: int, config: dict | None = None) -> str:
+    """What ldk_w8a16_matmul runs for a shape (and `config`), as 'path,block_n=..,split_k=..'
+    (the library's plan query; no GPU needed). Raises as the call would for a refused config."""
+    st, (bn, sk, fl) = _query(M, N, K, *_tuning(config, M, N, K))
+    _lib.check(st, "w8a16_config")
+    path = "gemm" if fl & _lib.PATH_GEMM else "mfma" if fl & _lib.PATH_MFMA else "valu"
+    return f"{path},block_n={bn},split_k={sk}"
+
+
 def w8a16_matmul(x, wq, scale, bias=None, config=None):
     """y = x @ (wq * scale).T (+ bias). x: [..., K] fp16, wq: float8 [K, N], scale: fp16 [N]
-    (fp8.py:200-223). `config` honours `GEMV` (force the VALU kernel), `MFMA` (force the MFMA
-    kernel), `prefill` (see PREFILL_PATHS), `block_n` and `split_k`; Triton tile keys are
-    ignored."""
+    (fp8.py:200-223). N % 4 == 0 (the reference's column masks take any N; N = 40 in its tests).
+    `config` honours `GEMV` (force the VALU kernel), `MFMA` (force the MFMA kernel), `prefill`
+    (see PREFILL_PATHS), `block_n` and `split_k`, and maps the reference's `SPLIT_K` and `BLOCK_N`
+    (see _tuning); other Triton tile keys are ignored."""
     K = x.shape[-1]
     N = wq.shape[1]
     assert wq.shape[0] == K
@@ -79,21 +124,12 @@ def w8a16_matmul(x, wq, scale, bias=None, config=None):
     q = wq if wq.is_contiguous() else wq.contiguous()
     s = scale.contiguous()
     b = None if bias is None else bias.to(torch.float16).contiguous()
-    cfg = config or {}
-    prefill = cfg.get("prefill")
-    if prefill is not None and prefill not in PREFILL_PATHS:
-        raise ValueError(f"w8a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
-    flags = _lib.PATH_VALU if cfg.get("GEMV") else 0
-    if cfg.get("MFMA") or (M > 16 and prefill == "blocks"):
-        flags |= _lib.PATH_MFMA
-    elif M > 16 and prefill == "gemm":
-        flags |= _lib.PATH_GEMM
+    block_n, split_k, flags = _tuning(config, M, N, K)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     with _lib.device_guard(dev):
         ws, ws_bytes = _lib.workspace(dev)
         st = _lib.load().ldk_w8a16_matmul(
             _lib.ptr(x2), x2.stride(0), _lib.ptr(q), _lib.ptr(s), _lib.ptr(b), _lib.ptr(out),
-            out.stride(0), M, N, K, int(cfg.get("block_n", 0)), int(cfg.get("split_k", 0)),
-            flags, ws, ws_bytes, _lib.stream(dev))
+            out.stride(0), M, N, K, block_n, split_k, flags, ws, ws_bytes, _lib.stream(dev))
     _lib.check(st, "w8a16_matmul")
     return out.view(*x.shape[:-1], N)

@@ -167,6 +167,11 @@ def attn_linear_rmsnorm_w4a16_matmul(ranges, qweight1, scales1, zeros1, bias1, r
         raise ValueError("attn_linear_rmsnorm_w4a16_matmul: K must be 128 * the attention's heads")
     if residual.dtype != torch.float16 or residual.numel() != N1 or weight.dtype != torch.float16:
         raise ValueError("attn_linear_rmsnorm_w4a16_matmul: fp16 residual of N1 values and weight")
+    # the C entry reads qweight1/qweight2 as packed [K/8, N] and the norm weight as [K2], each
+    # with 16-byte loads: a strided view would be read as the wrong elements
+    if not _aligned(qweight1, qweight2, weight):
+        raise ValueError("attn_linear_rmsnorm_w4a16_matmul: qweight1, qweight2 and weight must be "
+                         "contiguous and 16-byte aligned")
     K2, N2 = N1, qweight2.shape[1]
     assert qweight2.shape[0] * 8 == K2 and weight.numel() == K2
     dev = _lib.require_gpu(ranges.pos, residual, weight, qweight1, scales1, zeros1, bias1, qweight2,
@@ -211,7 +216,7 @@ def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
     N = wq.shape[1]
     rows = gate_up.numel() // K2
     fuse = (rows == 1 and gate_up.dtype == torch.float16 and gate_up.is_cuda and K2 % 2 == 0
-            and K % 8 == 0 and N % 16 == 0 and wq.dtype == FP8 and scale.dtype == torch.float16
+            and K % 8 == 0 and N % 4 == 0 and wq.dtype == FP8 and scale.dtype == torch.float16
             and _aligned(gate_up, wq))
     if not fuse:
         return w8a16_matmul(swiglu_fused(gate_up), wq, scale, bias=bias)
@@ -240,7 +245,7 @@ def rmsnorm_w8a16_matmul(x, weight, eps, residual, wq, scale, bias=None):
     N = wq.shape[1]
     rows = x.numel() // K
     fuse = (rows == 1 and x.dtype == torch.float16 and weight.dtype == torch.float16 and x.is_cuda
-            and K % 8 == 0 and N % 16 == 0 and wq.dtype == FP8 and scale.dtype == torch.float16
+            and K % 8 == 0 and N % 4 == 0 and wq.dtype == FP8 and scale.dtype == torch.float16
             and _aligned(x, weight, residual, wq))
     if not fuse:
         if residual is None:

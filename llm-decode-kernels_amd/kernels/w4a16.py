@@ -27,8 +27,10 @@ wins). `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is t
 VALU kernels, M <= 8),
 `block_n` (columns per workgroup: 16, 32 or 64; 64 or 128 on the MFMA kernel), `split_k`
 (workgroups splitting K per column tile) and `chunks_per_wave` (1, 2 or 4: load chunks a wave
-keeps in flight per round). Triton tile keys (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, GROUP_M)
-describe Triton programs and are ignored.
+keeps in flight per round). Of the reference's Triton keys, `SPLIT_K` maps onto `split_k` and
+`BLOCK_N` onto `block_n` where the kernel the call runs takes that width; BLOCK_M, BLOCK_K and
+GROUP_M describe Triton programs and are ignored. `config_for(M, N, K, group_size, config)`
+reports what a config runs.
 """
 
 from __future__ import annotations
@@ -49,7 +51,23 @@ def _next_pow2(n: int) -> int:
     return 1 << max(0, (n - 1).bit_length())
 
 
-def _flags_from_config(config: dict | None, M: int) -> tuple[int, int, int]:
+def _query(M: int, N: int, K: int, group_size: int, block_n: int, split_k: int, flags: int):
+    """(status, (block_n, split_k, flags)) of the library's plan query: what a call with these
+    tuning arguments runs, or the status it would fail with."""
+    bn, sk, fl = ctypes.c_int(block_n), ctypes.c_int(split_k), ctypes.c_int(flags)
+    st = _lib.load().ldk_w4a16_config(M, N, K, group_size, ctypes.byref(bn), ctypes.byref(sk),
+                                      ctypes.byref(fl))
+    return st, (bn.value, sk.value, fl.value)
+
+
+def _tuning(config: dict | None, M: int, N: int, K: int, group_size: int) -> tuple[int, int, int]:
+    """(block_n, split_k, flags) of a call's `config`. This build's keys (`block_n`, `split_k`,
+    `GEMV`, `MFMA`, `FACTORED`, `chunks_per_wave`, `prefill`) are passed as given. The reference's
+    Triton keys map where they mean the same thing here (w4a16.py:301-330): `SPLIT_K` is the
+    number of workgroups splitting K per column tile (1: no split; the groups are dealt evenly
+    over exactly that many), and `BLOCK_N`, the output columns per program, becomes `block_n`
+    when the kernel the call runs takes that width (checked with the library's plan query),
+    else it is ignored, as are BLOCK_M, BLOCK_K and GROUP_M (Triton tile shapes)."""
     if not config:
         return 0, 0, 0
     flags = 0
@@ -64,7 +82,20 @@ def _flags_from_config(config: dict | None, M: int) -> tuple[int, int, int]:
             flags |= _lib.EXACT
     if config.get("chunks_per_wave"):
         flags |= _lib.CPW_FLAGS[int(config["chunks_per_wave"])]
-    return int(config.get("block_n", 0)), int(config.get("split_k", 0)), flags
+    prefill = config.get("prefill")
+    if prefill is not None and prefill not in PREFILL_PATHS:
+        raise ValueError(f"w4a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
+    if M > 16 and prefill == "gemm":
+        flags |= _lib.PATH_GEMM
+    elif M > 16 and prefill == "blocks":
+        flags |= _lib.PATH_MFMA
+    split_k = int(config["split_k"] if "split_k" in config else config.get("SPLIT_K", 0))
+    block_n = int(config.get("block_n", 0))
+    if "block_n" not in config and config.get("BLOCK_N"):
+        want = int(config["BLOCK_N"])
+        if _query(M, N, K, group_size, want, split_k, flags)[0] == _lib.OK:
+            block_n = want
+    return block_n, split_k, flags
 
 
 def _decode(x2, qweight, scales, zeros, bias, group_size, block_n, split_k, flags, out):
@@ -97,14 +128,7 @@ def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=No
     s = scales if scales.is_contiguous() else scales.contiguous()
     z = zeros if zeros.is_contiguous() else zeros.contiguous()
     b = None if bias is None else bias.to(torch.float16).contiguous()
-    prefill = (config or {}).get("prefill")
-    if prefill is not None and prefill not in PREFILL_PATHS:
-        raise ValueError(f"w4a16_matmul: config['prefill']={prefill!r}, expected one of {PREFILL_PATHS}")
-    block_n, split_k, flags = _flags_from_config(config, M)
-    if M > 16 and prefill == "gemm":
-        flags |= _lib.PATH_GEMM
-    elif M > 16 and prefill == "blocks":
-        flags |= _lib.PATH_MFMA
+    block_n, split_k, flags = _tuning(config, M, N, K, group_size)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     _decode(x2, qw, s, z, b, group_size, block_n, split_k, flags, out)
     # the library's choice is recorded for the decode shapes it chose (w4a16.py:322-326): a call
@@ -115,16 +139,19 @@ def w4a16_matmul(x, qweight, scales, zeros, group_size=128, bias=None, config=No
     return out.view(*x.shape[:-1], N)
 
 
-def config_for(M: int, N: int, K: int, group_size: int = 128) -> str:
-    """The library's table choice for a decode shape, as 'block_n=..,split_k=..,flags=..'."""
-    bn, sk, fl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    _lib.check(_lib.load().ldk_w4a16_config(M, N, K, group_size, ctypes.byref(bn),
-                                            ctypes.byref(sk), ctypes.byref(fl)), "w4a16_config")
-    mode = "factored" if fl.value & _lib.FACTORED else "exact"
-    path = "mfma" if fl.value & _lib.PATH_MFMA else "valu"
-    cpw = {v: k for k, v in _lib.CPW_FLAGS.items()}.get(fl.value & _lib.CPW_MASK)
+def config_for(M: int, N: int, K: int, group_size: int = 128, config: dict | None = None) -> str:
+    """What the library runs for a shape, as 'path,block_n=..,split_k=..,mode': its table choice,
+    or with `config` what a call with that config runs (the library's plan query; no GPU
+    needed). Raises as the call would for a config it refuses."""
+    st, (bn, sk, fl) = _query(M, N, K, group_size, *_tuning(config, M, N, K, group_size))
+    _lib.check(st, "w4a16_config")
+    if fl & _lib.PATH_GEMM:
+        return f"gemm,block_n={bn},split_k={sk}"
+    mode = "factored" if fl & _lib.FACTORED else "exact"
+    path = "mfma" if fl & _lib.PATH_MFMA else "valu"
+    cpw = {v: k for k, v in _lib.CPW_FLAGS.items()}.get(fl & _lib.CPW_MASK)
     extra = f",chunks_per_wave={cpw}" if cpw else ""
-    return f"{path},block_n={bn.value},split_k={sk.value},{mode}{extra}"
+    return f"{path},block_n={bn},split_k={sk},{mode}{extra}"
 
 
 def kernel_name(M: int, N: int, K: int, group_size: int = 128) -> str:

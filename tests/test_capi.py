@@ -109,8 +109,8 @@ def test_exact_is_not_the_mfma_kernel():
 def test_w8a16_swiglu_validates_before_launch():
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    st, msg = _err(lib.ldk_w8a16_swiglu_matmul(p, p, p, None, p, 40, 256, None, 0, None))
-    assert st == _lib.ERR_UNSUPPORTED and "multiple of 16" in msg
+    st, msg = _err(lib.ldk_w8a16_swiglu_matmul(p, p, p, None, p, 42, 256, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "multiple of 4" in msg
     st, _ = _err(lib.ldk_w8a16_swiglu_matmul(p, p, p, None, p, 64, 100, None, 0, None))
     assert st == _lib.ERR_UNSUPPORTED
     st, _ = _err(lib.ldk_w8a16_swiglu_matmul(p, ctypes.c_void_p(264), p, None, p, 64, 256, None, 0, None))
@@ -129,7 +129,7 @@ def test_w8a16_rmsnorm_validates_before_launch():
     st, _ = _err(lib.ldk_w8a16_rmsnorm_matmul(ctypes.c_void_p(258), None, None, p, 1e-6, p, p, None,
                                               p, 64, 256, None, 0, None))
     assert st == _lib.ERR_ALIGN
-    st, _ = _err(lib.ldk_w8a16_rmsnorm_matmul(p, None, None, p, 1e-6, p, p, None, p, 40, 256, None,
+    st, _ = _err(lib.ldk_w8a16_rmsnorm_matmul(p, None, None, p, 1e-6, p, p, None, p, 42, 256, None,
                                               0, None))
     assert st == _lib.ERR_UNSUPPORTED
 
@@ -181,29 +181,45 @@ def test_fused_entries_validate_before_launch():
     assert st == _lib.ERR_INVALID
 
 
-def test_w8a16_n_multiple_of_16():
+def test_w8a16_n_multiple_of_4():
+    """The reference masks columns, so any N runs there (N = 40 in tests/test_fp8.py:40); here N
+    must be a multiple of 4 (N = 40 plans, N = 42 is refused before any launch)."""
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    st, _ = _err(lib.ldk_w8a16_matmul(p, 64, p, p, None, p, 40, 1, 40, 64, 0, 0, 0, None, 0, None))
-    assert st == _lib.ERR_UNSUPPORTED
+    st, msg = _err(lib.ldk_w8a16_matmul(p, 64, p, p, None, p, 42, 1, 42, 64, 0, 0, 0, None, 0, None))
+    assert st == _lib.ERR_UNSUPPORTED and "multiple of 4" in msg
+    for M in (1, 5, 17, 100):
+        bn, sk, fl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()  # in: the library's choice
+        st = lib.ldk_w8a16_config(M, 40, 96, ctypes.byref(bn), ctypes.byref(sk), ctypes.byref(fl))
+        assert st == 0, (M, lib.ldk_last_error())
+
+
+def _config(M, N, K, gs=128, block_n=0, split_k=0, flags=0):
+    """ldk_w4a16_config's plan for a call with these tuning arguments (in/out parameters)."""
+    bn, sk, fl = ctypes.c_int(block_n), ctypes.c_int(split_k), ctypes.c_int(flags)
+    st = _lib.load().ldk_w4a16_config(M, N, K, gs, ctypes.byref(bn), ctypes.byref(sk), ctypes.byref(fl))
+    return st, bn.value, sk.value, fl.value
 
 
 def test_config_query():
-    bn, sk, fl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    st = _lib.load().ldk_w4a16_config(1, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
-                                      ctypes.byref(fl))
-    assert st == 0 and bn.value in (16, 32, 64) and sk.value >= 1
-    assert fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU
-    st = _lib.load().ldk_w4a16_config(16, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
-                                      ctypes.byref(fl))
-    assert st == 0 and fl.value & _lib.PATH_MFMA and bn.value == 64  # x staged in LDS, 64-column tiles
+    st, bn, sk, fl = _config(1, 17920, 1536)
+    assert st == 0 and bn in (16, 32, 64) and sk >= 1
+    assert fl & _lib.FACTORED and fl & _lib.PATH_VALU
+    st, bn, sk, fl = _config(16, 17920, 1536)
+    assert st == 0 and fl & _lib.PATH_MFMA and bn == 64  # x staged in LDS, 64-column tiles
     # two rows: the factored VALU kernel; from three rows the MFMA kernel, also on small shapes
-    st = _lib.load().ldk_w4a16_config(2, 17920, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
-                                      ctypes.byref(fl))
-    assert st == 0 and fl.value & _lib.FACTORED and fl.value & _lib.PATH_VALU and bn.value == 32
-    st = _lib.load().ldk_w4a16_config(3, 1536, 1536, 128, ctypes.byref(bn), ctypes.byref(sk),
-                                      ctypes.byref(fl))
-    assert st == 0 and fl.value & _lib.PATH_MFMA
+    st, bn, sk, fl = _config(2, 17920, 1536)
+    assert st == 0 and fl & _lib.FACTORED and fl & _lib.PATH_VALU and bn == 32
+    st, bn, sk, fl = _config(3, 1536, 1536)
+    assert st == 0 and fl & _lib.PATH_MFMA
+    # the prefill GEMM for many rows, and a call's tuning arguments as inputs
+    st, bn, sk, fl = _config(2048, 17920, 1536)
+    assert st == 0 and fl == _lib.PATH_GEMM
+    st, bn, sk, fl = _config(1, 1536, 1536, block_n=16, split_k=3)
+    assert st == 0 and (bn, sk) == (16, 3)
+    # a query returns the status the call would: block_n 128 is not a VALU width
+    st, *_ = _config(1, 1536, 1536, block_n=128, flags=_lib.PATH_VALU)
+    assert st == _lib.ERR_UNSUPPORTED
 
 
 def test_decode_rows_plan_kernels():

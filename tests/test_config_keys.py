@@ -1,0 +1,84 @@
+"""The reference's Triton config keys (SPLIT_K, BLOCK_N) as this build reads them, checked through
+the library's plan query (ldk_w4a16_config / ldk_w8a16_config, host code only: no GPU needed).
+The reference's tests force splits and tile widths with these keys (tests/test_w4a16.py:33-66,
+tests/test_fp8.py:37-48); here a forced SPLIT_K must run that many workgroups along K, and a
+BLOCK_N must become the tile width where the kernel the call runs takes it."""
+
+import pytest
+
+from kernels import fp8, w4a16
+
+CFG = dict(BLOCK_M=16, BLOCK_N=32, BLOCK_K=64, SPLIT_K=1, GROUP_M=8)
+GEMV = dict(GEMV=True, BLOCK_N=32, BLOCK_K=64, SPLIT_K=1)
+FP8_CFG = dict(BLOCK_M=16, BLOCK_N=32, BLOCK_K=32, SPLIT_K=1, GROUP_M=8)
+
+
+def _fields(desc: str) -> dict:
+    return dict(kv.split("=") for kv in desc.split(",") if "=" in kv)
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 4])
+def test_w4a16_split_k_runs_that_many_splits(split):
+    """K = 512 at group 128 is 4 groups: 3 splits deal them 2 + 1 + 1 (the reference's
+    test_split_k_small, tests/test_w4a16.py:41-44)."""
+    f = _fields(w4a16.config_for(2, 48, 512, 128, {**CFG, "SPLIT_K": split}))
+    assert int(f["split_k"]) == split
+
+
+def test_w4a16_split_k_at_most_the_groups():
+    """A split is a range of quantization groups: K = 256 (2 groups) takes at most 2."""
+    assert _fields(w4a16.config_for(1, 64, 256, 128, {**GEMV, "SPLIT_K": 3}))["split_k"] == "2"
+    assert _fields(w4a16.config_for(1, 96, 128, 128, {**GEMV, "SPLIT_K": 3}))["split_k"] == "1"
+    assert _fields(w4a16.config_for(1, 40, 384, 128, {**GEMV, "SPLIT_K": 3}))["split_k"] == "3"
+
+
+def test_w4a16_lowercase_keys_win():
+    f = _fields(w4a16.config_for(1, 1536, 1536, 128, {**CFG, "split_k": 4, "block_n": 16}))
+    assert f["split_k"] == "4" and f["block_n"] == "16"
+
+
+@pytest.mark.parametrize("M,N,K,bn", [(1, 64, 256, 32), (3, 40, 128, 32), (5, 64, 256, 64),
+                                      (16, 1536, 1536, 32), (17, 96, 384, 32)])
+def test_w4a16_block_n_taken_where_the_kernel_has_it(M, N, K, bn):
+    f = _fields(w4a16.config_for(M, N, K, 128, {**CFG, "BLOCK_N": bn}))
+    assert int(f["block_n"]) == bn
+
+
+def test_w4a16_block_n_ignored_where_the_kernel_lacks_it():
+    """The VALU kernels stop at 64 columns: BLOCK_N = 128 with GEMV keeps the table's width, where
+    an explicit block_n = 128 is refused as the call would refuse it."""
+    table = _fields(w4a16.config_for(1, 1536, 1536, 128, {"GEMV": True}))
+    f = _fields(w4a16.config_for(1, 1536, 1536, 128, {**GEMV, "BLOCK_N": 128}))
+    assert f["block_n"] == table["block_n"]
+    with pytest.raises(RuntimeError):
+        w4a16.config_for(1, 1536, 1536, 128, {"GEMV": True, "block_n": 128})
+
+
+def test_w4a16_table_choices_unchanged_by_the_query():
+    assert w4a16.config_for(1, 17920, 1536) == w4a16.config_for(1, 17920, 1536, 128, {})
+    assert w4a16.config_for(2048, 17920, 1536).startswith("gemm,")
+    assert w4a16.config_for(16, 1536, 8960).startswith("mfma,")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (5, 40, 96), (17, 96, 256)])
+def test_fp8_reference_direct_cases_plan(M, N, K):
+    f = _fields(fp8.config_for(M, N, K, FP8_CFG))
+    assert f["split_k"] == "1"
+
+
+def test_fp8_split_and_gemv_keys():
+    assert _fields(fp8.config_for(2, 48, 256, {**FP8_CFG, "SPLIT_K": 3}))["split_k"] == "3"
+    gemv = {"GEMV": True, "BLOCK_N": 32, "BLOCK_K": 64, "SPLIT_K": 2}
+    assert fp8.config_for(1, 48, 256, gemv) == "valu,block_n=32,split_k=2"
+
+
+def test_fp8_column_tails_plan():
+    """N % 16 != 0: 64-column MFMA tiles where N % 8 != 0, 128-column VALU tiles, no prefill GEMM."""
+    assert fp8.config_for(5, 44, 96).startswith("mfma,block_n=64")
+    assert fp8.config_for(1, 44, 96).startswith("valu,block_n=128")
+    assert fp8.config_for(512, 1000, 1536).startswith("mfma,")
+    assert fp8.config_for(512, 1024, 1536).startswith("gemm,")
+    with pytest.raises(RuntimeError):
+        fp8.config_for(1, 42, 96)
+    with pytest.raises(RuntimeError):
+        fp8.config_for(5, 44, 96, {"MFMA": True, "block_n": 128})

@@ -7,7 +7,7 @@ import torch
 
 from _util import assert_north_star, bits16, dev, to_np
 from kernels.bench import cases
-from kernels.fp8 import FP8, dequantize_fp8, quantize_fp8, w8a16_matmul
+from kernels.fp8 import FP8, config_for, dequantize_fp8, quantize_fp8, w8a16_matmul
 from oracle import fp8 as of
 
 pytestmark = pytest.mark.gpu
@@ -71,6 +71,51 @@ def _run(M, N, K, seed=3, bias=False, config=None):
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 128), (5, 48, 96), (17, 96, 256), (2, 48, 256)])
 def test_small(M, N, K):
+    _run(M, N, K)
+
+
+# The reference's own cases (tests/test_fp8.py:37-48): its Triton config keys, N = 40 (not a
+# multiple of 16), a forced three-way split and the GEMV path with bias and a two-way split.
+REF_CFG = dict(BLOCK_M=16, BLOCK_N=32, BLOCK_K=32, SPLIT_K=1, GROUP_M=8)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (5, 40, 96), (17, 96, 256)])
+def test_reference_direct_cases(M, N, K):
+    _run(M, N, K, config=REF_CFG)
+
+
+def test_reference_split_and_gemv_cases():
+    cfg = {**REF_CFG, "SPLIT_K": 3}
+    assert config_for(2, 48, 256, cfg).endswith("split_k=3")
+    _run(2, 48, 256, config=cfg)
+    gemv = {"GEMV": True, "BLOCK_N": 32, "BLOCK_K": 64, "SPLIT_K": 2}
+    assert config_for(1, 48, 256, gemv) == "valu,block_n=32,split_k=2"
+    _run(1, 48, 256, bias=True, config=gemv)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 16, 17, 100])
+@pytest.mark.parametrize("N,K", [(40, 96), (4, 128), (8, 64), (1000, 1024), (2044, 1536), (264, 8960)])
+def test_column_tails(M, N, K):
+    """N % 16 != 0 (N % 4 == 0): the VALU kernel's dword loads, the MFMA kernel's 64-column tiles
+    (128 where N % 8 == 0), the 16-row blocks in place of the prefill GEMM; bias on the last
+    column; the default plan, the VALU kernel forced where it takes the rows, and the MFMA kernel
+    forced with a K split."""
+    _run(M, N, K, bias=True)
+    if M <= 16:
+        _run(M, N, K, config={"GEMV": True})
+    _run(M, N, K, config={"MFMA": True, "split_k": 3})
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_reference_decode_shape_8960x1536(M):
+    """The reference's extra decode shape (tests/test_w4a16.py:84: N = 8960, K = 1536)."""
+    _run(M, 8960, 1536)
+
+
+@pytest.mark.parametrize("M", [33, 128, 2048])
+@pytest.mark.parametrize("N,K", [(1536, 1536), (8960, 1536), (1536, 8960)])
+def test_reference_prefill_shapes(M, N, K):
+    """The reference's prefill rows (tests/test_w4a16.py:89-97) in this format."""
     _run(M, N, K)
 
 

@@ -105,3 +105,29 @@ def test_w8a16_cancelling_partials(scale, M, cfg):
     for _ in range(3):
         out = w8a16_matmul(x, wq, sc, config={**cfg, "split_k": 2}).float().cpu().numpy()
         assert np.array_equal(out, np.full((M, N), 32.0 * scale, np.float32)), np.unique(out)
+
+
+def test_workspace_first_use_under_capture_is_refused():
+    """The split-K workspace is allocated by the first call on a device. A first call under graph
+    capture would take it from the graph's private pool: refused with a message, before any
+    launch. Made outside capture, the same call is then capturable."""
+    from kernels import _lib
+
+    x = torch.randn(1, 1536, dtype=torch.float16, device="cuda")
+    qw = torch.zeros(192, 1536, dtype=torch.int32, device="cuda")
+    s = torch.ones(12, 1536, dtype=torch.float16, device="cuda")
+    z = torch.zeros(12, 1536, dtype=torch.float16, device="cuda")
+    saved = dict(_lib._workspaces)
+    _lib._workspaces.clear()
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="graph capture"):
+            with torch.cuda.graph(graph):
+                w4a16_matmul(x, qw, s, z)
+    finally:
+        _lib._workspaces.clear()
+        _lib._workspaces.update(saved)
+    torch.cuda.synchronize()
+    y = w4a16_matmul(x, qw, s, z)  # the workspace is back: the eager call runs, and again alike
+    assert torch.equal(y, w4a16_matmul(x, qw, s, z))
+    torch.cuda.synchronize()

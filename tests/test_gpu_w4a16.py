@@ -10,7 +10,7 @@ import torch
 from _util import assert_north_star, bits16, dev, to_np
 from kernels.bench import cases
 from kernels.cuda.w4a16_cuda import w4a16_decode_cuda
-from kernels.w4a16 import w4a16_matmul
+from kernels.w4a16 import config_for, w4a16_matmul
 from oracle import quant as oq
 from oracle.reference import dequantize_ref, w4a16_ref
 
@@ -350,8 +350,85 @@ def test_qkv_fused_with_bias():
 
 # ---------------------------------------------------------------- the native decode entry
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 16])
-def test_decode_entry(M):
-    _run(M, 1536, 1536, entry=w4a16_decode_cuda)
+@pytest.mark.parametrize("split", [None, 1, 3, 4])
+def test_decode_entry(M, split):
+    """The reference's cases (tests/test_w4a16_cuda.py:23-27) with its explicit splits 1 and 4,
+    a three-way split, and the library's table."""
+    x, qw, s, z, _ = _make(M, 1536, 1536, 2)
+    out = w4a16_decode_cuda(dev(x), dev(qw), dev(s), dev(z), split_k=split)
+    assert out.shape == (M, 1536) and out.dtype == torch.float16
+    assert_north_star(out, w4a16_ref(x, qw, s, z))
+
+
+@pytest.mark.parametrize("N,K", [(2048, 1536), (17920, 1536), (1536, 8960), (4096, 14336)])
+def test_decode_entry_autosplit(N, K):
+    """tests/test_w4a16_cuda.py:30-33: one and 16 rows on the library's split table."""
+    _run(1, N, K, entry=w4a16_decode_cuda)
+    _run(16, N, K, entry=w4a16_decode_cuda)
+
+
+def test_decode_entry_odd_n_split_bias_and_rows():
+    """tests/test_w4a16_cuda.py:36-45: N = 1000 split 3 with bias, N = 132, and 17 rows refused."""
+    for M, N, K, split in ((5, 1000, 1024, 3), (1, 132, 256, 1)):
+        x, qw, s, z, b = _make(M, N, K, 5, bias=True)
+        out = w4a16_decode_cuda(dev(x), dev(qw), dev(s), dev(z), bias=dev(b), split_k=split)
+        assert_north_star(out, w4a16_ref(x, qw, s, z, 128, b))
+    x, qw, s, z, _ = _make(17, 128, 128, 5)
+    with pytest.raises(RuntimeError):
+        w4a16_decode_cuda(dev(x), dev(qw), dev(s), dev(z), split_k=1)
+
+
+# ------------------------------------------- the reference's config keys (tests/test_w4a16.py)
+REF_CFG = dict(BLOCK_M=16, BLOCK_N=32, BLOCK_K=64, SPLIT_K=1, GROUP_M=8)
+REF_GEMV = dict(GEMV=True, BLOCK_N=32, BLOCK_K=64, SPLIT_K=1)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (3, 40, 128), (17, 96, 384)])
+def test_reference_direct_small(M, N, K):
+    _run(M, N, K, config=REF_CFG)
+
+
+@pytest.mark.parametrize("split", [2, 3])
+def test_reference_split_k_small(split):
+    """SPLIT_K is honoured: K = 512 is 4 groups of 128, dealt evenly over 2 or 3 workgroups."""
+    cfg = {**REF_CFG, "SPLIT_K": split}
+    assert config_for(2, 48, 512, 128, cfg) == f"valu,block_n=32,split_k={split},factored"
+    _run(2, 48, 512, config=cfg)
+
+
+def test_reference_bias_both_paths():
+    _run(1, 64, 256, bias=True, config=REF_CFG)
+    _run(1, 64, 256, bias=True, config={**REF_CFG, "SPLIT_K": 2})
+
+
+@pytest.mark.parametrize("N,K", [(64, 256), (40, 384), (96, 128)])
+@pytest.mark.parametrize("split", [1, 3])
+def test_reference_gemv(N, K, split):
+    _run(1, N, K, config={**REF_GEMV, "SPLIT_K": split})
+
+
+@pytest.mark.parametrize("split", [1, 2])
+def test_reference_gemv_factored(split):
+    _run(1, 96, 384, config={**REF_GEMV, "SPLIT_K": split, "FACTORED": True})
+    _run(1, 64, 256, bias=True, config={**REF_GEMV, "FACTORED": True, "BLOCK_K": 128})
+
+
+def test_reference_gemv_bias_and_block_k_128():
+    _run(1, 64, 256, bias=True, config=REF_GEMV)
+    _run(1, 64, 256, bias=True, config={**REF_GEMV, "SPLIT_K": 2, "BLOCK_K": 128})
+    _run(5, 64, 256, config={**REF_CFG, "BLOCK_K": 128, "BLOCK_N": 64})
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_reference_decode_shape_8960x1536(M):
+    """The reference's extra decode shape (tests/test_w4a16.py:84: N = 8960, K = 1536)."""
+    _run(M, 8960, 1536)
+
+
+@pytest.mark.parametrize("M", [33, 128, 2048])
+def test_reference_prefill_8960x1536(M):
+    """tests/test_w4a16.py:89-97: the (8960, 1536) prefill shape at the reference's rows."""
+    _run(M, 8960, 1536)
 
 
 # ------------------------------------------------------------- prefill rows (M > 16)
