@@ -149,12 +149,17 @@ def e2e_leg(steps: int) -> dict:
                 "ms_per_token": {k: round(v["decode"]["ms_per_token"], 3) for k, v in b.items()},
                 "layers_only_ms": {k: round(v["layers_only_ms"], 3) for k, v in b.items()},
                 "speedup_vs_fp16": {k: round(v["speedup_vs_fp16"], 3) for k, v in b.items()},
+                "prefill_tok_s": {k: round(v["prefill"]["tok_s"], 1) for k, v in b.items()},
+                "prefill_ms": {k: round(v["prefill"]["ms"], 3) for k, v in b.items()},
+                "prefill_speedup_vs_fp16": {k: round(v["prefill_speedup_vs_fp16"], 3)
+                                            for k, v in b.items()},
                 "linear_bytes_per_token": {k: v["weights"]["linear_layers"] for k, v in b.items()}}
 
     out = {"metric": "Qwen2.5-1.5B-arch batch-1 decode tok/s", "unit": "tok/s",
            "workload": "random-init Qwen2.5-1.5B architecture (seed 4), prompt 128, "
-                       f"{steps} greedy steps, hipGraph per step, median of 3"}
-    for head, backends in (("gemv", ["fp16", "ours", "ours_lm"]), ("torch", ["fp16", "ours"])):
+                       f"{steps} greedy steps, hipGraph per step, median of 3; prefill: the "
+                       "128-token prompt's forward as one hipGraph, median of 5"}
+    for head, backends in (("gemv", ["fp16", "ours", "ours_lm", "ours_fp8"]), ("torch", ["fp16", "ours"])):
         out[f"head_{head}"] = table(run({"backends": backends, "decode_steps": steps,
                                          "prompt_len": 128, "head": head}))
         gc.collect()

@@ -497,6 +497,11 @@ struct W8Plan {
 };
 
 constexpr int kW8MfmaWaves = 8;
+// 64-column tiles at 9-16 rows run 16 waves: each wave then carries half the K steps of a piece
+// into the 16-row LDS reduction. Graph-timed on MI355X at M = 16 (8 -> 16 waves): down 9.20 ->
+// 8.23 us, q/o 5.82 -> 4.95, k/v 5.02 -> 4.16; at M = 4 and 8 within 1%; 128-column tiles (gate_up)
+// lose with 16 (M = 4 / 8 / 16: 8.42 / 9.30 / 10.62 -> 11.00 / 9.93 / 11.03 us).
+constexpr int kW8MfmaWavesWide = 16;
 
 // MFMA plan. Shapes of at least 128 tiles of 128 columns (gate_up: 140) keep 128-column tiles
 // and, from 5 rows, split K only as far as one pass of at most 6 K steps per wave needs, so
@@ -546,18 +551,20 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
     p.splits = 1;
     p.kps = (int)(steps * 32);
   }
+  if (p.ln == 4 && M > 8 && M <= 16) p.nw = kW8MfmaWavesWide;
   const int64_t per_wave = ((p.kps / 32) + p.nw - 1) / p.nw;
-  p.ksw = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : 6;
+  // K steps per wave and pass: 16 waves hold at most 4 each in registers (1024 lanes: 128 VGPRs)
+  p.ksw = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : (per_wave <= 4 || p.nw == kW8MfmaWavesWide) ? 4 : 6;
   return p;
 }
 
-template <int KSW, int CW>
+template <int NW, int KSW, int CW>
 int launch_w8_mfma_t(const W8Args& a, const W8Split& sp, hipStream_t s) {
-  constexpr int NW = kW8MfmaWaves;
   const unsigned tiles = (unsigned)((a.N + CW - 1) / CW), blocks = (unsigned)((a.M + 15) / 16);
   // 64-column tiles: one dimension over (tile, split) pieces (w8_pair_piece)
   const dim3 grid = CW == 64 ? dim3(tiles * (unsigned)sp.splits, 1, blocks) : dim3(tiles, (unsigned)sp.splits, blocks);
   const size_t lds = (size_t)NW * 16 * CW * 4;
+  static_assert((size_t)NW * 16 * CW * 4 <= 64 * 1024, "the LDS reduction fits the default dynamic LDS limit");
   (void)hipGetLastError();
   w8a16_mfma_kernel<NW, KSW, CW><<<grid, NW * 64, lds, s>>>(a, sp);
   return ldk::check_launch("w8a16_mfma");
@@ -565,11 +572,22 @@ int launch_w8_mfma_t(const W8Args& a, const W8Split& sp, hipStream_t s) {
 
 template <int CW>
 int launch_w8_mfma_cw(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s) {
+  if constexpr (CW == 64) {
+    if (p.nw == kW8MfmaWavesWide) {
+      switch (p.ksw) {
+        case 1: return launch_w8_mfma_t<kW8MfmaWavesWide, 1, CW>(a, sp, s);
+        case 2: return launch_w8_mfma_t<kW8MfmaWavesWide, 2, CW>(a, sp, s);
+        case 4: return launch_w8_mfma_t<kW8MfmaWavesWide, 4, CW>(a, sp, s);
+      }
+      return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d K steps per wave not instantiated for 16 waves", p.ksw);
+    }
+  }
+  if (p.nw != kW8MfmaWaves) return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d waves not instantiated", p.nw);
   switch (p.ksw) {
-    case 1: return launch_w8_mfma_t<1, CW>(a, sp, s);
-    case 2: return launch_w8_mfma_t<2, CW>(a, sp, s);
-    case 4: return launch_w8_mfma_t<4, CW>(a, sp, s);
-    case 6: return launch_w8_mfma_t<6, CW>(a, sp, s);
+    case 1: return launch_w8_mfma_t<kW8MfmaWaves, 1, CW>(a, sp, s);
+    case 2: return launch_w8_mfma_t<kW8MfmaWaves, 2, CW>(a, sp, s);
+    case 4: return launch_w8_mfma_t<kW8MfmaWaves, 4, CW>(a, sp, s);
+    case 6: return launch_w8_mfma_t<kW8MfmaWaves, 6, CW>(a, sp, s);
   }
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w8a16: %d K steps per wave not instantiated", p.ksw);
 }

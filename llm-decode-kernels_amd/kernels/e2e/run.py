@@ -7,6 +7,8 @@ kernels/e2e/run.py measures on its GPUs):
   greedy steps, each step one graph replay (forward + argmax + bookkeeping), median of 3 runs;
 - the swapped layers alone: all 28 layers' projections, fused add+norms and the activation for
   one decode step, as one graph (`layers_only_ms`, the reference's run.py:166-201);
+- prefill tokens/s: the whole 128-token prompt's forward as one graph, median of 5 replays
+  (`prefill_speed`, the reference's run.py:142-162);
 - the layer weight bytes each backend reads per token.
 Every backend runs the same lm_head (`--head gemv|torch`, kernels/e2e/model.py's QwenRunner).
 
@@ -98,6 +100,23 @@ def decode_speed(runner, ids, steps: int, repeats: int = 3) -> dict:
             "ms_per_token": 1e3 / med, "steps": steps, "tokens": runs[-1][0]}
 
 
+def prefill_speed(runner, ids: torch.Tensor, repeats: int = 5) -> dict:
+    """The whole-prompt forward as one hipGraph (the reference's run.py:142-162): the T prompt
+    tokens at positions 0..T-1 (KV cache written, last position's logits), two eager warm-up
+    forwards, then the median of `repeats` single replays, HIP events on the replay stream."""
+    T = ids.shape[1]
+    pos = torch.arange(T, device=ids.device)
+    for _ in range(2):
+        runner.forward(ids, pos)
+    torch.cuda.synchronize()
+    graph, _ = capture(lambda: runner.forward(ids, pos))
+    graph.replay()
+    torch.cuda.synchronize()
+    ms = statistics.median(replay_ms(graph, 1) for _ in range(repeats))
+    del graph
+    return {"T": T, "ms": ms, "tok_s": T / (ms * 1e-3)}
+
+
 def layers_only_ms(runner, M: int = 1, samples: int = 7, replays: int = 10) -> float:
     """Graph time of the swapped ops alone for one decode step (the reference's run.py:166-201):
     per layer the qkv, o, gate_up and down projections, two add+norms and the activation,
@@ -149,9 +168,12 @@ def run(params: dict) -> dict:
         r = {"weights": runner.weight_bytes()}
         r["decode"] = decode_speed(runner, ids, steps)
         r["layers_only_ms"] = layers_only_ms(runner)
+        r["prefill"] = prefill_speed(runner, ids)
         result["backends"][name] = r
         print(f"[e2e] {name}: {r['decode']['tok_s']:.1f} tok/s, layers only "
-              f"{r['layers_only_ms']:.3f} ms ({time.time() - t0:.0f}s)", file=sys.stderr, flush=True)
+              f"{r['layers_only_ms']:.3f} ms, prefill {r['prefill']['T']} tokens "
+              f"{r['prefill']['ms']:.3f} ms ({r['prefill']['tok_s']:.0f} tok/s) "
+              f"({time.time() - t0:.0f}s)", file=sys.stderr, flush=True)
         del runner
         gc.collect()
         torch.cuda.empty_cache()
@@ -159,6 +181,7 @@ def run(params: dict) -> dict:
         base = result["backends"]["fp16"]
         for name, r in result["backends"].items():
             r["speedup_vs_fp16"] = r["decode"]["tok_s"] / base["decode"]["tok_s"]
+            r["prefill_speedup_vs_fp16"] = r["prefill"]["tok_s"] / base["prefill"]["tok_s"]
             r["layers_speedup_vs_fp16"] = base["layers_only_ms"] / r["layers_only_ms"]
             toks, ref = r["decode"]["tokens"], base["decode"]["tokens"]
             r["first_token_divergence_vs_fp16"] = next(

@@ -248,3 +248,25 @@ def test_gemv_head_matches_torch_head(backend):
         r.forward(ids[:, :11], torch.arange(11, device="cuda"))
         outs[head] = r.forward(ids[:, 11:], torch.tensor([11], device="cuda")).float()
     torch.testing.assert_close(outs["gemv"], outs["torch"], atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", ["fp16", "ours", "ours_fp8"])
+def test_prefill_speed_graph_matches_eager(backend):
+    """The e2e prefill measurement (kernels.e2e.run.prefill_speed, the reference's
+    run.py:142-162) replays a captured whole-prompt forward: its logits equal the eager
+    forward's bit for bit (the same kernels on the same inputs), and it reports T tokens."""
+    from kernels.bench.harness import capture
+    from kernels.e2e.run import prefill_speed
+
+    model = _tiny_model(torch.float16, "cuda")
+    runner = QwenRunner(model, make_backend(backend), max_len=64)
+    ids = torch.randint(0, 512, (1, 24), device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    pos = torch.arange(24, device="cuda")
+    eager = runner.forward(ids, pos).clone()
+    graph, out = capture(lambda: runner.forward(ids, pos))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+    res = prefill_speed(runner, ids)
+    assert res["T"] == 24 and res["ms"] > 0 and res["tok_s"] > 0
