@@ -293,6 +293,22 @@ int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, const float
                                 float scale, const void* const* warm, const int64_t* warm_bytes, int nwarm,
                                 void* stream);
 
+/* Prompt attention: T tokens of one sequence at positions pos[T] (int64 device array), in two
+ * launches on `stream`: RoPE on q and k (the fp16 steps of ldk_decode_attention), the roped q
+ * written to q_scratch [T][nq][128] fp16 (a caller-provided 16-byte aligned device buffer of
+ * T * nq * 128 halves), k and v written into the tiled caches at every pos[t] in [0, max_len)
+ * (others write nothing), then causal grouped-query softmax attention of each token t over the
+ * cache positions 0..pos[t] (the cache then holds all T tokens; a negative pos[t] gives zeros).
+ * qkv [T] rows of ldqkv >= (nq + 2 nkv) * 128 fp16 (projection output, bias added); out [T] rows
+ * of ldo >= nq * 128 fp16. Cache layout, head_dim (128), nq % nkv and max_len rules as
+ * ldk_decode_attention. Replaces the prompt branch of the reference runner's attention
+ * (kernels/e2e/model.py:212-243: RoPE, k/v index_copy_ into the cache, scaled_dot_product_attention
+ * with the causal mask), which is about twenty small launches per layer. */
+int ldk_prefill_attention(const void* qkv, int64_t ldqkv, const int64_t* pos, int64_t T,
+                          const float* inv_freq, void* k_cache, void* vt_cache, void* q_scratch,
+                          void* out, int64_t ldo, int nq, int nkv, int head_dim, int64_t max_len,
+                          float scale, void* stream);
+
 /* Residual + RMSNorm carried across the two projections around it (decode, one row), as a pair
  * of launches that replaces linear + rmsnorm(x, residual) + linear of the reference's layer
  * (kernels/e2e/model.py:79-97, 226-233: o_proj, post_attention_layernorm, gate_up). Group size

@@ -463,6 +463,200 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
   out[(int64_t)h * kHD + lane + 64] = (half_t)(lg > 0.0f ? o1 / lg : 0.0f);
 }
 
+// ------------------------------------------------------------ prompt (many-token) attention
+//
+// ldk_prefill_attention: T tokens of one sequence at positions pos[T], in two launches.
+//  1. prefill_rope_kv_kernel, one workgroup per token: the decode kernel's fp16 RoPE (same cos and
+//     sin of pos * inv_freq, same roundings) on the token's q heads, written to q_scratch
+//     [T][nq][128], and on its k heads, written with its v heads into the tiled caches at pos[t]
+//     (a position outside [0, max_len) writes nothing).
+//  2. prefill_attention_kernel, one workgroup per (block of 16 tokens, query head): the decode
+//     kernel's score and P.V steps with the MFMA tile's 16 columns the block's tokens instead of
+//     a kv head's query heads. Column c16 (token t0 + c16) attends to the cache positions
+//     0..pos[t0 + c16] with its own mask, so every token is causal whatever the order of pos.
+//     Wave w takes the 32-position chunks w, w + 4, ... up to the block's last position, two
+//     chunks' tiles in flight at a time; the waves' (m, l, O) meet through LDS.
+// The launch boundary orders the cache writes of launch 1 before the reads of launch 2.
+constexpr int kPWaves = 4;
+
+__global__ __launch_bounds__(256) void prefill_rope_kv_kernel(const half_t* qkv, int64_t ldqkv, const int64_t* pos,
+                                                              const float* inv_freq, half_t* kc, half_t* vt,
+                                                              half_t* qs, int nq, int nkv, int L) {
+  __shared__ half_t cs[2][64];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const int64_t p = pos[t];
+  if (tid < 64) {
+    const float ang = (float)p * inv_freq[tid];
+    cs[0][tid] = (half_t)cosf(ang);
+    cs[1][tid] = (half_t)sinf(ang);
+  }
+  __syncthreads();
+  const half_t* row = qkv + (int64_t)t * ldqkv;
+  half_t* qo = qs + (int64_t)t * nq * kHD;
+  for (int e = tid; e < nq * 64; e += 256) {  // (head, dim pair j < 64): dims j and j + 64
+    const int h = e >> 6, j = e & 63;
+    half_t x0 = row[h * kHD + j], x1 = row[h * kHD + j + 64];
+    rope_rotate(x0, x1, cs[0][j], cs[1][j]);
+    qo[h * kHD + j] = x0;
+    qo[h * kHD + j + 64] = x1;
+  }
+  if (p < 0 || p >= L) return;  // uniform
+  const int pp = (int)p;
+  for (int e = tid; e < nkv * 64; e += 256) {
+    const int h = e >> 6, j = e & 63;
+    half_t x0 = row[(nq + h) * kHD + j], x1 = row[(nq + h) * kHD + j + 64];
+    rope_rotate(x0, x1, cs[0][j], cs[1][j]);
+    half_t* kw = kc + (int64_t)h * L * kHD;
+    kw[k_offset(pp, j)] = x0;
+    kw[k_offset(pp, j + 64)] = x1;
+  }
+  for (int e = tid; e < nkv * kHD; e += 256) {
+    const int h = e >> 7, d = e & (kHD - 1);
+    vt[(int64_t)h * kHD * L + vt_offset(d, pp)] = row[(nq + nkv + h) * kHD + d];
+  }
+}
+
+__global__ __launch_bounds__(kPWaves * 64) void prefill_attention_kernel(const half_t* qs, const int64_t* pos, int T,
+                                                                        const half_t* kc, const half_t* vt, half_t* out,
+                                                                        int64_t ldo, int nq, int nkv, int L,
+                                                                        float scale) {
+  __shared__ float mw[kPWaves][kTile], lw[kPWaves][kTile];
+  __shared__ __align__(16) float ow[kPWaves][kTile][kHD];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kb = lane >> 4;
+  const int h = (int)blockIdx.y, t0 = (int)blockIdx.x * kTile;
+  const int kvh = h / (nq / nkv);
+  const int nt = min(kTile, T - t0);  // tokens of this block
+  // this lane's column: token t0 + c16 and the last cache position it attends to (-1: none)
+  int plim = -1;
+  if (c16 < nt) {
+    const int64_t pp = pos[t0 + c16];
+    plim = pp < 0 ? -1 : pp >= L ? L - 1 : (int)pp;
+  }
+  const int pmax = (int)wave_max((float)plim);  // the block's last position (exact: < 2^24)
+  const int nch = pmax < 0 ? 0 : pmax / kChunk + 1;
+  const int nk = nch > wave ? (nch - wave + kPWaves - 1) / kPWaves : 0;  // this wave's chunks
+  const auto krs = ldk::buffer_rsrc(kc + (int64_t)kvh * L * kHD, (uint32_t)L * kHD * 2);
+  const auto vrs = ldk::buffer_rsrc(vt + (int64_t)kvh * kHD * L, (uint32_t)L * kHD * 2);
+  const uint32_t lane_off = (uint32_t)(c16 * 64 + kb * 16);
+  // B operands of the scores: lane (c16, kb) holds q of token t0 + c16 at dims 8kb + 32s .. +7
+  u32x4 qb[4];
+  {
+    const auto qrs = ldk::buffer_rsrc(qs, (uint32_t)((int64_t)T * nq * kHD * 2));
+    uint32_t dq = c16 < nt ? 0u : kDead;
+    asm volatile("" : "+v"(dq));
+    const uint32_t oq = (uint32_t)(((int64_t)(t0 + c16) * nq + h) * kHD * 2) | dq;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qb[s] = ldk::buffer_load16(qrs, oq + (uint32_t)((8 * kb + 32 * s) * 2));
+  }
+
+  float m_run = -__builtin_inff(), l_lane = 0.0f;  // token c16's running max; this lane's sum
+  float4_t o[8];  // O[tokens 4kb .. 4kb+3][dim 16b + c16] per dim block b, unnormalised
+#pragma unroll
+  for (int b = 0; b < 8; ++b) o[b] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto chunks = [&](auto ncc, int k0) __attribute__((always_inline)) {
+    constexpr int NC = decltype(ncc)::value;
+    u32x4 kr[NC][8], vr[NC][8];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+      const int c = wave + kPWaves * (k0 + n);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) kr[n][t] = ldk::buffer_load16(krs, (uint32_t)((c * 8 + t) * kTileHalves * 2) + lane_off);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) vr[n][t] = ldk::buffer_load16(vrs, (uint32_t)((c * 8 + t) * kTileHalves * 2) + lane_off);
+    }
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+      const int cb = kChunk * (wave + kPWaves * (k0 + n));
+      float4_t acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        acc[0] = mfma16(kr[n][s], qb[s], acc[0]);
+        acc[1] = mfma16(kr[n][4 + s], qb[s], acc[1]);
+      }
+      float sv[8];
+      float mc = -__builtin_inff();
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = cb + 8 * kb + 4 * hb + r;
+          sv[4 * hb + r] = p <= plim ? acc[hb][r] * scale : -__builtin_inff();
+          mc = fmaxf(mc, sv[4 * hb + r]);
+        }
+      }
+      mc = max_xor32(max_xor16(mc));  // token c16's max over the chunk (-inf: none live)
+      const float m_new = fmaxf(m_run, mc);
+      // a token with no live position so far keeps m = -inf; its exponents are taken against 0
+      // (every numerator is then exp(-inf) = 0) instead of the NaN of -inf - -inf
+      const float m_ref = m_new == -__builtin_inff() ? 0.0f : m_new;
+      const float alpha = __expf(m_run - m_ref);
+      m_run = m_new;
+      half8_t ph;
+      float ls = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = __expf(sv[e] - m_ref);  // 0 for masked positions
+        ls += x;
+        ph[e] = (half_t)x;
+      }
+      l_lane = l_lane * alpha + ls;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {  // the tokens of this lane's accumulator rows are 4kb .. 4kb+3
+        const float al = __shfl(alpha, 4 * kb + r);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) o[b][r] *= al;
+      }
+      const u32x4 pa = __builtin_bit_cast(u32x4, ph);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) o[b] = mfma16(pa, vr[n][b], o[b]);
+    }
+  };
+  for (int k = 0; k < nk; k += 2) {
+    if (nk - k >= 2)
+      chunks(IntC<2>(), k);
+    else
+      chunks(IntC<1>(), k);
+  }
+
+  // ---- the waves meet: per-wave (m, l) per token and O rows of the block's tokens
+  const float l_w = ldk::add_xor32(ldk::add_xor16(l_lane));
+  if (kb == 0) {
+    mw[wave][c16] = m_run;
+    lw[wave][c16] = l_w;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (4 * kb + r < nt) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) ow[wave][4 * kb + r][16 * b + c16] = o[b][r];
+    }
+  ldk::lds_barrier();
+  for (int e = tid; e < nt * kHD; e += kPWaves * 64) {
+    const int j = e >> 7, d = e & (kHD - 1);
+    float mv[kPWaves], lv[kPWaves], ov[kPWaves];
+#pragma unroll
+    for (int w = 0; w < kPWaves; ++w) {
+      mv[w] = mw[w][j];
+      lv[w] = lw[w][j];
+      ov[w] = ow[w][j][d];
+    }
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < kPWaves; ++w) M = fmaxf(M, mv[w]);
+    float l = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kPWaves; ++w) {
+      const float f = mv[w] != -__builtin_inff() ? __expf(mv[w] - M) : 0.0f;
+      l = __builtin_fmaf(lv[w], f, l);
+      acc = __builtin_fmaf(ov[w], f, acc);
+    }
+    out[(int64_t)(t0 + j) * ldo + (int64_t)h * kHD + d] = (half_t)(l > 0.0f ? acc / l : 0.0f);
+  }
+}
+
 }  // namespace
 
 namespace ldk {
@@ -610,3 +804,37 @@ int attention_partials(const char* what, void* stream, const int64_t* pos, int64
 }
 
 }  // namespace ldk
+
+// Prompt attention (launches prefill_rope_kv_kernel, then prefill_attention_kernel).
+extern "C" int ldk_prefill_attention(const void* qkv, int64_t ldqkv, const int64_t* pos, int64_t T, const float* inv_freq,
+                                     void* k_cache, void* vt_cache, void* q_scratch, void* out, int64_t ldo, int nq,
+                                     int nkv, int head_dim, int64_t max_len, float scale, void* stream) {
+  static const char* fn = "prefill_attention";
+  if (!qkv || !pos || !inv_freq || !k_cache || !vt_cache || !q_scratch || !out)
+    return ldk::fail(LDK_ERR_INVALID, "%s: null pointer", fn);
+  if (head_dim != kHD) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: head_dim=%d (only 128)", fn, head_dim);
+  if (nq <= 0 || nkv <= 0 || nq % nkv || nq > 65535)
+    return ldk::fail(LDK_ERR_INVALID, "%s: nq=%d must be a positive multiple of nkv=%d (at most 65535)", fn, nq, nkv);
+  if (T <= 0 || T > (int64_t(1) << 24)) return ldk::fail(LDK_ERR_INVALID, "%s: T=%lld outside 1..2^24", fn, (long long)T);
+  if (max_len < kChunk || max_len > kMaxLen || max_len % kChunk)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: max_len=%lld must be a multiple of 32 in 32..%lld", fn, (long long)max_len,
+                     (long long)kMaxLen);
+  if (ldqkv < (int64_t)(nq + 2 * nkv) * kHD || ldo < (int64_t)nq * kHD)
+    return ldk::fail(LDK_ERR_INVALID, "%s: row strides ldqkv=%lld ldo=%lld below the rows", fn, (long long)ldqkv, (long long)ldo);
+  // the q scratch is one buffer resource (32-bit offsets)
+  if (T * nq * kHD * 2 > (int64_t)UINT32_MAX) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: T * nq too large", fn);
+  if (!ldk::aligned(k_cache, 16) || !ldk::aligned(vt_cache, 16) || !ldk::aligned(q_scratch, 16) ||
+      !ldk::aligned(qkv, 2) || !ldk::aligned(out, 2) || !ldk::aligned(pos, 8) || !ldk::aligned(inv_freq, 4))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: k_cache, vt_cache and q_scratch 16-byte, pos 8-byte aligned", fn);
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  prefill_rope_kv_kernel<<<(unsigned)T, 256, 0, s>>>((const half_t*)qkv, ldqkv, pos, inv_freq, (half_t*)k_cache,
+                                                     (half_t*)vt_cache, (half_t*)q_scratch, nq, nkv, (int)max_len);
+  int st = ldk::check_launch("prefill_rope_kv");
+  if (st) return st;
+  const dim3 grid((unsigned)((T + kTile - 1) / kTile), (unsigned)nq);
+  prefill_attention_kernel<<<grid, kPWaves * 64, 0, s>>>((const half_t*)q_scratch, pos, (int)T, (const half_t*)k_cache,
+                                                         (const half_t*)vt_cache, (half_t*)out, ldo, nq, nkv,
+                                                         (int)max_len, scale);
+  return ldk::check_launch("prefill_attention");
+}

@@ -75,6 +75,8 @@ SIGNATURES = {
                              _vp],
     "ldk_decode_attention_ranges": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _f32, _vp, _vp,
                                     _i32, _vp],
+    "ldk_prefill_attention": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64,
+                              _f32, _vp],
     "ldk_w4a16_attn_matmul_residual_stats": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _i64, _i64, _i32, _vp, _i64, _vp],
 }

@@ -1,6 +1,7 @@
-"""Fused decode attention on gfx950 (libldk_amd.so `ldk_decode_attention`): for one new token,
-RoPE on q and k, the KV-cache write at `pos` and grouped-query softmax attention over positions
-0..pos, one launch per layer.
+"""Fused attention on gfx950 (libldk_amd.so): `decode_attention` (`ldk_decode_attention`) for
+one new token, RoPE on q and k, the KV-cache write at `pos` and grouped-query softmax attention
+over positions 0..pos, one launch per layer; `prefill_attention` (`ldk_prefill_attention`) the
+same for the T tokens of a prompt, causal, in two launches.
 
 It replaces, for decode steps, the attention block of the reference's Qwen2 runner
 (kernels/e2e/model.py:212-243), which is about twenty small torch launches per layer.
@@ -122,6 +123,51 @@ def decode_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tenso
             len(warm), _lib.stream(dev))
     _lib.check(st, "decode_attention")
     return out
+
+
+def prefill_attention(qkv: torch.Tensor, pos: torch.Tensor, inv_freq: torch.Tensor,
+                      k_cache: torch.Tensor, vt_cache: torch.Tensor, n_heads: int, n_kv: int,
+                      scale: float) -> torch.Tensor:
+    """The prompt's attention block (ldk_prefill_attention): qkv [1, T, (n_heads + 2 n_kv) * 128]
+    fp16 (the qkv projection's rows), pos int64 [T], inv_freq fp32 [64], one layer's tiled caches
+    as decode_attention takes them. RoPE on q and k, k and v written into the cache at every
+    pos[t], and causal grouped-query attention of token t over the cache positions 0..pos[t].
+    Returns [1, T, n_heads * 128] fp16 (the reference's prompt branch, kernels/e2e/model.py:
+    212-243, in two launches instead of about twenty)."""
+    hd = HEAD_DIM
+    width = (n_heads + 2 * n_kv) * hd
+    T = pos.numel()
+    assert qkv.shape[-1] == width and qkv.numel() == T * width
+    L = k_cache.shape[-5] * CHUNK
+    assert k_cache.shape[-6:] == k_cache_shape(n_kv, L) and k_cache.numel() == n_kv * L * hd
+    assert vt_cache.shape[-5:] == vt_cache_shape(n_kv, L) and vt_cache.numel() == n_kv * L * hd
+    assert k_cache.is_contiguous() and vt_cache.is_contiguous()
+    if qkv.dtype != torch.float16 or k_cache.dtype != torch.float16 or vt_cache.dtype != torch.float16:
+        raise ValueError("prefill_attention: qkv and the cache must be float16")
+    if pos.dtype != torch.int64 or inv_freq.dtype != torch.float32:
+        raise ValueError("prefill_attention: pos int64, inv_freq float32")
+    rows = qkv.reshape(T, width)
+    if rows.stride(1) != 1:
+        rows = rows.contiguous()
+    p = pos.contiguous()
+    dev = _lib.require_gpu(rows, p, inv_freq, k_cache, vt_cache, what="prefill_attention")
+    q_scratch = torch.empty((T, n_heads * hd), dtype=torch.float16, device=dev)
+    out = torch.empty((1, T, n_heads * hd), dtype=torch.float16, device=dev)
+    freq = inv_freq.contiguous()
+    with _lib.device_guard(dev):
+        st = _lib.load().ldk_prefill_attention(
+            _lib.ptr(rows), rows.stride(0), _lib.ptr(p), T, _lib.ptr(freq), _lib.ptr(k_cache),
+            _lib.ptr(vt_cache), _lib.ptr(q_scratch), _lib.ptr(out), n_heads * hd, n_heads, n_kv,
+            hd, L, float(scale), _lib.stream(dev))
+    _lib.check(st, "prefill_attention")
+    return out
+
+
+def prefill_supported(head_dim: int, max_len: int, batch: int, tokens: int) -> bool:
+    """prefill_attention's domain: head_dim 128, one sequence, a cache length that is a multiple
+    of 32."""
+    return (head_dim == HEAD_DIM and CHUNK <= max_len <= MAX_LEN and max_len % CHUNK == 0
+            and batch == 1 and 1 <= tokens <= 1 << 24)
 
 
 # Most position ranges the o projection's merge takes (csrc/w4a16.hip, kAttnRanges).

@@ -415,6 +415,9 @@ class QwenRunner:
         self.warm_weights = True  # see warm_set: the attention launch warms the next weights
         self.fused_attention = (attention == "fused" and dev.type == "cuda"
                                 and fa.supported(d, max_len, batch, 1))
+        # prompt rows (T > 1) through kernels.attention.prefill_attention with the fused runner
+        self.fused_prefill = (attention == "fused" and dev.type == "cuda" and dt == torch.float16
+                              and fa.prefill_supported(d, max_len, batch, 2))
 
     def weight_bytes(self) -> dict:
         """Bytes of the swapped layers and of the parts that stay fp16 (model.py:196-210). A
@@ -496,6 +499,7 @@ class QwenRunner:
         nq, nkv, hd = self.n_heads, self.n_kv, self.head_dim
         x = F.embedding(tokens, self.embed)
         fused = self.fused_attention and B == 1 and T == 1
+        prompt = self.fused_prefill and B == 1 and T > 1
         # the attention's ranges merged in the o projection's x staging (one launch fewer per
         # layer, and ranges of a quarter of the cache instead of one range per kv head)
         merge = fused and self.merge_attention and be.merges_attention
@@ -506,6 +510,8 @@ class QwenRunner:
             merge = -(-self.max_len // rlen) <= MERGE_MAX_RANGES and config.GROUP_SIZE == 128
         if fused:
             from kernels.attention import decode_attention
+        elif prompt:
+            from kernels.attention import prefill_attention
         else:
             freqs = pos[:, None].float() * self.inv_freq[None, :]
             emb = torch.cat((freqs, freqs), dim=-1)
@@ -530,6 +536,9 @@ class QwenRunner:
                 attn = decode_attention(qkv, pos, self.inv_freq, self.k_cache[i], self.vt_cache[i],
                                         nq, nkv, hd ** -0.5,
                                         self.warm_set(i) if self.warm_weights and be.warms else ())
+            elif prompt:
+                attn = prefill_attention(qkv, pos, self.inv_freq, self.k_cache[i], self.vt_cache[i],
+                                         nq, nkv, hd ** -0.5)
             else:
                 q, k, v = qkv.split([nq * hd, nkv * hd, nkv * hd], dim=-1)
                 q = self._rope(q.view(B, T, nq, hd), cos, sin)

@@ -270,3 +270,32 @@ def test_prefill_speed_graph_matches_eager(backend):
     assert torch.equal(out, eager)
     res = prefill_speed(runner, ids)
     assert res["T"] == 24 and res["ms"] > 0 and res["tok_s"] > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", ["fp16", "ours"])
+@pytest.mark.parametrize("P", [2, 40, 130])
+def test_fused_prefill_matches_torch_path(backend, P):
+    """The prompt through ldk_prefill_attention (RoPE + KV write + causal GQA in two launches per
+    layer) against the torch ops of the same runner: close logits for every prompt row, close
+    KV caches (v of layer 0 identical), then decode steps that read the prompt's cache."""
+    model = _qwen_heads_model("cuda")
+    ref = QwenRunner(model, make_backend(backend), max_len=160, attention="torch")
+    fused = QwenRunner(model, make_backend(backend), max_len=160, attention="fused")
+    assert fused.fused_prefill and not ref.fused_prefill
+    ids = torch.randint(0, 512, (1, P + 6), device="cuda")
+    pos = torch.arange(P, device="cuda")
+    a = ref.forward(ids[:, :P], pos, all_logits=True)
+    b = fused.forward(ids[:, :P], pos, all_logits=True)
+    torch.testing.assert_close(b.float(), a.float(), atol=3e-2, rtol=3e-2)
+    from kernels.attention import k_from_tiles, v_from_tiles
+
+    kf, kr = k_from_tiles(fused.k_cache)[..., :P, :].float(), k_from_tiles(ref.k_cache)[..., :P, :].float()
+    vf, vr = v_from_tiles(fused.vt_cache)[..., :P, :], v_from_tiles(ref.vt_cache)[..., :P, :]
+    assert (kf[0] - kr[0]).abs().max() < 1e-2
+    assert torch.equal(vf[0], vr[0])
+    torch.testing.assert_close(kf[1:], kr[1:], atol=2e-2, rtol=2e-2)
+    for t in range(P, P + 6):
+        step = torch.tensor([t], device="cuda")
+        torch.testing.assert_close(fused.forward(ids[:, t: t + 1], step).float(),
+                                   ref.forward(ids[:, t: t + 1], step).float(), atol=3e-2, rtol=3e-2)

@@ -354,3 +354,80 @@ def test_decode_attention_warm_changes_nothing(L, pos):
     a = decode_attention(qkv, p, inv_freq, kt_a, vt_a, nq, nkv, hd ** -0.5)
     b = decode_attention(qkv, p, inv_freq, kt_b, vt_b, nq, nkv, hd ** -0.5, warm=warm)
     assert torch.equal(a, b) and torch.equal(kt_a, kt_b) and torch.equal(vt_a, vt_b)
+
+
+@pytest.mark.parametrize("nq,nkv,L,p0,T", [(12, 2, 416, 0, 128), (12, 2, 416, 0, 1), (12, 2, 416, 0, 17),
+                                           (12, 2, 416, 100, 60), (12, 2, 416, 380, 36),
+                                           (4, 4, 64, 0, 64), (8, 1, 512, 0, 300), (16, 2, 160, 33, 7),
+                                           (12, 2, 2048, 0, 1000), (40, 2, 288, 5, 90)])
+def test_prefill_against_float64(nq, nkv, L, p0, T):
+    """ldk_prefill_attention: T prompt tokens at positions p0 .. p0 + T - 1 over a cache whose
+    positions below p0 already hold earlier tokens. The cache rows at the prompt's positions
+    hold its roped k and its v, every other row is unchanged, and token t attends causally to
+    positions 0..p0 + t (float64 reference from the stored fp16 cache). Cases cover one token,
+    a ragged last 16-token block, prompts after a filled prefix, a prompt ending at the cache's
+    last position, one kv head per query head and more than 16 query heads per kv head."""
+    from kernels.attention import prefill_attention
+
+    g = torch.Generator().manual_seed(p0 + 13 * T + nq)
+    hd = 128
+    qkv = torch.randn(T, (nq + 2 * nkv) * hd, generator=g).half()
+    kc, vc, kt_d, vt_d = _caches(g, nkv, L)
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd)))
+    pos = torch.arange(p0, p0 + T, dtype=torch.int64)
+    out = prefill_attention(qkv.cuda().view(1, T, -1), pos.cuda(), inv_freq.cuda(), kt_d, vt_d, nq,
+                            nkv, hd ** -0.5)
+    assert out.shape == (1, T, nq * hd)
+    x = qkv.double().numpy()
+    fr = inv_freq.numpy()
+    k_got = k_from_tiles(kt_d.cpu()).double().numpy()[0]
+    v_got = v_from_tiles(vt_d.cpu()).double().numpy()[0]
+    new = np.zeros(L, dtype=bool)
+    new[p0:p0 + T] = True
+    assert np.array_equal(k_got[:, ~new], kc.double().numpy()[0][:, ~new])
+    assert np.array_equal(v_got[:, ~new], vc.double().numpy()[0][:, ~new])
+    gq = nq // nkv
+    got = out.view(T, nq, hd).cpu().double().numpy()
+    ref = np.zeros((T, nq, hd))
+    for t in range(T):
+        p = p0 + t
+        k = x[t, nq * hd:(nq + nkv) * hd].reshape(nkv, hd)
+        v = x[t, (nq + nkv) * hd:].reshape(nkv, hd)
+        kr = _rope64(k, p, fr)
+        assert np.abs(k_got[:, p] - kr).max() <= 4e-3 * max(1.0, np.abs(kr).max())
+        assert np.array_equal(v_got[:, p], v.astype(np.float16).astype(np.float64))
+        qr = _rope64(x[t, : nq * hd].reshape(nq, hd), p, fr)
+        for h in range(nq):
+            s = k_got[h // gq, : p + 1] @ qr[h] / math.sqrt(hd)
+            w = np.exp(s - s.max())
+            ref[t, h] = (w / w.sum()) @ v_got[h // gq, : p + 1]
+    err = np.abs(got - ref)
+    assert err.max() <= 2e-2 and np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2e-3, (err.max(),)
+
+
+def test_prefill_positions_out_of_order_and_out_of_range():
+    """Each token is masked by its own position, not by its index: a shuffled prompt gives each
+    token the row its position gives in order. A position past the cache writes nothing and
+    attends to the whole cache; a negative one writes nothing and returns zeros."""
+    from kernels.attention import prefill_attention
+
+    nq, nkv, L, T, hd = 12, 2, 96, 40, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(T, (nq + 2 * nkv) * hd, generator=g).half()
+    inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    perm = torch.randperm(T, generator=g)
+    runs = []
+    for order in (torch.arange(T), perm):
+        _, _, kt, vt = _caches(torch.Generator().manual_seed(9), nkv, L)
+        out = prefill_attention(qkv[order].cuda().view(1, T, -1), order.cuda(), inv, kt, vt, nq, nkv,
+                                hd ** -0.5)
+        runs.append((out[0], kt, vt, order))
+    (o0, k0, v0, _), (o1, k1, v1, order) = runs
+    assert torch.equal(k0, k1) and torch.equal(v0, v1)
+    assert torch.equal(o1, o0[order.cuda()])
+    _, _, kt, vt = _caches(torch.Generator().manual_seed(9), nkv, L)
+    kt0, vt0 = kt.clone(), vt.clone()
+    pos = torch.tensor([L, -1, L + 5], dtype=torch.int64)
+    out = prefill_attention(qkv[:3].cuda().view(1, 3, -1), pos.cuda(), inv, kt, vt, nq, nkv, hd ** -0.5)
+    assert torch.equal(kt, kt0) and torch.equal(vt, vt0)
+    assert torch.isfinite(out).all() and torch.equal(out[0, 1], torch.zeros_like(out[0, 1]))
