@@ -164,14 +164,15 @@ __device__ __forceinline__ void store_fact_record(unsigned char* dst, u32x4 d) {
 // Shared epilogue of the multi-row kernels: the workgroup's NW wave partials of n outputs sit
 // wave-major in `red`; sum them and store (or hand them to the cross-workgroup split-K
 // reduction).
+// `words`: the tile's first accumulator word (split tiles only).
 template <typename Store>
 __device__ __forceinline__ void finish_tile(const float* red, int n, int NW, const TileWork& tw,
-                                            const SplitArgs& sp, Store store) {
+                                            const SplitArgs& sp, uint64_t* words, Store store) {
   auto part = [&](int o) { return ldk::sum_waves(red + o, n, NW); };
   if (tw.whole) {
     for (int o = threadIdx.x; o < n; o += blockDim.x) store(o, part(o));
   } else {
-    ldk::splitk_accumulate(split_ctx(sp, tw), sp.acc + (size_t)(tw.tile - sp.full) * n, n, part, store);
+    ldk::splitk_accumulate(split_ctx(sp, tw), words, n, part, store);
   }
 }
 
@@ -858,7 +859,7 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
           float4_t{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
   }
   __syncthreads();
-  finish_tile(red, MT * CW, NW, tw, sp, [&](int o, float v) {
+  finish_tile(red, MT * CW, NW, tw, sp, sp.acc + (size_t)(tw.tile - sp.full) * MT * CW, [&](int o, float v) {
     const int m = o / CW, n = n0 + (o - m * CW);
     if (m < a.M && n < a.N) {
       if (a.bias) v += (float)a.bias[n];
@@ -1049,7 +1050,12 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
     }
   }
   __syncthreads();
-  finish_tile(red, n, NW, tw, sp, [&](int o, float v) {
+  // split words: [row block][split tile][outputs of the block], the block's stride its full rows
+  // (M rows when a single block of M <= 16 rows)
+  const int wstride = a.M <= 16 ? n : 16 * MT * CW;
+  const int stiles = (a.N + CW - 1) / CW - sp.full;
+  uint64_t* const words = sp.acc + ((size_t)blockIdx.y * stiles + (tw.tile - sp.full)) * wstride;
+  finish_tile(red, n, NW, tw, sp, words, [&](int o, float v) {
     const int m = o / CW, nn = n0 + (o - m * CW);
     if (nn < a.N) {
       if (a.bias) v += (float)a.bias[nn];
@@ -1265,10 +1271,12 @@ size_t plan_lds_bytes(const Plan& p, int64_t M) {
 
 int plan_cw(const Plan& p) { return 4 * p.ln; }
 
-// Accumulator words of a split launch: one per output of every split tile.
+// Accumulator words of a split launch: one per output of every split tile (the MFMA kernel's row
+// blocks of more than 16 rows: each block's full 16 * mtile rows).
 int64_t split_words(const Plan& p, int64_t M, int64_t N) {
   const int cw = plan_cw(p);
   const int64_t tiles = (N + cw - 1) / cw - p.full;
+  if (p.kern == kMfma && M > 16) return tiles * ((M + 16 * p.mtile - 1) / (16 * p.mtile)) * 16 * p.mtile * cw;
   const int64_t n = p.kern == kMfma ? std::min<int64_t>(M, 16) * cw : (int64_t)p.mt * cw;
   return tiles * n;
 }
@@ -1416,7 +1424,19 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // 5.3 / 5.2 / 5.5 / 6.9)
   if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20) && M <= 16)
     splits = m1 ? std::max<int64_t>(2, 256 / tiles) : ((M <= 4 ? 240 : 192) + tiles - 1) / tiles;
-  if (M > 16) splits = 1;  // row blocks fill the grid; a K split would carry every row through atomics
+  // Prefill rows in 32-row blocks: a long-K shape whose tiles and blocks leave most CUs idle
+  // splits K toward 256 workgroups, at most 8 ways and about 400K split-K atomics (every row of
+  // every block carries one per split); otherwise the row blocks fill the grid. down 1536x8960
+  // (24 tiles), graph-timed, whole K -> split: M = 17 18.5 -> 9.0 us (8 ways), M = 65 24.6 ->
+  // 12.7 (4), M = 128 25.4 -> 17.5 (2; 3 ways 25.4: the atomics), M = 256 (192 workgroups) stays
+  // whole, 25.7 against 32.9 split 2; the short-K shapes (q/o/qkv, 12 groups) lose with any split
+  // (o M = 128 8.5 -> 10.9 us at 2).
+  if (M > 16 && split_k <= 0) {
+    const int64_t base = tiles * ((M + 31) / 32);
+    splits = 1;
+    if (mfma && ng >= 24 && base < 160)
+      splits = std::max<int64_t>(1, std::min<int64_t>({(256 + base - 1) / base, 8, 400000 / (M * N)}));
+  }
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
   p.splits = (int)((ng + p.gps - 1) / p.gps);
@@ -1603,7 +1623,6 @@ int launch_mfma_t(const W4Args& a, const SplitArgs& sp, int nw, size_t lds, hipS
     return ldk::fail(LDK_ERR_LAUNCH, "w4a16: cannot raise the LDS limit to %zu B", lds);
   const int64_t mblocks = (a.M + 16 * MT - 1) / (16 * MT);
   if (mblocks > 65535) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: M=%d needs more than 65535 row blocks", a.M);
-  if (MT > 1 && sp.splits > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: row blocks of 32 take no K split");
   if ((int64_t)(16 * MT - 1) * a.ldx * 2 + (int64_t)a.K * 2 >= (int64_t(1) << 31))
     return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: a row block of x spans 2 GiB or more (ldx=%lld)", (long long)a.ldx);
   (void)hipGetLastError();
@@ -1798,7 +1817,6 @@ static int plan_check(const char* fn, const Plan& p, int64_t M, int64_t N, int64
         return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: group_size 256 with M > 16 takes block_n=64", fn);
       if ((M + 16 * p.mtile - 1) / (16 * p.mtile) > 65535)
         return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld needs more than 65535 row blocks", fn, (long long)M);
-      if (p.mtile > 1 && p.splits > 1) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: row blocks of 32 take no K split", fn);
       if ((int64_t)(16 * p.mtile - 1) * ldx * 2 + K * 2 >= (int64_t(1) << 31))
         return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: a row block of x spans 2 GiB or more (ldx=%lld)", fn, (long long)ldx);
       return LDK_OK;

@@ -583,3 +583,19 @@ def test_choice_export_records_only_the_library_choice():
     mod._decode_choice.clear()
     mod.import_choices(exported)
     assert mod.export_choices() == exported
+
+
+@pytest.mark.parametrize("M", [17, 33, 65, 100, 128])
+@pytest.mark.parametrize("split", [None, 2, 3, 8])
+def test_prefill_blocks_split_k(M, split):
+    """Prefill rows of a long-K shape on the 32-row MFMA blocks with K split over workgroups
+    (the library's choice below about 200 rows on down; explicit splits too): each row block's
+    split tiles meet in their own fixed-point words, the last row block ragged. Repeated calls
+    give the same bits (every word is back to zero after a call)."""
+    cfg = {"prefill": "blocks"} if split is None else {"prefill": "blocks", "split_k": split}
+    _run(M, 1536, 8960, bias=True, config=cfg)
+    x, qw, s, z, b = _make(M, 1536, 8960, 9, bias=True)
+    args = (dev(x), dev(qw), dev(s), dev(z))
+    y0 = w4a16_matmul(*args, bias=dev(b), config=cfg)
+    y1 = w4a16_matmul(*args, bias=dev(b), config=cfg)
+    assert torch.equal(y0, y1)
