@@ -1419,11 +1419,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // workgroup per CU). Multi-row splits carry M outputs per column through returning atomics,
   // so small shapes keep whole tiles and split K over the waves of a workgroup instead (q/o at
   // M = 16: 5.9 us whole, 25 us split twelve ways).
-  // (MFMA: about 240 workgroups for up to 4 rows, 192 beyond, where each split's atomics carry
-  // more rows: down M = 2 / 4 / 8 / 16 in 10 splits 4.9 / 5.0 / 5.9 / 7.6 us, in 8 splits
-  // 5.3 / 5.2 / 5.5 / 6.9)
+  // (MFMA: about 240 workgroups, with one returning atomic per thread below: down M = 2 / 4 /
+  // 8 / 16 in 10 splits 4.9 / 5.0 / 5.45 / 6.70 us, in 8 splits 5.2 / 5.2 / 5.6 / 6.73)
   if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20) && M <= 16)
-    splits = m1 ? std::max<int64_t>(2, 256 / tiles) : ((M <= 4 ? 240 : 192) + tiles - 1) / tiles;
+    splits = m1 ? std::max<int64_t>(2, 256 / tiles) : (240 + tiles - 1) / tiles;
   // Prefill rows in 32-row blocks: a long-K shape whose tiles and blocks leave most CUs idle
   // splits K toward 256 workgroups, at most 8 ways and about 400K split-K atomics (every row of
   // every block carries one per split); otherwise the row blocks fill the grid. down 1536x8960
@@ -1492,6 +1491,11 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     cpw = std::min(cpw, rpg <= 16 && p.mtile == 1 ? 2 : 1);
     p.cpw = cpw;
     p.nw = (int)std::min<int64_t>(wmax, (chunks + cpw - 1) / cpw);
+    // a split tile's outputs leave through one returning atomic each, a thread's in turn: with
+    // more outputs than lanes, the workgroup takes extra waves (no groups of their own) so that
+    // every thread carries one (down M = 16 in 10 splits: 7.60 -> 6.70 us; M = 8: 5.99 -> 5.45)
+    if (p.splits > 1 && M > 4)
+      p.nw = std::max<int>(p.nw, std::min<int>(wmax, (int)((std::min<int64_t>(M, 16) * plan_cw(p) + 63) / 64)));
     return p;
   }
   while (cpw > 1 && !gemv_shape_ok(p.mt, p.ln, p.rpl, cpw)) cpw >>= 1;
