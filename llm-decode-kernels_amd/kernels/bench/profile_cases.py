@@ -146,6 +146,22 @@ def case_attention(reps, L=416, pos=300):
     _rotate(lambda k, v: decode_attention(qkv, p, inv, k, v, nq, nkv, hd ** -0.5), sets, reps)
 
 
+def case_prefill_attention(reps, T=128, L=416):
+    """The prompt's attention block (kernels.attention.prefill_attention): T tokens at positions
+    0..T-1 of a cache of L, Qwen2.5-1.5B heads (12 / 2 of 128)."""
+    from kernels.attention import k_cache_shape, prefill_attention, vt_cache_shape
+
+    g = cases.gen(6)
+    nq, nkv, hd = 12, 2, 128
+    qkv = torch.randn(1, T, (nq + 2 * nkv) * hd, generator=g).half().cuda()
+    kc = torch.randn((1,) + k_cache_shape(nkv, L), generator=g).half().cuda()
+    vt = torch.randn((1,) + vt_cache_shape(nkv, L), generator=g).half().cuda()
+    inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    p = torch.arange(T, device="cuda")
+    sets = [(kc.clone(), vt.clone()) for _ in range(n_copies(tensor_bytes((kc, vt))))]
+    _rotate(lambda k, v: prefill_attention(qkv, p, inv, k, v, nq, nkv, hd ** -0.5), sets, reps)
+
+
 def case_rmsnorm(M, N, reps):
     from kernels.rmsnorm import rmsnorm
 
@@ -199,6 +215,10 @@ CASES = {
     "fp8_swiglu_down_m1": lambda r: case_swiglu_fp8(1536, 8960, r),
     "attention_l416": lambda r: case_attention(r),
     "attention_l4096": lambda r: case_attention(r, L=4096, pos=4000),
+    "prefill_attention_t128": lambda r: case_prefill_attention(r),
+    # prefill rows of down on the 32-row MFMA blocks with K split over workgroups
+    "w4a16_down_m65": lambda r: case_w4a16(65, 1536, 8960, r),
+    "w4a16_down_m128": lambda r: case_w4a16(128, 1536, 8960, r),
     "rmsnorm_res_m2048": lambda r: case_rmsnorm(2048, 1536, r),
     "swiglu_m2048": lambda r: case_swiglu(2048, 8960, r),
     # decode rows 4 and 8 on the VALU kernel (forced) against the library's MFMA kernel
