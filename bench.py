@@ -136,7 +136,9 @@ def e2e_leg(steps: int) -> dict:
     runs the same lm_head: `head_gemv` sends the fp16 table (and the final norm) through this
     build's one-row GEMV on all backends, `head_torch` keeps the reference's norm then
     `F.linear(h, lm_head)` (model.py:250-253) on all backends. `ours_lm` quantizes the head
-    instead. Reported beside the headline, not as `value`."""
+    instead. `decode_check` checks each timed generation teacher-forced against a reference
+    runner on the same weights (kernels.e2e.run.decode_check). Reported beside the headline, not
+    as `value`."""
     import gc
 
     import torch
@@ -153,7 +155,10 @@ def e2e_leg(steps: int) -> dict:
                 "prefill_ms": {k: round(v["prefill"]["ms"], 3) for k, v in b.items()},
                 "prefill_speedup_vs_fp16": {k: round(v["prefill_speedup_vs_fp16"], 3)
                                             for k, v in b.items()},
-                "linear_bytes_per_token": {k: v["weights"]["linear_layers"] for k, v in b.items()}}
+                "linear_bytes_per_token": {k: v["weights"]["linear_layers"] for k, v in b.items()},
+                "decode_check": {k: {f: v["check"][f] for f in ("reference", "positions", "agree",
+                                                              "max_margin", "beyond_tol")}
+                                 for k, v in b.items() if "check" in v}}
 
     out = {"metric": "Qwen2.5-1.5B-arch batch-1 decode tok/s", "unit": "tok/s",
            "workload": "random-init Qwen2.5-1.5B architecture (seed 4), prompt 128, "

@@ -136,6 +136,29 @@ class W4RefBackend(_Int4, Backend):
         return F.linear(x, p.w, p.bias)
 
 
+class FP8RefBackend(Backend):
+    """OCP e4m3 weights with per-channel scales (kernels.fp8.quantize_fp8), dequantized once to
+    fp16 (bit-exact HIP dequantizer, fp8.py:33-35) then the fp16 GEMM: the same quantized model
+    as `ours_fp8` through library GEMMs, the FP8 counterpart of `w4_ref`."""
+
+    name = "fp8_ref"
+    quantized = True
+    warms = False  # its GEMMs read the dequantized fp16 copy
+
+    def pack(self, w, b) -> Linear:
+        from kernels.fp8 import quantize_fp8
+
+        wq, per_channel = quantize_fp8(w)
+        return Linear(qweight=wq, scales=per_channel, bias=b)
+
+    def linear(self, x, p: Linear):
+        if p.w is None:
+            from kernels.fp8 import dequantize_fp8
+
+            p.w = dequantize_fp8(p.qweight, p.scales)
+        return F.linear(x, p.w, p.bias)
+
+
 class OursBackend(_Int4, Backend):
     """This build's kernels: W4A16 GEMV/GEMM, fused RMSNorm+residual, fused SwiGLU
     (model.py:70-97).
@@ -275,6 +298,7 @@ BACKENDS = {
     "ours": OursBackend,
     "ours_cuda": lambda: OursBackend("decode"),
     "ours_fp8": OursFP8Backend,
+    "fp8_ref": FP8RefBackend,
 }
 
 

@@ -9,11 +9,14 @@ kernels/e2e/run.py measures on its GPUs):
   one decode step, as one graph (`layers_only_ms`, the reference's run.py:166-201);
 - prefill tokens/s: the whole 128-token prompt's forward as one graph, median of 5 replays
   (`prefill_speed`, the reference's run.py:142-162);
-- the layer weight bytes each backend reads per token.
+- the layer weight bytes each backend reads per token;
+- a teacher-forced check of the timed generation (`decode_check`): one forward of the generated
+  sequence through a reference runner (`CHECK_REFERENCE`) whose argmax at every position should
+  be the emitted token.
 Every backend runs the same lm_head (`--head gemv|torch`, kernels/e2e/model.py's QwenRunner).
 
     python -m kernels.e2e.run [--backends fp16,ours] [--steps 256] [--prompt 128] [--head gemv]
-                              [--json out]
+                              [--json out] [--no-check]
 """
 
 from __future__ import annotations
@@ -117,6 +120,41 @@ def prefill_speed(runner, ids: torch.Tensor, repeats: int = 5) -> dict:
     return {"T": T, "ms": ms, "tok_s": T / (ms * 1e-3)}
 
 
+# The backend whose teacher-forced logits check each backend's timed generation: the same
+# quantized weights through dequantize + library GEMMs (the reference's w4_ref role), and for
+# fp16 the fp16 runner's own prompt path (library GEMMs and head, prompt attention) against its
+# decode path (the one-row kernels).
+CHECK_REFERENCE = {"fp16": "fp16", "w4_ref": "w4_ref", "ours": "w4_ref", "ours_cuda": "w4_ref",
+                   "ours_fp8": "fp8_ref", "fp8_ref": "fp8_ref"}
+
+
+def check_reference(name: str) -> str:
+    """CHECK_REFERENCE for a backend name, `_lm` kept (the reference then quantizes its head too)."""
+    base, lm = (name[:-3], "_lm") if name.endswith("_lm") else (name, "")
+    return CHECK_REFERENCE[base] + lm
+
+
+def decode_check(runner: QwenRunner, ids: torch.Tensor, tokens: list[int], tol: float = 5e-2) -> dict:
+    """Teacher-forced check of a greedy generation: `tokens` are the steps + 1 tokens a decoder
+    emitted after the prompt `ids` (the first predicted from the prompt's last position). One
+    forward of `runner` over prompt + tokens[:-1] gives the logits at every position the decoder
+    predicted from; its argmax should be the emitted token. Where it is not, `margin` is how far
+    the emitted token's logit is below the argmax's (a near tie, flipped by the decode path's
+    different summation order, has a margin within `tol`, the bound the runner tests hold the
+    logits to, test_runner.py:48-85). Returns positions, agreements, the largest margin and how
+    many margins exceed `tol`."""
+    P = ids.shape[1]
+    emitted = torch.tensor(tokens, dtype=torch.long, device=ids.device)
+    seq = torch.cat([ids, emitted[None, :-1]], dim=1)
+    with torch.no_grad():
+        logits = runner.forward(seq, torch.arange(seq.shape[1], device=ids.device), all_logits=True)
+    lg = logits[0, P - 1:].float()
+    top = lg.argmax(-1)
+    margin = lg.gather(1, top[:, None]) - lg.gather(1, emitted[:, None])
+    return {"positions": len(tokens), "agree": int((top == emitted).sum()),
+            "max_margin": float(margin.max()), "beyond_tol": int((margin > tol).sum()), "tol": tol}
+
+
 def layers_only_ms(runner, M: int = 1, samples: int = 7, replays: int = 10) -> float:
     """Graph time of the swapped ops alone for one decode step (the reference's run.py:166-201):
     per layer the qkv, o, gate_up and down projections, two add+norms and the activation,
@@ -154,6 +192,7 @@ def run(params: dict) -> dict:
     prompt_len = int(params.get("prompt_len", 128))
     seed = int(params.get("seed", 4))
     head = params.get("head", "gemv")
+    check = bool(params.get("check", True))
     t0 = time.time()
     hf = random_qwen2(seed=seed)
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -177,6 +216,17 @@ def run(params: dict) -> dict:
         del runner
         gc.collect()
         torch.cuda.empty_cache()
+        if check:
+            ref_name = check_reference(name)
+            ref = QwenRunner(hf, make_backend(ref_name), max_len=max_len, head=head)
+            r["check"] = {"reference": ref_name, **decode_check(ref, ids, r["decode"]["tokens"])}
+            c = r["check"]
+            print(f"[e2e] {name} against {ref_name}, teacher-forced: {c['agree']}/{c['positions']} "
+                  f"tokens agree, largest margin {c['max_margin']:.4f}, {c['beyond_tol']} beyond "
+                  f"{c['tol']} ({time.time() - t0:.0f}s)", file=sys.stderr, flush=True)
+            del ref
+            gc.collect()
+            torch.cuda.empty_cache()
     if "fp16" in result["backends"]:
         base = result["backends"]["fp16"]
         for name, r in result["backends"].items():
@@ -198,9 +248,11 @@ def main(argv=None) -> int:
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--head", default="gemv", choices=QwenRunner.HEADS)
     ap.add_argument("--json", default=None)
+    ap.add_argument("--no-check", action="store_true",
+                    help="skip the teacher-forced check of each timed generation")
     args = ap.parse_args(argv)
     res = run({"backends": args.backends.split(","), "decode_steps": args.steps,
-               "prompt_len": args.prompt, "head": args.head})
+               "prompt_len": args.prompt, "head": args.head, "check": not args.no_check})
     text = json.dumps(res, indent=1)
     if args.json:
         with open(args.json, "w") as f:

@@ -51,6 +51,39 @@ def test_runner_incremental_decode_matches_full():
         torch.testing.assert_close(step[0, -1], full[0, t], atol=1e-4, rtol=1e-4)
 
 
+def test_decode_check_counts_agreement_and_margins():
+    """decode_check (the teacher-forced check of bench's timed generations) on the CPU fp32
+    runner: tokens of incremental greedy decoding agree at every position; a last token replaced
+    by the least likely one is one disagreement, with the logit gap as its margin."""
+    from kernels.e2e.run import decode_check
+
+    model = _tiny_model(torch.float32, "cpu")
+    runner = QwenRunner(model, make_backend("fp16"), max_len=64)
+    ids = torch.randint(0, 512, (1, 8), generator=torch.Generator().manual_seed(2))
+    logits = runner.forward(ids, torch.arange(8))
+    toks = [int(logits[0, -1].argmax())]
+    for t in range(8, 18):
+        logits = runner.forward(torch.tensor([[toks[-1]]]), torch.tensor([t]))
+        toks.append(int(logits[0, -1].argmax()))
+    checker = QwenRunner(model, make_backend("fp16"), max_len=64)
+    res = decode_check(checker, ids, toks)
+    assert res["positions"] == 11 and res["agree"] == 11
+    assert res["beyond_tol"] == 0 and res["max_margin"] == 0.0
+    last = logits[0, -1]
+    worst = int(last.argmin())
+    bad = decode_check(checker, ids, toks[:-1] + [worst], tol=0.0)
+    assert bad["agree"] == 10 and bad["beyond_tol"] == 1
+    assert abs(bad["max_margin"] - float(last.max() - last.min())) < 1e-4
+
+
+def test_check_reference_names():
+    from kernels.e2e.run import check_reference
+
+    assert check_reference("ours") == "w4_ref" and check_reference("ours_lm") == "w4_ref_lm"
+    assert check_reference("ours_fp8") == "fp8_ref" and check_reference("fp16") == "fp16"
+    assert make_backend("fp8_ref_lm").quant_lm_head
+
+
 def test_lm_suffix_needs_quantized_backend():
     with pytest.raises(ValueError):
         make_backend("fp16_lm")
@@ -226,13 +259,42 @@ def test_fused_attention_graph_decoder_matches_eager_steps():
 
 
 def test_make_backend_names():
-    for name in ("fp16", "w4_ref", "ours", "ours_cuda", "ours_fp8"):
+    for name in ("fp16", "w4_ref", "ours", "ours_cuda", "ours_fp8", "fp8_ref"):
         assert make_backend(name).name == name and not make_backend(name).quant_lm_head
-    for name in ("w4_ref_lm", "ours_lm", "ours_cuda_lm", "ours_fp8_lm"):
+    for name in ("w4_ref_lm", "ours_lm", "ours_cuda_lm", "ours_fp8_lm", "fp8_ref_lm"):
         be = make_backend(name)
         assert be.name == name and be.quant_lm_head and be.quantized
     with pytest.raises(KeyError):
         make_backend("ours_triton")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", ["ours", "ours_lm", "ours_fp8", "fp16"])
+def test_graph_generation_passes_decode_check(backend):
+    """A GraphDecoder generation (what bench times) checked teacher-forced against the reference
+    runner bench uses for it (dequantize + library GEMMs on the same weights; fp16: its own prompt
+    path): no emitted token's logit is more than 5e-2 below the reference's argmax."""
+    from kernels.e2e.run import GraphDecoder, check_reference, decode_check
+
+    model = _tiny_model(torch.float16, "cuda")
+    ids = torch.randint(0, 512, (1, 9), device="cuda", generator=torch.Generator("cuda").manual_seed(4))
+    runner = QwenRunner(model, make_backend(backend), max_len=64)
+    dec = GraphDecoder(runner)
+    dec.capture(ids)
+    toks, _ = dec.generate(ids, 24)
+    ref = QwenRunner(model, make_backend(check_reference(backend)), max_len=64)
+    res = decode_check(ref, ids, toks)
+    assert res["positions"] == 25 and res["beyond_tol"] == 0, res
+
+
+@pytest.mark.gpu
+def test_fp8_ref_matches_ours_fp8():
+    model = _tiny_model(torch.float16, "cuda")
+    ids = torch.randint(0, 512, (1, 5), device="cuda")
+    pos = torch.arange(5, device="cuda")
+    ref = QwenRunner(model, make_backend("fp8_ref"), max_len=32).forward(ids, pos, all_logits=True)
+    f8 = QwenRunner(model, make_backend("ours_fp8"), max_len=32).forward(ids, pos, all_logits=True)
+    torch.testing.assert_close(f8.float(), ref.float(), atol=5e-2, rtol=5e-2)
 
 
 @pytest.mark.gpu
