@@ -510,7 +510,8 @@ constexpr int kW8MfmaWavesWide = 16;
 // 10.6 us at M = 4 / 8 / 16). Narrower decode shapes take 64-column tiles and pieces of 16 K
 // steps (2 per wave), halved down to 4 while the grid has fewer than 128 workgroups. On MI355X
 // (graph-timed, M = 4 / 8 / 16), against 128-column tiles in six pieces: down 1536x8960 (18
-// pieces of 16 steps, 432 workgroups) 9.41 / 10.61 / 12.55 -> 7.37 / 7.55 / 9.07 us; q/o
+// pieces of 16 steps, 432 workgroups; 10 pieces of 28 since, below) 9.41 / 10.61 / 12.55 ->
+// 7.37 / 7.55 / 9.07 us; q/o
 // 1536x1536 (6 pieces of 8, 144 workgroups) 5.02 / 6.03 / 7.80 -> 4.62 / 4.71 / 5.74 (3 pieces:
 // 5.04 / 5.17 / 6.26); k/v 256x1536 (12 pieces of 4) 4.44 / 5.44 / 7.11 -> 3.87 / 3.92 / 4.89.
 // Half the columns halve each workgroup's 16-row LDS reduction and its share of the epilogue's
@@ -541,6 +542,12 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
     int64_t piece = 16;
     while (piece > 4 && tiles * ((steps + piece - 1) / piece) < 128) piece /= 2;
     splits = std::max<int64_t>(one_pass, (steps + piece - 1) / piece);
+    // at most one workgroup per CU: a CU that runs two pieces finishes last, so a grid just past
+    // 256 loses a whole piece's time and one well past it loses to fewer, larger pieces. down
+    // 1536x8960 (24 tiles), graph-timed, M = 4 / 8 / 9 / 12 / 16: 18 splits (432 workgroups)
+    // 7.35 / 7.37 / 7.38 / 7.59 / 8.22 us, 11 (264) 8.60 / 9.05 / 9.43 / 9.84 / 10.41, 10 (240)
+    // 7.13 / 7.30 / 7.27 / 7.47 / 7.72
+    if (tiles * splits > 256 && tiles <= 256) splits = std::max<int64_t>(one_pass, 256 / tiles);
   }
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, kW8MaxSplits));
   const int64_t sps = (steps + splits - 1) / splits;  // K steps per split
