@@ -1096,18 +1096,19 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 // Measured on MI355X (graph replays, rotating sets), wide-tile kernel against this one: gate_up
 // M = 4 / 8 / 16 7.50 / 8.07 / 9.37 -> 5.91 / 6.68 / 7.48 us, q/o 4.26 / 4.40 / 5.12 -> 3.48 /
 // 3.69 / 3.99, k/v (8 tiles) 4.12 / 4.29 / 5.00 -> 3.33 / 3.49 / 3.85.
-template <int MP, int NW, int GPW, int CPL>
+template <int MP, int NW, int GPW, int CPL, bool X5>
 __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "row tile");
   static_assert(CPL == 2 || CPL == 4, "two or four columns per lane");
+  static_assert(!X5 || CPL == 4, "the fifth 16-column tile follows four columns per lane");
   constexpr int NG = NW * GPW, WUNITS = GPW * MP * 16, WUPT = WUNITS / 64;
-  constexpr int CWT = 16 * CPL;  // columns of the tile
+  constexpr int CWT = 16 * CPL + (X5 ? 16 : 0);  // columns of the tile
   static_assert(WUNITS % 64 == 0, "whole staging units per lane");
-  static_assert(NW * MP * CWT * 4 <= NG * 16 * MP * 16, "the partial tiles fit over the records");
+  constexpr int NREC = NG * 16 * MP, NRED = (NW * MP * CWT + 3) / 4;  // records, partial tiles (u32x4)
   typedef _Float16 half8v __attribute__((ext_vector_type(8)));
   typedef uint32_t wrow_t __attribute__((ext_vector_type(CPL)));      // CPL packed words of a row
   typedef uint32_t sz_t __attribute__((ext_vector_type(CPL / 2)));    // CPL fp16 scales or zeros
-  __shared__ __align__(16) u32x4 xs[NG * 16 * MP];  // A records; the waves' partial tiles at the end
+  __shared__ __align__(16) u32x4 xs[NREC > NRED ? NREC : NRED];  // A records; the waves' partial tiles at the end
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c16 = lane & 15, kb = lane >> 4;
   ldk::pin_sgpr(a.x);
@@ -1115,6 +1116,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   const int ng = (a.K >> 3) >> 4;  // groups of 16 packed rows, <= NG
   const int n0 = blockIdx.x * CWT;
   const int col = min(n0 + CPL * c16, a.N - CPL);  // clamped: tail lanes load valid memory, store nothing
+  const int col5 = min(n0 + 16 * CPL + c16, a.N - 1);  // X5: the fifth tile's column of the lane
   const int M = a.M;
   // ---- this wave's x rows first (unit u = lane + 64 i: packed row rr of group wave * GPW + u / (16 MP),
   //      row m)
@@ -1129,15 +1131,23 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   //      col + CPL - 1
   wrow_t w[GPW][4];
   sz_t sv[GPW], zv[GPW];
+  uint32_t w5[X5 ? GPW : 1][4];  // X5: one word of the fifth tile per K step
+  half_t s5[X5 ? GPW : 1], z5[X5 ? GPW : 1];
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
     const int g = min(wave * GPW + gi, ng - 1);  // clamped: surplus waves load valid memory, use nothing
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 4; ++ks) {
       w[gi][ks] = __builtin_nontemporal_load(
           reinterpret_cast<const wrow_t*>(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + col));
+      if constexpr (X5) w5[gi][ks] = __builtin_nontemporal_load(a.qw + (int64_t)(16 * g + 4 * ks + kb) * a.N + col5);
+    }
     sv[gi] = *reinterpret_cast<const sz_t*>(a.s + (int64_t)g * a.N + col);
     zv[gi] = *reinterpret_cast<const sz_t*>(a.z + (int64_t)g * a.N + col);
+    if constexpr (X5) {
+      s5[gi] = a.s[(int64_t)g * a.N + col5];
+      z5[gi] = a.z[(int64_t)g * a.N + col5];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
   // ---- A records
@@ -1159,14 +1169,14 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   // ---- MFMA over the wave's groups: tile t holds columns n0 + CPL c16 + t
   const uint32_t magic = ldk::vgpr_const<kMagic>();
   const uint32_t mlo = ldk::sgpr_const<0x000F000Fu>(), mhi = ldk::sgpr_const<0x00F000F0u>();
-  float4_t acc[CPL];
+  float4_t acc[CPL], acc5 = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int t = 0; t < CPL; ++t) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int gi = 0; gi < GPW; ++gi) {
     const int g = wave * GPW + gi;
     if (g >= ng) break;  // uniform
-    float4_t tmp[CPL];
+    float4_t tmp[CPL], tmp5 = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < CPL; ++t) tmp[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float4_t sacc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};  // E (c16 < 8) or O (c16 >= 8) per row
@@ -1183,6 +1193,11 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
         const u32x4 b{(wc & mlo) | magic, (wc & mhi) | magic, (v & mlo) | magic, (v & mhi) | magic};
         tmp[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), tmp[t], 0, 0, 0);
       }
+      if constexpr (X5) {
+        const uint32_t wc = w5[gi][ks], v = wc >> 8;
+        const u32x4 b{(wc & mlo) | magic, (wc & mhi) | magic, (v & mlo) | magic, (v & mhi) | magic};
+        tmp5 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(half8v, b), tmp5, 0, 0, 0);
+      }
     }
     typedef _Float16 halfc_t __attribute__((ext_vector_type(CPL)));
     const halfc_t s2 = __builtin_bit_cast(halfc_t, sv[gi]), z2 = __builtin_bit_cast(halfc_t, zv[gi]);
@@ -1194,6 +1209,8 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
 #pragma unroll
       for (int t = 0; t < CPL; ++t)
         acc[t][i] = __builtin_fmaf((float)s2[t], tmp[t][i] - __builtin_fmaf((float)z2[t], sx, c), acc[t][i]);
+      if constexpr (X5)
+        acc5[i] = __builtin_fmaf((float)s5[gi], tmp5[i] - __builtin_fmaf((float)z5[gi], sx, c), acc5[i]);
     }
   }
   // ---- the NW partial tiles meet in LDS (over the records, once every wave is done with them)
@@ -1201,14 +1218,16 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   float* red = reinterpret_cast<float*>(xs);  // [NW][MP][CWT]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (4 * kb + i < M)
+    if (4 * kb + i < M) {
 #pragma unroll
       for (int t = 0; t < CPL; ++t) red[(wave * MP + 4 * kb + i) * CWT + CPL * c16 + t] = acc[t][i];
+      if constexpr (X5) red[(wave * MP + 4 * kb + i) * CWT + 16 * CPL + c16] = acc5[i];
+    }
   }
   ldk::lds_barrier();
   const int n = M * CWT;  // outputs o = row * CWT + column of the tile
   auto store = [&](int o, float v) {
-    const int nn = n0 + (o & (CWT - 1));
+    const int nn = n0 + o % CWT;
     if (nn < a.N) {
       if (a.bias) v += (float)a.bias[nn];
       a.out[(int64_t)(o / CWT) * a.ldo + nn] = (half_t)v;
@@ -1298,28 +1317,35 @@ bool mfma_x_applies(int64_t M, int64_t K, int gsh_rows, int block_n, int split_k
          !(flags & (LDK_EXACT | LDK_PATH_VALU | LDK_CPW_MASK));
 }
 
-template <int MP, int NW, int GPW, int CPL>
+template <int MP, int NW, int GPW, int CPL, bool X5>
 int launch_mfma_x_t(const W4Args& a, hipStream_t s) {
+  constexpr int CWT = 16 * CPL + (X5 ? 16 : 0);
   (void)hipGetLastError();
-  w4a16_mfma_x_kernel<MP, NW, GPW, CPL><<<(unsigned)((a.N + 16 * CPL - 1) / (16 * CPL)), NW * 64, 0, s>>>(a);
+  w4a16_mfma_x_kernel<MP, NW, GPW, CPL, X5><<<(unsigned)((a.N + CWT - 1) / CWT), NW * 64, 0, s>>>(a);
   return ldk::check_launch("w4a16_mfma_x");
 }
 
-template <int MP, int CPL>
+template <int MP, int CPL, bool X5 = false>
 int launch_mfma_x_mp(const W4Args& a, int nw, int gpw, hipStream_t s) {
-  if (nw == 12 && gpw == 1) return launch_mfma_x_t<MP, 12, 1, CPL>(a, s);
-  if (nw == 6 && gpw == 2) return launch_mfma_x_t<MP, 6, 2, CPL>(a, s);
-  if (nw == 6 && gpw == 1) return launch_mfma_x_t<MP, 6, 1, CPL>(a, s);
+  if (nw == 12 && gpw == 1) return launch_mfma_x_t<MP, 12, 1, CPL, X5>(a, s);
+  if (nw == 6 && gpw == 2) return launch_mfma_x_t<MP, 6, 2, CPL, X5>(a, s);
+  if (nw == 6 && gpw == 1) return launch_mfma_x_t<MP, 6, 1, CPL, X5>(a, s);
   return ldk::fail(LDK_ERR_UNSUPPORTED, "w4a16: x-staged MFMA kernel with %d waves of %d groups not instantiated", nw, gpw);
 }
 
 int launch_mfma_x(const W4Args& a, const Plan& p, hipStream_t s) {
-  // the kernel's LDS holds nw * cpw groups (all of K) and MP = mt rows; 64-column tiles (ln 16)
-  // take N a multiple of 4 (whole 16-byte loads of the clamped last lane)
+  // the kernel's LDS holds nw * cpw groups (all of K) and MP = mt rows; 64- and 80-column tiles
+  // (ln 16, 20) take N a multiple of 4 (whole 16-byte loads of the clamped last lane)
   if (a.gsh_rows != 4 || a.M > p.mt || ((a.K >> 3) >> 4) > p.nw * p.cpw || (a.N + 31) / 32 > INT32_MAX ||
-      (p.ln != 8 && p.ln != 16) || (p.ln == 16 && a.N % 4))
+      (p.ln != 8 && p.ln != 16 && p.ln != 20) || (p.ln != 8 && a.N % 4))
     return ldk::fail(LDK_ERR_INVALID, "w4a16: x-staged MFMA plan does not fit M=%d N=%d K=%d", a.M, a.N, a.K);
-  if (p.ln == 16) {
+  if (p.ln == 20) {
+    switch (p.mt) {
+      case 4: return launch_mfma_x_mp<4, 4, true>(a, p.nw, p.cpw, s);
+      case 8: return launch_mfma_x_mp<8, 4, true>(a, p.nw, p.cpw, s);
+      case 16: return launch_mfma_x_mp<16, 4, true>(a, p.nw, p.cpw, s);
+    }
+  } else if (p.ln == 16) {
     switch (p.mt) {
       case 4: return launch_mfma_x_mp<4, 4>(a, p.nw, p.cpw, s);
       case 8: return launch_mfma_x_mp<8, 4>(a, p.nw, p.cpw, s);
@@ -1376,6 +1402,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     // on the narrow shapes with their half as many workgroups, 32 columns stay faster: gate_up
     // M = 4 5.88 against 6.67 us, q/o M = 16 3.98 against 4.54)
     p.ln = (M > 4 && N % 64 == 0 && N / 64 >= 256) ? 16 : 8;
+    // a grid past 256 workgroups runs a second round on the CUs that take two tiles: where 64
+    // columns give more than 256 tiles and 80 give at most 256, 80-column tiles
+    if (M > 4 && N % 4 == 0 && (N + 63) / 64 > 256 && (N + 79) / 80 <= 256) p.ln = 20;
     p.rpl = 4;
     p.nw = ngx <= 6 ? 6 : (M <= 4 && N / 32 >= 256) ? 6 : 12;
     p.cpw = (ngx + p.nw - 1) / p.nw;
@@ -1761,7 +1790,8 @@ static int plan_kernel_name(const Plan& p, int gsh_rows, char* buf, size_t len) 
   if (p.kern == kM1) {
     n = snprintf(buf, len, "w4a16_m1_kernel<%d, %d, %d, 0, %d>", p.ln, p.nw, gsh_rows == 4 ? 4 : 0, p.mt);
   } else if (p.kern == kMfmaX) {
-    n = snprintf(buf, len, "w4a16_mfma_x_kernel<%d, %d, %d, %d>", p.mt, p.nw, p.cpw, p.ln / 4);
+    n = snprintf(buf, len, "w4a16_mfma_x_kernel<%d, %d, %d, %d, %s>", p.mt, p.nw, p.cpw, p.ln == 8 ? 2 : 4,
+                 p.ln == 20 ? "true" : "false");
   } else if (p.kern == kValu) {
     n = snprintf(buf, len, "w4a16_gemv_kernel<%d, %d, %d, %d>", p.mt, p.ln, p.rpl, p.cpw);
   } else {
@@ -1812,7 +1842,8 @@ static int plan_check(const char* fn, const Plan& p, int64_t M, int64_t N, int64
                          p.mt, 4 * p.ln, p.rpl, p.cpw);
       return LDK_OK;
     case kMfmaX:
-      if (gsh_rows != 4 || M > p.mt || ((K >> 3) >> 4) > p.nw * p.cpw || (p.ln != 8 && p.ln != 16))
+      if (gsh_rows != 4 || M > p.mt || ((K >> 3) >> 4) > p.nw * p.cpw || (p.ln != 8 && p.ln != 16 && p.ln != 20) ||
+          (p.ln != 8 && N % 4))
         return ldk::fail(LDK_ERR_INVALID, "%s: x-staged MFMA plan does not fit M=%lld N=%lld K=%lld", fn, (long long)M,
                          (long long)N, (long long)K);
       return LDK_OK;

@@ -206,7 +206,7 @@ def test_config_query():
     assert st == 0 and bn in (16, 32, 64) and sk >= 1
     assert fl & _lib.FACTORED and fl & _lib.PATH_VALU
     st, bn, sk, fl = _config(16, 17920, 1536)
-    assert st == 0 and fl & _lib.PATH_MFMA and bn == 64  # x staged in LDS, 64-column tiles
+    assert st == 0 and fl & _lib.PATH_MFMA and bn == 80  # x staged in LDS, 80-column tiles
     # two rows: the factored VALU kernel; from three rows the MFMA kernel, also on small shapes
     st, bn, sk, fl = _config(2, 17920, 1536)
     assert st == 0 and fl & _lib.FACTORED and fl & _lib.PATH_VALU and bn == 32
@@ -228,15 +228,18 @@ def test_decode_rows_plan_kernels():
     also takes two rows of down; one and two rows otherwise the factored VALU kernel; more than 16
     the MFMA blocks."""
     from kernels.w4a16 import kernel_name
-    assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 4>"  # 64-column tiles
-    assert kernel_name(8, 17920, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 4>"
-    assert kernel_name(5, 17920, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 4>"
-    assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2, 2>"
-    assert kernel_name(8, 1536, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 2>"
-    assert kernel_name(3, 4096, 512) == "w4a16_mfma_x_kernel<4, 6, 1, 2>"
-    assert kernel_name(16, 256, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2>"
-    assert kernel_name(16, 200, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2>"
-    assert kernel_name(16, 16400, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2>"  # N % 64 != 0
+    # 80-column tiles where 64 columns need more than 256 workgroups and 80 at most 256
+    assert kernel_name(16, 17920, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 4, true>"
+    assert kernel_name(8, 17920, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 4, true>"
+    assert kernel_name(5, 17920, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 4, true>"
+    assert kernel_name(16, 16400, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 4, true>"  # N % 64 != 0
+    assert kernel_name(16, 16384, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 4, false>"  # 256 x 64
+    assert kernel_name(16, 20484, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2, false>"  # past 256 x 80
+    assert kernel_name(4, 17920, 1536) == "w4a16_mfma_x_kernel<4, 6, 2, 2, false>"
+    assert kernel_name(8, 1536, 1536) == "w4a16_mfma_x_kernel<8, 12, 1, 2, false>"
+    assert kernel_name(3, 4096, 512) == "w4a16_mfma_x_kernel<4, 6, 1, 2, false>"
+    assert kernel_name(16, 256, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2, false>"
+    assert kernel_name(16, 200, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2, false>"
     assert kernel_name(16, 1536, 8960).startswith("w4a16_mfma_kernel<")
     assert kernel_name(8, 1536, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(16, 17920, 1536, 64).startswith("w4a16_mfma_kernel<")

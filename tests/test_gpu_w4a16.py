@@ -317,7 +317,7 @@ def test_mfma_x_64_column_tiles_one_hot(M):
     MFMA tiles): one-hot rows return columns of dequant(W) exactly over K = 1536, N = 16384."""
     from kernels.w4a16 import kernel_name
     N, K = 16384, 1536
-    assert kernel_name(M, N, K).endswith(", 4>")
+    assert kernel_name(M, N, K).endswith(", 4, false>")
     _, qw, s, z, _ = _make(1, N, K, 12)
     deq = dequantize_ref(qw, s, z, 128)
     qwd, sd, zd = dev(qw), dev(s), dev(z)
@@ -328,6 +328,37 @@ def test_mfma_x_64_column_tiles_one_hot(M):
         x[torch.arange(len(ks)), torch.as_tensor(ks)] = 1.0
         got = w4a16_matmul(x, qwd, sd, zd).cpu().numpy()
         assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, ks].T))), c
+
+
+@pytest.mark.parametrize("M", [16, 6])
+def test_mfma_x_80_column_tiles_one_hot(M):
+    """80-column tiles (64-column tiles would need more than 256 workgroups: gate_up's 17920
+    columns run 224): four words per lane and packed row feed four MFMA tiles and a fifth word
+    the fifth tile (column 64 + c16). One-hot rows return columns of dequant(W) exactly."""
+    from kernels.w4a16 import config_for, kernel_name
+    N, K = 17920, 1536
+    assert kernel_name(M, N, K).endswith(", 4, true>") and "block_n=80" in config_for(M, N, K)
+    _, qw, s, z, _ = _make(1, N, K, 13)
+    deq = dequantize_ref(qw, s, z, 128)
+    qwd, sd, zd = dev(qw), dev(s), dev(z)
+    order = np.random.default_rng(5).permutation(K)
+    for c in range(0, K, 4 * M):  # a quarter of K's positions, all twelve groups
+        ks = order[c:c + M]
+        x = torch.zeros(len(ks), K, dtype=torch.float16, device="cuda")
+        x[torch.arange(len(ks)), torch.as_tensor(ks)] = 1.0
+        got = w4a16_matmul(x, qwd, sd, zd).cpu().numpy()
+        assert np.array_equal(bits16(got), bits16(np.ascontiguousarray(deq[:, ks].T))), c
+
+
+@pytest.mark.parametrize("M", [5, 9, 16])
+@pytest.mark.parametrize("N", [16900, 16960, 20480])
+def test_mfma_x_80_column_tiles_tails(M, N):
+    """80-column tiles with a partial last tile (16900: 20 columns, so the fifth tile's lanes and
+    three quarters of the four-column lanes clamp; 16960: 16 columns) and the widest grid they
+    take (20480: 256 tiles), with bias."""
+    from kernels.w4a16 import kernel_name
+    assert kernel_name(M, N, 1536).endswith(", 4, true>")
+    _run(M, N, 1536, bias=True)
 
 
 # ---------------------------------------------------------------- config 0 and config 2
