@@ -1114,7 +1114,15 @@ __global__ __launch_bounds__(NW * 64) void w4a16_mfma_x_kernel(W4Args a) {
   ldk::pin_sgpr(a.x);
   ldk::pin_sgpr(a.qw);
   const int ng = (a.K >> 3) >> 4;  // groups of 16 packed rows, <= NG
-  const int n0 = blockIdx.x * CWT;
+  // X5: an 80-column tile is 2.5 lines of each packed row, so tiles 2q and 2q + 1 share a line.
+  // They run as workgroups L and L + 8 of a group of 16, which the dispatcher places on the same
+  // XCD (workgroup L goes to XCD L % 8) at about the same time: the shared line comes into that
+  // XCD's L2 once. Workgroups past the last whole group of 16 take their tiles in plain order.
+  int tile = blockIdx.x;
+  if constexpr (X5) {
+    if (tile < (int)(gridDim.x & ~15u)) tile = (tile & ~15) + 2 * (tile & 7) + ((tile >> 3) & 1);
+  }
+  const int n0 = tile * CWT;
   const int col = min(n0 + CPL * c16, a.N - CPL);  // clamped: tail lanes load valid memory, store nothing
   const int col5 = min(n0 + 16 * CPL + c16, a.N - 1);  // X5: the fifth tile's column of the lane
   const int M = a.M;
