@@ -1092,7 +1092,9 @@ __global__ __launch_bounds__(NH == 1 && MT == 1 ? 1024 : 512) void w4a16_mfma_ke
 // weights and no all-ones MFMA for sum(x). A lane loads CPL = 2 words (two columns) per packed
 // row, the M = 1 kernel's 128-byte tile, or 4 (64-column tiles, two lines per packed row, for the
 // wide shapes at 5-16 rows, where the x rows every workgroup stages cost more than the weights);
-// the waves' partial tiles meet in LDS at the end.
+// X5 adds a fifth 16-column tile to the four-word lanes (one more word per packed row, column
+// 64 + c16: 80-column tiles, for shapes whose 64-column tiles would need more than 256
+// workgroups); the waves' partial tiles meet in LDS at the end.
 // Measured on MI355X (graph replays, rotating sets), wide-tile kernel against this one: gate_up
 // M = 4 / 8 / 16 7.50 / 8.07 / 9.37 -> 5.91 / 6.68 / 7.48 us, q/o 4.26 / 4.40 / 5.12 -> 3.48 /
 // 3.69 / 3.99, k/v (8 tiles) 4.12 / 4.29 / 5.00 -> 3.33 / 3.49 / 3.85.
