@@ -1428,11 +1428,14 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   p.mtile = mfma && M > 16 ? 2 : 1;
   if (mfma) {  // 128 columns on shapes wide enough to fill the CUs with them, else 64 (and 64 for
               // 32-row blocks of group-256 weights, whose 128-column variant runs out of registers);
-              // decode rows on shapes of <= 2 MB take 32 columns (q/o/k/v at M = 8: 4.7 -> 4.4 us)
+              // decode rows on shapes of <= 2 MB take 32 columns (q/o/k/v at M = 8: 4.7 -> 4.4 us),
+              // and so do 13-16 rows of the narrow long shapes (down), where half the K splits
+              // halve the split-K words (below)
     p.ln = block_n == 32    ? 8
            : block_n == 64  ? 16
            : block_n == 128 ? 32
            : (M <= 16 && wbytes <= (2 << 20)) ? 8
+           : (M > 12 && M <= 16 && N < 128 * 128 && split_k <= 0) ? 8
            : (N >= 128 * 128 && !(M > 16 && rpg > 16) ? 32 : 16);
   } else if (block_n) {
     p.ln = block_n / 4;
@@ -1525,7 +1528,11 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   }
   if (mfma) {  // groups per wave and pass: all in one pass where registers allow (<= 16 waves at
               // 64 columns, <= 8 at 128)
-    const int wmax = p.ln == 16 && p.mtile == 1 ? 16 : 8;
+    // up to 16 waves on 64-column tiles, and on 32-column tiles from 9 rows: down M = 16 on 32
+    // columns in 5 splits (14 waves of one group) 6.41-6.42 us against 6.60 on 8 waves of two and
+    // 6.70-6.71 for 64 columns in 10 splits; at 12 rows and fewer the 64-column plan stays
+    // (M = 12 / 9 / 8 / 4: 5.94 / 5.67 / 5.56 / 5.33 against 5.84 / 5.61 / 5.50 / 5.06 us)
+    const int wmax = (p.ln == 16 || (p.ln == 8 && M > 8)) && p.mtile == 1 ? 16 : 8;
     if (!cpw_from_flags(flags)) cpw = chunks > wmax ? 2 : 1;
     cpw = std::min(cpw, rpg <= 16 && p.mtile == 1 ? 2 : 1);
     p.cpw = cpw;

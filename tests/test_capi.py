@@ -241,6 +241,10 @@ def test_decode_rows_plan_kernels():
     assert kernel_name(16, 256, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2, false>"
     assert kernel_name(16, 200, 1536) == "w4a16_mfma_x_kernel<16, 12, 1, 2, false>"
     assert kernel_name(16, 1536, 8960).startswith("w4a16_mfma_kernel<")
+    # down: 64 columns in 10 K splits up to 12 rows, 32 columns in 5 from 13 (half the words)
+    from kernels.w4a16 import config_for
+    assert config_for(12, 1536, 8960) == "mfma,block_n=64,split_k=10,factored"
+    assert config_for(13, 1536, 8960) == config_for(16, 1536, 8960) == "mfma,block_n=32,split_k=5,factored"
     assert kernel_name(8, 1536, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(16, 17920, 1536, 64).startswith("w4a16_mfma_kernel<")
     assert kernel_name(2, 17920, 1536).startswith("w4a16_m1_kernel<")
