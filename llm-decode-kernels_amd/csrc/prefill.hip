@@ -451,8 +451,8 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(float* partial, int sp
 //    that still gives most CUs one and, with two K groups, leaves LDS for two per CU (qkv M = 2048
 //    on 4 x 64 columns and two K groups: int4 20 us, against 29 us on one K group and 28 us for
 //    dequantize + hipBLASLt); where that leaves one column group, 32-row tiles on two.
-//  * Two K groups when a short-K shape leaves fewer than two waves per SIMD; long K splits over
-//    workgroups instead (the partials of few rows are cheap).
+//  * Two K groups when a short-K shape leaves fewer than two waves per SIMD (e4m3: one); long K
+//    splits over workgroups instead (the partials of few rows are cheap).
 struct GemmShape {
   int waves, mt, kg, splits;
   int mfast;  // grid x walks the row tiles (see gemm_body)
@@ -514,7 +514,10 @@ GemmShape pick_shape(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int s
   if (tiles(4, 8) >= 384) return {4, 8, 1, 1, 0};
   for (int w : {4, 2, 1}) {
     const int64_t t = tiles(w, 4);
-    const int kg = split_k <= 0 && t * w < 2048 && steps >= 16 ? 2 : 1;
+    // e4m3 takes two K groups only below half as many waves: its 4-wave two-group tiles do not
+    // fit the LDS, and the 2-wave ones lost to one group from 256 rows (gate_up M = 256 / 384:
+    // 28.7 / 34.9 us on 2 x 64 columns in two groups, 24.9 / 28.3 on 4 x 64 in one)
+    const int kg = split_k <= 0 && t * w < (f == WFmt::kE4M3 ? 1025 : 2048) && steps >= 16 ? 2 : 1;
     if (w > 1 && !(t >= 192 && lds_of(f, w, 4, kg) <= 80 * 1024)) continue;
     // one column group of 64-row tiles: 32-row tiles on two column groups when they still give
     // most CUs a workgroup (qkv M = 512: 10.5 against 12.7 us int4, 10.4 against 12.1 us e4m3)

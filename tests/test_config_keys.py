@@ -82,3 +82,11 @@ def test_fp8_column_tails_plan():
         fp8.config_for(1, 42, 96)
     with pytest.raises(RuntimeError):
         fp8.config_for(5, 44, 96, {"MFMA": True, "block_n": 128})
+
+
+def test_fp8_prefill_tiles_of_the_wide_shapes():
+    """The e4m3 prefill GEMM's tile on gate_up (17920 x 1536): 4 x 64 columns in one K group from
+    256 rows (its 4-wave two-group tiles do not fit the LDS), 2 x 64 columns below."""
+    assert fp8.config_for(128, 17920, 1536) == "gemm,block_n=128,split_k=1"
+    for M in (256, 384, 512, 2048):
+        assert fp8.config_for(M, 17920, 1536) == "gemm,block_n=256,split_k=1"
