@@ -519,6 +519,11 @@ GemmShape pick_shape(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int s
     // 28.7 / 34.9 us on 2 x 64 columns in two groups, 24.9 / 28.3 on 4 x 64 in one)
     const int kg = split_k <= 0 && t * w < (f == WFmt::kE4M3 ? 1025 : 2048) && steps >= 16 ? 2 : 1;
     if (w > 1 && !(t >= 192 && lds_of(f, w, 4, kg) <= 80 * 1024)) continue;
+    // 4-wave two-group tiles (two workgroups per CU) on 257-383 tiles leave some CUs a second
+    // workgroup after the others are done; 2-wave tiles spread twice the workgroups evenly
+    // (int4 gate_up M = 256 / 320: 30.1 / 31.0 -> 26.5 / 27.9 us; M = 192 (210 tiles) and
+    // 384 (420) keep the 4-wave tiles: 19.2 against 20.7, 32.7 against 35.2)
+    if (w == 4 && kg == 2 && t > 256 && t < 384) continue;
     // one column group of 64-row tiles: 32-row tiles on two column groups when they still give
     // most CUs a workgroup (qkv M = 512: 10.5 against 12.7 us int4, 10.4 against 12.1 us e4m3)
     if (w == 1 && kg == 2 && tiles(2, 2) >= 192) return {2, 2, 2, 1, 0};

@@ -90,3 +90,11 @@ def test_fp8_prefill_tiles_of_the_wide_shapes():
     assert fp8.config_for(128, 17920, 1536) == "gemm,block_n=128,split_k=1"
     for M in (256, 384, 512, 2048):
         assert fp8.config_for(M, 17920, 1536) == "gemm,block_n=256,split_k=1"
+
+
+def test_w4a16_prefill_tiles_of_the_wide_shapes():
+    """The int4 prefill GEMM's tile on gate_up: 4 x 64 columns in two K groups unless that gives
+    257-383 tiles (256 and 320 rows), where 2 x 64 columns spread twice the workgroups evenly."""
+    cfg = {"prefill": "gemm"}
+    for M, bn in ((128, 128), (192, 256), (256, 128), (320, 128), (384, 256), (512, 256)):
+        assert w4a16.config_for(M, 17920, 1536, 128, cfg) == f"gemm,block_n={bn},split_k=1", M
