@@ -739,12 +739,15 @@ static bool w8_gemm_applies(int64_t M, int64_t N, int64_t K, int64_t ldx, const 
   return ldk::gemm_supported(ldk::WFmt::kE4M3, M, N, K, 0, ldx) && ldk::aligned(out, 8) && ldo % 4 == 0;
 }
 
-// The library's choice: the GEMM for more than kW8GemmRows rows unless a tuning argument names
-// another kernel.
+// The library's choice: the GEMM for more than kW8GemmRows rows (on wide shapes more than 16)
+// unless a tuning argument names another kernel.
 static bool w8_uses_gemm(int64_t M, int64_t N, int64_t K, int64_t ldx, const void* out, int64_t ldo, int block_n,
                          int split_k, int flags) {
   if (flags & LDK_PATH_GEMM) return true;
-  if (M <= kW8GemmRows || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA))) return false;
+  // wide shapes (N >= 8192) from 17 rows: the 16-row blocks re-read all of their e4m3 weights per
+  // block (gate_up M = 17 / 32 / 64: 16.9 / 20.3 / 29.7 us on the blocks, 10.9 / 11.2 / 15.5 on the
+  // GEMM's 32-row tiles; qkv at M = 17-48 stays on the blocks: 8.1-9.5 against 9.9-10.4 us)
+  if (M <= (N >= 8192 ? 16 : kW8GemmRows) || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA))) return false;
   return w8_gemm_applies(M, N, K, ldx, out, ldo);
 }
 

@@ -524,9 +524,11 @@ GemmShape pick_shape(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int s
     // (int4 gate_up M = 256 / 320: 30.1 / 31.0 -> 26.5 / 27.9 us; M = 192 (210 tiles) and
     // 384 (420) keep the 4-wave tiles: 19.2 against 20.7, 32.7 against 35.2)
     if (w == 4 && kg == 2 && t > 256 && t < 384) continue;
-    // one column group of 64-row tiles: 32-row tiles on two column groups when they still give
-    // most CUs a workgroup (qkv M = 512: 10.5 against 12.7 us int4, 10.4 against 12.1 us e4m3)
-    if (w == 1 && kg == 2 && tiles(2, 2) >= 192) return {2, 2, 2, 1, 0};
+    // one column group of 64-row tiles: 32-row tiles on two column groups instead (qkv M = 512:
+    // 10.5 against 12.7 us int4, 10.4 against 12.1 us e4m3; e4m3 qkv / o at M = 65-256, 48-128
+    // tiles: 9.3-10.1 against 11.8-12.2 us; gate_up at M = 17-64 from the 32-row blocks: e4m3
+    // 16.9 / 20.3 / 29.7 -> 10.9 / 11.2 / 15.5 us at M = 17 / 32 / 64, int4 12.0 -> 10.5 at 32)
+    if (w == 1 && kg == 2) return {2, 2, 2, 1, 0};
     return {w, 4, kg, splits(t), 0};
   }
   return {1, 4, 1, 1, 0};  // not reached

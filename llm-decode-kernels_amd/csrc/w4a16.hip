@@ -1777,6 +1777,7 @@ extern "C" int64_t ldk_workspace_bytes(void) { return (int64_t)64 << 20; }
 
 // Rows from which the prefill GEMM (prefill.hip) may replace the MFMA kernel's 32-row blocks.
 static constexpr int64_t kGemmRows = 64;
+static constexpr int64_t kGemmWideRows = 32;  // from this many rows on shapes of N >= 8192
 
 static bool gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, bool forced) {
   return (forced || M > 16) && ldk::gemm_supported(ldk::WFmt::kInt4, M, N, K, group_size, ldx) && (!out || ldk::aligned(out, 8)) &&
@@ -1794,8 +1795,11 @@ static bool gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_
 static bool uses_gemm(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, int block_n,
                int split_k, int flags) {
   if (flags & LDK_PATH_GEMM) return true;
-  if (M <= kGemmRows || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA | LDK_EXACT | LDK_FACTORED)))
-    return false;
+  if (block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA | LDK_EXACT | LDK_FACTORED))) return false;
+  // wide shapes from 32 rows: the 32-row blocks re-read all the weights per block (gate_up M = 32 /
+  // 64: 12.0 / 22.6 us on the blocks, 10.5 / 15.3 on the GEMM's 32-row tiles; M = 17: 9.5 against
+  // 10.3)
+  if (M < (N >= 8192 ? kGemmWideRows : kGemmRows + 1)) return false;
   if (!(N >= 8192 || M >= 512)) return false;
   return gemm_applies(M, N, K, group_size, ldx, out, ldo, false);
 }

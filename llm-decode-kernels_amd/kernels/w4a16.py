@@ -16,10 +16,10 @@ libldk_amd.so whose tile and K-split come from the library's per-shape table:
 
 Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268) run hand-written
 kernels at every row count: the library picks, per shape, the prefill GEMM (csrc/prefill.hip:
-64/128-row tiles on the matrix cores, every weight dequantized exactly as dequantize_ref does it,
-fp32 accumulation, K split over workgroups for long K) or the MFMA kernel in 32-row blocks (the
-choice for 17-64 rows and for narrow shapes up to 512 rows, where the blocks' K split over waves
-wins). `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
+32/64/128-row tiles on the matrix cores, every weight dequantized exactly as dequantize_ref does
+it, fp32 accumulation, K split over workgroups for long K) or the MFMA kernel in 32-row blocks (the
+choice for 17-31 rows, for 17-64 rows of narrow shapes and for narrow shapes up to 512 rows, where
+the blocks' K split over waves wins; wide shapes, N >= 8192, take the GEMM from 32 rows). `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
 `GEMV` (force the VALU decode kernels, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`
