@@ -1789,8 +1789,9 @@ static bool gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_
 // the waves of a workgroup, which wins while the weights dominate and the tiles are few (qkv/o at
 // M <= 256: 8.0-8.5 us against 12.4 us; down at M = 256: 25.7 against 31.1 us); the GEMM reads
 // them once per 64/128-row tile and wins on wide shapes at every row count (gate_up M = 65: 18.4
-// against 22.2 us; M = 2048: 116 against 364 us) and on every shape from 512 rows (qkv M = 512:
-// 12.6 against 15.1 us; down M = 512: 34.8 against 47.5 us). A tuning argument that names another
+// against 22.2 us; M = 2048: 116 against 364 us) and on narrow shapes whose 32-row blocks would need more than 256
+// workgroups, or that have 512 rows or more (qkv M = 512: 12.6 against 15.1 us; down M = 512: 34.8
+// against 47.5 us). A tuning argument that names another
 // kernel keeps it.
 static bool uses_gemm(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, const void* out, int64_t ldo, int block_n,
                int split_k, int flags) {
@@ -1800,7 +1801,13 @@ static bool uses_gemm(int64_t M, int64_t N, int64_t K, int group_size, int64_t l
   // 64: 12.0 / 22.6 us on the blocks, 10.5 / 15.3 on the GEMM's 32-row tiles; M = 17: 9.5 against
   // 10.3)
   if (M < (N >= 8192 ? kGemmWideRows : kGemmRows + 1)) return false;
-  if (!(N >= 8192 || M >= 512)) return false;
+  // narrow shapes from 257 rows where the blocks need more than 256 workgroups, and from 512 rows:
+  // past 256 workgroups the blocks lose a round (qkv M = 288 / 384 on 9 / 12 x 32 blocks: 14.9 /
+  // 15.0 us against 10.3 on the GEMM; down M = 384 / 448: 47.7 / 47.4 against 28.8 / 29.7), below
+  // it they keep the lead (down M = 288 on 9 x 24 blocks: 25.8 against 33.0; M = 256: 25.6 against
+  // 28.4; qkv M = 256 on 8 x 32: 8.5 against 10.3)
+  const int64_t blocks = (N + 63) / 64 * ((M + 31) / 32);
+  if (!(N >= 8192 || M >= 512 || (M > 256 && blocks > 256))) return false;
   return gemm_applies(M, N, K, group_size, ldx, out, ldo, false);
 }
 

@@ -98,3 +98,21 @@ def test_w4a16_prefill_tiles_of_the_wide_shapes():
     cfg = {"prefill": "gemm"}
     for M, bn in ((128, 128), (192, 256), (256, 128), (320, 128), (384, 256), (512, 256)):
         assert w4a16.config_for(M, 17920, 1536, 128, cfg) == f"gemm,block_n={bn},split_k=1", M
+
+
+def test_w4a16_prefill_choice_of_the_narrow_shapes():
+    """int4 narrow shapes keep the 32-row blocks up to 256 rows, and up to 511 rows while the
+    blocks fit in 256 workgroups (64-column tiles x 32-row blocks); past that the prefill GEMM."""
+    cases = (
+        (256, 2048, 1536, "mfma"),   # qkv: 32 x 8 blocks
+        (288, 2048, 1536, "gemm"),   # qkv: 32 x 9
+        (288, 1536, 1536, "mfma"),   # o: 24 x 9
+        (320, 1536, 8960, "mfma"),   # down: 24 x 10
+        (352, 1536, 8960, "gemm"),   # down: 24 x 11
+        (512, 256, 1536, "gemm"),    # 4 x 16, but 512 rows
+        (64, 1536, 8960, "mfma"),
+        (32, 17920, 1536, "gemm"),   # wide from 32 rows
+        (31, 17920, 1536, "mfma"),
+    )
+    for M, N, K, path in cases:
+        assert w4a16.config_for(M, N, K).startswith(path + ","), (M, N, K, w4a16.config_for(M, N, K))
