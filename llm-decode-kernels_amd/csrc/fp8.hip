@@ -516,6 +516,19 @@ constexpr int kW8MfmaWavesWide = 16;
 // 5.04 / 5.17 / 6.26); k/v 256x1536 (12 pieces of 4) 4.44 / 5.44 / 7.11 -> 3.87 / 3.92 / 4.89.
 // Half the columns halve each workgroup's 16-row LDS reduction and its share of the epilogue's
 // outputs, which is where the 8- and 16-row cases spent their extra time.
+// Prefill rows (M > 16) in 16-row blocks. Short K (q/o/qkv) takes 64-column tiles and splits K
+// toward 256 workgroups; long K (down) keeps 128-column tiles and the split the decode rows take,
+// cut so that the grid stays within 256 workgroups: a CU that runs two finishes last (graph-timed,
+// qkv 2048x1536 M = 17 / 32 / 48 / 64: 128-column tiles in 4 splits, 64-512 workgroups, 7.9 / 8.4 /
+// 9.4 / 10.4 us -> 5.1 / 5.8 / 6.4 / 6.6 with 16 waves; down 1536x8960 M = 64: 6 splits on 288
+// workgroups 23.9 us, 5 on 240 18.5).
+bool w8_short_k(int64_t K) { return (K + 31) / 32 <= 64; }
+int64_t w8_prefill_splits(int64_t M, int64_t N, int64_t K, int ln, int64_t splits) {
+  const int64_t tiles = (N + 16 * ln - 1) / (16 * ln), steps = (K + 31) / 32;
+  const int64_t cap = std::max<int64_t>(1, 256 / (tiles * ((M + 15) / 16)));
+  return w8_short_k(K) && ln == 4 ? std::min<int64_t>(cap, steps) : std::min<int64_t>(splits, cap);
+}
+
 W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes) {
   W8Plan p{};
   p.mfma = true;
@@ -523,8 +536,8 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
   p.mblocks = 1;
   const bool narrow = (N + 127) / 128 < 128 && M <= 16;
   // 128-column tiles load 8 bytes of a row per lane: rows must be 8-byte aligned (N % 8 == 0);
-  // 64-column tiles load 4 (N % 4 == 0)
-  p.ln = block_n == 64 || (block_n == 0 && (narrow || N % 8)) ? 4 : 8;
+  // 64-column tiles load 4 (N % 4 == 0). Prefill rows of short K take 64 columns too.
+  p.ln = block_n == 64 || (block_n == 0 && (narrow || N % 8 || (M > 16 && w8_short_k(K)))) ? 4 : 8;
   p.nw = kW8MfmaWaves;
   const int64_t tiles = (N + 16 * p.ln - 1) / (16 * p.ln);
   const int64_t steps = (K + 31) / 32;
@@ -538,6 +551,7 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
     splits = std::max<int64_t>(one_pass, (steps + 15) / 16);
   } else if (tiles >= 128 || M > 16) {
     splits = std::max<int64_t>(one_pass, std::min<int64_t>(steps / 8, (64 + tiles - 1) / tiles));
+    if (M > 16 && block_n == 0) splits = w8_prefill_splits(M, N, K, p.ln, splits);
   } else {
     int64_t piece = 16;
     while (piece > 4 && tiles * ((steps + piece - 1) / piece) < 128) piece /= 2;
@@ -559,6 +573,9 @@ W8Plan make_w8_mfma_plan(int64_t M, int64_t N, int64_t K, int block_n, int split
     p.kps = (int)(steps * 32);
   }
   if (p.ln == 4 && M > 8 && M <= 16) p.nw = kW8MfmaWavesWide;
+  // prefill rows of short K in K splits: 16 waves (qkv M = 17 / 64: 5.9 / 7.7 -> 5.1 / 6.6 us);
+  // whole K stays on 8 (M = 128: 8.0 against 8.7 us with 16)
+  if (p.ln == 4 && M > 16 && p.splits > 1 && w8_short_k(K)) p.nw = kW8MfmaWavesWide;
   const int64_t per_wave = ((p.kps / 32) + p.nw - 1) / p.nw;
   // K steps per wave and pass: 16 waves hold at most 4 each in registers (1024 lanes: 128 VGPRs)
   p.ksw = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : (per_wave <= 4 || p.nw == kW8MfmaWavesWide) ? 4 : 6;
@@ -740,14 +757,23 @@ static bool w8_gemm_applies(int64_t M, int64_t N, int64_t K, int64_t ldx, const 
 }
 
 // The library's choice: the GEMM for more than kW8GemmRows rows (on wide shapes more than 16)
-// unless a tuning argument names another kernel.
+// unless the blocks still fit, or a tuning argument names another kernel.
 static bool w8_uses_gemm(int64_t M, int64_t N, int64_t K, int64_t ldx, const void* out, int64_t ldo, int block_n,
                          int split_k, int flags) {
   if (flags & LDK_PATH_GEMM) return true;
   // wide shapes (N >= 8192) from 17 rows: the 16-row blocks re-read all of their e4m3 weights per
   // block (gate_up M = 17 / 32 / 64: 16.9 / 20.3 / 29.7 us on the blocks, 10.9 / 11.2 / 15.5 on the
-  // GEMM's 32-row tiles; qkv at M = 17-48 stays on the blocks: 8.1-9.5 against 9.9-10.4 us)
+  // GEMM's 32-row tiles)
   if (M <= (N >= 8192 ? 16 : kW8GemmRows) || block_n || split_k || (flags & (LDK_PATH_VALU | LDK_PATH_MFMA))) return false;
+  // narrow shapes past 64 rows keep the blocks while they fit in 256 workgroups: short K on
+  // 64-column tiles (qkv M = 96 / 128: 8.1 / 8.0 us against 10.2 / 10.1 on the GEMM, o M = 160 8.3
+  // against 9.7; qkv M = 160, 320 workgroups, 13.4 against 10.2), long K while they still split K
+  // at least twice (down M = 96 / 128 / 160: 19.8 / 23.4 / 23.6 against 26.0 / 26.5 / 24.2; M = 192
+  // in whole K 41.0 against 24.6)
+  if (N < 8192) {
+    const int64_t blocks = (M + 15) / 16;
+    if (w8_short_k(K) ? (N + 63) / 64 * blocks <= 256 : (N + 127) / 128 * blocks <= 128) return false;
+  }
   return w8_gemm_applies(M, N, K, ldx, out, ldo);
 }
 

@@ -870,9 +870,10 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(W4Args a, SplitArgs sp
 
 // ------------------------------------------------------------------------------ MFMA kernel
 //
-// Rows in blocks of 16 * MT (MT = 1 for decode, padded to 16; MT = 2 for M > 16, one block per
-// grid row, the decoded weights of a K step serving both 16-row tiles; the other blocks re-read
-// the weights from the MALL) on v_mfma_f32_16x16x32_f16. A workgroup owns CW = 64 * NH output
+// Rows in blocks of 16 * MT on v_mfma_f32_16x16x32_f16, one block per grid row: MT = 1 for decode
+// (padded to 16) and for prefill rows whose 16-row blocks fit in 256 workgroups (up to 16 waves
+// each); MT = 2 otherwise, the decoded weights of a K step serving both 16-row tiles. The other
+// blocks re-read the weights from the MALL. A workgroup owns CW = 64 * NH output
 // columns (NH 128-byte line halves of the packed rows: 128 columns on wide shapes, 140 workgroups
 // for gate_up, one per CU, instead of 280 that put two 64-column tiles on 24 CUs) and a range of
 // quantization groups; its waves (up to 16 at 64 columns, 8 at 128) take groups round-robin, CPW
@@ -1465,18 +1466,31 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
   // 8 / 16 in 10 splits 4.9 / 5.0 / 5.45 / 6.70 us, in 8 splits 5.2 / 5.2 / 5.6 / 6.73)
   if (split_k <= 0 && tiles < 128 && wbytes > (2 << 20) && M <= 16)
     splits = m1 ? std::max<int64_t>(2, 256 / tiles) : (240 + tiles - 1) / tiles;
-  // Prefill rows in 32-row blocks: a long-K shape whose tiles and blocks leave most CUs idle
-  // splits K toward 256 workgroups, at most 8 ways and about 400K split-K atomics (every row of
-  // every block carries one per split); otherwise the row blocks fill the grid. down 1536x8960
-  // (24 tiles), graph-timed, whole K -> split: M = 17 18.5 -> 9.0 us (8 ways), M = 65 24.6 ->
-  // 12.7 (4), M = 128 25.4 -> 17.5 (2; 3 ways 25.4: the atomics), M = 256 (192 workgroups) stays
-  // whole, 25.7 against 32.9 split 2; the short-K shapes (q/o/qkv, 12 groups) lose with any split
-  // (o M = 128 8.5 -> 10.9 us at 2).
+  // Prefill rows in row blocks of 32 (mtile 2, at most 8 waves) or 16 (mtile 1, up to 16 waves).
+  // A long-K shape whose tiles and blocks leave most CUs idle splits K toward 256 workgroups, at
+  // most 8 ways and never past 256 (a CU with two finishes last: down 1536x8960 M = 128 in 32-row
+  // blocks, 2 splits 17.5 us, 3 splits on 288 workgroups 25.4); the short-K shapes (q/o/qkv, 12
+  // groups) lose with any split (o M = 128 8.5 -> 10.9 us at 2). 16-row blocks, twice the
+  // workgroups with twice the waves each, win wherever they fit in 256 workgroups on short K
+  // (qkv M = 17 / 32 / 128: 6.6 / 8.1 / 8.4 -> 5.3 / 5.5 / 5.7 us; at 144 rows, 288 workgroups,
+  // 9.8 against 8.4) and on long K where they split K at least twice over 192 or more workgroups,
+  // or fill more of the grid than the 32-row blocks (down M = 17 / 32 / 48 / 64 / 80: 9.0 / 10.8 /
+  // 12.1 / 12.8 / 14.4 -> 7.1 / 7.7 / 10.4 / 11.5 / 11.8 us in 5 / 5 / 3 / 2 / 2 splits). Whole
+  // K over all of it in 16-row blocks reads the weights twice as often and stays level with the
+  // 32-row blocks at the same grid (M = 128: 17.8 against 17.5; M = 96: 144 workgroups, 17.8,
+  // against 14.7 for 32-row blocks in 3 splits on 216).
   if (M > 16 && split_k <= 0) {
-    const int64_t base = tiles * ((M + 31) / 32);
-    splits = 1;
-    if (mfma && ng >= 24 && base < 160)
-      splits = std::max<int64_t>(1, std::min<int64_t>({(256 + base - 1) / base, 8, 400000 / (M * N)}));
+    const bool long_k = mfma && ng >= 24;
+    auto fill = [&](int64_t base) {  // splits toward 256 workgroups, at most 8, none past 256
+      return long_k && base < 160 ? std::max<int64_t>(1, std::min<int64_t>(256 / base, 8)) : int64_t(1);
+    };
+    const int64_t b32 = tiles * ((M + 31) / 32), b16 = tiles * ((M + 15) / 16);
+    const int64_t s32 = fill(b32), s16 = long_k ? std::max<int64_t>(1, std::min<int64_t>(256 / b16, 8)) : 1;
+    splits = s32;
+    if (mfma && b16 <= 256 && (!long_k || (s16 >= 2 && b16 * s16 >= 192) || b16 * s16 > b32 * s32)) {
+      p.mtile = 1;
+      splits = s16;
+    }
   }
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);
   p.gps = (int)((ng + splits - 1) / splits);
@@ -1785,9 +1799,10 @@ static bool gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_
 }
 
 // The library's choice for prefill rows, from graph-timed sweeps on MI355X over the Qwen2.5-1.5B
-// shapes (M = 65 .. 2048): the 32-row blocks re-read the packed weights per block but split K over
+// shapes (M = 65 .. 2048): the row blocks re-read the packed weights per block but split K over
 // the waves of a workgroup, which wins while the weights dominate and the tiles are few (qkv/o at
-// M <= 256: 8.0-8.5 us against 12.4 us; down at M = 256: 25.7 against 31.1 us); the GEMM reads
+// M <= 128: 5.3-5.7 us on 16-row blocks, at M <= 256: 8.5 us on 32-row blocks, against 10.3-12.4
+// us; down at M = 256: 25.7 against 31.1 us); the GEMM reads
 // them once per 64/128-row tile and wins on wide shapes at every row count (gate_up M = 65: 18.4
 // against 22.2 us; M = 2048: 116 against 364 us) and on narrow shapes whose 32-row blocks would need more than 256
 // workgroups, or that have 512 rows or more (qkv M = 512: 12.6 against 15.1 us; down M = 512: 34.8

@@ -8,10 +8,12 @@ bit for bit; like the reference's torch code they take CPU tensors too (run on t
 GPU, results returned on the CPU). Decode shapes run the wave64 VALU GEMV with an in-workgroup
 split-K at M = 1 and the MFMA kernel (in-register byte transpose, exact e4m3 -> fp16) from 2 rows.
 Prefill rows (the reference's tensor-core GEMM, fp8.py:42-91 run at fp8.py:221-222) run
-hand-written kernels at every row count: 17-64 rows the MFMA kernel in 16-row blocks, more rows
-(and from 17 rows on wide shapes, N >= 8192) the prefill GEMM (csrc/prefill.hip: 32/64/128-row
-tiles, e4m3 tiles transposed and converted to fp16 in registers, column scale after the K loop, K
-split over workgroups for long K).
+hand-written kernels at every row count: the MFMA kernel in 16-row blocks (17-64 rows, and on
+narrow shapes while the blocks fit in 256 workgroups: short K on 64-column tiles with K split
+toward 256 workgroups, long K while they still split K at least twice), else (and from 17 rows on
+wide shapes, N >= 8192) the prefill GEMM (csrc/prefill.hip: 32/64/128-row tiles, e4m3 tiles
+transposed and converted to fp16 in registers, column scale after the K loop, K split over
+workgroups for long K).
 `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
 N must be a multiple of 4: rows of any such N run the VALU kernel with 4-byte loads where N % 16
 != 0, the MFMA kernel on 64-column tiles where N % 8 != 0, and the 16-row MFMA blocks instead of

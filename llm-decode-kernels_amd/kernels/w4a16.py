@@ -17,10 +17,11 @@ libldk_amd.so whose tile and K-split come from the library's per-shape table:
 Prefill shapes (the reference's Triton tensor-core GEMM path, w4a16.py:264-268) run hand-written
 kernels at every row count: the library picks, per shape, the prefill GEMM (csrc/prefill.hip:
 32/64/128-row tiles on the matrix cores, every weight dequantized exactly as dequantize_ref does
-it, fp32 accumulation, K split over workgroups for long K) or the MFMA kernel in 32-row blocks (the
-choice for 17-31 rows and for narrow shapes up to 256 rows, and up to 511 rows while the blocks fit
-in 256 workgroups, where the blocks' K split over waves wins; wide shapes, N >= 8192, take the GEMM
-from 32 rows). `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
+it, fp32 accumulation, K split over workgroups for long K) or the MFMA kernel in 16- or 32-row blocks
+(the choice for 17-31 rows and for narrow shapes up to 256 rows, and up to 511 rows while the
+blocks fit in 256 workgroups, where the blocks' K split over waves wins; 16-row blocks wherever
+they fit in 256 workgroups, with K split over workgroups on long K; wide shapes, N >= 8192, take
+the GEMM from 32 rows). `config={"prefill": "gemm" | "blocks"}` forces one of them; "native" is the library's choice.
 
 `config` (dict) forces a variant, as in the reference (w4a16.py:301-306). Honoured keys:
 `GEMV` (force the VALU decode kernels, M <= 8), `MFMA` (force the MFMA kernel), `FACTORED`

@@ -116,3 +116,37 @@ def test_w4a16_prefill_choice_of_the_narrow_shapes():
     )
     for M, N, K, path in cases:
         assert w4a16.config_for(M, N, K).startswith(path + ","), (M, N, K, w4a16.config_for(M, N, K))
+
+
+def test_w4a16_prefill_row_blocks():
+    """Prefill rows on the MFMA blocks: 16-row blocks (MT = 1, the fourth template argument)
+    wherever they fit in 256 workgroups on short K; on long K where they split K at least twice
+    over 192 or more workgroups, else 32-row blocks (MT = 2) with K split toward 256 workgroups,
+    never past it."""
+    cases = (  # M, N, K, MT, split_k
+        (17, 2048, 1536, 1, 1), (128, 2048, 1536, 1, 1), (144, 2048, 1536, 2, 1),
+        (160, 1536, 1536, 1, 1), (176, 1536, 1536, 2, 1),
+        (17, 1536, 8960, 1, 5), (48, 1536, 8960, 1, 3), (80, 1536, 8960, 1, 2),
+        (96, 1536, 8960, 2, 3), (128, 1536, 8960, 2, 2), (160, 1536, 8960, 2, 2),
+        (192, 1536, 8960, 2, 1), (20, 17920, 1536, 2, 1),
+    )
+    for M, N, K, mt, sk in cases:
+        name = w4a16.kernel_name(M, N, K)
+        assert name.startswith("w4a16_mfma_kernel<") and name.split(", ")[3] == str(mt), (M, N, K, name)
+        assert _fields(w4a16.config_for(M, N, K))["split_k"] == str(sk), (M, N, K)
+
+
+def test_fp8_prefill_row_blocks():
+    """e4m3 prefill rows: the 16-row blocks on narrow shapes while they fit in 256 workgroups,
+    short K on 64-column tiles with K split toward 256 workgroups, long K (128-column tiles) while
+    it still splits at least twice; the prefill GEMM past that and from 17 rows on wide shapes."""
+    cases = (  # M, N, K, expected
+        (17, 2048, 1536, "mfma,block_n=64,split_k=4"), (64, 2048, 1536, "mfma,block_n=64,split_k=2"),
+        (128, 2048, 1536, "mfma,block_n=64,split_k=1"), (160, 2048, 1536, "gemm,"),
+        (17, 1536, 1536, "mfma,block_n=64,split_k=5"), (160, 1536, 1536, "mfma,block_n=64,split_k=1"),
+        (176, 1536, 1536, "gemm,"), (64, 1536, 8960, "mfma,block_n=128,split_k=5"),
+        (128, 1536, 8960, "mfma,block_n=128,split_k=2"), (176, 1536, 8960, "gemm,"),
+        (17, 17920, 1536, "gemm,"),
+    )
+    for M, N, K, want in cases:
+        assert fp8.config_for(M, N, K).startswith(want), (M, N, K, fp8.config_for(M, N, K))

@@ -140,8 +140,8 @@ def test_mfma_tile_widths(M, N, block_n):
 
 
 def test_mfma_32_column_tiles_split_and_prefill():
-    """32-column MFMA tiles with the cross-workgroup K split (down projection) and in 32-row
-    prefill blocks, with bias."""
+    """32-column MFMA tiles with the cross-workgroup K split (down projection) and in prefill
+    row blocks (16 rows at M = 40: 64 tiles x 3 blocks), with bias."""
     _run(8, 1536, 8960, bias=True, config={"MFMA": True, "block_n": 32})
     _run(16, 1536, 8960, config={"MFMA": True, "block_n": 32, "split_k": 7})
     _run(40, 2048, 1536, bias=True, config={"MFMA": True, "block_n": 32})
@@ -469,7 +469,7 @@ def test_reference_prefill_8960x1536(M):
 @pytest.mark.parametrize("path", ["blocks", "gemm"])
 def test_prefill_native_rows(M, N, K, bias, path):
     """Prefill rows (the reference's prefill path, w4a16.py:264-268 and tests/test_w4a16.py:93-97)
-    through the MFMA kernel in 32-row blocks and through the prefill GEMM: row tails inside a
+    through the MFMA kernel in 16- or 32-row blocks and through the prefill GEMM: row tails inside a
     tile, bias, every Qwen width class."""
     _run(M, N, K, bias=bias, config={"prefill": path})
 
@@ -489,7 +489,7 @@ def test_prefill_gemm_group_sizes(gs):
 
 
 def test_prefill_group_32_takes_the_blocks():
-    """The GEMM steps K by 64; group 32 keeps the 32-row blocks, still correct."""
+    """The GEMM steps K by 64; group 32 keeps the row blocks, still correct."""
     _run(200, 1024, 512, gs=32)
 
 
@@ -544,7 +544,7 @@ def test_prefill_native_group_sizes(gs):
 
 
 def test_prefill_paths_agree():
-    """The prefill paths (GEMM, 32-row blocks, the library's choice) meet the bar on the same
+    """The prefill paths (GEMM, row blocks, the library's choice) meet the bar on the same
     inputs, and an unknown path name is rejected."""
     for path in ("gemm", "blocks", "native"):
         _run(300, 2048, 1536, config={"prefill": path})
@@ -619,8 +619,9 @@ def test_choice_export_records_only_the_library_choice():
 @pytest.mark.parametrize("M", [17, 33, 65, 100, 128])
 @pytest.mark.parametrize("split", [None, 2, 3, 8])
 def test_prefill_blocks_split_k(M, split):
-    """Prefill rows of a long-K shape on the 32-row MFMA blocks with K split over workgroups
-    (the library's choice below about 200 rows on down; explicit splits too): each row block's
+    """Prefill rows of a long-K shape on the MFMA row blocks with K split over workgroups
+    (the library's choice below about 200 rows on down: 16-row blocks in 5 / 3 / 2 splits at
+    17 / 33 / 65 rows, 32-row blocks in 2 at 100 and 128; explicit splits run 32-row blocks): each row block's
     split tiles meet in their own fixed-point words, the last row block ragged. Repeated calls
     give the same bits (every word is back to zero after a call)."""
     cfg = {"prefill": "blocks"} if split is None else {"prefill": "blocks", "split_k": split}
