@@ -355,3 +355,31 @@ def test_mfma_64_column_tiles_every_code_exact():
         nz = ref != 0
         assert np.array_equal(bits16(got)[nz], bits16(ref)[nz]), k0
         assert np.all(got[~nz] == 0)
+
+
+# ------------------------------------------------------- prefill rows on the 16-row blocks (plan)
+@pytest.mark.parametrize("M", [17, 40, 64, 65, 100, 160])
+@pytest.mark.parametrize("N,K", [(1536, 1536), (2048, 1536), (1536, 8960), (1000, 1536), (2064, 512)])
+def test_prefill_row_blocks_default_plan(M, N, K):
+    """The library's choice at prefill rows: short K on 64-column 16-row blocks with K split toward
+    256 workgroups (16 waves where split), long K on 128-column blocks in at least two splits, the
+    prefill GEMM past where the blocks fit; ragged last row block, N % 8 != 0 (1000)."""
+    _run(M, N, K, bias=(N == 2048))
+
+
+def test_prefill_row_blocks_one_hot_rows_exact():
+    """16-wave 64-column blocks with K split at prefill rows (M = 40, K = 1536: 3 row blocks in
+    three splits): one-hot x rows return e4m3(wq[k, n]) * scale exactly, so the split words, the
+    row blocks and the 16-wave reduction are checked bit for bit."""
+    M, K, N = 40, 1536, 1536
+    g = torch.Generator().manual_seed(6)
+    codes = torch.randint(0, 256, (K, N), generator=g, dtype=torch.int64).to(torch.uint8).numpy()
+    codes[(codes & 0x7F) == 0x7F] = 0
+    ks = (torch.arange(M) * 37) % K
+    x = torch.zeros(M, K, dtype=torch.float16, device="cuda")
+    x[torch.arange(M), ks.cuda()] = 1.0
+    assert config_for(M, N, K) == "mfma,block_n=64,split_k=3"
+    out = w8a16_matmul(x, dev(codes).view(FP8), torch.ones(N, dtype=torch.float16, device="cuda"))
+    ref = of.e4m3_decode(codes[ks.numpy()]).astype(np.float16)
+    assert np.array_equal(bits16(to_np(out)) & 0x7FFF | (bits16(ref) & 0x8000) * (ref != 0),
+                          bits16(ref) & 0x7FFF | (bits16(ref) & 0x8000) * (ref != 0))

@@ -10,7 +10,7 @@ import torch
 from _util import assert_north_star, bits16, dev, to_np
 from kernels.bench import cases
 from kernels.cuda.w4a16_cuda import w4a16_decode_cuda
-from kernels.w4a16 import config_for, w4a16_matmul
+from kernels.w4a16 import config_for, kernel_name, w4a16_matmul
 from oracle import quant as oq
 from oracle.reference import dequantize_ref, w4a16_ref
 
@@ -631,3 +631,28 @@ def test_prefill_blocks_split_k(M, split):
     y0 = w4a16_matmul(*args, bias=dev(b), config=cfg)
     y1 = w4a16_matmul(*args, bias=dev(b), config=cfg)
     assert torch.equal(y0, y1)
+
+
+# ---------------------------------------------------- prefill rows on 16- and 32-row blocks (plan)
+@pytest.mark.parametrize("M", [17, 40, 65, 100, 144, 160])
+@pytest.mark.parametrize("N,K", [(1536, 1536), (2048, 1536), (1536, 8960), (1000, 1536), (2064, 512)])
+def test_prefill_row_blocks_default_plan(M, N, K):
+    """The library's choice at prefill rows: 16-row blocks where they fit in 256 workgroups (short
+    K whole, long K in 2-5 splits), 32-row blocks in K splits up to 256 workgroups, the prefill
+    GEMM past that; ragged last row block, a partial last column tile (N = 1000, 2064)."""
+    _run(M, N, K, bias=(N == 2048))
+
+
+@pytest.mark.parametrize("N,K", [(1536, 8960), (2048, 1536)])
+def test_prefill_16_row_blocks_one_hot_rows_exact(N, K):
+    """x = e_k rows through the 16-row blocks (M = 40: three blocks, the last ragged; down in
+    three K splits, qkv whole): row m of the output is column k of dequant(W) bit for bit."""
+    M = 40
+    assert kernel_name(M, N, K).split(", ")[3] == "1"
+    _, qw, s, z, _ = _make(1, N, K, 7)
+    ks = [(m * 211) % K for m in range(M)]
+    x = np.zeros((M, K), dtype=np.float16)
+    x[np.arange(M), ks] = 1.0
+    out = w4a16_matmul(dev(x), dev(qw), dev(s), dev(z))
+    deq = dequantize_ref(qw, s, z)
+    assert np.array_equal(bits16(out), bits16(deq[:, ks].T))
