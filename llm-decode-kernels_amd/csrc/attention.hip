@@ -482,21 +482,19 @@ constexpr int kPWaves = 4;
 __global__ __launch_bounds__(256) void prefill_rope_kv_kernel(const half_t* qkv, int64_t ldqkv, const int64_t* pos,
                                                               const float* inv_freq, half_t* kc, half_t* vt,
                                                               half_t* qs, int nq, int nkv, int L) {
-  __shared__ half_t cs[2][64];
-  const int t = blockIdx.x, tid = threadIdx.x;
+  // every element a thread ropes has dim pair j = tid % 64 (the loops step by 256), so each thread
+  // forms its own cos and sin: no shared table and no barrier, and the row loads need not wait
+  // for the position
+  const int t = blockIdx.x, tid = threadIdx.x, jt = tid & 63;
   const int64_t p = pos[t];
-  if (tid < 64) {
-    const float ang = (float)p * inv_freq[tid];
-    cs[0][tid] = (half_t)cosf(ang);
-    cs[1][tid] = (half_t)sinf(ang);
-  }
-  __syncthreads();
+  const float ang = (float)p * inv_freq[jt];
+  const half_t cj = (half_t)cosf(ang), sj = (half_t)sinf(ang);
   const half_t* row = qkv + (int64_t)t * ldqkv;
   half_t* qo = qs + (int64_t)t * nq * kHD;
   for (int e = tid; e < nq * 64; e += 256) {  // (head, dim pair j < 64): dims j and j + 64
     const int h = e >> 6, j = e & 63;
     half_t x0 = row[h * kHD + j], x1 = row[h * kHD + j + 64];
-    rope_rotate(x0, x1, cs[0][j], cs[1][j]);
+    rope_rotate(x0, x1, cj, sj);
     qo[h * kHD + j] = x0;
     qo[h * kHD + j + 64] = x1;
   }
@@ -505,7 +503,7 @@ __global__ __launch_bounds__(256) void prefill_rope_kv_kernel(const half_t* qkv,
   for (int e = tid; e < nkv * 64; e += 256) {
     const int h = e >> 6, j = e & 63;
     half_t x0 = row[(nq + h) * kHD + j], x1 = row[(nq + h) * kHD + j + 64];
-    rope_rotate(x0, x1, cs[0][j], cs[1][j]);
+    rope_rotate(x0, x1, cj, sj);
     half_t* kw = kc + (int64_t)h * L * kHD;
     kw[k_offset(pp, j)] = x0;
     kw[k_offset(pp, j + 64)] = x1;
