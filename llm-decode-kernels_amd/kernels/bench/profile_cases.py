@@ -162,6 +162,20 @@ def case_prefill_attention(reps, T=128, L=416):
     _rotate(lambda k, v: prefill_attention(qkv, p, inv, k, v, nq, nkv, hd ** -0.5), sets, reps)
 
 
+def case_prefill_forward(reps, backend="ours", T=128):
+    """The config-4 runner's prompt forward (random-init Qwen2.5-1.5B architecture, seed 4, a
+    T-token prompt at positions 0..T-1), eager, reps times: every prefill launch of a layer."""
+    from kernels.e2e.model import QwenRunner, make_backend, random_qwen2
+
+    hf = random_qwen2(seed=4)
+    ids = torch.randint(0, hf.config.vocab_size, (1, T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(4))
+    runner = QwenRunner(hf, make_backend(backend), max_len=416)
+    pos = torch.arange(T, device="cuda")
+    for _ in range(reps):
+        runner.forward(ids, pos)
+
+
 def case_rmsnorm(M, N, reps):
     from kernels.rmsnorm import rmsnorm
 
@@ -190,6 +204,8 @@ def case_copy(reps):
 CASES = {
     "calib_neg64MiB": lambda r: case_copy(r),
     "w4a16_gate_up_m1": lambda r: case_w4a16(1, 17920, 1536, r),
+    "prefill_forward_ours": lambda r: case_prefill_forward(r, "ours"),
+    "prefill_forward_ours_fp8": lambda r: case_prefill_forward(r, "ours_fp8"),
     # the M = 1 kernel and the read floors at K = 1536 and wider N (2x, 4x gate_up, and the
     # 151936-row vocabulary of the quantized lm_head): where launch and ramp stop dominating
     **{f"w4a16_m1_n{n}": (lambda r, n=n: case_w4a16(1, n, 1536, r)) for n in (35840, 71680, 151936)},
