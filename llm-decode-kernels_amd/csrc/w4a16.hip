@@ -1490,6 +1490,16 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int gsh_rows, int block_n, int s
     if (mfma && b16 <= 256 && (!long_k || (s16 >= 2 && b16 * s16 >= 192) || b16 * s16 > b32 * s32)) {
       p.mtile = 1;
       splits = s16;
+    } else if (long_k && block_n == 0 && p.ln == 16 && rpg <= 16) {
+      // 128-column tiles where their K split fills a grid half again as large (down M = 192:
+      // 64-column blocks over all of K on 144 workgroups 25.5 us, 128-column in 3 splits on 216
+      // 22.4; M = 128 / 160 give 192 / 240 workgroups either way, and 64 columns stay faster,
+      // 17.9 / 18.4 against 20.5 / 20.3)
+      const int64_t b2 = (N + 127) / 128 * ((M + 31) / 32), s2 = fill(b2);
+      if (2 * b2 * s2 >= 3 * b32 * s32) {
+        p.ln = 32;
+        splits = s2;
+      }
     }
   }
   splits = std::min<int64_t>(std::min<int64_t>(splits, ng), kMaxSplits);

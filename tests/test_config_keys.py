@@ -122,18 +122,20 @@ def test_w4a16_prefill_row_blocks():
     """Prefill rows on the MFMA blocks: 16-row blocks (MT = 1, the fourth template argument)
     wherever they fit in 256 workgroups on short K; on long K where they split K at least twice
     over 192 or more workgroups, else 32-row blocks (MT = 2) with K split toward 256 workgroups,
-    never past it."""
+    never past it, on 128-column tiles where those split into a grid half again as large."""
     cases = (  # M, N, K, MT, split_k
         (17, 2048, 1536, 1, 1), (128, 2048, 1536, 1, 1), (144, 2048, 1536, 2, 1),
         (160, 1536, 1536, 1, 1), (176, 1536, 1536, 2, 1),
         (17, 1536, 8960, 1, 5), (48, 1536, 8960, 1, 3), (80, 1536, 8960, 1, 2),
         (96, 1536, 8960, 2, 3), (128, 1536, 8960, 2, 2), (160, 1536, 8960, 2, 2),
-        (192, 1536, 8960, 2, 1), (20, 17920, 1536, 2, 1),
+        (192, 1536, 8960, 2, 3), (256, 1536, 8960, 2, 1), (20, 17920, 1536, 2, 1),
     )
     for M, N, K, mt, sk in cases:
         name = w4a16.kernel_name(M, N, K)
         assert name.startswith("w4a16_mfma_kernel<") and name.split(", ")[3] == str(mt), (M, N, K, name)
         assert _fields(w4a16.config_for(M, N, K))["split_k"] == str(sk), (M, N, K)
+    assert w4a16.config_for(192, 1536, 8960).startswith("mfma,block_n=128,split_k=3")
+    assert w4a16.config_for(192, 1536, 8960, 256).startswith("mfma,block_n=64,")  # group 256: 64 columns
 
 
 def test_fp8_prefill_row_blocks():

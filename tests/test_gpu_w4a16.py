@@ -634,12 +634,13 @@ def test_prefill_blocks_split_k(M, split):
 
 
 # ---------------------------------------------------- prefill rows on 16- and 32-row blocks (plan)
-@pytest.mark.parametrize("M", [17, 40, 65, 100, 144, 160])
+@pytest.mark.parametrize("M", [17, 40, 65, 100, 144, 160, 192])
 @pytest.mark.parametrize("N,K", [(1536, 1536), (2048, 1536), (1536, 8960), (1000, 1536), (2064, 512)])
 def test_prefill_row_blocks_default_plan(M, N, K):
     """The library's choice at prefill rows: 16-row blocks where they fit in 256 workgroups (short
-    K whole, long K in 2-5 splits), 32-row blocks in K splits up to 256 workgroups, the prefill
-    GEMM past that; ragged last row block, a partial last column tile (N = 1000, 2064)."""
+    K whole, long K in 2-5 splits), 32-row blocks in K splits up to 256 workgroups (128-column
+    tiles in 3 splits for down at 192 rows), the prefill GEMM past that; ragged last row block, a
+    partial last column tile (N = 1000, 2064)."""
     _run(M, N, K, bias=(N == 2048))
 
 
