@@ -90,3 +90,24 @@ def test_full_size_graph_decode_matches_eager(model, prompt):
     del dec, runner
     gc.collect()
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("P", [40, 200])
+def test_full_size_prompt_lengths_match_dequantized_reference(model, P):
+    """Other prompt lengths at full size run other prefill plans (40 rows: 16-row blocks on qkv, o
+    and down, down in 3 K splits; 200 rows: 32-row blocks on qkv and o, 128-column tiles in 3 K
+    splits on down):
+    every prompt row's logits of `ours` against `w4_ref` within the reference's 5e-2."""
+    print(f"[config4] ours vs w4_ref: prompt {P}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(40 + P)
+    ids = torch.randint(0, model.config.vocab_size, (1, P), device="cuda", generator=g)
+    pos = torch.arange(P, device="cuda")
+    r_ref = QwenRunner(model, make_backend("w4_ref"), max_len=MAX_LEN)
+    r_ours = QwenRunner(model, make_backend("ours"), max_len=MAX_LEN)
+    a = r_ref.forward(ids, pos, all_logits=True)
+    b = r_ours.forward(ids, pos, all_logits=True)
+    assert torch.isfinite(b).all()
+    torch.testing.assert_close(b.float(), a.float(), atol=5e-2, rtol=5e-2)
+    del r_ref, r_ours
+    gc.collect()
+    torch.cuda.empty_cache()
