@@ -359,11 +359,13 @@ def test_mfma_64_column_tiles_every_code_exact():
 
 # ------------------------------------------------------- prefill rows on the 16-row blocks (plan)
 @pytest.mark.parametrize("M", [17, 40, 64, 65, 100, 160])
-@pytest.mark.parametrize("N,K", [(1536, 1536), (2048, 1536), (1536, 8960), (1000, 1536), (2064, 512)])
+@pytest.mark.parametrize("N,K", [(1536, 1536), (2048, 1536), (1536, 8960), (1000, 1536), (2064, 512),
+                                 (1536, 1000), (1536, 2600)])
 def test_prefill_row_blocks_default_plan(M, N, K):
     """The library's choice at prefill rows: short K on 64-column 16-row blocks with K split toward
     256 workgroups (16 waves where split), long K on 128-column blocks in at least two splits, the
-    prefill GEMM past where the blocks fit; ragged last row block, N % 8 != 0 (1000)."""
+    prefill GEMM past where the blocks fit; ragged last row block, N % 8 != 0 (1000), K not a
+    multiple of the 32-row K step (1000) and long K not a multiple of 64 (2600)."""
     _run(M, N, K, bias=(N == 2048))
 
 
