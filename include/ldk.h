@@ -230,6 +230,20 @@ int ldk_w8a16_rmsnorm_matmul(const void* x, const void* residual, void* residual
                              const void* scale, const void* bias, void* out, int64_t N, int64_t K,
                              void* workspace, int64_t workspace_bytes, void* stream);
 
+/* out [1, N] = x @ dequant_fp8(wq) (+ bias) with x [K] the decode attention output that
+ * ldk_decode_attention_ranges left as partials (nq heads, max_len positions in ranges of rlen,
+ * at *pos): each x value is the ranges' merge exp(m_r - max m)-weighted, o / l rounded once to
+ * fp16, formed in the W8A16 GEMV's x staging with the arithmetic of
+ * ldk_w4a16_attn_matmul_residual_stats's merge. K = nq * 128, at most 4 ranges
+ * (ceil(max_len / rlen) <= 4), N % 4 == 0, pos 8-byte and wq 16-byte aligned; the pending
+ * partials must be this stream's, max_len's, rlen's and nq's as for that entry (else
+ * LDK_ERR_INVALID, no launch). One launch in place of the attention's merge launch and the FP8
+ * o projection (the reference's attention block and FP8 linear, kernels/e2e/model.py:100-118,
+ * 236-243). No counterpart entry exists in the reference. */
+int ldk_w8a16_attn_matmul(const int64_t* pos, int64_t max_len, int64_t rlen, int nq, const uint8_t* wq,
+                          const void* scale, const void* bias, void* out, int64_t N, int64_t K,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------- RMSNorm and SwiGLU */
 
 /* Per row of x [M, N]: h = x (+ residual, fp16 add, written to res_out); out = weight * fp16(

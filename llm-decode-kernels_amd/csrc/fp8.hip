@@ -15,6 +15,7 @@
 // per-channel scale is applied once after the K reduction (fp8.py:120).
 #include <algorithm>
 
+#include "attention.h"
 #include "ldk_common.h"
 #include "prefill.h"
 
@@ -148,6 +149,12 @@ struct W8Args {
   half_t* res_out;
   const half_t* nw;
   float eps;
+  // attention-merge prologue (PRO 4): the decode attention's per-range partials (attention.h),
+  // its position and range geometry
+  const float* att_o = nullptr;
+  const float* att_ml = nullptr;
+  const int64_t* att_pos = nullptr;
+  int att_len = 0, att_rlen = 0;
 };
 
 struct W8Split {
@@ -174,11 +181,20 @@ __device__ __forceinline__ ldk::SplitK w8_split_ctx(const W8Split& sp, int split
 //           row statistic over the whole row itself: its first row vectors are loaded ahead of
 //           the pass (one LDS barrier, which waits for those loads only). The statistic's order
 //           differs from the RMSNorm kernel's, so a staged value can differ from its output by
-//           one fp16 ulp.
+//           one fp16 ulp;
+//  PRO = 4: x is the decode attention's output, merged from its per-range partials
+//           (ldk_decode_attention_ranges) as it is staged: for dim d of head h,
+//           x = sum_r f_r o_r / sum_r f_r l_r with f_r = exp(m_r - max m) over the ranges live at
+//           pos, rounded once to fp16, the W4A16 o projection's merge (a chain in range order,
+//           one reciprocal per value). The partials of all kW8AttnRanges ranges are loaded with
+//           the x loads (in bounds: the partials hold kAttnMaxSplits ranges); the ranges past
+//           the live ones are left out by selects when x is formed.
+constexpr int kW8AttnRanges = 4;  // attention ranges a PRO 4 launch merges (registers)
+
 template <int MT, int LN, int NW, int RPL, int PRO, bool TAIL>
 __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split sp) {
   static_assert(PRO == 0 || MT == 1, "the prologues take one row");
-  constexpr bool kRms = PRO == 2 || PRO == 3, kRes = PRO == 3;
+  constexpr bool kRms = PRO == 2 || PRO == 3, kRes = PRO == 3, kAttn = PRO == 4;
   constexpr int CW = 16 * LN;
   constexpr int LKW = 64 / LN;
   constexpr int RPP = LKW * NW * RPL;  // K rows per pass
@@ -215,17 +231,36 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
     if constexpr (kRes) sr0 = ldk::buffer_load16(ldk::buffer_rsrc(a.res, (uint32_t)a.K * 2u), 16u * tid);
   }
   float rs = 0.0f;
+  // PRO 4: the ranges live at the attention's position (its clamping of pos)
+  int att_live = 1;
+  if constexpr (kAttn) {
+    const int64_t pin = *a.att_pos;
+    const int pos = pin >= 0 && pin < a.att_len ? (int)pin : pin < 0 ? -1 : a.att_len - 1;
+    att_live = pos < 0 ? 1 : pos / a.att_rlen + 1;
+  }
 
   for (int p0 = rb; p0 < re; p0 += RPP) {
     // loads in consumption order: this wave's x values, then the weight rows (clamped, branch
     // free; rows past re and x rows past M are zeroed when staged)
     half_t xl[XPL], xu[XPL], xn[XPL];
+    float ao[kAttn ? XPL : 1][kW8AttnRanges];  // PRO 4: dim d of head h of each range
+    float2_t am[kAttn ? XPL : 1][kW8AttnRanges];  // and its {m, l}
 #pragma unroll
     for (int i = 0; i < XPL; ++i) {
       const int e = lane + 64 * i, m = min(e / RPW, MT - 1), rr = e % RPW;
       const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
       const int64_t xo = (int64_t)min(m0 + m, a.M - 1) * a.ldx + min(k, a.K - 1);
-      xl[i] = a.x[xo];
+      if constexpr (kAttn) {
+        const int kk = min(k, a.K - 1), h = kk / ldk::kAttnHeadDim, d = kk % ldk::kAttnHeadDim;
+#pragma unroll
+        for (int r = 0; r < kW8AttnRanges; ++r) {
+          ao[i][r] = a.att_o[(h * ldk::kAttnMaxSplits + r) * ldk::kAttnHeadDim + d];
+          const float* ml = a.att_ml + (h * ldk::kAttnMaxSplits + r) * 2;
+          am[i][r] = float2_t{ml[0], ml[1]};
+        }
+      } else {
+        xl[i] = a.x[xo];
+      }
       if constexpr (PRO == 1) xu[i] = a.x[xo + a.K];
       if constexpr (kRes) xu[i] = a.res[xo];
       if constexpr (kRms) xn[i] = a.nw[xo];
@@ -276,7 +311,31 @@ __global__ __launch_bounds__(NW * 64) void w8a16_gemv_kernel(W8Args a, W8Split s
     for (int i = 0; i < XPL; ++i) {
       const int e = lane + 64 * i, m = e / RPW, rr = e % RPW;
       const int k = p0 + wave * LKW + rr % LKW + (rr / LKW) * LKW * NW;
-      half_t v = xl[i];
+      half_t v;
+      if constexpr (kAttn) {
+        // the ranges past the live ones hold an earlier call's values (any bits): selects, not
+        // products with a zero weight, leave them out
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < kW8AttnRanges; ++r) mx = fmaxf(mx, r < att_live ? am[i][r][0] : -__builtin_inff());
+        float f[kW8AttnRanges], l = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kW8AttnRanges; ++r) {
+          f[r] = __expf(am[i][r][0] - mx);
+          const float lr = __builtin_fmaf(am[i][r][1], f[r], l);
+          l = r < att_live ? lr : l;
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kW8AttnRanges; ++r) {
+          const float orr = __builtin_fmaf(ao[i][r], f[r], o);
+          o = r < att_live ? orr : o;
+        }
+        v = (half_t)(l > 0.0f ? o * inv : 0.0f);  // no live position: 0 (o may be NaN)
+      } else {
+        v = xl[i];
+      }
       if constexpr (PRO == 1) v = ldk::silu_f16(xl[i]) * xu[i];  // fp16 multiply
       if constexpr (kRms) v = ldk::rms_f16(kRes ? xl[i] + xu[i] : xl[i], rs, xn[i]);
       if (e < RPW * MT) xs[wave][m][rr] = (m0 + m < a.M && k < re) ? v : (half_t)0.0f;
@@ -703,6 +762,7 @@ int launch_w8(const W8Args& a, const W8Split& sp, const W8Plan& p, hipStream_t s
       case 1: return launch_w8_ln<1, 1>(a, sp, p, s);
       case 2: return launch_w8_ln<1, 2>(a, sp, p, s);
       case 3: return launch_w8_ln<1, 3>(a, sp, p, s);
+      case 4: return launch_w8_ln<1, 4>(a, sp, p, s);
     }
     return ldk::fail(LDK_ERR_INVALID, "w8a16: unknown prologue %d", pro);
   }
@@ -926,4 +986,41 @@ extern "C" int ldk_w8a16_rmsnorm_matmul(const void* x, const void* residual, voi
   const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr,
                    p.splits > 1 ? ldk::splitk_side(workspace, p.words) : nullptr};
   return launch_w8(a, sp, p, (hipStream_t)stream, residual ? 3 : 2);
+}
+
+// Fused decode entry (one row): the o projection with x the decode attention output that
+// ldk_decode_attention_ranges left as per-range partials, merged in the W8A16 GEMV's x staging,
+// so the attention's merge and the projection are one launch (the reference runs the attention
+// block and the FP8 linear as separate ops, kernels/e2e/model.py:100-118,236-243).
+extern "C" int ldk_w8a16_attn_matmul(const int64_t* pos, int64_t max_len, int64_t rlen, int nq, const uint8_t* wq,
+                                     const void* scale, const void* bias, void* out, int64_t N, int64_t K,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* fn = "w8a16_attn_matmul";
+  if (!pos || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "%s: null pointer", fn);
+  if (N <= 0 || K <= 0) return ldk::fail(LDK_ERR_INVALID, "%s: N, K must be positive", fn);
+  if (N % 4) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N=%lld must be a multiple of 4", fn, (long long)N);
+  if (nq <= 0 || nq > ldk::kAttnMaxHeads || K != (int64_t)nq * ldk::kAttnHeadDim)
+    return ldk::fail(LDK_ERR_INVALID, "%s: K=%lld must be nq * 128 with 1 <= nq <= %d", fn, (long long)K, ldk::kAttnMaxHeads);
+  if (max_len <= 0 || rlen <= 0 || rlen % 32 || (max_len + rlen - 1) / rlen > kW8AttnRanges || max_len > INT32_MAX)
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: max_len=%lld in ranges of rlen=%lld (a multiple of 32) must give 1..%d ranges",
+                     fn, (long long)max_len, (long long)rlen, kW8AttnRanges);
+  if (!ldk::aligned(pos, 8) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2) || !ldk::aligned(out, 2) ||
+      (bias && !ldk::aligned(bias, 2)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: pos 8-byte and wq 16-byte aligned", fn);
+  if (N > INT32_MAX / 16) return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: N too large", fn);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
+  const float *po = nullptr, *pm = nullptr;
+  int st = ldk::attention_partials(fn, stream, pos, max_len, rlen, nq, &po, &pm);
+  if (st) return st;
+  const W8Plan p = make_w8_plan(1, N, K, 0, 0, workspace ? workspace_bytes : 0);
+  W8Args a{nullptr, K, wq, (const half_t*)scale, (const half_t*)bias, (half_t*)out, N, 1, (int)N, (int)K};
+  a.att_o = po;
+  a.att_ml = pm;
+  a.att_pos = pos;
+  a.att_len = (int)max_len;
+  a.att_rlen = (int)rlen;
+  const W8Split sp{p.splits, p.kps, p.splits > 1 ? static_cast<uint64_t*>(workspace) : nullptr,
+                   p.splits > 1 ? ldk::splitk_side(workspace, p.words) : nullptr};
+  return launch_w8(a, sp, p, (hipStream_t)stream, 4);
 }

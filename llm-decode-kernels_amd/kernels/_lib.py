@@ -79,6 +79,7 @@ SIGNATURES = {
                               _f32, _vp],
     "ldk_w4a16_attn_matmul_residual_stats": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _i64, _i64, _i32, _vp, _i64, _vp],
+    "ldk_w8a16_attn_matmul": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp],
 }
 
 _lock = threading.Lock()

@@ -250,7 +250,6 @@ class OursFP8Backend(OursBackend):
     (model.py:100-118). `Linear.qweight` holds wq [K, N], `Linear.scales` the per-channel
     scale."""
 
-    merges_attention = False  # its o projection is e4m3
     warms = False  # twice the int4 bytes: warming them measured slower (1105 -> 1042 tok/s)
 
     def __init__(self):
@@ -281,6 +280,15 @@ class OursFP8Backend(OursBackend):
         return rmsnorm_w8a16_matmul(x, w, eps, residual, p.qweight, p.scales, bias=p.bias)
 
     linear_norm_linear = Backend.linear_norm_linear  # the residual-statistics pair is W4A16
+
+    def attn_linear_norm_linear(self, ranges, p1: Linear, residual, w, eps, p2: Linear):
+        """linear_norm_linear with x the decode attention left as range partials: the FP8 o
+        projection merges the ranges in its x staging (kernels.fused.attn_w8a16_matmul), then the
+        residual + RMSNorm forms gate_up's activation (kernels.fused.rmsnorm_w8a16_matmul)."""
+        from kernels.fused import attn_w8a16_matmul, rmsnorm_w8a16_matmul
+
+        y = attn_w8a16_matmul(ranges, p1.qweight, p1.scales, p1.bias).view(residual.shape)
+        return rmsnorm_w8a16_matmul(y, w, eps, residual, p2.qweight, p2.scales, bias=p2.bias)
 
     def act_linear(self, gate_up, p: Linear):
         """One launch at decode: SwiGLU forms the FP8 down projection's activation

@@ -271,5 +271,36 @@ def rmsnorm_w8a16_matmul(x, weight, eps, residual, wq, scale, bias=None):
     return out, res_out
 
 
+def attn_w8a16_matmul(ranges, wq, scale, bias=None):
+    """y = w8a16_matmul(attention output, wq, scale) (+ bias) with the attention output the
+    per-range partials kernels.attention.decode_attention_ranges left (`ranges`): the projection
+    merges the ranges in its x staging (ldk_w8a16_attn_matmul), so the attention's merge launch
+    and the FP8 o projection are one launch. One row, K = 128 * heads, at most four ranges.
+    Returns [1, N] fp16."""
+    from kernels.fp8 import FP8
+
+    K, N = wq.shape
+    if wq.dtype != FP8 or scale.dtype != torch.float16 or scale.numel() != N:
+        raise ValueError("attn_w8a16_matmul: wq [K, N] float8_e4m3fn and fp16 scale [N]")
+    if K != 128 * ranges.n_heads:
+        raise ValueError("attn_w8a16_matmul: K must be 128 * the attention's heads")
+    # the C entry reads wq as [K, N] rows with 16-byte loads: a strided view would be read as
+    # the wrong elements
+    if not _aligned(wq):
+        raise ValueError("attn_w8a16_matmul: wq must be contiguous and 16-byte aligned")
+    dev = _lib.require_gpu(ranges.pos, wq, scale, bias, what="attn_w8a16_matmul")
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    sc = scale.contiguous()
+    out = torch.empty((1, N), dtype=torch.float16, device=dev)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w8a16_attn_matmul(
+            _lib.ptr(ranges.pos), ranges.max_len, ranges.rlen, ranges.n_heads, _lib.ptr(wq),
+            _lib.ptr(sc), _lib.ptr(b), _lib.ptr(out), N, K, ws, ws_bytes, _lib.stream(dev))
+    _lib.check(st, "attn_w8a16_matmul")
+    return out
+
+
 __all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "linear_rmsnorm_w4a16_matmul",
-           "rmsnorm_w8a16_matmul", "swiglu_w8a16_matmul"]
+           "attn_linear_rmsnorm_w4a16_matmul", "rmsnorm_w8a16_matmul", "swiglu_w8a16_matmul",
+           "attn_w8a16_matmul"]

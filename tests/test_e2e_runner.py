@@ -196,13 +196,16 @@ def test_fused_decode_attention_matches_torch_path(backend):
 
 
 @pytest.mark.gpu
-def test_attention_merged_in_o_projection_matches_merge_launch():
+@pytest.mark.parametrize("backend", ["ours", "ours_fp8"])
+def test_attention_merged_in_o_projection_matches_merge_launch(backend):
     """The default decode step (the attention's four position ranges merged in the o
-    projection's x staging) against the same runner with the attention's own output (one range,
-    no merge): close logits at every step across the range edges, identical KV caches."""
+    projection's x staging, W4A16 or e4m3) against the same runner with the attention's own
+    output (one range, no merge): close logits at every step across the range edges, identical
+    KV caches."""
     model = _qwen_heads_model("cuda")
-    merged = QwenRunner(model, make_backend("ours"), max_len=416)
-    plain = QwenRunner(model, make_backend("ours"), max_len=416)
+    merged = QwenRunner(model, make_backend(backend), max_len=416)
+    plain = QwenRunner(model, make_backend(backend), max_len=416)
+    assert merged.backend.merges_attention
     plain.merge_attention = False
     ids = torch.randint(0, 512, (1, 140), device="cuda")
     P = 120

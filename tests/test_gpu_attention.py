@@ -216,6 +216,79 @@ def test_ranges_merged_in_o_projection(L, pos):
         assert (d <= 2e-3 * ref.float().abs() + 2e-3).float().mean() >= 0.999
 
 
+@pytest.mark.parametrize("L,pos", [(416, 0), (416, 127), (416, 128), (416, 300), (416, 415),
+                                   (416, 700), (416, -3), (256, 255), (32, 5)])
+def test_ranges_merged_in_fp8_o_projection(L, pos):
+    """decode_attention_ranges + attn_w8a16_matmul (the ranges merged in the e4m3 o projection's
+    x staging) against decode_attention + w8a16_matmul on the same inputs, with bias: pos in and
+    at the edges of the four ranges of 416 positions, past the cache, negative (zeros), shorter
+    caches. The cache updates are bit-identical; y agrees to the north-star bound (the merged x
+    can differ from the merge launch's in the last fp16 bit)."""
+    from _util import assert_north_star
+    from kernels.attention import decode_attention_ranges, ranges_len
+    from kernels.fp8 import quantize_fp8, w8a16_matmul
+    from kernels.fused import attn_w8a16_matmul
+
+    nq, nkv, hd, H = 12, 2, 128, 1536
+    g = torch.Generator().manual_seed(2000 + L + pos)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    _, _, kt_a, vt_a = _caches(g, nkv, L)
+    kt_b, vt_b = kt_a.clone(), vt_a.clone()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    p = torch.tensor([pos], device="cuda")
+    wq, sc = quantize_fp8((torch.randn(H, nq * hd, generator=g) * 0.02).half().cuda())
+    bo = (torch.randn(H, generator=g) * 0.1).half().cuda()
+
+    attn = decode_attention(qkv, p, inv_freq, kt_a, vt_a, nq, nkv, hd ** -0.5)
+    y_ref = w8a16_matmul(attn.view(1, -1), wq, sc, bias=bo)
+    rng = decode_attention_ranges(qkv, p, inv_freq, kt_b, vt_b, nq, nkv, hd ** -0.5, ranges_len(L))
+    y = attn_w8a16_matmul(rng, wq, sc, bo)
+    assert torch.equal(kt_a, kt_b) and torch.equal(vt_a, vt_b)
+    assert torch.isfinite(y).all() and y.shape == (1, H)
+    assert_north_star(y.cpu(), y_ref.float().cpu().numpy())
+    d = (y.float() - y_ref.float()).abs()
+    assert (d <= 2e-3 * y_ref.float().abs() + 2e-3).float().mean() >= 0.999
+
+
+def test_fp8_ranges_consumer_checks_stream_and_geometry():
+    """The e4m3 o projection that merges the ranges is refused on another stream, with another
+    range length, or after decode_attention's own range launch overwrote the partials; the
+    attention's stream works; more than four ranges is refused before any launch."""
+    from kernels import _lib
+    from kernels.attention import decode_attention_ranges, ranges_len
+    from kernels.fp8 import quantize_fp8
+    from kernels.fused import attn_w8a16_matmul
+
+    nq, nkv, hd, H, L = 12, 2, 128, 1536, 416
+    g = torch.Generator().manual_seed(79)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    _, _, kt, vt = _caches(g, nkv, L)
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    wq, sc = quantize_fp8((torch.randn(H, nq * hd, generator=g) * 0.02).half().cuda())
+    p = torch.tensor([300], device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        rng = decode_attention_ranges(qkv, p, inv_freq, kt, vt, nq, nkv, hd ** -0.5, ranges_len(L))
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="another stream"):
+        attn_w8a16_matmul(rng, wq, sc)
+    with torch.cuda.stream(side):
+        y = attn_w8a16_matmul(rng, wq, sc)
+        with pytest.raises(ValueError, match="rlen"):
+            attn_w8a16_matmul(rng._replace(rlen=L), wq, sc)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    _, _, kt2, vt2 = _caches(g, nkv, 1024)
+    decode_attention(qkv, torch.tensor([900], device="cuda"), inv_freq, kt2, vt2, nq, nkv, hd ** -0.5)
+    with pytest.raises(ValueError, match="pending"):
+        attn_w8a16_matmul(rng, wq, sc)
+    lib = _lib.load()
+    st = lib.ldk_w8a16_attn_matmul(_lib.ptr(p), 416, 64, 12, _lib.ptr(wq), _lib.ptr(sc), None,
+                                   _lib.ptr(wq), H, nq * hd, None, 0, None)
+    assert st == _lib.ERR_UNSUPPORTED
+
+
 def test_ranges_entry_rejects_bad_ranges():
     """More than the four ranges the o projection merges, or a range length that is not a
     multiple of 32, is refused before any launch."""
