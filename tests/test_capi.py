@@ -181,6 +181,39 @@ def test_fused_entries_validate_before_launch():
     assert st == _lib.ERR_INVALID
 
 
+def test_attention_merge_entries_validate_before_launch():
+    """The o projections that merge the decode attention's range partials in their x staging
+    (int4 and e4m3) check the head geometry, the ranges and the pointers before they look for the
+    partials or launch."""
+    lib = _lib.load()
+    p, q = ctypes.c_void_p(256), ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(264)  # 8-byte but not 16-byte aligned
+
+    def w8(pos=p, max_len=416, rlen=128, nq=12, wq=p, N=1536, K=1536, ws=None, ws_bytes=0):
+        return _err(lib.ldk_w8a16_attn_matmul(pos, max_len, rlen, nq, wq, q, None, q, N, K, ws, ws_bytes, None))
+
+    assert w8(pos=None)[0] == _lib.ERR_INVALID
+    assert w8(nq=11)[0] == _lib.ERR_INVALID  # K != nq * 128
+    assert w8(nq=0, K=0)[0] == _lib.ERR_INVALID
+    st, msg = w8(rlen=48)  # not a multiple of 32
+    assert st == _lib.ERR_UNSUPPORTED and "ranges" in msg
+    assert w8(max_len=4096)[0] == _lib.ERR_UNSUPPORTED  # 32 ranges of 128: more than the merge holds
+    assert w8(N=42)[0] == _lib.ERR_UNSUPPORTED
+    assert w8(wq=odd)[0] == _lib.ERR_ALIGN
+    assert w8(ws_bytes=1 << 20)[0] == _lib.ERR_ALIGN  # a workspace size without a workspace
+
+    def w4(pos=p, max_len=416, rlen=128, nq=12, K=1536, gs=128, h_out=q):
+        return _err(lib.ldk_w4a16_attn_matmul_residual_stats(pos, max_len, rlen, nq, p, h_out, q, p, p, p, None,
+                                                             1536, K, gs, None, 0, None))
+
+    assert w4(pos=None)[0] == _lib.ERR_INVALID
+    assert w4(nq=11)[0] == _lib.ERR_INVALID
+    assert w4(gs=64)[0] == _lib.ERR_UNSUPPORTED
+    assert w4(rlen=48)[0] == _lib.ERR_UNSUPPORTED
+    assert w4(max_len=1024)[0] == _lib.ERR_UNSUPPORTED  # 8 ranges of 128
+    assert w4(h_out=ctypes.c_void_p(4100))[0] == _lib.ERR_ALIGN
+
+
 def test_w8a16_n_multiple_of_4():
     """The reference masks columns, so any N runs there (N = 40 in tests/test_fp8.py:40); here N
     must be a multiple of 4 (N = 40 plans, N = 42 is refused before any launch)."""
