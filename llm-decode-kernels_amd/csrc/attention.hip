@@ -33,12 +33,15 @@
 //    softmax across the wave's chunks, sums in fp32.
 //  - The waves' (m, l, O) meet once through LDS at the end.
 // The cache at pos is stale while the workgroup holding pos writes the new k/v, so the score at
-// pos is taken from q . k_new and the V^T registers at pos are replaced by v_new. With several
-// ranges, every range stores its partial (running max m, sum l, unnormalised output o[128] per
-// head) to library-owned device memory, and a second launch on the same stream merges them: the
-// kernel boundary orders the stores before the loads, which a last-arriver merge inside the range
-// kernel pays for with three device-coherent round trips (partial stores, a counter atomic,
-// partial loads). Calls on one device must be stream-ordered (the partials are shared).
+// pos is taken from q . k_new and the V^T registers at pos are replaced by v_new. The rows past
+// pos in the last live chunk may hold any bits (an earlier generation's, or never written): their
+// scores are selected to -inf and their V^T entries zeroed in registers, so NaN or inf there
+// cannot reach P.V as 0 x NaN.
+// With several ranges, every range stores its partial (running max m, sum l, unnormalised output
+// o[128] per head) to library-owned device memory, and a second launch on the same stream merges
+// them: the kernel boundary orders the stores before the loads, which a last-arriver merge inside
+// the range kernel pays for with three device-coherent round trips (partial stores, a counter
+// atomic, partial loads). Calls on one device must be stream-ordered (the partials are shared).
 // The range entry can give the launch extra workgroups, dispatched after the attention's, that
 // read byte ranges (the next projections' weights) into the caches while the attention's few
 // workgroups leave the other CUs idle.
@@ -132,6 +135,22 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ float4_t mfma16(u32x4 a, u32x4 b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
+
+// Clears the V^T operand entries of the positions past the last one attended to. In each of a
+// chunk's 8 V^T tiles, lane (c16, kb) holds 8 consecutive positions of one dim, entry e (the
+// halves of dword e / 2) at position 8kb + e of the chunk; entries e > last are zeroed. Their
+// softmax weights are exactly 0, but those cache rows are not this call's data and may hold any
+// bits, and 0 x NaN or 0 x inf in P.V would be NaN. Finite values there give the same sums with
+// or without the clearing.
+__device__ __forceinline__ void keep_v_through(u32x4 (&v)[8], int last) {
+  uint32_t mk[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) mk[j] = (2 * j <= last ? 0x0000FFFFu : 0u) | (2 * j + 1 <= last ? 0xFFFF0000u : 0u);
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[t][j] &= mk[j];
 }
 
 // Warming workgroups (warm.h) of the attention's launch: 16 loads per lane, at most one per CU
@@ -334,6 +353,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
           vr[n][b] = __builtin_bit_cast(u32x4, hv);
         }
       }
+      if (cb + kChunk - 1 > pos) keep_v_through(vr[n], pos - cb - 8 * kb);  // uniform per wave
       // rescale O: the heads of this lane's accumulator rows are 4kb .. 4kb+3
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -475,7 +495,8 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(const int64_t* pos_
 //     a kv head's query heads. Column c16 (token t0 + c16) attends to the cache positions
 //     0..pos[t0 + c16] with its own mask, so every token is causal whatever the order of pos.
 //     Wave w takes the 32-position chunks w, w + 4, ... up to the block's last position, two
-//     chunks' tiles in flight at a time; the waves' (m, l, O) meet through LDS.
+//     chunks' tiles in flight at a time; the waves' (m, l, O) meet through LDS. The V^T entries
+//     past the block's last position are zeroed in registers, as in the decode kernel.
 // The launch boundary orders the cache writes of launch 1 before the reads of launch 2.
 constexpr int kPWaves = 4;
 
@@ -601,6 +622,7 @@ __global__ __launch_bounds__(kPWaves * 64) void prefill_attention_kernel(const h
         ph[e] = (half_t)x;
       }
       l_lane = l_lane * alpha + ls;
+      if (cb + kChunk - 1 > pmax) keep_v_through(vr[n], pmax - cb - 8 * kb);  // uniform per wave
 #pragma unroll
       for (int r = 0; r < 4; ++r) {  // the tokens of this lane's accumulator rows are 4kb .. 4kb+3
         const float al = __shfl(alpha, 4 * kb + r);

@@ -504,3 +504,54 @@ def test_prefill_positions_out_of_order_and_out_of_range():
     out = prefill_attention(qkv[:3].cuda().view(1, 3, -1), pos.cuda(), inv, kt, vt, nq, nkv, hd ** -0.5)
     assert torch.equal(kt, kt0) and torch.equal(vt, vt0)
     assert torch.isfinite(out).all() and torch.equal(out[0, 1], torch.zeros_like(out[0, 1]))
+
+
+def _fill_past(kc, vc, last, fill):
+    """Copies of the [1, nkv, L, hd] caches with every row past position `last` set to `fill`."""
+    k2, v2 = kc.clone(), vc.clone()
+    k2[:, :, last + 1:] = fill
+    v2[:, :, last + 1:] = fill
+    return k_to_tiles(k2).cuda(), vt_to_tiles(v2).cuda()
+
+
+_FILLS = (0.0, float("nan"), float("inf"), float("-inf"))
+
+
+@pytest.mark.parametrize("L,pos", [(416, 0), (416, 130), (416, 383), (416, 414), (2144, 2100),
+                                   (4096, 1000), (4096, 4000)])
+def test_cache_rows_past_pos_can_hold_any_bits(L, pos):
+    """The cache rows past pos are not this call's data (an earlier generation's, or never
+    written) and may hold any bits. Their softmax weights are 0; the output with NaN or inf in
+    them is the output with zeros in them, bit for bit, with one position range (416) and with
+    ranges merged by the second launch (2144, 4096). A P.V that multiplied those rows by their
+    zero weights would give NaN."""
+    nq, nkv, hd = 12, 2, 128
+    g = torch.Generator().manual_seed(pos + L)
+    qkv = torch.randn((nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, 1, -1)
+    kc, vc, _, _ = _caches(g, nkv, L)
+    inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    p = torch.tensor([pos], device="cuda")
+    outs = [decode_attention(qkv, p, inv, *_fill_past(kc, vc, pos, f), nq, nkv, hd ** -0.5) for f in _FILLS]
+    assert torch.isfinite(outs[0]).all()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+@pytest.mark.parametrize("p0,T", [(0, 17), (100, 50), (5, 40)])
+def test_prefill_cache_rows_past_the_prompt_can_hold_any_bits(p0, T):
+    """ldk_prefill_attention: rows past the prompt's last position hold NaN or inf, and every
+    token's output is the one with zeros there, bit for bit. In each case the prompt ends inside
+    a 32-position chunk, which its last 16-token block reads whole."""
+    from kernels.attention import prefill_attention
+
+    nq, nkv, L, hd = 12, 2, 416, 128
+    g = torch.Generator().manual_seed(p0 + T)
+    qkv = torch.randn(T, (nq + 2 * nkv) * hd, generator=g).half().cuda().view(1, T, -1)
+    kc, vc, _, _ = _caches(g, nkv, L)
+    inv = (1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))).cuda()
+    pos = torch.arange(p0, p0 + T, dtype=torch.int64, device="cuda")
+    outs = [prefill_attention(qkv, pos, inv, *_fill_past(kc, vc, p0 + T - 1, f), nq, nkv, hd ** -0.5)
+            for f in _FILLS]
+    assert torch.isfinite(outs[0]).all()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
