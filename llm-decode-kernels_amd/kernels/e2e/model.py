@@ -473,14 +473,14 @@ class QwenRunner:
     def warm_set(self, i: int) -> list:
         """What the fused decode attention of layer i reads into the caches with its spare
         workgroups (kernels.attention.decode_attention_ranges / decode_attention) while its few
-        workgroups run: the weights of the o, gate_up and down projections after it, the o and
-        gate_up scales and zeros, and the next layer's qkv weight (at most 8 ranges)."""
+        workgroups run: the weights of the o and gate_up projections after it, their scales and
+        zeros, and the next layer's qkv weight (at most 8 ranges). The down projection's weight
+        is left out: the warming then ends earlier than down's own reads gain from it."""
         def main(p: Linear):
             return p.qweight if p.qweight is not None else p.w
 
         L = self.layers[i]
-        ts = [main(L.o), main(L.gate_up), main(L.down), L.o.scales, L.o.zeros,
-              L.gate_up.scales, L.gate_up.zeros]
+        ts = [main(L.o), main(L.gate_up), L.o.scales, L.o.zeros, L.gate_up.scales, L.gate_up.zeros]
         if i + 1 < len(self.layers):
             ts.append(main(self.layers[i + 1].qkv))
         return [t for t in ts if t is not None]
