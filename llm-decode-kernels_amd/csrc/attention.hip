@@ -15,12 +15,12 @@
 //    dims 16b .. 16b + 15 at positions 32t .. 32t + 31.
 // max_len is a multiple of 32.
 //
-// Work split. One workgroup of 8 waves serves up to 16 query heads of one kv head (all of them
-// for every GQA shape up to 16 heads per kv head), so each K and V byte of a head is read once
-// per launch, and its products run on the matrix cores (v_mfma_f32_16x16x32_f16, the 16 heads are
-// the tile's columns). Caches of more than 512 positions are cut into up to 32 position ranges
+// Work split. One workgroup of NW waves (8; 4 where a range holds at most 4 chunks) serves up to
+// 16 query heads of one kv head (all of them for every GQA shape up to 16 heads per kv head), so
+// each K and V byte of a head is read once per launch, and its products run on the matrix cores
+// (v_mfma_f32_16x16x32_f16, the 16 heads are the tile's columns). Caches of more than 512 positions are cut into up to 32 position ranges
 // of at least 128 positions, with one workgroup per (head tile, range).
-//  - Wave w takes the 32-position chunks w, w + 8, ... of its range, two at a time, and loads
+//  - Wave w takes the 32-position chunks w, w + NW, ... of its range, two at a time, and loads
 //    each chunk's 8 K tiles and 8 V^T tiles (16 KB, all live) before its first use. The RoPE
 //    needs no barrier: each lane ropes exactly the q and k dims of its own MFMA operands from
 //    loads issued ahead of its first chunk's. The number of chunks in flight is a template
@@ -60,7 +60,6 @@
 namespace {
 
 constexpr int kHD = 128;
-constexpr int kWaves = 8;
 constexpr int kTile = 16;    // query heads per workgroup: the MFMA tile's 16 columns
 constexpr int kChunk = 32;   // positions per score chunk and per P.V step
 constexpr int kBlock = 512;  // positions per softmax block: 16 chunks, two per wave
@@ -153,28 +152,36 @@ __device__ __forceinline__ void keep_v_through(u32x4 (&v)[8], int last) {
     for (int j = 0; j < 4; ++j) v[t][j] &= mk[j];
 }
 
-// Warming workgroups (warm.h) of the attention's launch: 16 loads per lane, at most one per CU
-// beside the attention's (208 VGPRs: one 512-lane workgroup per CU).
-constexpr int kWarmLoads = 16;
+// Warming workgroups (warm.h) of the attention's launch: 128 KB each (16 loads per lane at 8
+// waves, 32 at 4), at most one per CU beside the attention's.
+constexpr int kWarmLoads = 16;  // per lane at 8 waves
 constexpr int kWarmWorkgroups = 248;
+
+// Waves per attention workgroup: 4 where a range holds at most 4 chunks (each wave one chunk; 8
+// waves would leave four with no chunk that still rope their operands and join the LDS merge),
+// else 8. Graph-timed at a 416-position cache in ranges of 128: the range launch 5.50 / 6.00 /
+// 6.35 -> 5.14 / 5.24 / 5.54 us at pos 130 / 250 / 383.
+int attn_waves(int64_t rlen) { return rlen <= 4 * kChunk ? 4 : 8; }
+constexpr int warm_loads(int nw) { return kWarmLoads * 8 / nw; }
 
 template <int N>
 struct IntC {
   static constexpr int value = N;
 };
 
-__global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs a) {
-  __shared__ __align__(16) half_t vnew[kWaves][kHD];     // v_new by dim, one copy per wave
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void decode_attention_kernel(AttnArgs a) {
+  __shared__ __align__(16) half_t vnew[NW][kHD];     // v_new by dim, one copy per wave
   __shared__ __align__(16) half_t knew[kHD];              // the roped k_new, for wave 0's cache write
-  __shared__ __align__(16) half_t cs[kWaves][2][64];      // RoPE cos, sin by dim, per wave
-  __shared__ float mw[kWaves][kTile], lw[kWaves][kTile];  // per-wave max and sum per head
-  __shared__ __align__(16) float ow[kWaves][kTile][kHD];  // per-wave unnormalised outputs
+  __shared__ __align__(16) half_t cs[NW][2][64];      // RoPE cos, sin by dim, per wave
+  __shared__ float mw[NW][kTile], lw[NW][kTile];  // per-wave max and sum per head
+  __shared__ __align__(16) float ow[NW][kTile][kHD];  // per-wave unnormalised outputs
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, no waterfalls
   const int c16 = lane & 15, kb = lane >> 4;
   const int gq = a.nq / a.nkv;
   if ((int)blockIdx.x >= a.nattn) {  // uniform: a warming workgroup (dispatched after the attention's)
-    ldk::warm_read<kWaves * 64, kWarmLoads>(a.warm, blockIdx.x - a.nattn);
+    ldk::warm_read<NW * 64, warm_loads(NW)>(a.warm, blockIdx.x - a.nattn);
     return;
   }
   // workgroup b = split * (nkv * ntile) + kvh * ntile + tile
@@ -194,7 +201,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   if (split >= nlive) return;  // uniform over the workgroup
   const int cend = min(s0 + S, pos + 1);  // live positions [s0, cend): empty when pos < 0
   const int ncl = cend > s0 ? (cend - s0 + kChunk - 1) / kChunk : 0;  // live chunks of the range
-  const int nk = ncl > wave ? (ncl - wave + kWaves - 1) / kWaves : 0; // this wave's chunks
+  const int nk = ncl > wave ? (ncl - wave + NW - 1) / NW : 0; // this wave's chunks
   const auto krs = ldk::buffer_rsrc(a.k + (int64_t)kvh * L * kHD, (uint32_t)L * kHD * 2);
   const auto vrs = ldk::buffer_rsrc(a.vt + (int64_t)kvh * kHD * L, (uint32_t)L * kHD * 2);
   // a tile is 16 rows of 64 bytes; lane (c16, kb) takes row c16, bytes 16kb .. 16kb + 15 (its
@@ -298,7 +305,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     constexpr int NC = decltype(ncc)::value;
     u32x4 kr[NC][8], vr[NC][8];
     auto load = [&](int n) __attribute__((always_inline)) {
-      const int c = (s0 >> 5) + wave + kWaves * (k0 + n);
+      const int c = (s0 >> 5) + wave + NW * (k0 + n);
 #pragma unroll
       for (int t = 0; t < 8; ++t) kr[n][t] = ldk::buffer_load16(krs, (uint32_t)((c * 8 + t) * kTileHalves * 2) + lane_off);
 #pragma unroll
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     for (int n = 1; n < NC; ++n) load(n);
 #pragma unroll
     for (int n = 0; n < NC; ++n) {
-      const int cb = s0 + kChunk * (wave + kWaves * (k0 + n));
+      const int cb = s0 + kChunk * (wave + NW * (k0 + n));
       float4_t acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -411,25 +418,25 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     }
   ldk::lds_barrier();
   // thread item (head j, dim d): weights exp(m_w - M) of the waves that saw a live position. All
-  // 3 x kWaves LDS reads are issued before the first use and the dead waves get weight 0 (their l
+  // 3 x NW LDS reads are issued before the first use and the dead waves get weight 0 (their l
   // and O are 0, so the FMA adds nothing) instead of a branch, which made each wave's reads wait
   // for the previous wave's exp (0.65 us of a 6.4 us launch at 130 live positions)
   const bool single = nlive == 1 && !a.partials;
-  for (int e = tid; e < nh * kHD; e += kWaves * 64) {
+  for (int e = tid; e < nh * kHD; e += NW * 64) {
     const int j = e >> 7, d = e & (kHD - 1);
-    float mv[kWaves], lv[kWaves], ov[kWaves];
+    float mv[NW], lv[NW], ov[NW];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       mv[w] = mw[w][j];
       lv[w] = lw[w][j];
       ov[w] = ow[w][j][d];
     }
     float M = -__builtin_inff();
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mv[w]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, mv[w]);
     float l = 0.0f, acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float f = mv[w] != -__builtin_inff() ? __expf(mv[w] - M) : 0.0f;
       l = __builtin_fmaf(lv[w], f, l);
       acc = __builtin_fmaf(ov[w], f, acc);
@@ -713,13 +720,18 @@ extern "C" int ldk_decode_attention(const void* qkv, const int64_t* pos, const f
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
   ldk::WarmRanges w;
   uint32_t nwg = 0;
-  if (const int st = ldk::make_warm(warm, warm_bytes, nwarm, "decode_attention", kWaves * 64, kWarmLoads, kWarmWorkgroups, w, nwg))
+  const int nw = attn_waves(rlen);
+  if (const int st = ldk::make_warm(warm, warm_bytes, nwarm, "decode_attention", nw * 64, warm_loads(nw),
+                                    kWarmWorkgroups, w, nwg))
     return st;
   const int nattn = nkv * ntile * nsplit;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, (half_t*)out,
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 0, nattn, w};
   (void)hipGetLastError();
-  decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
+  if (nw == 4)
+    decode_attention_kernel<4><<<nattn + nwg, 4 * 64, 0, (hipStream_t)stream>>>(a);
+  else
+    decode_attention_kernel<8><<<nattn + nwg, 8 * 64, 0, (hipStream_t)stream>>>(a);
   if (nsplit > 1) {
     attention_merge_kernel<<<nq, 64, 0, (hipStream_t)stream>>>(pos, (half_t*)out, (int)max_len, (int)rlen);
     ldk::note_partials(false, stream, nullptr, 0, 0, 0);  // the partials of a pending range call are overwritten
@@ -752,14 +764,18 @@ extern "C" int ldk_decode_attention_ranges(const void* qkv, const int64_t* pos, 
   const int gq = nq / nkv, ntile = (gq + kTile - 1) / kTile;
   ldk::WarmRanges w;
   uint32_t nwg = 0;
-  if (const int st = ldk::make_warm(warm, warm_bytes, nwarm, "decode_attention_ranges", kWaves * 64, kWarmLoads,
+  const int nw = attn_waves(rlen);
+  if (const int st = ldk::make_warm(warm, warm_bytes, nwarm, "decode_attention_ranges", nw * 64, warm_loads(nw),
                                     kWarmWorkgroups, w, nwg))
     return st;
   const int nattn = nkv * ntile * nsplit;
   const AttnArgs a{(const half_t*)qkv, pos, inv_freq, (half_t*)k_cache, (half_t*)vt_cache, nullptr,
                    nq, nkv, (int)max_len, ntile, (int)rlen, scale, 1, nattn, w};
   (void)hipGetLastError();
-  decode_attention_kernel<<<nattn + nwg, kWaves * 64, 0, (hipStream_t)stream>>>(a);
+  if (nw == 4)
+    decode_attention_kernel<4><<<nattn + nwg, 4 * 64, 0, (hipStream_t)stream>>>(a);
+  else
+    decode_attention_kernel<8><<<nattn + nwg, 8 * 64, 0, (hipStream_t)stream>>>(a);
   const int st = ldk::check_launch("decode_attention_ranges");
   ldk::note_partials(st == LDK_OK, stream, pos, max_len, rlen, nq);
   return st;
