@@ -363,6 +363,19 @@ int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int ns
                                    void* out, int64_t N, int64_t K, int group_size,
                                    void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Prefill rows of a gate_up projection with SwiGLU in the prefill GEMM's epilogue. No counterpart
+ * entry exists in the reference, whose runner runs the activation as a kernel of its own
+ * (kernels/e2e/model.py:79-97, kernels/swiglu.py:49-61). out [M, N/2] (row stride ldo >= N/2,
+ * ldo % 4 == 0, 8-byte aligned) = swiglu_fused(x @ dequant(W)^T (+ bias)) with g the product's
+ * columns [0, N/2) and u [N/2, N): the standalone SwiGLU's steps on the fp16 products, so bit for
+ * bit ldk_w4a16_matmul then ldk_swiglu. Only where ldk_w4a16_matmul_swiglu_applies(M, N, K,
+ * group_size) returns 1 (the library's plan for the shape is the prefill GEMM on paired column
+ * groups of at most 4 row tiles, with no K split); else LDK_ERR_UNSUPPORTED and no launch. */
+int ldk_w4a16_matmul_swiglu_applies(int64_t M, int64_t N, int64_t K, int group_size);
+int ldk_w4a16_matmul_swiglu(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                            const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N,
+                            int64_t K, int group_size, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------- greedy decode bookkeeping */
 
 /* idx = argmax(logits[0:V]) (torch.argmax order: NaN largest, lowest index on ties), then

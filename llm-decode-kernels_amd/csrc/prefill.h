@@ -30,6 +30,11 @@ struct GemmArgs {
   int64_t workspace_bytes;
   int block_n;       // output-tile width 128 or 256 (0: the library's choice)
   int split_k;       // workgroups splitting K per tile (0: the library's choice)
+  // 1: SwiGLU fused into the epilogue. The product's columns [0, N/2) are g and [N/2, N) are u
+  // (the reference's swiglu_fused halves); out [M, N/2] (row stride ldo) receives
+  // fp16(silu(g)) * u of the fp16-rounded products, the standalone SwiGLU's steps. Only where
+  // gemm_swiglu_applies.
+  int swiglu = 0;
 };
 
 // Whether the prefill GEMM takes this shape (K a multiple of 64; kInt4: group_size >= 64, N a
@@ -44,6 +49,12 @@ int gemm_launch(WFmt f, const GemmArgs& a, hipStream_t stream);
 // shape with these tuning arguments and a workspace of ws_bytes (for plan queries).
 void gemm_plan(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes, int* tile_n,
                int* splits);
+
+// Whether gemm_launch takes GemmArgs::swiglu for this shape: a plan of at least two column groups
+// per workgroup (half of them compute g, the other half the matching u columns), no K split, and
+// N / 2 a multiple of the workgroup's g columns.
+bool gemm_swiglu_applies(WFmt f, int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, int block_n,
+                         int split_k, int64_t ws_bytes);
 
 // Name of the kernel instantiation gemm_launch runs for a shape (for reports).
 const char* gemm_kernel_name(WFmt f, int64_t M, int64_t N, int64_t K, int block_n);

@@ -162,7 +162,7 @@ struct GemmCfg {
 // WAVES waves walks its half through its own ring (the second half of every stage array), and the
 // groups' accumulators meet in LDS at the end. That doubles the waves on a tile without the fp32
 // partials in memory that a split over workgroups costs.
-template <WFmt F, int WAVES, int MT, int S, int KG>
+template <WFmt F, int WAVES, int MT, int S, int KG, bool SW>
 __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float* partial, int mfast) {
   using C = GemmCfg<F, WAVES, MT, S>;
   using T = Fmt<F>;
@@ -188,7 +188,13 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
   // subset of the row tiles: its slice of x stays in its L2 and each weight tile it reads serves
   // all of its row tiles. Otherwise x walks the column tiles.
   const int bn = mfast ? blockIdx.y : blockIdx.x, bm = mfast ? blockIdx.x : blockIdx.y;
-  const int n0 = bn * (64 * WAVES) + 64 * wave;
+  // SwiGLU fused (SW, a.swiglu): column groups [0, WAVES/2) take g columns, the others the
+  // matching u columns N/2 further on
+  static_assert(!SW || (WAVES >= 2 && WAVES % 2 == 0), "SwiGLU pairs column groups");
+  constexpr int HW = WAVES / 2;
+  const bool up = SW && wave >= HW;
+  const int n0 = !SW ? bn * (64 * WAVES) + 64 * wave
+                     : (up ? a.N / 2 : 0) + bn * (64 * HW) + 64 * (up ? wave - HW : wave);
   const int m0 = bm * BM;
   const int mrows = min(a.M - m0, BM);
   // K-steps [kbeg, kbeg + nks) of split blockIdx.z; K group g takes [kbeg + g h, + gn) of them
@@ -366,6 +372,56 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
       for (int j = 0; j < NT; ++j) acc[t][j] += (t < MH ? red0 : red1)[((wave * MH + t % MH) * NT + j) * 64 + lane];
   }
 
+  if constexpr (SW) {
+    {
+      // every wave rounds its tile as the plain epilogue does (column scale, bias, fp16); the u
+      // waves hand theirs to the g waves through LDS, lane for lane (the same rows and columns
+      // of the pair), and the g waves store fp16(silu(g)) * u
+      static_assert(MT * 4 * 64 * 8 <= SLOT, "a wave's fp16 tile fits one stage slot");
+      const int c = n0 + 4 * c16;
+      if constexpr (!kInt4) {  // the plain epilogue's steps: column scale, then bias, then fp16
+        const float cs[4] = {(float)a.s[c], (float)a.s[c + 1], (float)a.s[c + 2], (float)a.s[c + 3]};
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[t][j] *= cs[j];
+      }
+      float4_t b4 = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      if (a.bias) b4 = float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
+      half4_t o[MT][4];
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[t][i] = half4_t{(half_t)(acc[t][0][i] + b4[0]), (half_t)(acc[t][1][i] + b4[1]), (half_t)(acc[t][2][i] + b4[2]),
+                            (half_t)(acc[t][3][i] + b4[3])};
+      ring_barrier();  // every wave is past its last read of the stage slots
+      static_assert(HW <= 2, "the pairs' exchange slots are st0 and st1");
+      half4_t* xs = reinterpret_cast<half4_t*>((up ? wave - HW : wave) == 0 ? st0 : st1);
+      if (up) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xs[(t * 4 + i) * 64 + lane] = o[t][i];
+      }
+      ring_barrier();
+      if (up) return;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * t + 4 * kb + i;
+          const half4_t u = xs[(t * 4 + i) * 64 + lane];
+          half4_t v;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = ldk::silu_f16(o[t][i][j]);
+          if (r < mrows) *reinterpret_cast<half4_t*>(a.out + (int64_t)(m0 + r) * a.ldo + c) = v * u;  // fp16 multiply
+        }
+      }
+      return;
+    }
+  }
+
   // acc[t][j][i] is row 16t + 4kb + i of the tile, column n0 + 4 * c16 + j
   const int c = n0 + 4 * c16;
   if (c >= a.N) return;
@@ -408,14 +464,31 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
 template <int WAVES, int MT, int S, int KG>
 __global__ __launch_bounds__(WAVES * KG * 64) __attribute__((amdgpu_waves_per_eu(2))) void w4a16_gemm_kernel(
     ldk::GemmArgs a, int kps, float* partial, int mfast) {
-  gemm_body<WFmt::kInt4, WAVES, MT, S, KG>(a, kps, partial, mfast);
+  gemm_body<WFmt::kInt4, WAVES, MT, S, KG, false>(a, kps, partial, mfast);
 }
 
 template <int WAVES, int MT, int S, int KG>
 __global__ __launch_bounds__(WAVES * KG * 64) __attribute__((amdgpu_waves_per_eu(2))) void w8a16_gemm_kernel(
     ldk::GemmArgs a, int kps, float* partial, int mfast) {
-  gemm_body<WFmt::kE4M3, WAVES, MT, S, KG>(a, kps, partial, mfast);
+  gemm_body<WFmt::kE4M3, WAVES, MT, S, KG, false>(a, kps, partial, mfast);
 }
+
+// The same GEMMs with SwiGLU in the epilogue (GemmArgs::swiglu; no K split).
+template <int WAVES, int MT, int S, int KG>
+__global__ __launch_bounds__(WAVES * KG * 64) __attribute__((amdgpu_waves_per_eu(2))) void w4a16_gemm_swiglu_kernel(
+    ldk::GemmArgs a, int kps, int mfast) {
+  gemm_body<WFmt::kInt4, WAVES, MT, S, KG, true>(a, kps, nullptr, mfast);
+}
+
+template <int WAVES, int MT, int S, int KG>
+__global__ __launch_bounds__(WAVES * KG * 64) __attribute__((amdgpu_waves_per_eu(2))) void w8a16_gemm_swiglu_kernel(
+    ldk::GemmArgs a, int kps, int mfast) {
+  gemm_body<WFmt::kE4M3, WAVES, MT, S, KG, true>(a, kps, nullptr, mfast);
+}
+
+// Tiles that take the SwiGLU epilogue: paired column groups, and at most 4 row tiles (the 8-row-tile
+// accumulators leave no registers for the rounded pair)
+constexpr bool swiglu_tile(int waves, int mt) { return waves >= 2 && waves % 2 == 0 && mt <= 4; }
 
 // y[m, n] = fp16(sum over splits of partial[split][m][n] (x colscale[n]) (+ bias[n])), the splits
 // added in index order (the result does not depend on which split finished first). 4 columns per
@@ -543,6 +616,16 @@ int launch(const ldk::GemmArgs& a, int splits, int mfast, hipStream_t s) {
   if (tn > 65535) mfast = 0;  // the column tiles then stay in the grid's x dimension
   const dim3 grid = mfast ? dim3((unsigned)tm, (unsigned)tn, (unsigned)nz) : dim3((unsigned)tn, (unsigned)tm, (unsigned)nz);
   (void)hipGetLastError();
+  if constexpr (swiglu_tile(WAVES, MT)) {
+    if (a.swiglu) {  // gemm_launch has checked the plan: no K split
+      if constexpr (F == WFmt::kInt4)
+        w4a16_gemm_swiglu_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, mfast);
+      else
+        w8a16_gemm_swiglu_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, mfast);
+      return ldk::check_launch(F == WFmt::kInt4 ? "w4a16_gemm_swiglu" : "w8a16_gemm_swiglu");
+    }
+  }
+  if (a.swiglu) return ldk::fail(LDK_ERR_UNSUPPORTED, "gemm: SwiGLU epilogue not built for %d x %d tiles", WAVES, MT);
   if constexpr (F == WFmt::kInt4)
     w4a16_gemm_kernel<WAVES, MT, S, KG><<<grid, WAVES * KG * 64, 0, s>>>(a, kps, partial, mfast);
   else
@@ -602,9 +685,21 @@ int gemm_launch(WFmt f, const GemmArgs& a, hipStream_t s) {
   if (!gemm_supported(f, a.M, a.N, a.K, a.group_size, a.ldx))
     return fail(LDK_ERR_UNSUPPORTED, "%s: shape M=%d N=%d K=%d group_size=%d not supported", fn, a.M, a.N, a.K,
                 a.group_size);
+  if (a.swiglu && !gemm_swiglu_applies(f, a.M, a.N, a.K, a.group_size, a.ldx, a.block_n, a.split_k,
+                                       a.workspace ? a.workspace_bytes : 0))
+    return fail(LDK_ERR_UNSUPPORTED, "%s: SwiGLU in the epilogue needs a plan of two or more column groups with no K "
+                "split (M=%d N=%d K=%d)", fn, a.M, a.N, a.K);
   if (a.block_n && a.block_n != 128 && a.block_n != 256)
     return fail(LDK_ERR_UNSUPPORTED, "%s: block_n=%d must be 128 or 256", fn, a.block_n);
   return f == WFmt::kInt4 ? launch_fmt<WFmt::kInt4>(a, s) : launch_fmt<WFmt::kE4M3>(a, s);
+}
+
+bool gemm_swiglu_applies(WFmt f, int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, int block_n,
+                         int split_k, int64_t ws_bytes) {
+  if (N % 2 || !gemm_supported(f, M, N, K, group_size, ldx)) return false;
+  const GemmShape sh = pick_shape(f, M, N, K, block_n, split_k, ws_bytes);
+  const int steps = (int)(K / kStep), kps = (steps + sh.splits - 1) / sh.splits;
+  return swiglu_tile(sh.waves, sh.mt) && (steps + kps - 1) / kps == 1 && (N / 2) % (64 * (sh.waves / 2)) == 0;
 }
 
 void gemm_plan(WFmt f, int64_t M, int64_t N, int64_t K, int block_n, int split_k, int64_t ws_bytes, int* tile_n,

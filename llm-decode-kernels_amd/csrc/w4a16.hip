@@ -1992,6 +1992,40 @@ static int w4a16_matmul_impl(const char* fn, const void* x, int64_t ldx, const i
   return launch_plan(a, c.p, workspace, (hipStream_t)stream);
 }
 
+// Prefill rows of the gate_up projection with SwiGLU in the GEMM's epilogue: out [M, N/2] =
+// swiglu_fused(x @ dequant(W)^T (+ bias)) with the standalone SwiGLU's steps on the fp16 products,
+// where the library's plan for [M, N, K] is the prefill GEMM with two or more column groups and no
+// K split (ldk_w4a16_matmul_swiglu_applies); the fused SwiGLU launch and the [M, N] round trip
+// through memory go away.
+static bool swiglu_gemm_applies(int64_t M, int64_t N, int64_t K, int group_size, int64_t ldx, int64_t ws_bytes) {
+  return N % 8 == 0 && uses_gemm(M, N, K, group_size, ldx, nullptr, N, 0, 0, 0) &&
+         ldk::gemm_swiglu_applies(ldk::WFmt::kInt4, M, N, K, group_size, ldx, 0, 0, ws_bytes);
+}
+
+extern "C" int ldk_w4a16_matmul_swiglu_applies(int64_t M, int64_t N, int64_t K, int group_size) {
+  return M > 0 && N > 0 && K > 0 && group_size > 0 && swiglu_gemm_applies(M, N, K, group_size, K, ldk_workspace_bytes()) ? 1 : 0;
+}
+
+extern "C" int ldk_w4a16_matmul_swiglu(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                                       const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N,
+                                       int64_t K, int group_size, void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* fn = "w4a16_matmul_swiglu";
+  int gsh_rows = 0;
+  int st = validate(fn, x, ldx, qweight, scales, zeros, out, N, M, N, K, group_size, &gsh_rows);  // out checked below
+  if (st) return st;
+  if (N % 2 || ldo < N / 2 || ldo % 4 || !ldk::aligned(out, 8))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: out [M, N/2] 8-byte aligned with ldo >= N/2 and ldo %% 4 == 0", fn);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
+  if (!swiglu_gemm_applies(M, N, K, group_size, ldx, workspace ? workspace_bytes : 0))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld N=%lld K=%lld does not run the prefill GEMM with paired column "
+                     "groups (ldk_w4a16_matmul_swiglu_applies)", fn, (long long)M, (long long)N, (long long)K);
+  ldk::GemmArgs g{(const half_t*)x, ldx, qweight, (const half_t*)scales, (const half_t*)zeros, (const half_t*)bias,
+                  (half_t*)out, ldo, (int)M, (int)N, (int)K, group_size, workspace, workspace ? workspace_bytes : 0, 0, 0};
+  g.swiglu = 1;
+  return ldk::gemm_launch(ldk::WFmt::kInt4, g, (hipStream_t)stream);
+}
+
 extern "C" int ldk_w4a16_config(int64_t M, int64_t N, int64_t K, int group_size, int* block_n, int* split_k, int* flags) {
   static const char* fn = "w4a16_config";
   if (!block_n || !split_k || !flags) return ldk::fail(LDK_ERR_INVALID, "%s: null block_n, split_k or flags", fn);

@@ -72,6 +72,7 @@ class Backend:
     name = "fp16"
     quantized = False
     merges_attention = False  # attn_linear_norm_linear takes the attention's range partials
+    fuses_prompt_act = False  # linear_norm_linear_act forms the activation in gate_up (prompt rows)
     # the fused attention's launch warms the next weights (QwenRunner.warm_set): fp16 254 -> 259
     # tok/s, W4A16 1305 -> 1361 (e2e, one MI355X)
     warms = True
@@ -107,6 +108,12 @@ class Backend:
         """linear, then norm (+ residual) then linear: the attention output projection, the
         post-attention norm and gate_up (model.py:226-233). Returns (y2, new residual)."""
         return self.norm_linear(self.linear(x, p1), w, eps, residual, p2)
+
+    def linear_norm_linear_act(self, x, p1: Linear, residual, w, eps, p2: Linear):
+        """linear_norm_linear, then the activation of its gate_up output (model.py:226-234).
+        Returns (act, new residual)."""
+        y2, res = self.linear_norm_linear(x, p1, residual, w, eps, p2)
+        return self.act(y2), res
 
 
 class _Int4:
@@ -235,6 +242,20 @@ class OursBackend(_Int4, Backend):
                                            w, eps, p2.qweight, p2.scales, p2.zeros, p2.bias,
                                            config.GROUP_SIZE)
 
+    @property
+    def fuses_prompt_act(self) -> bool:
+        return self.fused
+
+    def linear_norm_linear_act(self, x, p1: Linear, residual, w, eps, p2: Linear):
+        """Prompt rows: the o projection, the post-attention norm with the residual, then gate_up
+        with SwiGLU in the prefill GEMM's epilogue (kernels.fused.w4a16_matmul_swiglu: the same
+        bits as gate_up then SwiGLU, one launch and no [T, 2I] intermediate where the plan is the
+        prefill GEMM). Returns (act, new residual)."""
+        from kernels.fused import w4a16_matmul_swiglu
+
+        h, res = self.norm(self.linear(x, p1), w, eps, residual=residual)
+        return w4a16_matmul_swiglu(h, p2.qweight, p2.scales, p2.zeros, config.GROUP_SIZE, p2.bias), res
+
     def act_linear(self, gate_up, p: Linear):
         """One launch at decode: SwiGLU forms the down projection's activation (kernels.fused)."""
         if not self.fused:
@@ -251,6 +272,7 @@ class OursFP8Backend(OursBackend):
     scale."""
 
     warms = False  # twice the int4 bytes: warming them measured slower (1105 -> 1042 tok/s)
+    fuses_prompt_act = False  # the GEMM's SwiGLU epilogue is wired for W4A16
 
     def __init__(self):
         super().__init__("matmul")
@@ -444,6 +466,7 @@ class QwenRunner:
         self.vt_cache = torch.zeros((n, batch) + fa.vt_cache_shape(self.n_kv, max_len, d), device=dev, dtype=dt)
         self.keys = torch.arange(max_len, device=dev)
         self.merge_attention = True  # see forward: the o projection merges the attention's ranges
+        self.fuse_prompt_act = True  # see forward: SwiGLU in the prompt's gate_up GEMM
         self.warm_weights = True  # see warm_set: the attention launch warms the next weights
         self.fused_attention = (attention == "fused" and dev.type == "cuda"
                                 and fa.supported(d, max_len, batch, 1))
@@ -576,8 +599,12 @@ class QwenRunner:
                 q = self._rope(q.view(B, T, nq, hd), cos, sin)
                 k = self._rope(k.view(B, T, nkv, hd), cos, sin)
                 attn = self._attend(i, q, k, v.view(B, T, nkv, hd), pos)
-            gate_up, residual = be.linear_norm_linear(attn, L.o, residual, L.ln2, eps, L.gate_up)
-            h = be.act_linear(gate_up, L.down)
+            if prompt and self.fuse_prompt_act and be.fuses_prompt_act:
+                act, residual = be.linear_norm_linear_act(attn, L.o, residual, L.ln2, eps, L.gate_up)
+                h = be.linear(act, L.down)
+            else:
+                gate_up, residual = be.linear_norm_linear(attn, L.o, residual, L.ln2, eps, L.gate_up)
+                h = be.act_linear(gate_up, L.down)
         if not all_logits:  # the final norm is per row: normalize the last row only
             h, residual = h[:, -1:], residual[:, -1:]
         return self._logits(h, residual)

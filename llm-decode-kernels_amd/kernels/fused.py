@@ -205,6 +205,35 @@ def attn_linear_rmsnorm_w4a16_matmul(ranges, qweight1, scales1, zeros1, bias1, r
     return y2, h
 
 
+def w4a16_matmul_swiglu(x, qweight, scales, zeros, group_size=128, bias=None):
+    """swiglu_fused(w4a16_matmul(x, W) (+ bias)) for prefill rows, x [..., K] fp16 -> [..., N/2]:
+    one launch where the library's plan for the shape is the prefill GEMM on paired column groups
+    (ldk_w4a16_matmul_swiglu: the g and u halves of the product meet in the GEMM's epilogue), else
+    the two ops; bit for bit the two ops either way."""
+    K = x.shape[-1]
+    N = qweight.shape[1]
+    rows = x.numel() // K
+    fuse = (rows > 16 and x.dtype == torch.float16 and x.is_cuda and N % 2 == 0
+            and _aligned(x, qweight)
+            and bool(_lib.load().ldk_w4a16_matmul_swiglu_applies(rows, N, K, group_size)))
+    if not fuse:
+        return swiglu_fused(w4a16_matmul(x, qweight, scales, zeros, group_size, bias))
+    assert qweight.shape[0] * 8 == K
+    dev = _lib.require_gpu(x, qweight, scales, zeros, bias, what="w4a16_matmul_swiglu")
+    if scales.dtype != torch.float16 or zeros.dtype != torch.float16:
+        raise ValueError("w4a16_matmul_swiglu: scales and zeros must be float16")
+    s, z = scales.contiguous(), zeros.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    out = torch.empty((*x.shape[:-1], N // 2), dtype=torch.float16, device=dev)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w4a16_matmul_swiglu(
+            _lib.ptr(x), K, _lib.ptr(qweight), _lib.ptr(s), _lib.ptr(z), _lib.ptr(b), _lib.ptr(out), N // 2,
+            rows, N, K, group_size, ws, ws_bytes, _lib.stream(dev))
+    _lib.check(st, "w4a16_matmul_swiglu")
+    return out
+
+
 def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
     """y = w8a16_matmul(swiglu_fused(gate_up), wq, scale) (+ bias); gate_up: [..., 2K] fp16,
     wq: [K, N] float8_e4m3fn, scale: [N] fp16. One row runs one launch (ldk_w8a16_swiglu_matmul),
@@ -302,5 +331,5 @@ def attn_w8a16_matmul(ranges, wq, scale, bias=None):
 
 
 __all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "linear_rmsnorm_w4a16_matmul",
-           "attn_linear_rmsnorm_w4a16_matmul", "rmsnorm_w8a16_matmul", "swiglu_w8a16_matmul",
-           "attn_w8a16_matmul"]
+           "attn_linear_rmsnorm_w4a16_matmul", "w4a16_matmul_swiglu", "rmsnorm_w8a16_matmul",
+           "swiglu_w8a16_matmul", "attn_w8a16_matmul"]

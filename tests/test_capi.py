@@ -214,6 +214,28 @@ def test_attention_merge_entries_validate_before_launch():
     assert w4(h_out=ctypes.c_void_p(4100))[0] == _lib.ERR_ALIGN
 
 
+def test_matmul_swiglu_plan_and_validation():
+    """ldk_w4a16_matmul_swiglu runs where the library's plan is the prefill GEMM on paired column
+    groups of 64-row tiles with no K split, and refuses other shapes and bad outputs before any
+    launch."""
+    lib = _lib.load()
+    assert lib.ldk_w4a16_matmul_swiglu_applies(128, 17920, 1536, 128) == 1
+    assert lib.ldk_w4a16_matmul_swiglu_applies(512, 17920, 1536, 128) == 1
+    assert lib.ldk_w4a16_matmul_swiglu_applies(2048, 17920, 1536, 128) == 0  # 128-row tiles
+    assert lib.ldk_w4a16_matmul_swiglu_applies(1, 17920, 1536, 128) == 0     # decode rows
+    assert lib.ldk_w4a16_matmul_swiglu_applies(128, 1536, 8960, 128) == 0    # down: row blocks
+    p = ctypes.c_void_p(256)
+
+    def call(M=128, N=17920, out=p, ldo=8960):
+        return _err(lib.ldk_w4a16_matmul_swiglu(p, 1536, p, p, p, None, out, ldo, M, N, 1536, 128, None, 0, None))
+
+    assert call(ldo=4000)[0] == _lib.ERR_ALIGN       # ldo < N / 2
+    assert call(ldo=8962)[0] == _lib.ERR_ALIGN       # ldo % 4
+    assert call(out=ctypes.c_void_p(260))[0] == _lib.ERR_ALIGN
+    st, msg = call(M=2048)
+    assert st == _lib.ERR_UNSUPPORTED and "applies" in msg
+
+
 def test_w8a16_n_multiple_of_4():
     """The reference masks columns, so any N runs there (N = 40 in tests/test_fp8.py:40); here N
     must be a multiple of 4 (N = 40 plans, N = 42 is refused before any launch)."""

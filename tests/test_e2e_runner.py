@@ -146,10 +146,10 @@ def test_graph_decoder_matches_eager_steps(vocab):
     assert P == 9 and toks == eager
 
 
-def _qwen_heads_model(device, vocab=512, layers=2):
+def _qwen_heads_model(device, vocab=512, layers=2, intermediate=512):
     """Qwen2.5-1.5B attention geometry (12 query / 2 KV heads of 128) in a 2-layer model."""
     cfg = transformers.Qwen2Config(
-        vocab_size=vocab, hidden_size=1536, intermediate_size=512, num_hidden_layers=layers,
+        vocab_size=vocab, hidden_size=1536, intermediate_size=intermediate, num_hidden_layers=layers,
         num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=1024,
         tie_word_embeddings=True, rms_norm_eps=1e-6, rope_theta=1e6,
     )
@@ -218,6 +218,27 @@ def test_attention_merged_in_o_projection_matches_merge_launch(backend):
         torch.testing.assert_close(b.float(), a.float(), atol=2e-2, rtol=2e-2)
     torch.testing.assert_close(merged.k_cache.float(), plain.k_cache.float(), atol=2e-2, rtol=2e-2)
     torch.testing.assert_close(merged.vt_cache.float(), plain.vt_cache.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.gpu
+def test_prompt_swiglu_in_gate_up_changes_no_logit():
+    """The prompt forward on `ours` runs gate_up with SwiGLU in the prefill GEMM's epilogue
+    (QwenRunner.fuse_prompt_act, kernels.fused.w4a16_matmul_swiglu): the prompt's logits at every
+    position and the KV caches are bit-identical to the runner running gate_up then SwiGLU.
+    Qwen2.5-1.5B's MLP (8960) at 128 prompt rows, where the fused epilogue applies."""
+    from kernels import _lib
+
+    assert _lib.load().ldk_w4a16_matmul_swiglu_applies(128, 2 * 8960, 1536, 128) == 1
+    model = _qwen_heads_model("cuda", layers=2, intermediate=8960)
+    fused = QwenRunner(model, make_backend("ours"), max_len=416)
+    plain = QwenRunner(model, make_backend("ours"), max_len=416)
+    plain.fuse_prompt_act = False
+    ids = torch.randint(0, 512, (1, 128), device="cuda")
+    pos = torch.arange(128, device="cuda")
+    a = plain.forward(ids, pos, all_logits=True)
+    b = fused.forward(ids, pos, all_logits=True)
+    assert torch.equal(a, b)
+    assert torch.equal(plain.k_cache, fused.k_cache) and torch.equal(plain.vt_cache, fused.vt_cache)
 
 
 @pytest.mark.gpu

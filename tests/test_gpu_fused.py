@@ -16,7 +16,8 @@ from _util import assert_north_star, bits16, to_np
 from kernels.bench import cases
 from kernels.fp8 import FP8, quantize_fp8, w8a16_matmul
 from kernels.fused import (linear_rmsnorm_w4a16_matmul, rmsnorm_w4a16_matmul,
-                           rmsnorm_w8a16_matmul, swiglu_w4a16_matmul, swiglu_w8a16_matmul)
+                           rmsnorm_w8a16_matmul, swiglu_w4a16_matmul, swiglu_w8a16_matmul,
+                           w4a16_matmul_swiglu)
 from kernels.quant import quantize_rtn
 from kernels.rmsnorm import rmsnorm
 from kernels.swiglu import swiglu_fused
@@ -246,3 +247,30 @@ def test_linear_rmsnorm_pair_column_sliced_scales_and_zeros():
     assert torch.equal(h, hc) and torch.equal(y2, y2c)
     xn = rmsnorm_ref(to_np(hc), wn.numpy(), 1e-6)
     assert_north_star(to_np(y2), _oracle_linear(xn, qw2c, s2v.contiguous(), z2v.contiguous(), None))
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(128, 17920, 1536, False), (65, 17920, 1536, False),
+                                        (256, 17920, 1536, False), (512, 17920, 1536, False),
+                                        (200, 8192, 1536, True), (129, 17920, 1536, False),
+                                        (2048, 17920, 1536, False), (8, 17920, 1536, False)])
+def test_matmul_swiglu_prefill_rows(M, N, K, bias):
+    """w4a16_matmul_swiglu (ldk_w4a16_matmul_swiglu: SwiGLU in the prefill GEMM's epilogue, the g
+    and u halves computed by paired column groups of one workgroup) against w4a16_matmul then
+    swiglu_fused, bit for bit, at prompt rows where the plan is the prefill GEMM on 64-row tiles
+    (ragged last tiles at 65, 129 and 200 rows, a bias, 2 x 64 and 4 x 64 column workgroups) and
+    where it is not (2048 rows: 128-row tiles; 8 rows: the decode kernels), which compose the two
+    ops; and against the oracle chain."""
+    from kernels import _lib
+
+    qw, s, z, b = _weights(N, K, 81, bias)
+    b = None if b is None else b.cuda()
+    x = (torch.randn(M, K, generator=cases.gen(82)) * 0.5).half().cuda()
+    fused = bool(_lib.load().ldk_w4a16_matmul_swiglu_applies(M, N, K, 128))
+    assert fused == (M not in (2048, 8))
+    act = w4a16_matmul_swiglu(x, qw, s, z, 128, b)
+    ref = swiglu_fused(w4a16_matmul(x, qw, s, z, 128, b))
+    assert act.shape == (M, N // 2)
+    assert np.array_equal(bits16(act), bits16(ref))
+    if M <= 256:
+        y = _oracle_linear(x.cpu().numpy(), qw, s, z, None if b is None else b.cpu())
+        assert_north_star(to_np(act), swiglu_ref(y[:, : N // 2].astype(np.float16), y[:, N // 2:].astype(np.float16)))
