@@ -376,6 +376,16 @@ int ldk_w4a16_matmul_swiglu(const void* x, int64_t ldx, const int32_t* qweight, 
                             const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N,
                             int64_t K, int group_size, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The e4m3 twin (weights wq [K, N] e4m3 with the per-column scale, as ldk_w8a16_matmul): out
+ * [M, N/2] = swiglu_fused(x @ (wq * scale) (+ bias)), bit for bit ldk_w8a16_matmul then
+ * ldk_swiglu; no counterpart entry in the reference (its FP8 runner runs the activation as a
+ * kernel of its own, kernels/e2e/model.py:100-118). Only where ldk_w8a16_matmul_swiglu_applies
+ * returns 1; else LDK_ERR_UNSUPPORTED and no launch. */
+int ldk_w8a16_matmul_swiglu_applies(int64_t M, int64_t N, int64_t K);
+int ldk_w8a16_matmul_swiglu(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias,
+                            void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------- greedy decode bookkeeping */
 
 /* idx = argmax(logits[0:V]) (torch.argmax order: NaN largest, lowest index on ties), then

@@ -921,6 +921,43 @@ extern "C" int ldk_w8a16_matmul(const void* x, int64_t ldx, const uint8_t* wq, c
   return p.mfma ? launch_w8_mfma(a, sp, p, (hipStream_t)stream) : launch_w8(a, sp, p, (hipStream_t)stream);
 }
 
+// Prefill rows of gate_up with SwiGLU in the prefill GEMM's epilogue, the e4m3 twin of
+// ldk_w4a16_matmul_swiglu: out [M, N/2] = silu(g) * u of the product's halves, bit for bit
+// ldk_w8a16_matmul then ldk_swiglu, where the library's plan for the shape is the GEMM on paired
+// column groups of at most 4 row tiles with no K split.
+static bool w8_swiglu_gemm_applies(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ws_bytes) {
+  return N % 8 == 0 && w8_uses_gemm(M, N, K, ldx, nullptr, N, 0, 0, 0) &&
+         ldk::gemm_swiglu_applies(ldk::WFmt::kE4M3, M, N, K, 0, ldx, 0, 0, ws_bytes);
+}
+
+extern "C" int ldk_w8a16_matmul_swiglu_applies(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 && w8_swiglu_gemm_applies(M, N, K, K, ldk_workspace_bytes()) ? 1 : 0;
+}
+
+extern "C" int ldk_w8a16_matmul_swiglu(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias,
+                                       void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  static const char* fn = "w8a16_matmul_swiglu";
+  if (!x || !wq || !scale || !out) return ldk::fail(LDK_ERR_INVALID, "%s: null pointer", fn);
+  if (!ldk::aligned(x, 2) || !ldk::aligned(wq, 16) || !ldk::aligned(scale, 2))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: wq must be 16-byte aligned", fn);
+  if (workspace_bytes && (!workspace || !ldk::aligned(workspace, 256)))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: workspace must be a 256-byte aligned pointer", fn);
+  const int64_t wsb = workspace ? workspace_bytes : 0;
+  W8Call c;
+  const int st = w8_plan_call(fn, M, N, K, ldx, nullptr, N, 0, 0, 0, wsb, &c);  // out checked below
+  if (st) return st;
+  if (N % 2 || ldo < N / 2 || ldo % 4 || !ldk::aligned(out, 8))
+    return ldk::fail(LDK_ERR_ALIGN, "%s: out [M, N/2] 8-byte aligned with ldo >= N/2 and ldo %% 4 == 0", fn);
+  if (!w8_swiglu_gemm_applies(M, N, K, ldx, wsb))
+    return ldk::fail(LDK_ERR_UNSUPPORTED, "%s: M=%lld N=%lld K=%lld does not run the prefill GEMM with paired column "
+                     "groups (ldk_w8a16_matmul_swiglu_applies)", fn, (long long)M, (long long)N, (long long)K);
+  ldk::GemmArgs g{(const half_t*)x, ldx, wq, (const half_t*)scale, nullptr, (const half_t*)bias, (half_t*)out, ldo,
+                  (int)M, (int)N, (int)K, 0, workspace, wsb, 0, 0};
+  g.swiglu = 1;
+  return ldk::gemm_launch(ldk::WFmt::kE4M3, g, (hipStream_t)stream);
+}
+
 extern "C" int ldk_w8a16_config(int64_t M, int64_t N, int64_t K, int* block_n, int* split_k, int* flags) {
   static const char* fn = "w8a16_config";
   if (!block_n || !split_k || !flags) return ldk::fail(LDK_ERR_INVALID, "%s: null block_n, split_k or flags", fn);

@@ -49,7 +49,12 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 __device__ __forceinline__ half_t silu_f16(half_t g) {
   const float f = (float)g;
   const float e = __builtin_amdgcn_exp2f(f * -1.44269504088896341f);
-  return (half_t)(f * __builtin_amdgcn_rcpf(1.0f + e));
+  float p = f * __builtin_amdgcn_rcpf(1.0f + e);
+  // the product is an fp32 value, then rounded to fp16: without this the compiler may form
+  // v_fma_mix*_f16 in some kernels, one rounding of the exact product, which differs from the
+  // fp32-then-fp16 result in about 1 of 8000 values
+  asm volatile("" : "+v"(p));
+  return (half_t)p;
 }
 
 // RMSNorm's staged value of one element with the steps of the standalone RMSNorm kernel:

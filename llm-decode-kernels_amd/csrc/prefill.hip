@@ -70,6 +70,11 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("" : : : "memory");
 }
 
+// The e4m3 epilogue's scaled accumulators are fp32 values, then the bias is added in fp32, then
+// the sum is rounded to fp16 (the split-K reduction's steps). Without this the compiler may
+// contract the three into one v_fma_mixlo_f16, a single rounding, in some kernels and not others.
+__device__ __forceinline__ void pin_f32(float4_t& v) { asm volatile("" : "+v"(v)); }
+
 // Workgroup barrier that is also a compiler memory barrier, without the vmcnt(0) a C++ fence adds
 // (the ring keeps later stages' loads in flight across it).
 __device__ __forceinline__ void ring_barrier() {
@@ -384,7 +389,10 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
-          for (int j = 0; j < NT; ++j) acc[t][j] *= cs[j];
+          for (int j = 0; j < NT; ++j) {
+            acc[t][j] *= cs[j];
+            pin_f32(acc[t][j]);
+          }
       }
       float4_t b4 = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
       if (a.bias) b4 = float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
@@ -443,7 +451,10 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[t][j] *= cs[j];
+      for (int j = 0; j < NT; ++j) {
+        acc[t][j] *= cs[j];
+        pin_f32(acc[t][j]);
+      }
   }
   float4_t b4 = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
   if (a.bias) b4 = float4_t{(float)a.bias[c], (float)a.bias[c + 1], (float)a.bias[c + 2], (float)a.bias[c + 3]};
@@ -699,6 +710,12 @@ bool gemm_swiglu_applies(WFmt f, int64_t M, int64_t N, int64_t K, int group_size
   if (N % 2 || !gemm_supported(f, M, N, K, group_size, ldx)) return false;
   const GemmShape sh = pick_shape(f, M, N, K, block_n, split_k, ws_bytes);
   const int steps = (int)(K / kStep), kps = (steps + sh.splits - 1) / sh.splits;
+  // e4m3 on 2-wave tiles: a wave's 64 columns are 64 bytes per K row, so the g (or u) wave of a
+  // workgroup reads half of each 128-byte line and the next workgroup (on another XCD) the other
+  // half; gate_up M = 32 / 128 measured 13.50 / 20.25 us composed against 14.63 / 24.51 fused.
+  // From 4 waves (M = 256 / 512: 28.20 / 42.02 -> 26.38 / 39.26 us) the pair's g waves cover
+  // whole lines. int4 rows are 256 bytes per wave.
+  if (f == WFmt::kE4M3 && sh.waves < 4) return false;
   return swiglu_tile(sh.waves, sh.mt) && (steps + kps - 1) / kps == 1 && (N / 2) % (64 * (sh.waves / 2)) == 0;
 }
 

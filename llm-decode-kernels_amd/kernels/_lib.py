@@ -83,6 +83,8 @@ SIGNATURES = {
     "ldk_w4a16_matmul_swiglu_applies": [_i64, _i64, _i64, _i32],
     "ldk_w4a16_matmul_swiglu": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64,
                                 _vp],
+    "ldk_w8a16_matmul_swiglu_applies": [_i64, _i64, _i64],
+    "ldk_w8a16_matmul_swiglu": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp],
 }
 
 _lock = threading.Lock()

@@ -272,7 +272,6 @@ class OursFP8Backend(OursBackend):
     scale."""
 
     warms = False  # twice the int4 bytes: warming them measured slower (1105 -> 1042 tok/s)
-    fuses_prompt_act = False  # the GEMM's SwiGLU epilogue is wired for W4A16
 
     def __init__(self):
         super().__init__("matmul")
@@ -302,6 +301,15 @@ class OursFP8Backend(OursBackend):
         return rmsnorm_w8a16_matmul(x, w, eps, residual, p.qweight, p.scales, bias=p.bias)
 
     linear_norm_linear = Backend.linear_norm_linear  # the residual-statistics pair is W4A16
+
+    def linear_norm_linear_act(self, x, p1: Linear, residual, w, eps, p2: Linear):
+        """Prompt rows: the o projection, the post-attention norm with the residual, then gate_up
+        with SwiGLU in the e4m3 prefill GEMM's epilogue (kernels.fused.w8a16_matmul_swiglu, the
+        same bits as gate_up then SwiGLU). Returns (act, new residual)."""
+        from kernels.fused import w8a16_matmul_swiglu
+
+        h, res = self.norm(self.linear(x, p1), w, eps, residual=residual)
+        return w8a16_matmul_swiglu(h, p2.qweight, p2.scales, bias=p2.bias), res
 
     def attn_linear_norm_linear(self, ranges, p1: Linear, residual, w, eps, p2: Linear):
         """linear_norm_linear with x the decode attention left as range partials: the FP8 o

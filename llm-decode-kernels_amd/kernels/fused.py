@@ -234,6 +234,35 @@ def w4a16_matmul_swiglu(x, qweight, scales, zeros, group_size=128, bias=None):
     return out
 
 
+def w8a16_matmul_swiglu(x, wq, scale, bias=None):
+    """swiglu_fused(w8a16_matmul(x, wq, scale) (+ bias)) for prefill rows, x [..., K] fp16, wq
+    [K, N] float8_e4m3fn -> [..., N/2]: one launch where the library's plan for the shape is the
+    prefill GEMM on paired column groups (ldk_w8a16_matmul_swiglu), else the two ops; bit for bit
+    the two ops either way."""
+    from kernels.fp8 import FP8, w8a16_matmul
+
+    K = x.shape[-1]
+    N = wq.shape[1]
+    rows = x.numel() // K
+    fuse = (rows > 16 and x.dtype == torch.float16 and x.is_cuda and N % 2 == 0 and wq.dtype == FP8
+            and scale.dtype == torch.float16 and _aligned(x, wq)
+            and bool(_lib.load().ldk_w8a16_matmul_swiglu_applies(rows, N, K)))
+    if not fuse:
+        return swiglu_fused(w8a16_matmul(x, wq, scale, bias=bias))
+    assert wq.shape[0] == K
+    dev = _lib.require_gpu(x, wq, scale, bias, what="w8a16_matmul_swiglu")
+    s = scale.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    out = torch.empty((*x.shape[:-1], N // 2), dtype=torch.float16, device=dev)
+    with _lib.device_guard(dev):
+        ws, ws_bytes = _lib.workspace(dev)
+        st = _lib.load().ldk_w8a16_matmul_swiglu(
+            _lib.ptr(x), K, _lib.ptr(wq), _lib.ptr(s), _lib.ptr(b), _lib.ptr(out), N // 2, rows, N, K,
+            ws, ws_bytes, _lib.stream(dev))
+    _lib.check(st, "w8a16_matmul_swiglu")
+    return out
+
+
 def swiglu_w8a16_matmul(gate_up, wq, scale, bias=None):
     """y = w8a16_matmul(swiglu_fused(gate_up), wq, scale) (+ bias); gate_up: [..., 2K] fp16,
     wq: [K, N] float8_e4m3fn, scale: [N] fp16. One row runs one launch (ldk_w8a16_swiglu_matmul),
@@ -331,5 +360,5 @@ def attn_w8a16_matmul(ranges, wq, scale, bias=None):
 
 
 __all__ = ["rmsnorm_w4a16_matmul", "swiglu_w4a16_matmul", "linear_rmsnorm_w4a16_matmul",
-           "attn_linear_rmsnorm_w4a16_matmul", "w4a16_matmul_swiglu", "rmsnorm_w8a16_matmul",
+           "attn_linear_rmsnorm_w4a16_matmul", "w4a16_matmul_swiglu", "w8a16_matmul_swiglu", "rmsnorm_w8a16_matmul",
            "swiglu_w8a16_matmul", "attn_w8a16_matmul"]

@@ -236,6 +236,28 @@ def test_matmul_swiglu_plan_and_validation():
     assert st == _lib.ERR_UNSUPPORTED and "applies" in msg
 
 
+def test_w8a16_matmul_swiglu_plan_and_validation():
+    """The e4m3 twin: the GEMM on paired 4-wave column groups (gate_up from 200 to 512 rows),
+    refused on 2-wave tiles (whose waves read half lines), the decode rows, the row blocks and
+    bad outputs before any launch."""
+    lib = _lib.load()
+    assert lib.ldk_w8a16_matmul_swiglu_applies(256, 17920, 1536) == 1
+    assert lib.ldk_w8a16_matmul_swiglu_applies(512, 17920, 1536) == 1
+    assert lib.ldk_w8a16_matmul_swiglu_applies(128, 17920, 1536) == 0    # 2-wave tiles
+    assert lib.ldk_w8a16_matmul_swiglu_applies(8, 17920, 1536) == 0      # decode rows
+    assert lib.ldk_w8a16_matmul_swiglu_applies(256, 1536, 8960) == 0     # down
+    p = ctypes.c_void_p(256)
+
+    def call(M=256, N=17920, out=p, ldo=8960):
+        return _err(lib.ldk_w8a16_matmul_swiglu(p, 1536, p, p, None, out, ldo, M, N, 1536, None, 0, None))
+
+    assert call(ldo=4000)[0] == _lib.ERR_ALIGN
+    assert call(out=ctypes.c_void_p(260))[0] == _lib.ERR_ALIGN
+    assert call(N=17922)[0] == _lib.ERR_UNSUPPORTED  # N % 4
+    st, msg = call(M=8)
+    assert st == _lib.ERR_UNSUPPORTED and "applies" in msg
+
+
 def test_w8a16_n_multiple_of_4():
     """The reference masks columns, so any N runs there (N = 40 in tests/test_fp8.py:40); here N
     must be a multiple of 4 (N = 40 plans, N = 42 is refused before any launch)."""

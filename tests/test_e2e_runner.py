@@ -221,20 +221,27 @@ def test_attention_merged_in_o_projection_matches_merge_launch(backend):
 
 
 @pytest.mark.gpu
-def test_prompt_swiglu_in_gate_up_changes_no_logit():
-    """The prompt forward on `ours` runs gate_up with SwiGLU in the prefill GEMM's epilogue
-    (QwenRunner.fuse_prompt_act, kernels.fused.w4a16_matmul_swiglu): the prompt's logits at every
+@pytest.mark.parametrize("backend,T", [("ours", 128), ("ours_fp8", 256)])
+def test_prompt_swiglu_in_gate_up_changes_no_logit(backend, T):
+    """The prompt forward on `ours` and `ours_fp8` runs gate_up with SwiGLU in the prefill GEMM's
+    epilogue (QwenRunner.fuse_prompt_act, kernels.fused.w4a16_matmul_swiglu and
+    w8a16_matmul_swiglu): the prompt's logits at every
     position and the KV caches are bit-identical to the runner running gate_up then SwiGLU.
-    Qwen2.5-1.5B's MLP (8960) at 128 prompt rows, where the fused epilogue applies."""
+    Qwen2.5-1.5B's MLP (8960) at 128 prompt rows (int4) and 256 (e4m3), where the fused epilogue
+    applies."""
     from kernels import _lib
 
-    assert _lib.load().ldk_w4a16_matmul_swiglu_applies(128, 2 * 8960, 1536, 128) == 1
+    lib = _lib.load()
+    applies = (lib.ldk_w4a16_matmul_swiglu_applies(T, 2 * 8960, 1536, 128) if backend == "ours"
+               else lib.ldk_w8a16_matmul_swiglu_applies(T, 2 * 8960, 1536))
+    assert applies == 1
     model = _qwen_heads_model("cuda", layers=2, intermediate=8960)
-    fused = QwenRunner(model, make_backend("ours"), max_len=416)
-    plain = QwenRunner(model, make_backend("ours"), max_len=416)
+    fused = QwenRunner(model, make_backend(backend), max_len=416)
+    plain = QwenRunner(model, make_backend(backend), max_len=416)
+    assert fused.backend.fuses_prompt_act
     plain.fuse_prompt_act = False
-    ids = torch.randint(0, 512, (1, 128), device="cuda")
-    pos = torch.arange(128, device="cuda")
+    ids = torch.randint(0, 512, (1, T), device="cuda")
+    pos = torch.arange(T, device="cuda")
     a = plain.forward(ids, pos, all_logits=True)
     b = fused.forward(ids, pos, all_logits=True)
     assert torch.equal(a, b)

@@ -17,7 +17,7 @@ from kernels.bench import cases
 from kernels.fp8 import FP8, quantize_fp8, w8a16_matmul
 from kernels.fused import (linear_rmsnorm_w4a16_matmul, rmsnorm_w4a16_matmul,
                            rmsnorm_w8a16_matmul, swiglu_w4a16_matmul, swiglu_w8a16_matmul,
-                           w4a16_matmul_swiglu)
+                           w4a16_matmul_swiglu, w8a16_matmul_swiglu)
 from kernels.quant import quantize_rtn
 from kernels.rmsnorm import rmsnorm
 from kernels.swiglu import swiglu_fused
@@ -274,3 +274,26 @@ def test_matmul_swiglu_prefill_rows(M, N, K, bias):
     if M <= 256:
         y = _oracle_linear(x.cpu().numpy(), qw, s, z, None if b is None else b.cpu())
         assert_north_star(to_np(act), swiglu_ref(y[:, : N // 2].astype(np.float16), y[:, N // 2:].astype(np.float16)))
+
+
+@pytest.mark.parametrize("M,N,K,bias,fused", [(256, 17920, 1536, False, True), (300, 17920, 1536, True, True),
+                                              (512, 17920, 1536, False, True), (1024, 8192, 1536, True, True),
+                                              (128, 17920, 1536, False, False), (33, 17920, 1536, True, False),
+                                              (8, 17920, 1536, False, False)])
+def test_w8a16_matmul_swiglu_prefill_rows(M, N, K, bias, fused):
+    """w8a16_matmul_swiglu (ldk_w8a16_matmul_swiglu, the e4m3 prefill GEMM with SwiGLU in its
+    epilogue) against w8a16_matmul then swiglu_fused, bit for bit, where the plan fuses (4-wave
+    tiles; ragged 300 rows, a bias) and where it composes the two ops (2-wave tiles at 33 and 128
+    rows, the decode kernels at 8). The fused epilogue keeps the column scale, the bias add and
+    the fp16 rounding as three steps, as the plain GEMM and the split-K reduction do."""
+    from kernels import _lib
+
+    w = (torch.randn(N, K, generator=cases.gen(91)) * 0.05).half().cuda()
+    wq, sc = quantize_fp8(w)
+    b = (torch.randn(N, generator=cases.gen(92)) * 0.1).half().cuda() if bias else None
+    x = (torch.randn(M, K, generator=cases.gen(93)) * 0.5).half().cuda()
+    assert bool(_lib.load().ldk_w8a16_matmul_swiglu_applies(M, N, K)) == fused
+    act = w8a16_matmul_swiglu(x, wq, sc, b)
+    ref = swiglu_fused(w8a16_matmul(x, wq, sc, bias=b))
+    assert act.shape == (M, N // 2)
+    assert np.array_equal(bits16(act), bits16(ref))
