@@ -405,27 +405,45 @@ __device__ __forceinline__ void gemm_body(const ldk::GemmArgs& a, int kps, float
                             (half_t)(acc[t][3][i] + b4[3])};
       ring_barrier();  // every wave is past its last read of the stage slots
       static_assert(HW <= 2, "the pairs' exchange slots are st0 and st1");
-      half4_t* xs = reinterpret_cast<half4_t*>((up ? wave - HW : wave) == 0 ? st0 : st1);
-      if (up) {
+      static_assert(MT % 2 == 0, "the pair splits the row tiles");
+      // the g wave finishes row tiles [0, MT/2) and the u wave [MT/2, MT): each hands the other
+      // the half of its tile that the other finishes, so both waves evaluate silu and store
+      constexpr int MH2 = MT / 2;
+      half4_t* const xs = reinterpret_cast<half4_t*>((up ? wave - HW : wave) == 0 ? st0 : st1);
+      half4_t* const to_u = xs;                 // g of tiles [MH2, MT)
+      half4_t* const to_g = xs + MH2 * 4 * 64;  // u of tiles [0, MH2)
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xs[(t * 4 + i) * 64 + lane] = o[t][i];
-      }
-      ring_barrier();
-      if (up) return;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
+      for (int t = 0; t < MH2; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = 16 * t + 4 * kb + i;
-          const half4_t u = xs[(t * 4 + i) * 64 + lane];
-          half4_t v;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] = ldk::silu_f16(o[t][i][j]);
-          if (r < mrows) *reinterpret_cast<half4_t*>(a.out + (int64_t)(m0 + r) * a.ldo + c) = v * u;  // fp16 multiply
+          if (up)
+            to_g[(t * 4 + i) * 64 + lane] = o[t][i];
+          else
+            to_u[(t * 4 + i) * 64 + lane] = o[MH2 + t][i];
         }
-      }
+      ring_barrier();
+      auto finish = [&](auto tb_) {
+        constexpr int TB = decltype(tb_)::value;  // the first row tile this wave finishes
+        const int co = TB ? c - a.N / 2 : c;      // the g column of the pair
+        const half4_t* from = TB ? to_u : to_g;
+#pragma unroll
+        for (int t = 0; t < MH2; ++t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * (TB + t) + 4 * kb + i;
+            const half4_t mine = o[TB + t][i], other = from[(t * 4 + i) * 64 + lane];
+            const half4_t g = TB ? other : mine, u = TB ? mine : other;
+            half4_t v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = ldk::silu_f16(g[j]);
+            if (r < mrows) *reinterpret_cast<half4_t*>(a.out + (int64_t)(m0 + r) * a.ldo + co) = v * u;  // fp16 multiply
+          }
+        }
+      };
+      if (up)
+        finish(std::integral_constant<int, MH2>{});
+      else
+        finish(std::integral_constant<int, 0>{});
       return;
     }
   }
