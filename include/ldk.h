@@ -369,8 +369,9 @@ int ldk_w4a16_rmsnorm_stats_matmul(const void* h, const float* row_stats, int ns
  * ldo % 4 == 0, 8-byte aligned) = swiglu_fused(x @ dequant(W)^T (+ bias)) with g the product's
  * columns [0, N/2) and u [N/2, N): the standalone SwiGLU's steps on the fp16 products, so bit for
  * bit ldk_w4a16_matmul then ldk_swiglu. Only where ldk_w4a16_matmul_swiglu_applies(M, N, K,
- * group_size) returns 1 (the library's plan for the shape is the prefill GEMM on paired column
- * groups of at most 4 row tiles, with no K split); else LDK_ERR_UNSUPPORTED and no launch. */
+ * group_size) returns 1 (the library's plan for the shape is the prefill GEMM on tiles of at most
+ * 64 rows with an even number of column groups and no K split); else LDK_ERR_UNSUPPORTED and no
+ * launch. */
 int ldk_w4a16_matmul_swiglu_applies(int64_t M, int64_t N, int64_t K, int group_size);
 int ldk_w4a16_matmul_swiglu(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
                             const void* zeros, const void* bias, void* out, int64_t ldo, int64_t M, int64_t N,
@@ -380,7 +381,8 @@ int ldk_w4a16_matmul_swiglu(const void* x, int64_t ldx, const int32_t* qweight, 
  * [M, N/2] = swiglu_fused(x @ (wq * scale) (+ bias)), bit for bit ldk_w8a16_matmul then
  * ldk_swiglu; no counterpart entry in the reference (its FP8 runner runs the activation as a
  * kernel of its own, kernels/e2e/model.py:100-118). Only where ldk_w8a16_matmul_swiglu_applies
- * returns 1; else LDK_ERR_UNSUPPORTED and no launch. */
+ * returns 1 (as above, on 4-wave tiles only: gate_up 17920x1536 from 200 to 512 rows); else
+ * LDK_ERR_UNSUPPORTED and no launch. */
 int ldk_w8a16_matmul_swiglu_applies(int64_t M, int64_t N, int64_t K);
 int ldk_w8a16_matmul_swiglu(const void* x, int64_t ldx, const uint8_t* wq, const void* scale, const void* bias,
                             void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
